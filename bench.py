@@ -1,0 +1,191 @@
+#!/usr/bin/env python3
+"""Benchmark of the small-M affine-quantised matmul on one MI355X.
+
+Workload (the headline configuration): y[M,17408] = x[M,5120] . dequant(W)^T, W 4-bit
+group 64 in MLX's affine layout, bf16 activations / scales / biases / output, M swept over
+1, 2, 4, 6, 8.  A "step" is one call at M = 8 (a verify pass's width).
+
+Method:
+  * 8 distinct weight sets (~400 MB, more than the 256 MB Infinity Cache) are rotated so
+    every call streams its weights from HBM;
+  * the `steps` calls of one M are captured into one HIP graph on a non-default stream and
+    replayed; HIP events on that stream bracket the replay (plus a device synchronize on
+    both sides), so `us_per_call` is back-to-back time per call including launch gaps;
+  * algorithmic bytes per call = N*K*bits/8 + 2*N*(K/gs)*2 + M*K*2 + M*N*2;
+  * the CPU baseline is the oracle's fp32 restatement of MLX's CPU algorithm (dequantise a
+    group, multiply-accumulate), OpenMP over the host cores, timed on a bounded sample.
+
+Prints ONE JSON line.  --gpus > 1 is refused: this build measures one GPU.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "dflash-swift_amd"))
+
+N_OUT, K_IN, BITS, GS = 17408, 5120, 4, 64
+HBM_PEAK_GBS = 8000.0
+
+
+def algorithmic_bytes(M, N=N_OUT, K=K_IN, bits=BITS, gs=GS):
+    return N * K * bits // 8 + 2 * N * (K // gs) * 2 + M * K * 2 + M * N * 2
+
+
+def make_sets(torch, nsets, N, K, bits, gs, dev, seed=1):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    sets = []
+    for _ in range(nsets):
+        w = torch.randint(-(2 ** 31), 2 ** 31 - 1, (N, K * bits // 32), dtype=torch.int32,
+                          device=dev, generator=g)
+        s = (torch.randn(N, K // gs, device=dev, generator=g) * 0.02).abs().to(torch.bfloat16)
+        b = (torch.randn(N, K // gs, device=dev, generator=g) * 0.01).to(torch.bfloat16)
+        sets.append((w, s, b))
+    return sets
+
+
+def time_m(torch, ctx, stream, sets, M, steps, warmup, N, K, bits, gs, ws, wsb):
+    """Average microseconds per call over `steps` graph-replayed calls at row count M."""
+    import dflash_qmm
+    dev = sets[0][0].device
+    g = torch.Generator(device=dev)
+    g.manual_seed(100 + M)
+    x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+    y = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+    B = dflash_qmm.BF16
+
+    def issue(count, start):
+        for i in range(count):
+            w, s, b = sets[(start + i) % len(sets)]
+            ctx.qmm_raw(x, w, s, b, y, M, N, K, bits, gs, B, B, B, ws=ws, ws_bytes=wsb,
+                        stream=stream)
+
+    torch.cuda.synchronize()
+    ctx.graph_begin(stream)
+    issue(steps, 0)
+    graph = ctx.graph_end(stream)
+    with torch.cuda.stream(stream):
+        issue(warmup, 1)               # eager warm-up (also checks the eager path)
+        graph.launch(stream)           # graph warm-up
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        graph.launch(stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+    graph.close()
+    return e0.elapsed_time(e1) * 1000.0 / steps
+
+
+def cpu_baseline(seconds):
+    """The oracle's OpenMP fp32 restatement on a bounded sample of the M=8 workload."""
+    import numpy as np
+    from oracle.qmm_oracle import COracle, make_case
+    orc = COracle()
+    n_sample = 2048
+    c = make_case(8, n_sample, K_IN, bits=BITS, gs=GS, seed=5)
+    orc.qmm_f32(c)  # warm
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        orc.qmm_f32(c)
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or calls >= 1000:
+            break
+    per_call_sample = el / calls
+    per_call_full = per_call_sample * (N_OUT / n_sample)  # rows are independent
+    us = per_call_full * 1e6
+    return {
+        "value": round(algorithmic_bytes(8) / per_call_full / 1e9, 3),
+        "unit": "GB/s",
+        "us_per_call": round(us, 1),
+        "cores": orc.num_threads(),
+        "kind": "port",
+        "sample": (f"M=8 K=5120 4-bit g64 bf16, {n_sample} of 17408 output rows, {calls} calls "
+                   f"in {el:.1f}s, scaled to all rows"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--sets", type=int, default=8, help="rotated weight sets")
+    ap.add_argument("--ms", default="1,2,4,6,8")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the path is single-GPU, see the sharding notes in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import dflash_qmm
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    ctx = dflash_qmm.Context(0)
+    stream = torch.cuda.Stream(device=dev)
+    sets = make_sets(torch, args.sets, N_OUT, K_IN, BITS, GS, dev)
+    ms = [int(v) for v in args.ms.split(",")]
+    if 8 not in ms:
+        ms.append(8)
+    wsb = max(ctx.workspace_bytes(m, N_OUT, K_IN, BITS, GS) for m in ms)
+    ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
+
+    torch.cuda.synchronize()
+    us = {}
+    for m in ms:
+        us[m] = time_m(torch, ctx, stream, sets, m, args.steps, args.warmup, N_OUT, K_IN, BITS,
+                       GS, ws, ws.numel())
+        print(f"[bench] M={m}: {us[m]:.2f} us/call, "
+              f"{algorithmic_bytes(m) / us[m] / 1e3:.0f} GB/s", file=sys.stderr, flush=True)
+
+    gbs = {m: algorithmic_bytes(m) / (us[m] * 1e-6) / 1e9 for m in ms}
+    achieved = gbs[8]
+    out = {
+        "metric": "us/call + HBM GB/s, 4-bit qmatmul K5120xN17408, M=1..8; M8/M1 time ratio",
+        "value": round(achieved, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us[8] / 1000.0, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "affine qmm 4-bit g64, K=5120, N=17408, bf16, M=8 per step",
+            "M_sweep": ms,
+            "rotated_weight_sets": args.sets,
+        },
+        "us_per_call": {str(m): round(us[m], 3) for m in ms},
+        "gbs_by_M": {str(m): round(gbs[m], 1) for m in ms},
+        "m8_m1_ratio": round(us[8] / us[1], 4) if 1 in us else None,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,39 @@
+/*
+ * qmm_internal.h -- declarations shared by the runtime and the drop-in layer sources.
+ */
+#ifndef DFQ_QMM_INTERNAL_H
+#define DFQ_QMM_INTERNAL_H
+
+#include <cstddef>
+
+#include "dflash_qmm.h"
+
+namespace dfq {
+
+/* The fast kernel's work split for one problem shape (see qmm_params.h). */
+struct Plan {
+    int kss = 0;        /* k per super-step                                  */
+    int T = 0;          /* column tiles of 16                                */
+    int SS = 0;         /* super-steps per k-block                           */
+    int nkb = 0;        /* k-blocks                                          */
+    int Gkb = 0;        /* workgroups per k-block                            */
+    int nslot_kb = 0;   /* partial slots per tile per k-block                */
+    int kr = 0;         /* k elements per k-block                            */
+    int rs = 0;         /* LDS bytes per staged x row                        */
+    int xsum_off = 0;   /* LDS offset of the per-group x sums                */
+    int slot_off = 0;   /* LDS offset of the wave partial slots              */
+    int lds_bytes = 0;  /* dynamic LDS requested per workgroup               */
+    bool need_ws = false;
+    size_t ws_counter_bytes = 0;
+    size_t ws_bytes = 0;
+};
+
+dfq_status fail(dfq_status s, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int kss_for(int bits, int gs);
+bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_max, Plan* pl);
+dfq_status check_fast_args(const dfq_ctx* ctx, int M, int N, int K, int bits, int gs,
+                           dfq_dtype xdt, dfq_dtype sdt, dfq_dtype ydt);
+
+}  // namespace dfq
+
+#endif

@@ -1,0 +1,598 @@
+/*
+ * qmm_runtime.cpp -- the C ABI of include/dflash_qmm.h: code-object loading, the work
+ * split of the fast kernel, launches, workspace, graph capture.
+ *
+ * The gfx950 code object built from qmm_kernels.hip is linked into this library with
+ * .incbin and loaded with hipModuleLoadData, so the library is one self-contained file.
+ */
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "dflash_qmm.h"
+#include "qmm_internal.h"
+#include "qmm_params.h"
+
+#ifndef DFQ_HSACO_PATH
+#error "DFQ_HSACO_PATH must name the gfx950 code object to embed"
+#endif
+
+__asm__(".section .rodata.dfq_hsaco,\"a\",@progbits\n"
+        ".p2align 12\n"
+        ".globl dfq_hsaco_begin\n"
+        ".hidden dfq_hsaco_begin\n"
+        "dfq_hsaco_begin:\n"
+        ".incbin \"" DFQ_HSACO_PATH "\"\n"
+        ".globl dfq_hsaco_end\n"
+        ".hidden dfq_hsaco_end\n"
+        "dfq_hsaco_end:\n"
+        ".byte 0\n"
+        ".previous\n");
+extern "C" const char dfq_hsaco_begin[];
+extern "C" const char dfq_hsaco_end[];
+
+namespace {
+
+thread_local std::string g_last_error;
+
+constexpr int kThreads = 512;         // qmm_mt8 workgroup size (8 waves)
+constexpr int kMaxStageItems = 12;    // must match qmm_kernels.hip
+constexpr int kWaveSlotsBytes = 8 * 2 * 512;
+
+struct PlanKey {
+    int M, N, K, bits, gs;
+    bool operator==(const PlanKey& o) const {
+        return M == o.M && N == o.N && K == o.K && bits == o.bits && gs == o.gs;
+    }
+};
+struct PlanKeyHash {
+    size_t operator()(const PlanKey& k) const {
+        uint64_t h = 1469598103934665603ull;
+        for (int v : {k.M, k.N, k.K, k.bits, k.gs}) {
+            h ^= (uint64_t)(uint32_t)v;
+            h *= 1099511628211ull;
+        }
+        return (size_t)h;
+    }
+};
+
+}  // namespace
+
+struct dfq_ctx {
+    int device = 0;
+    int num_cus = 0;
+    size_t lds_max = 0;
+    hipModule_t module = nullptr;
+    hipFunction_t mt8[2][3][2] = {};  // [bits 4/8][gs 32/64/128][bf16/f16]
+    hipFunction_t generic = nullptr;
+    hipFunction_t fill = nullptr;
+    std::mutex mu;
+    std::unordered_map<PlanKey, dfq::Plan, PlanKeyHash> plans;
+};
+
+struct dfq_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int device = 0;
+};
+
+namespace dfq {
+
+dfq_status fail(dfq_status s, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return s;
+}
+
+dfq_status hip_fail(hipError_t e, const char* what) {
+    return fail(DFQ_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+/* Makes ctx's device current for the scope and restores the caller's afterwards. */
+struct DeviceGuard {
+    int prev = -1;
+    bool ok = true;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) ok = hipSetDevice(dev) == hipSuccess;
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+int kss_for(int bits, int gs) {
+    const int kstep = 512 / bits;
+    const int ns = bits == 4 ? (gs == 128 ? 2 : 1) : gs / 32;
+    return kstep * ns;
+}
+
+static int64_t owner_wg(int64_t u, int64_t U, int64_t G) { return (G * (u + 1) - 1) / U; }
+
+bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_max, Plan* pl) {
+    const int kss = kss_for(bits, gs);
+    if (M < 1 || M > 8 || N < 1 || K < kss || K % kss) return false;
+    const int ss_total = K / kss;
+    int nkb = 0, kr = 0;
+    size_t lds = 0;
+    for (int d = 1; d <= ss_total; ++d) {
+        if (ss_total % d) continue;
+        const int k = K / d;
+        if ((int64_t)M * (k / 8) > (int64_t)kMaxStageItems * kThreads) continue;
+        const size_t rs = (size_t)2 * k + 16;
+        const size_t need = (size_t)(M + 1) * rs + (size_t)(k / gs) * 32 + kWaveSlotsBytes;
+        if (need > lds_max) continue;
+        nkb = d;
+        kr = k;
+        lds = need;
+        break;
+    }
+    if (!nkb) return false;
+    Plan p{};
+    p.kss = kss;
+    p.T = (N + 15) / 16;
+    p.nkb = nkb;
+    p.kr = kr;
+    p.SS = ss_total / nkb;
+    const int64_t U = (int64_t)p.T * p.SS;
+    int64_t G = std::max(1, num_cus / nkb);
+    if (G > U) G = U;
+    p.Gkb = (int)G;
+    int nslot = 1;
+    for (int64_t t = 0; t < p.T; ++t) {
+        const int64_t c0 = owner_wg(t * p.SS, U, G), c1 = owner_wg(t * p.SS + p.SS - 1, U, G);
+        nslot = std::max<int>(nslot, (int)(c1 - c0 + 1));
+    }
+    p.nslot_kb = nslot;
+    p.rs = 2 * kr + 16;
+    p.xsum_off = (M + 1) * p.rs;
+    p.xsum_off = (p.xsum_off + 15) & ~15;
+    p.slot_off = p.xsum_off + (kr / gs) * 32;
+    /* Ask for more than half the CU's LDS so that exactly one workgroup lands per CU. */
+    size_t want = std::max(lds, lds_max / 2 + 256);
+    p.lds_bytes = (int)std::min(want, lds_max);
+    p.need_ws = nkb > 1 || nslot > 1;
+    p.ws_counter_bytes = ((size_t)p.T * 4 + 255) & ~(size_t)255;
+    p.ws_bytes = p.need_ws ? p.ws_counter_bytes + (size_t)p.T * nkb * nslot * 128 * 4 : 0;
+    *pl = p;
+    return true;
+}
+
+static dfq_status get_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, Plan* out) {
+    PlanKey key{M, N, K, bits, gs};
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    auto it = ctx->plans.find(key);
+    if (it != ctx->plans.end()) {
+        *out = it->second;
+        return DFQ_OK;
+    }
+    Plan p;
+    if (!make_plan(M, N, K, bits, gs, ctx->num_cus, ctx->lds_max, &p))
+        return fail(DFQ_ERR_UNSUPPORTED, "no work split for M=%d N=%d K=%d bits=%d gs=%d", M, N,
+                    K, bits, gs);
+    ctx->plans.emplace(key, p);
+    *out = p;
+    return DFQ_OK;
+}
+
+static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+dfq_status check_fast_args(const dfq_ctx* ctx, int M, int N, int K, int bits, int gs,
+                           dfq_dtype xdt, dfq_dtype sdt, dfq_dtype ydt) {
+    if (!ctx) return fail(DFQ_ERR_INVALID_ARGUMENT, "null context");
+    if (M < 1 || N < 1 || K < 1) return fail(DFQ_ERR_INVALID_ARGUMENT, "M, N, K must be >= 1");
+    if (M > 16) return fail(DFQ_ERR_UNSUPPORTED, "fast kernel handles M <= 16 (got %d)", M);
+    if (bits != 4 && bits != 8) return fail(DFQ_ERR_UNSUPPORTED, "bits must be 4 or 8");
+    if (gs != 32 && gs != 64 && gs != 128)
+        return fail(DFQ_ERR_UNSUPPORTED, "group size must be 32, 64 or 128");
+    if ((xdt != DFQ_BF16 && xdt != DFQ_F16) || sdt != xdt || ydt != xdt)
+        return fail(DFQ_ERR_UNSUPPORTED, "fast kernel needs x, scales and y all bf16 or all fp16");
+    const int kss = kss_for(bits, gs);
+    if (K % kss) return fail(DFQ_ERR_UNSUPPORTED, "K=%d is not a multiple of %d", K, kss);
+    if ((int64_t)N * K * bits / 8 >= (int64_t)1 << 31)
+        return fail(DFQ_ERR_UNSUPPORTED, "weights must be smaller than 2 GiB");
+    return DFQ_OK;
+}
+
+}  // namespace dfq
+
+using namespace dfq;
+
+extern "C" {
+
+const char* dfq_last_error(void) { return g_last_error.c_str(); }
+
+const char* dfq_status_string(dfq_status s) {
+    switch (s) {
+        case DFQ_OK: return "ok";
+        case DFQ_ERR_INVALID_ARGUMENT: return "invalid argument";
+        case DFQ_ERR_UNSUPPORTED: return "unsupported";
+        case DFQ_ERR_WORKSPACE: return "workspace";
+        case DFQ_ERR_HIP: return "hip error";
+        case DFQ_ERR_NO_DEVICE: return "no device";
+        case DFQ_ERR_STATE: return "bad state";
+    }
+    return "unknown";
+}
+
+int dfq_abi_version(void) { return DFQ_ABI_VERSION; }
+
+dfq_status dfq_init(int device, dfq_ctx** out) {
+    if (!out) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
+    *out = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count <= 0) return fail(DFQ_ERR_NO_DEVICE, "no HIP device visible");
+    if (device < 0 || device >= count)
+        return fail(DFQ_ERR_INVALID_ARGUMENT, "device %d out of range (%d devices)", device, count);
+    DeviceGuard g(device);
+    if (!g.ok) return fail(DFQ_ERR_HIP, "hipSetDevice(%d) failed", device);
+    hipDeviceProp_t prop;
+    if ((e = hipGetDeviceProperties(&prop, device)) != hipSuccess)
+        return hip_fail(e, "hipGetDeviceProperties");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(DFQ_ERR_NO_DEVICE, "device %d is %s, the code object is built for gfx950",
+                    device, prop.gcnArchName);
+    auto* ctx = new dfq_ctx();
+    ctx->device = device;
+    ctx->num_cus = prop.multiProcessorCount;
+    ctx->lds_max = prop.sharedMemPerBlock;
+    if ((e = hipModuleLoadData(&ctx->module, dfq_hsaco_begin)) != hipSuccess) {
+        delete ctx;
+        return hip_fail(e, "hipModuleLoadData(gfx950 code object)");
+    }
+    static const int kBits[2] = {4, 8};
+    static const int kGs[3] = {32, 64, 128};
+    static const char* kDt[2] = {"bf16", "f16"};
+    for (int b = 0; b < 2; ++b)
+        for (int g2 = 0; g2 < 3; ++g2)
+            for (int d = 0; d < 2; ++d) {
+                char name[64];
+                snprintf(name, sizeof name, "dfq_qmm_mt8_b%d_g%d_%s", kBits[b], kGs[g2], kDt[d]);
+                if ((e = hipModuleGetFunction(&ctx->mt8[b][g2][d], ctx->module, name)) !=
+                    hipSuccess) {
+                    (void)hipModuleUnload(ctx->module);
+                    delete ctx;
+                    return hip_fail(e, name);
+                }
+            }
+    if ((e = hipModuleGetFunction(&ctx->generic, ctx->module, "dfq_qmm_generic")) != hipSuccess ||
+        (e = hipModuleGetFunction(&ctx->fill, ctx->module, "dfq_fill_u32")) != hipSuccess) {
+        (void)hipModuleUnload(ctx->module);
+        delete ctx;
+        return hip_fail(e, "hipModuleGetFunction");
+    }
+    *out = ctx;
+    return DFQ_OK;
+}
+
+dfq_status dfq_destroy(dfq_ctx* ctx) {
+    if (!ctx) return DFQ_OK;
+    {
+        DeviceGuard g(ctx->device);
+        if (ctx->module) (void)hipModuleUnload(ctx->module);
+    }
+    delete ctx;
+    return DFQ_OK;
+}
+
+int dfq_num_cus(const dfq_ctx* ctx) { return ctx ? ctx->num_cus : 0; }
+
+/* ---- memory and streams ----------------------------------------------------------- */
+
+dfq_status dfq_malloc(dfq_ctx* ctx, size_t bytes, void** out) {
+    if (!ctx || !out) return fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
+    DeviceGuard g(ctx->device);
+    hipError_t e = hipMalloc(out, bytes ? bytes : 1);
+    return e == hipSuccess ? DFQ_OK : hip_fail(e, "hipMalloc");
+}
+
+dfq_status dfq_free(dfq_ctx* ctx, void* ptr) {
+    if (!ctx) return fail(DFQ_ERR_INVALID_ARGUMENT, "null context");
+    if (!ptr) return DFQ_OK;
+    DeviceGuard g(ctx->device);
+    hipError_t e = hipFree(ptr);
+    return e == hipSuccess ? DFQ_OK : hip_fail(e, "hipFree");
+}
+
+dfq_status dfq_memcpy_h2d(dfq_ctx* ctx, void* dst, const void* src, size_t bytes, void* stream) {
+    if (!ctx || (bytes && (!dst || !src))) return fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
+    DeviceGuard g(ctx->device);
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream);
+    if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+    return e == hipSuccess ? DFQ_OK : hip_fail(e, "hipMemcpyAsync(H2D)");
+}
+
+dfq_status dfq_memcpy_d2h(dfq_ctx* ctx, void* dst, const void* src, size_t bytes, void* stream) {
+    if (!ctx || (bytes && (!dst || !src))) return fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
+    DeviceGuard g(ctx->device);
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream);
+    if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+    return e == hipSuccess ? DFQ_OK : hip_fail(e, "hipMemcpyAsync(D2H)");
+}
+
+dfq_status dfq_stream_create(dfq_ctx* ctx, void** stream) {
+    if (!ctx || !stream) return fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
+    DeviceGuard g(ctx->device);
+    hipStream_t s = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamCreate");
+    *stream = s;
+    return DFQ_OK;
+}
+
+dfq_status dfq_stream_destroy(dfq_ctx* ctx, void* stream) {
+    if (!ctx) return fail(DFQ_ERR_INVALID_ARGUMENT, "null context");
+    if (!stream) return DFQ_OK;
+    DeviceGuard g(ctx->device);
+    hipError_t e = hipStreamDestroy((hipStream_t)stream);
+    return e == hipSuccess ? DFQ_OK : hip_fail(e, "hipStreamDestroy");
+}
+
+dfq_status dfq_stream_sync(dfq_ctx* ctx, void* stream) {
+    if (!ctx) return fail(DFQ_ERR_INVALID_ARGUMENT, "null context");
+    DeviceGuard g(ctx->device);
+    hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+    return e == hipSuccess ? DFQ_OK : hip_fail(e, "hipStreamSynchronize");
+}
+
+/* ---- eligibility -------------------------------------------------------------------- */
+
+int dfq_is_eligible(int out_features, int in_features, int bits, int group_size,
+                    int mode_affine, int has_biases) {
+    if (!mode_affine || !has_biases) return 0;
+    if ((bits != 4 && bits != 8) || group_size != DFQ_REQUIRED_GROUP_SIZE) return 0;
+    return out_features >= DFQ_MINIMUM_OUTPUT_FEATURES &&
+           in_features % DFQ_INPUT_FEATURE_MULTIPLE == 0;
+}
+
+int dfq_tiles_for(int rows) { return rows <= DFQ_ROWS_PER_TILE ? 1 : 2; }
+
+int dfq_qmm_supported(const dfq_ctx* ctx, int M, int N, int K, int bits, int gs,
+                      dfq_dtype xdt, dfq_dtype sdt, dfq_dtype ydt) {
+    std::string saved = g_last_error;
+    dfq_status s = check_fast_args(ctx, M, N, K, bits, gs, xdt, sdt, ydt);
+    int ok = s == DFQ_OK;
+    if (ok) {
+        Plan p;
+        ok = make_plan(std::min(M, 8), N, K, bits, gs, ctx->num_cus, ctx->lds_max, &p) &&
+             (M <= 8 || make_plan(M - 8, N, K, bits, gs, ctx->num_cus, ctx->lds_max, &p));
+    }
+    g_last_error = saved;
+    return ok;
+}
+
+/* ---- the matmul ----------------------------------------------------------------------- */
+
+dfq_status dfq_qmm_workspace_bytes(dfq_ctx* ctx, int M, int N, int K, int bits, int gs,
+                                   size_t* bytes) {
+    if (!bytes) return fail(DFQ_ERR_INVALID_ARGUMENT, "null bytes");
+    *bytes = 0;
+    dfq_status s = check_fast_args(ctx, M, N, K, bits, gs, DFQ_BF16, DFQ_BF16, DFQ_BF16);
+    if (s) return s;
+    Plan p;
+    if ((s = get_plan(ctx, std::min(M, 8), N, K, bits, gs, &p))) return s;
+    size_t need = p.ws_bytes;
+    if (M > 8) {
+        if ((s = get_plan(ctx, M - 8, N, K, bits, gs, &p))) return s;
+        need = std::max(need, p.ws_bytes);
+    }
+    *bytes = need;
+    return DFQ_OK;
+}
+
+dfq_status dfq_workspace_clear(dfq_ctx* ctx, void* ws, size_t bytes, void* stream) {
+    if (!ctx) return fail(DFQ_ERR_INVALID_ARGUMENT, "null context");
+    if (!bytes) return DFQ_OK;
+    if (!ws || !aligned(ws, 4) || bytes % 4)
+        return fail(DFQ_ERR_INVALID_ARGUMENT, "workspace must be 4-byte aligned and sized");
+    DeviceGuard g(ctx->device);
+    uint32_t* p = (uint32_t*)ws;
+    uint32_t v = 0;
+    uint64_t count = bytes / 4;
+    void* args[] = {&p, &v, &count};
+    unsigned grid = (unsigned)std::min<uint64_t>((count + 255) / 256, 4096);
+    hipError_t e = hipModuleLaunchKernel(ctx->fill, grid, 1, 1, 256, 1, 1, 0,
+                                         (hipStream_t)stream, args, nullptr);
+    return e == hipSuccess ? DFQ_OK : hip_fail(e, "launch dfq_fill_u32");
+}
+
+static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
+                             const void* biases, const void* lbias, void* y, int M, int N, int K,
+                             int bits, int gs, dfq_dtype dt, void* ws, size_t wsb,
+                             hipStream_t stream) {
+    Plan pl;
+    dfq_status s = get_plan(ctx, M, N, K, bits, gs, &pl);
+    if (s) return s;
+    QmmParams p{};
+    p.x = x;
+    p.w = w;
+    p.scales = scales;
+    p.biases = biases;
+    p.lbias = lbias;
+    p.y = y;
+    if (pl.need_ws) {
+        if (!ws || wsb < pl.ws_bytes)
+            return fail(DFQ_ERR_WORKSPACE, "workspace of %zu bytes needed (got %zu)", pl.ws_bytes,
+                        ws ? wsb : (size_t)0);
+        if (!aligned(ws, 256)) return fail(DFQ_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+        p.counters = (uint32_t*)ws;
+        p.slots = (float*)((char*)ws + pl.ws_counter_bytes);
+    }
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.T = pl.T;
+    p.SS = pl.SS;
+    p.nkb = pl.nkb;
+    p.Gkb = pl.Gkb;
+    p.nslot_kb = pl.nslot_kb;
+    p.kr = pl.kr;
+    p.lds_row_stride = pl.rs;
+    p.lds_xsum_off = pl.xsum_off;
+    p.lds_slot_off = pl.slot_off;
+    p.w_bytes = (uint32_t)((int64_t)N * K * bits / 8);
+    p.s_bytes = (uint32_t)((int64_t)N * (K / gs) * 2);
+    const int bi = bits == 4 ? 0 : 1;
+    const int gi = gs == 32 ? 0 : gs == 64 ? 1 : 2;
+    const int di = dt == DFQ_BF16 ? 0 : 1;
+    void* args[] = {&p};
+    hipError_t e = hipModuleLaunchKernel(ctx->mt8[bi][gi][di], (unsigned)(pl.nkb * pl.Gkb), 1, 1,
+                                         kThreads, 1, 1, (unsigned)pl.lds_bytes, stream, args,
+                                         nullptr);
+    return e == hipSuccess ? DFQ_OK : hip_fail(e, "launch dfq_qmm_mt8");
+}
+
+dfq_status dfq_qmm(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
+                   const void* biases, const void* lbias, void* y, int M, int N, int K, int bits,
+                   int gs, dfq_dtype xdt, dfq_dtype sdt, dfq_dtype ydt, void* ws, size_t wsb,
+                   void* stream) {
+    dfq_status s = check_fast_args(ctx, M, N, K, bits, gs, xdt, sdt, ydt);
+    if (s) return s;
+    if (!x || !w || !scales || !biases || !y)
+        return fail(DFQ_ERR_INVALID_ARGUMENT, "null x, w, scales, biases or y");
+    if (!aligned(x, 16) || !aligned(w, 16) || !aligned(scales, 4) || !aligned(biases, 4) ||
+        !aligned(y, 2) || (lbias && !aligned(lbias, 2)))
+        return fail(DFQ_ERR_INVALID_ARGUMENT,
+                    "x and w must be 16-byte aligned, scales/biases 4-byte aligned");
+    DeviceGuard g(ctx->device);
+    const size_t esz = 2;
+    /* Rows beyond 8 run as a second 8-row pass over the same weights. */
+    for (int m0 = 0; m0 < M; m0 += 8) {
+        const int mc = std::min(8, M - m0);
+        s = launch_mt8(ctx, (const char*)x + (size_t)m0 * K * esz, w, scales, biases, lbias,
+                       (char*)y + (size_t)m0 * N * esz, mc, N, K, bits, gs, xdt, ws, wsb,
+                       (hipStream_t)stream);
+        if (s) return s;
+    }
+    return DFQ_OK;
+}
+
+dfq_status dfq_qmm_fallback(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
+                            const void* biases, const void* lbias, void* y, int M, int N, int K,
+                            int bits, int gs, dfq_dtype xdt, dfq_dtype sdt, dfq_dtype ydt,
+                            void* stream) {
+    if (!ctx) return fail(DFQ_ERR_INVALID_ARGUMENT, "null context");
+    if (!x || !w || !scales || !biases || !y)
+        return fail(DFQ_ERR_INVALID_ARGUMENT, "null x, w, scales, biases or y");
+    if (M < 1 || N < 1 || K < 1) return fail(DFQ_ERR_INVALID_ARGUMENT, "M, N, K must be >= 1");
+    if (M > 65535) return fail(DFQ_ERR_UNSUPPORTED, "generic path handles M <= 65535");
+    if (bits != 2 && bits != 4 && bits != 8)
+        return fail(DFQ_ERR_UNSUPPORTED, "generic path handles bits 2, 4, 8 (got %d)", bits);
+    if (gs < 32 / bits || gs <= 0 || K % gs || (gs % (32 / bits)))
+        return fail(DFQ_ERR_UNSUPPORTED, "group size %d must divide K=%d and hold whole words",
+                    gs, K);
+    for (dfq_dtype d : {xdt, sdt, ydt})
+        if (d != DFQ_BF16 && d != DFQ_F16 && d != DFQ_F32)
+            return fail(DFQ_ERR_INVALID_ARGUMENT, "bad dtype");
+    if (!aligned(w, 4)) return fail(DFQ_ERR_INVALID_ARGUMENT, "w must be 4-byte aligned");
+    DeviceGuard g(ctx->device);
+    QmmGenericParams p{};
+    p.x = x;
+    p.w = w;
+    p.scales = scales;
+    p.biases = biases;
+    p.lbias = lbias;
+    p.y = y;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.bits = bits;
+    p.gs = gs;
+    p.xdt = xdt;
+    p.sdt = sdt;
+    p.ydt = ydt;
+    void* args[] = {&p};
+    hipError_t e = hipModuleLaunchKernel(ctx->generic, (unsigned)N, (unsigned)M, 1, 64, 1, 1, 0,
+                                         (hipStream_t)stream, args, nullptr);
+    return e == hipSuccess ? DFQ_OK : hip_fail(e, "launch dfq_qmm_generic");
+}
+
+/* ---- graphs -------------------------------------------------------------------------- */
+
+dfq_status dfq_graph_begin(dfq_ctx* ctx, void* stream) {
+    if (!ctx) return fail(DFQ_ERR_INVALID_ARGUMENT, "null context");
+    if (!stream) return fail(DFQ_ERR_INVALID_ARGUMENT, "the default stream cannot be captured");
+    DeviceGuard g(ctx->device);
+    hipError_t e = hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal);
+    return e == hipSuccess ? DFQ_OK : hip_fail(e, "hipStreamBeginCapture");
+}
+
+dfq_status dfq_graph_end(dfq_ctx* ctx, void* stream, dfq_graph** out) {
+    if (!ctx || !out) return fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    DeviceGuard g(ctx->device);
+    hipStreamCaptureStatus st;
+    hipError_t e = hipStreamIsCapturing((hipStream_t)stream, &st);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+    if (st != hipStreamCaptureStatusActive) return fail(DFQ_ERR_STATE, "stream is not capturing");
+    auto* gr = new dfq_graph();
+    gr->device = ctx->device;
+    if ((e = hipStreamEndCapture((hipStream_t)stream, &gr->graph)) != hipSuccess) {
+        delete gr;
+        return hip_fail(e, "hipStreamEndCapture");
+    }
+    if ((e = hipGraphInstantiate(&gr->exec, gr->graph, nullptr, nullptr, 0)) != hipSuccess) {
+        (void)hipGraphDestroy(gr->graph);
+        delete gr;
+        return hip_fail(e, "hipGraphInstantiate");
+    }
+    *out = gr;
+    return DFQ_OK;
+}
+
+dfq_status dfq_graph_launch(dfq_graph* gr, void* stream) {
+    if (!gr) return fail(DFQ_ERR_INVALID_ARGUMENT, "null graph");
+    DeviceGuard g(gr->device);
+    hipError_t e = hipGraphLaunch(gr->exec, (hipStream_t)stream);
+    return e == hipSuccess ? DFQ_OK : hip_fail(e, "hipGraphLaunch");
+}
+
+dfq_status dfq_graph_destroy(dfq_graph* gr) {
+    if (!gr) return DFQ_OK;
+    DeviceGuard g(gr->device);
+    if (gr->exec) (void)hipGraphExecDestroy(gr->exec);
+    if (gr->graph) (void)hipGraphDestroy(gr->graph);
+    delete gr;
+    return DFQ_OK;
+}
+
+/* ---- introspection used by tests and the benchmark (not part of the drop-in surface) -- */
+
+/* Fills the work split the fast kernel uses for a shape: {T, SS, nkb, Gkb, nslot_kb, kr,
+ * lds_bytes, need_ws}. */
+dfq_status dfq_debug_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, int* out8) {
+    if (!out8) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
+    Plan p;
+    dfq_status s = get_plan(ctx, M, N, K, bits, gs, &p);
+    if (s) return s;
+    int v[8] = {p.T, p.SS, p.nkb, p.Gkb, p.nslot_kb, p.kr, p.lds_bytes, p.need_ws ? 1 : 0};
+    std::memcpy(out8, v, sizeof v);
+    return DFQ_OK;
+}
+
+/* The same split computed without a device, for a given CU count and LDS limit. */
+dfq_status dfq_debug_make_plan(int M, int N, int K, int bits, int gs, int num_cus,
+                               size_t lds_max, int* out8) {
+    if (!out8) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
+    Plan p;
+    if (!make_plan(M, N, K, bits, gs, num_cus, lds_max, &p))
+        return fail(DFQ_ERR_UNSUPPORTED, "no work split");
+    int v[8] = {p.T, p.SS, p.nkb, p.Gkb, p.nslot_kb, p.kr, p.lds_bytes, p.need_ws ? 1 : 0};
+    std::memcpy(out8, v, sizeof v);
+    return DFQ_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,429 @@
+"""Python binding of the MI355X small-M affine-quantised matmul (ctypes over the C ABI).
+
+The compute lives in ``libdflash_qmm.so`` (built by ``make -C dflash-swift_amd``): hand-
+written gfx950 kernels behind the C ABI of ``include/dflash_qmm.h``.  This module only
+marshals pointers; there is no Python or CPU compute path, and importing it raises if the
+library is missing.
+
+The classes mirror DFlashKit's Swift surface (paths relative to the reference repository
+root):
+
+* :class:`SmallMQuantizedMatmul` -- the window constants, ``is_eligible`` and ``tiles``
+  (``Sources/DFlashKit/SmallMQuantizedMatmul.swift:27-225``);
+* :class:`QuantizedLinear` / :class:`SmallMQuantizedLinear` -- the stock layer and the
+  drop-in subclass that shares its arrays (``:227-293``);
+* :func:`enable_small_m_quantized_matmul` -- the module-tree swap (``:295-317``).
+
+Device buffers may be torch tensors (``torch`` is used only as a device allocator here) or
+raw integer device pointers.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+__all__ = [
+    "BF16", "F16", "F32", "DfqError", "Context", "SmallMQuantizedMatmul", "QuantizedLinear",
+    "SmallMQuantizedLinear", "Model", "enable_small_m_quantized_matmul", "library_path",
+    "load_library",
+]
+
+BF16, F16, F32 = 0, 1, 2
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_NAME = "libdflash_qmm.so"
+
+
+def library_path() -> str:
+    return os.path.join(_HERE, _LIB_NAME)
+
+
+class DfqError(RuntimeError):
+    """A dfq_* call returned a non-zero status."""
+
+    def __init__(self, status: int, where: str, message: str):
+        super().__init__(f"{where}: status {status}: {message}")
+        self.status = status
+
+
+class _LinearDesc(ctypes.Structure):
+    _fields_ = [
+        ("weight", ctypes.c_void_p), ("scales", ctypes.c_void_p), ("biases", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p), ("out_features", ctypes.c_int),
+        ("in_features", ctypes.c_int), ("bits", ctypes.c_int), ("group_size", ctypes.c_int),
+        ("mode_affine", ctypes.c_int), ("dtype", ctypes.c_int),
+    ]
+
+
+_lib = None
+
+
+def load_library(path: str | None = None) -> ctypes.CDLL:
+    """Load libdflash_qmm.so once; raise loudly if it is not built."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = path or library_path()
+    if not os.path.exists(p):
+        raise ImportError(f"{p} is not built: run `make -C dflash-swift_amd` (no CPU fallback)")
+    lib = ctypes.CDLL(p)
+    P, I, S, Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)
+    PP = ctypes.POINTER(ctypes.c_void_p)
+    sig = {
+        "dfq_init": ([I, PP], I), "dfq_destroy": ([P], I), "dfq_last_error": ([], ctypes.c_char_p),
+        "dfq_status_string": ([I], ctypes.c_char_p), "dfq_abi_version": ([], I),
+        "dfq_num_cus": ([P], I), "dfq_malloc": ([P, S, PP], I), "dfq_free": ([P, P], I),
+        "dfq_memcpy_h2d": ([P, P, P, S, P], I), "dfq_memcpy_d2h": ([P, P, P, S, P], I),
+        "dfq_stream_create": ([P, PP], I), "dfq_stream_destroy": ([P, P], I),
+        "dfq_stream_sync": ([P, P], I),
+        "dfq_is_eligible": ([I, I, I, I, I, I], I), "dfq_tiles_for": ([I], I),
+        "dfq_qmm_supported": ([P, I, I, I, I, I, I, I, I], I),
+        "dfq_qmm_workspace_bytes": ([P, I, I, I, I, I, Z], I),
+        "dfq_workspace_clear": ([P, P, S, P], I),
+        "dfq_qmm": ([P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, P, S, P], I),
+        "dfq_qmm_fallback": ([P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, P], I),
+        "dfq_graph_begin": ([P, P], I), "dfq_graph_end": ([P, P, PP], I),
+        "dfq_graph_launch": ([P, P], I), "dfq_graph_destroy": ([P], I),
+        "dfq_linear_create": ([P, ctypes.POINTER(_LinearDesc), PP], I),
+        "dfq_small_m_linear_create": ([P, PP], I), "dfq_linear_destroy": ([P], I),
+        "dfq_linear_is_small_m": ([P], I), "dfq_linear_output_dtype": ([P, I], I),
+        "dfq_linear_forward": ([P, P, I, I, P, P, S, P, ctypes.POINTER(I)], I),
+        "dfq_linear_workspace_bytes": ([P, I, Z], I),
+        "dfq_model_create": ([PP], I), "dfq_model_destroy": ([P], I),
+        "dfq_model_set_leaf": ([P, ctypes.c_char_p, P], I),
+        "dfq_model_leaf": ([P, ctypes.c_char_p], P), "dfq_model_leaf_count": ([P], I),
+        "dfq_enable_small_m_quantized_matmul": ([P], I),
+        "dfq_debug_plan": ([P, I, I, I, I, I, ctypes.POINTER(I)], I),
+        "dfq_debug_make_plan": ([I, I, I, I, I, I, S, ctypes.POINTER(I)], I),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    if lib.dfq_abi_version() != 1:
+        raise ImportError("libdflash_qmm.so ABI version mismatch")
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def _check(status: int, where: str):
+    if status:
+        lib = load_library()
+        raise DfqError(status, where, lib.dfq_last_error().decode(errors="replace"))
+
+
+def _ptr(a) -> int | None:
+    """Device address of a torch tensor, an int, or None."""
+    if a is None:
+        return None
+    if isinstance(a, int):
+        return a
+    return a.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        try:
+            import torch
+            if torch.cuda.is_available():
+                return torch.cuda.current_stream().cuda_stream or None
+        except ImportError:
+            pass
+        return None
+    if isinstance(stream, int):
+        return stream or None
+    return stream.cuda_stream or None
+
+
+def dtype_code(t) -> int:
+    """dfq dtype code of a torch dtype (or tensor)."""
+    import torch
+    dt = t.dtype if hasattr(t, "dtype") else t
+    return {torch.bfloat16: BF16, torch.float16: F16, torch.float32: F32}[dt]
+
+
+class Context:
+    """A dfq_ctx: the gfx950 code object loaded on one device."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load_library()
+        h = ctypes.c_void_p()
+        _check(self.lib.dfq_init(device, ctypes.byref(h)), "dfq_init")
+        self.handle = h
+        self.device = device
+        self._ws = None  # lazily grown torch workspace for the convenience calls
+
+    def close(self):
+        if self.handle:
+            self.lib.dfq_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def num_cus(self) -> int:
+        return self.lib.dfq_num_cus(self.handle)
+
+    # ---- raw pointer API -------------------------------------------------------------
+    def supported(self, M, N, K, bits, gs, xdt=BF16, sdt=None, ydt=None) -> bool:
+        sdt = xdt if sdt is None else sdt
+        ydt = xdt if ydt is None else ydt
+        return bool(self.lib.dfq_qmm_supported(self.handle, M, N, K, bits, gs, xdt, sdt, ydt))
+
+    def workspace_bytes(self, M, N, K, bits, gs) -> int:
+        b = ctypes.c_size_t()
+        _check(self.lib.dfq_qmm_workspace_bytes(self.handle, M, N, K, bits, gs, ctypes.byref(b)),
+               "dfq_qmm_workspace_bytes")
+        return b.value
+
+    def workspace_clear(self, ws, nbytes, stream=None):
+        _check(self.lib.dfq_workspace_clear(self.handle, _ptr(ws), nbytes, _stream(stream)),
+               "dfq_workspace_clear")
+
+    def plan(self, M, N, K, bits, gs) -> dict:
+        out = (ctypes.c_int * 8)()
+        _check(self.lib.dfq_debug_plan(self.handle, M, N, K, bits, gs, out), "dfq_debug_plan")
+        keys = ["T", "SS", "nkb", "Gkb", "nslot_kb", "kr", "lds_bytes", "need_ws"]
+        return dict(zip(keys, list(out)))
+
+    def qmm_raw(self, x, w, scales, biases, y, M, N, K, bits, gs, xdt, sdt, ydt, lbias=None,
+                ws=None, ws_bytes=0, stream=None):
+        _check(self.lib.dfq_qmm(self.handle, _ptr(x), _ptr(w), _ptr(scales), _ptr(biases),
+                                _ptr(lbias), _ptr(y), M, N, K, bits, gs, xdt, sdt, ydt, _ptr(ws),
+                                ws_bytes, _stream(stream)), "dfq_qmm")
+
+    def fallback_raw(self, x, w, scales, biases, y, M, N, K, bits, gs, xdt, sdt, ydt,
+                     lbias=None, stream=None):
+        _check(self.lib.dfq_qmm_fallback(self.handle, _ptr(x), _ptr(w), _ptr(scales),
+                                         _ptr(biases), _ptr(lbias), _ptr(y), M, N, K, bits, gs,
+                                         xdt, sdt, ydt, _stream(stream)), "dfq_qmm_fallback")
+
+    # ---- torch conveniences -------------------------------------------------------------
+    def workspace(self, nbytes: int):
+        """A zeroed device workspace of at least nbytes, owned by this context."""
+        import torch
+        if nbytes == 0:
+            return None
+        if self._ws is None or self._ws.numel() < nbytes:
+            self._ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8,
+                                   device=f"cuda:{self.device}")
+        return self._ws
+
+    def qmm(self, x, w, scales, biases, bits, gs, lbias=None, out=None, ws=None, stream=None):
+        """y = x @ dequant(w).T on the fast kernel; x [M,K], w [N,K*bits/32] int32/uint32."""
+        import torch
+        M, K = x.shape
+        N = w.shape[0]
+        dt = dtype_code(x)
+        if out is None:
+            out = torch.empty((M, N), dtype=x.dtype, device=x.device)
+        need = self.workspace_bytes(M, N, K, bits, gs)
+        if ws is None:
+            ws = self.workspace(need)
+        self.qmm_raw(x, w, scales, biases, out, M, N, K, bits, gs, dt, dtype_code(scales), dt,
+                     lbias=lbias, ws=ws, ws_bytes=(ws.numel() if ws is not None else 0),
+                     stream=stream)
+        return out
+
+    def fallback(self, x, w, scales, biases, bits, gs, lbias=None, out=None, out_dtype=None,
+                 stream=None):
+        import torch
+        M, K = x.shape
+        N = w.shape[0]
+        xdt, sdt = dtype_code(x), dtype_code(scales)
+        if out is None:
+            ydt = xdt if xdt == sdt else F32
+            if out_dtype is not None:
+                ydt = dtype_code(out_dtype)
+            tdt = {BF16: torch.bfloat16, F16: torch.float16, F32: torch.float32}[ydt]
+            out = torch.empty((M, N), dtype=tdt, device=x.device)
+        self.fallback_raw(x, w, scales, biases, out, M, N, K, bits, gs, xdt, sdt,
+                          dtype_code(out), lbias=lbias, stream=stream)
+        return out
+
+    # ---- graphs ---------------------------------------------------------------------------
+    def graph_begin(self, stream):
+        _check(self.lib.dfq_graph_begin(self.handle, _stream(stream)), "dfq_graph_begin")
+
+    def graph_end(self, stream) -> "Graph":
+        g = ctypes.c_void_p()
+        _check(self.lib.dfq_graph_end(self.handle, _stream(stream), ctypes.byref(g)),
+               "dfq_graph_end")
+        return Graph(self.lib, g)
+
+
+class Graph:
+    def __init__(self, lib, handle):
+        self.lib, self.handle = lib, handle
+
+    def launch(self, stream=None):
+        _check(self.lib.dfq_graph_launch(self.handle, _stream(stream)), "dfq_graph_launch")
+
+    def close(self):
+        if self.handle:
+            self.lib.dfq_graph_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class SmallMQuantizedMatmul:
+    """The reference enum's statics (SmallMQuantizedMatmul.swift:29-49, 193-207)."""
+
+    minimum_rows = 6
+    maximum_rows = 16
+    rows_per_tile = 8
+    minimum_output_features = 4096
+    input_feature_multiple = 512
+    required_group_size = 64
+
+    @staticmethod
+    def is_eligible(layer: "QuantizedLinear") -> bool:
+        return bool(load_library().dfq_is_eligible(
+            layer.out_features, layer.in_features, layer.bits, layer.group_size,
+            int(layer.mode == "affine"), int(layer.biases is not None)))
+
+    @staticmethod
+    def tiles(rows: int) -> int:
+        return load_library().dfq_tiles_for(rows)
+
+
+class QuantizedLinear:
+    """MLX's QuantizedLinear over device arrays (weight, scales, biases, bias)."""
+
+    def __init__(self, ctx: Context, weight, scales, biases, bias=None, group_size=64, bits=4,
+                 mode="affine", _handle=None):
+        self.ctx = ctx
+        self.weight, self.scales, self.biases, self.bias = weight, scales, biases, bias
+        self.group_size, self.bits, self.mode = group_size, bits, mode
+        self.out_features = weight.shape[0]
+        self.in_features = weight.shape[1] * 32 // bits
+        if _handle is not None:
+            self._h = _handle
+            return
+        d = _LinearDesc(_ptr(weight), _ptr(scales), _ptr(biases), _ptr(bias),
+                        self.out_features, self.in_features, bits, group_size,
+                        int(mode == "affine"), dtype_code(scales))
+        h = ctypes.c_void_p()
+        _check(ctx.lib.dfq_linear_create(ctx.handle, ctypes.byref(d), ctypes.byref(h)),
+               "dfq_linear_create")
+        self._h = h
+
+    def __del__(self):
+        try:
+            if self._h:
+                self.ctx.lib.dfq_linear_destroy(self._h)
+                self._h = None
+        except Exception:
+            pass
+
+    @property
+    def shape(self):
+        return (self.out_features, self.in_features)
+
+    def output_dtype(self, x):
+        import torch
+        code = self.ctx.lib.dfq_linear_output_dtype(self._h, dtype_code(x))
+        return {BF16: torch.bfloat16, F16: torch.float16, F32: torch.float32}[code]
+
+    def __call__(self, x, stream=None):
+        """callAsFunction: x[..., in] -> y[..., out]."""
+        import torch
+        lead = x.shape[:-1]
+        rows = 1
+        for d in lead:
+            rows *= d
+        flat = x.reshape(rows, x.shape[-1]).contiguous()
+        y = torch.empty((rows, self.out_features), dtype=self.output_dtype(x), device=x.device)
+        nb = ctypes.c_size_t()
+        _check(self.ctx.lib.dfq_linear_workspace_bytes(self._h, rows, ctypes.byref(nb)),
+               "dfq_linear_workspace_bytes")
+        ws = self.ctx.workspace(nb.value)
+        took = ctypes.c_int(0)
+        _check(self.ctx.lib.dfq_linear_forward(
+            self._h, _ptr(flat), dtype_code(x), rows, _ptr(y), _ptr(ws),
+            ws.numel() if ws is not None else 0, _stream(stream), ctypes.byref(took)),
+            "dfq_linear_forward")
+        self.last_took_kernel = bool(took.value)
+        return y.reshape(*lead, self.out_features)
+
+
+class SmallMQuantizedLinear(QuantizedLinear):
+    """SmallMQuantizedLinear(other): shares other's arrays (SmallMQuantizedMatmul.swift:243-252)."""
+
+    def __init__(self, other: QuantizedLinear):
+        h = ctypes.c_void_p()
+        _check(other.ctx.lib.dfq_small_m_linear_create(other._h, ctypes.byref(h)),
+               "dfq_small_m_linear_create")
+        super().__init__(other.ctx, other.weight, other.scales, other.biases, other.bias,
+                         other.group_size, other.bits, other.mode, _handle=h)
+
+
+class Model:
+    """A module tree reduced to named leaf layers."""
+
+    def __init__(self, ctx: Context, **leaves: QuantizedLinear):
+        self.ctx = ctx
+        h = ctypes.c_void_p()
+        _check(ctx.lib.dfq_model_create(ctypes.byref(h)), "dfq_model_create")
+        self._h = h
+        self._py = {}
+        for name, leaf in leaves.items():
+            self.set_leaf(name, leaf)
+
+    def set_leaf(self, path: str, leaf: QuantizedLinear):
+        # the model owns a handle of its own on the same layer object
+        if isinstance(leaf, SmallMQuantizedLinear):
+            h = ctypes.c_void_p()
+            _check(self.ctx.lib.dfq_small_m_linear_create(leaf._h, ctypes.byref(h)),
+                   "dfq_small_m_linear_create")
+        else:
+            d = _LinearDesc(_ptr(leaf.weight), _ptr(leaf.scales), _ptr(leaf.biases),
+                            _ptr(leaf.bias), leaf.out_features, leaf.in_features, leaf.bits,
+                            leaf.group_size, int(leaf.mode == "affine"), dtype_code(leaf.scales))
+            h = ctypes.c_void_p()
+            _check(self.ctx.lib.dfq_linear_create(self.ctx.handle, ctypes.byref(d),
+                                                  ctypes.byref(h)), "dfq_linear_create")
+        _check(self.ctx.lib.dfq_model_set_leaf(self._h, path.encode(), h), "dfq_model_set_leaf")
+        self._py[path] = leaf
+
+    def leaf(self, path: str) -> QuantizedLinear:
+        """The current leaf at `path`, as a Python layer sharing the model's layer object."""
+        h = self.ctx.lib.dfq_model_leaf(self._h, path.encode())
+        if not h:
+            raise KeyError(path)
+        h = ctypes.c_void_p(h)
+        src = self._py[path]
+        cls = SmallMQuantizedLinear if self.ctx.lib.dfq_linear_is_small_m(h) else QuantizedLinear
+        obj = cls.__new__(cls)
+        QuantizedLinear.__init__(obj, self.ctx, src.weight, src.scales, src.biases, src.bias,
+                                 src.group_size, src.bits, src.mode, _handle=h)
+        return obj
+
+    def __len__(self):
+        return self.ctx.lib.dfq_model_leaf_count(self._h)
+
+    def __del__(self):
+        try:
+            if self._h:
+                self.ctx.lib.dfq_model_destroy(self._h)
+                self._h = None
+        except Exception:
+            pass
+
+
+def enable_small_m_quantized_matmul(model: Model) -> int:
+    """Swap every eligible leaf for a SmallMQuantizedLinear; return how many were swapped."""
+    n = model.ctx.lib.dfq_enable_small_m_quantized_matmul(model._h)
+    if n < 0:
+        _check(2, "dfq_enable_small_m_quantized_matmul")
+    return n

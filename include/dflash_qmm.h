@@ -1,0 +1,192 @@
+/*
+ * dflash_qmm.h -- C ABI of the MI355X (gfx950) small-M affine-quantised matmul.
+ *
+ * This is the drop-in boundary for DFlashKit's SmallMQuantizedMatmul path.  In the
+ * reference (paths relative to the reference repository root) the path sits behind MLX's
+ * custom-kernel FFI and a Swift subclass of QuantizedLinear:
+ *
+ *   Sources/DFlashKit/SmallMQuantizedMatmul.swift:174-187  kernel objects built lazily
+ *                                                          through MLXFast.metalKernel
+ *   Sources/DFlashKit/SmallMQuantizedMatmul.swift:193-201  isEligible(_:)
+ *   Sources/DFlashKit/SmallMQuantizedMatmul.swift:205-207  tiles(for:)
+ *   Sources/DFlashKit/SmallMQuantizedMatmul.swift:210-224  apply(x:weight:scales:biases:...)
+ *   Sources/DFlashKit/SmallMQuantizedMatmul.swift:234-293  SmallMQuantizedLinear
+ *   Sources/DFlashKit/SmallMQuantizedMatmul.swift:303-317  enableSmallMQuantizedMatmul(in:)
+ *
+ * Each declaration below names the reference item it replaces.  Conventions:
+ *   - every function returns a dfq_status (0 = DFQ_OK) unless stated; nothing aborts or
+ *     throws across the ABI; dfq_last_error() returns a thread-local message;
+ *   - all device buffers are caller-owned (no allocation on the matmul path);
+ *   - streams are hipStream_t passed as void* (NULL = the default stream);
+ *   - weights are consumed in MLX's layout, in place: w uint32 [N][K*bits/32] with element 0
+ *     in the low bits, scales and biases [N][K/group_size];
+ *   - calls are re-entrant per stream; concurrent calls that share one workspace race.
+ */
+#ifndef DFLASH_QMM_H
+#define DFLASH_QMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DFQ_ABI_VERSION 1
+
+typedef enum dfq_status {
+    DFQ_OK = 0,
+    DFQ_ERR_INVALID_ARGUMENT = 1, /* null pointer, negative size, misaligned buffer      */
+    DFQ_ERR_UNSUPPORTED = 2,      /* shape / format outside what the called path handles */
+    DFQ_ERR_WORKSPACE = 3,        /* workspace missing or smaller than required          */
+    DFQ_ERR_HIP = 4,              /* a HIP runtime call failed                           */
+    DFQ_ERR_NO_DEVICE = 5,        /* no gfx950 device, or code object failed to load     */
+    DFQ_ERR_STATE = 6             /* call out of order (e.g. graph_end without begin)    */
+} dfq_status;
+
+typedef enum dfq_dtype { DFQ_BF16 = 0, DFQ_F16 = 1, DFQ_F32 = 2 } dfq_dtype;
+
+typedef struct dfq_ctx dfq_ctx;
+typedef struct dfq_graph dfq_graph;
+
+/* ---- the eligibility window (SmallMQuantizedMatmul.swift:29-49) -------------------- */
+#define DFQ_MINIMUM_ROWS 6               /* :32 minimumRows                              */
+#define DFQ_MAXIMUM_ROWS 16              /* :36 maximumRows                              */
+#define DFQ_ROWS_PER_TILE 8              /* :39 rowsPerTile (also read by the generator's
+                                            width snapping, DFlashSpeculativeGenerator.swift
+                                            :136-142, 325-326)                           */
+#define DFQ_MINIMUM_OUTPUT_FEATURES 4096 /* :41 minimumOutputFeatures                    */
+#define DFQ_INPUT_FEATURE_MULTIPLE 512   /* :45 inputFeatureMultiple                     */
+#define DFQ_REQUIRED_GROUP_SIZE 64       /* :47 requiredGroupSize                        */
+
+/* ---- context ---------------------------------------------------------------------- */
+
+/* Loads the gfx950 code object (hipModuleLoadData) and resolves every kernel.
+ * Replaces the lazily built kernel table, SmallMQuantizedMatmul.swift:169-187. */
+dfq_status dfq_init(int device, dfq_ctx** out);
+dfq_status dfq_destroy(dfq_ctx* ctx);
+const char* dfq_last_error(void);
+const char* dfq_status_string(dfq_status s);
+int dfq_abi_version(void);
+/* Number of compute units the work split is sized for. */
+int dfq_num_cus(const dfq_ctx* ctx);
+
+/* ---- device memory and streams (so a host without HIP headers can drive the path) -- */
+dfq_status dfq_malloc(dfq_ctx* ctx, size_t bytes, void** out);
+dfq_status dfq_free(dfq_ctx* ctx, void* ptr);
+dfq_status dfq_memcpy_h2d(dfq_ctx* ctx, void* dst, const void* src, size_t bytes, void* stream);
+dfq_status dfq_memcpy_d2h(dfq_ctx* ctx, void* dst, const void* src, size_t bytes, void* stream);
+dfq_status dfq_stream_create(dfq_ctx* ctx, void** stream);
+dfq_status dfq_stream_destroy(dfq_ctx* ctx, void* stream);
+dfq_status dfq_stream_sync(dfq_ctx* ctx, void* stream);
+
+/* ---- the eligibility gate ------------------------------------------------------------ */
+
+/* Static half of the gate: mode == affine, biases present, bits in {4, 8},
+ * group_size == 64, N >= 4096, K % 512 == 0.  Returns 1 / 0.
+ * Replaces SmallMQuantizedMatmul.isEligible(_:), SmallMQuantizedMatmul.swift:193-201. */
+int dfq_is_eligible(int out_features, int in_features, int bits, int group_size,
+                    int mode_affine, int has_biases);
+
+/* MMA tiles of 8 rows a pass of `rows` rows pays for: 1 up to 8, else 2.
+ * Replaces SmallMQuantizedMatmul.tiles(for:), SmallMQuantizedMatmul.swift:205-207. */
+int dfq_tiles_for(int rows);
+
+/* Whether dfq_qmm's kernels handle this problem (wider than the reference gate: any
+ * M in 1..8, N >= 1, group 32/64/128, bits 4/8, bf16 or fp16 throughout, K a multiple
+ * of the kernel's super-step).  Returns 1 / 0. */
+int dfq_qmm_supported(const dfq_ctx* ctx, int M, int N, int K, int bits, int group_size,
+                      dfq_dtype x_dtype, dfq_dtype sb_dtype, dfq_dtype y_dtype);
+
+/* ---- the matmul ------------------------------------------------------------------- */
+
+/* Workspace dfq_qmm needs for this shape (0 if none).  The workspace must be zero-filled
+ * once before its first use (dfq_workspace_clear); every call leaves it zeroed again. */
+dfq_status dfq_qmm_workspace_bytes(dfq_ctx* ctx, int M, int N, int K, int bits,
+                                   int group_size, size_t* bytes);
+dfq_status dfq_workspace_clear(dfq_ctx* ctx, void* workspace, size_t bytes, void* stream);
+
+/* y[M,N] = x[M,K] . dequant(w)[N,K]^T (+ linear_bias[N]) on the fast kernel.
+ * x, scales, biases, linear_bias and y share one dtype (bf16 or fp16); y dtype = x dtype.
+ * Asynchronous on `stream`; allocates nothing.
+ * Replaces SmallMQuantizedMatmul.apply(...) (SmallMQuantizedMatmul.swift:210-224) and the
+ * MLXFastKernel call it makes (:217-223); the optional linear bias is the `y + bias` of
+ * SmallMQuantizedLinear.callAsFunction (:288-290), fused before the final rounding. */
+dfq_status dfq_qmm(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
+                   const void* biases, const void* linear_bias, void* y, int M, int N, int K,
+                   int bits, int group_size, dfq_dtype x_dtype, dfq_dtype sb_dtype,
+                   dfq_dtype y_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The generic path: any M >= 1, bits 2/4/8, any group size dividing K; x and scales may
+ * differ in dtype (y dtype follows MLX promotion: equal -> same, else fp32).  Re-reads W
+ * for every row.  Stands in for the stock op MLX falls back to,
+ * QuantizedLinear.callAsFunction -> quantizedMatmul (reached at SmallMQuantizedMatmul.swift:265). */
+dfq_status dfq_qmm_fallback(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
+                            const void* biases, const void* linear_bias, void* y, int M, int N,
+                            int K, int bits, int group_size, dfq_dtype x_dtype,
+                            dfq_dtype sb_dtype, dfq_dtype y_dtype, void* stream);
+
+/* ---- graph capture of a layer's matmul chain ------------------------------------------ */
+/* Stream capture of whatever the caller enqueues on `stream` between begin and end
+ * (typically the q/k/v/o/gate/up/down dfq_qmm calls of one layer), instantiated once and
+ * replayed with dfq_graph_launch.  No counterpart in the reference (MLX builds a lazy graph
+ * per forward, DFlashSpeculativeGenerator.swift:389-398); it is the HIP-native way to issue
+ * one verify-pass layer. */
+dfq_status dfq_graph_begin(dfq_ctx* ctx, void* stream);
+dfq_status dfq_graph_end(dfq_ctx* ctx, void* stream, dfq_graph** out);
+dfq_status dfq_graph_launch(dfq_graph* graph, void* stream);
+dfq_status dfq_graph_destroy(dfq_graph* graph);
+
+/* ---- the drop-in layer (SmallMQuantizedMatmul.swift:227-317) -------------------------- */
+
+typedef struct dfq_linear dfq_linear;
+typedef struct dfq_model dfq_model;
+
+/* A quantised linear layer over caller-owned device arrays (MLX's QuantizedLinear fields:
+ * weight, scales, biases, bias, groupSize, bits, mode).  Nothing is copied. */
+typedef struct dfq_linear_desc {
+    const uint32_t* weight;   /* [out][in*bits/32]                                   */
+    const void* scales;       /* [out][in/group_size]                                */
+    const void* biases;       /* [out][in/group_size], NULL if the mode has none     */
+    const void* bias;         /* [out] linear bias or NULL                           */
+    int out_features, in_features, bits, group_size;
+    int mode_affine;          /* 1 = MLX .affine                                     */
+    dfq_dtype dtype;          /* dtype of scales / biases / bias                     */
+} dfq_linear_desc;
+
+/* A stock QuantizedLinear: every call goes to the generic path. */
+dfq_status dfq_linear_create(dfq_ctx* ctx, const dfq_linear_desc* desc, dfq_linear** out);
+/* SmallMQuantizedLinear(other): wraps `other`, sharing its arrays (:243-252). */
+dfq_status dfq_small_m_linear_create(dfq_linear* other, dfq_linear** out);
+dfq_status dfq_linear_destroy(dfq_linear* lin);
+/* 1 if `lin` is a SmallMQuantizedLinear. */
+int dfq_linear_is_small_m(const dfq_linear* lin);
+/* The dtype callAsFunction returns for input dtype x_dtype. */
+dfq_dtype dfq_linear_output_dtype(const dfq_linear* lin, dfq_dtype x_dtype);
+/* callAsFunction (:254-292): y[rows][out] for x[rows][in]; rows = product of the leading
+ * dimensions.  A SmallMQuantizedLinear takes the fast kernel when it is eligible,
+ * DFQ_MINIMUM_ROWS <= rows <= DFQ_MAXIMUM_ROWS and x is bf16, and falls through to the
+ * stock path otherwise; *took_kernel (may be NULL) reports which. */
+dfq_status dfq_linear_forward(dfq_linear* lin, const void* x, dfq_dtype x_dtype, int rows,
+                              void* y, void* workspace, size_t workspace_bytes, void* stream,
+                              int* took_kernel);
+/* Workspace the layer's forward needs at `rows` rows. */
+dfq_status dfq_linear_workspace_bytes(dfq_linear* lin, int rows, size_t* bytes);
+
+/* A module tree reduced to what the swap needs: named leaf layers. */
+dfq_status dfq_model_create(dfq_model** out);
+dfq_status dfq_model_destroy(dfq_model* model);
+/* Adds (or replaces) the leaf at `path`; the model takes ownership of `lin`. */
+dfq_status dfq_model_set_leaf(dfq_model* model, const char* path, dfq_linear* lin);
+dfq_linear* dfq_model_leaf(dfq_model* model, const char* path);
+int dfq_model_leaf_count(const dfq_model* model);
+/* Swaps every eligible stock leaf for a SmallMQuantizedLinear; returns how many were
+ * swapped (idempotent: already-swapped leaves are skipped), or -1 on error.
+ * Replaces enableSmallMQuantizedMatmul(in:), SmallMQuantizedMatmul.swift:303-317. */
+int dfq_enable_small_m_quantized_matmul(dfq_model* model);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DFLASH_QMM_H */

@@ -1,0 +1,135 @@
+"""Parity of the gfx950 fast kernel (through the C ABI) with the CPU oracle.
+
+Bar: max|y - y_ref| / max|y_ref| <= 1e-2 against the oracle's fp64 result on identical
+seeded inputs (bf16/fp16 output, fp32 accumulation), plus the reference test's own rule
+max|d| <= 0.02 * max(max|ref|, 1) (SmallMQuantizedMatmulTests.swift:74-79).  Integer and
+index behaviour (row independence, determinism, workspace re-arming) is checked bit-exact.
+"""
+import numpy as np
+import pytest
+
+from gpu_util import announce, download, upload
+from oracle.qmm_oracle import BF16, F16, config_case, make_case, tolerance_check
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+# (M, N, K, bits, gs, dtype): every format, ragged N, single-super-step K, k-block splits.
+SMALL_CASES = [
+    (1, 16, 128, 4, 64, BF16),
+    (8, 16, 128, 4, 64, BF16),
+    (3, 40, 256, 4, 64, BF16),
+    (8, 257, 640, 4, 64, BF16),
+    (5, 1000, 1024, 4, 64, BF16),
+    (8, 4096, 1024, 4, 64, BF16),
+    (7, 300, 512, 4, 32, BF16),
+    (8, 333, 768, 4, 128, BF16),
+    (8, 200, 512, 8, 32, BF16),
+    (6, 200, 512, 8, 64, BF16),
+    (8, 130, 1024, 8, 128, BF16),
+    (2, 64, 256, 4, 64, F16),
+    (8, 96, 512, 4, 32, F16),
+    (4, 96, 512, 4, 128, F16),
+    (8, 96, 512, 8, 32, F16),
+    (8, 96, 512, 8, 64, F16),
+    (8, 96, 512, 8, 128, F16),
+    (8, 48, 16384, 4, 64, BF16),     # several k-blocks and workgroups per tile
+    (1, 5000, 12288, 4, 64, BF16),   # k-blocks with many tiles
+    (8, 17, 8192, 8, 64, BF16),
+]
+
+
+def run_fast(ctx, c):
+    x, w, s, b, lb = upload(c)
+    return ctx.qmm(x, w, s, b, c.bits, c.gs, lbias=lb)
+
+
+@pytest.mark.parametrize("M,N,K,bits,gs,dt", SMALL_CASES)
+def test_small_shapes_match_oracle(ctx, oracle, M, N, K, bits, gs, dt):
+    c = make_case(M, N, K, bits=bits, gs=gs, xdt=dt, seed=M * 1000 + N + K + bits + gs,
+                  lbias=(N % 2 == 1))
+    announce(f"small M={M} N={N} K={K} bits={bits} gs={gs} dt={dt}")
+    y = download(run_fast(ctx, c))
+    ref = oracle.qmm_f64(c)
+    rel, ok = tolerance_check(y, ref)
+    assert rel <= TOL and ok, f"max rel err {rel:.3e}"
+
+
+@pytest.mark.parametrize("name,M", [
+    ("c1_m1_k4096_n4096_f16", 1),
+    ("c2_gateup_k5120_n17408", 1), ("c2_gateup_k5120_n17408", 2),
+    ("c2_gateup_k5120_n17408", 4), ("c2_gateup_k5120_n17408", 6),
+    ("c2_gateup_k5120_n17408", 8),
+    ("c3_down_k17408_n5120", 8),
+    ("c4_qkv_8bit_g64", 8), ("c4_o_8bit_g64", 8),
+    ("c4_qkv_4bit_g32", 8), ("c4_o_4bit_g32", 8),
+])
+def test_benchmark_configs_match_oracle(ctx, oracle, name, M):
+    c = config_case(name, M)
+    announce(f"config {name} M={M}")
+    y = download(run_fast(ctx, c))
+    ref = oracle.qmm_f64(c)
+    rel, ok = tolerance_check(y, ref)
+    assert rel <= TOL and ok, f"{name} M={M}: max rel err {rel:.3e}"
+
+
+def test_rows_are_independent_of_m(ctx):
+    """Row r of an 8-row call is bit-identical to the 1-row call on x[r]."""
+    import torch
+    c = config_case("c2_gateup_k5120_n17408", 8)
+    x, w, s, b, _ = upload(c)
+    announce("row independence c2 M=8 vs M=1")
+    y8 = ctx.qmm(x, w, s, b, 4, 64)
+    for r in (0, 3, 7):
+        y1 = ctx.qmm(x[r:r + 1].contiguous(), w, s, b, 4, 64)
+        assert torch.equal(y8[r:r + 1].view(torch.int16), y1.view(torch.int16)), f"row {r}"
+
+
+def test_repeat_calls_are_bit_identical(ctx):
+    """Deterministic fix-up order and a re-armed workspace: same bits on every call."""
+    import torch
+    c = config_case("c3_down_k17408_n5120", 8)
+    x, w, s, b, _ = upload(c)
+    announce("determinism c3 x3")
+    ys = [ctx.qmm(x, w, s, b, 4, 64).clone() for _ in range(3)]
+    for y in ys[1:]:
+        assert torch.equal(ys[0].view(torch.int16), y.view(torch.int16))
+
+
+def test_kernel_output_is_not_the_generic_path(ctx):
+    """Negative control (SmallMQuantizedMatmulTests.swift:94-102): the fast kernel's
+    accumulation order differs from the generic path's, so at least one output moves."""
+    import torch
+    c = config_case("c2_gateup_k5120_n17408", 8)
+    x, w, s, b, _ = upload(c)
+    announce("negative control c2 M=8 fast vs generic")
+    fast = ctx.qmm(x, w, s, b, 4, 64)
+    slow = ctx.fallback(x, w, s, b, 4, 64)
+    assert slow.dtype == fast.dtype
+    assert not torch.equal(fast.view(torch.int16), slow.view(torch.int16))
+    rel, ok = tolerance_check(download(fast), download(slow))
+    assert rel <= TOL and ok
+
+
+def test_generic_path_matches_oracle(ctx, oracle):
+    for (M, N, K, bits, gs, dt) in [(3, 50, 256, 4, 64, BF16), (2, 40, 256, 8, 32, F16),
+                                    (4, 33, 512, 2, 64, BF16), (5, 64, 384, 4, 128, BF16)]:
+        c = make_case(M, N, K, bits=bits, gs=gs, xdt=dt, seed=K + N, lbias=True)
+        x, w, s, b, lb = upload(c)
+        announce(f"generic M={M} N={N} K={K} bits={bits} gs={gs}")
+        y = download(ctx.fallback(x, w, s, b, bits, gs, lbias=lb))
+        rel, ok = tolerance_check(y, oracle.qmm_f64(c))
+        assert rel <= TOL and ok, (M, N, K, bits, gs, rel)
+
+
+def test_generic_path_promotes_mixed_dtypes(ctx, oracle):
+    """fp16 x against bf16 scales: MLX promotes to fp32, and so does the generic path."""
+    import torch
+    c = make_case(4, 64, 256, bits=4, gs=64, xdt=F16, sdt=BF16, seed=9)
+    x, w, s, b, _ = upload(c)
+    announce("generic mixed dtype")
+    y = ctx.fallback(x, w, s, b, 4, 64)
+    assert y.dtype == torch.float32
+    rel, ok = tolerance_check(download(y), oracle.qmm_f64(c))
+    assert rel <= 1e-5 and ok

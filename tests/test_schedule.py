@@ -1,0 +1,159 @@
+"""The fast kernel's work split, checked on the CPU.
+
+The runtime's planner (dfq_debug_make_plan, the same code dfq_qmm uses) is run for many
+shapes; the kernel's split and fix-up rules (qmm_kernels.hip: unit ranges per workgroup and
+wave, wave-level LDS slots, workgroup combine, workspace publish with a last-arriver sum)
+are replayed here unit by unit.  Every (k-block, tile, super-step) unit must be computed
+exactly once, every tile must be written exactly once with all of its units, and every
+workspace / LDS slot index must stay inside what the planner sized.
+"""
+import ctypes
+
+import pytest
+
+import dflash_qmm
+
+WAVES = 8
+
+
+def make_plan(M, N, K, bits, gs, cus=256, lds=163840):
+    lib = dflash_qmm.load_library()
+    out = (ctypes.c_int * 8)()
+    rc = lib.dfq_debug_make_plan(M, N, K, bits, gs, cus, lds, out)
+    if rc:
+        return None
+    keys = ["T", "SS", "nkb", "Gkb", "nslot_kb", "kr", "lds_bytes", "need_ws"]
+    return dict(zip(keys, list(out)))
+
+
+def owner_wg(u, U, G):
+    return (G * (u + 1) - 1) // U
+
+
+def replay(p):
+    T, SS, nkb, G, nslot = p["T"], p["SS"], p["nkb"], p["Gkb"], p["nslot_kb"]
+    U = T * SS
+    seen = set()
+    y_writes = {}
+    ws_slots = {}
+    arrivals = {}
+
+    def finalize(t, units):
+        assert t not in y_writes, f"tile {t} written twice"
+        assert units == {(kb, t, s) for kb in range(nkb) for s in range(SS)}, f"tile {t} units"
+        y_writes[t] = True
+
+    def publish(t, kb, j, units):
+        assert 0 <= j < nkb * nslot, (t, j, nslot)
+        assert (t, j) not in ws_slots, f"slot {(t, j)} written twice"
+        ws_slots[(t, j)] = units
+        nwg = owner_wg(t * SS + SS - 1, U, G) - owner_wg(t * SS, U, G) + 1
+        arrivals[t] = arrivals.get(t, 0) + 1
+        if arrivals[t] == nkb * nwg:
+            allu = set()
+            for kb2 in range(nkb):
+                for j2 in range(nwg):
+                    allu |= ws_slots[(t, kb2 * nslot + j2)]
+            finalize(t, allu)
+
+    for kb in range(nkb):
+        for cl in range(G):
+            a, b = U * cl // G, U * (cl + 1) // G
+            L = b - a
+            ranges = [(a + L * w // WAVES, a + L * (w + 1) // WAVES) for w in range(WAVES)]
+            wslot = {}
+            for w, (aw, bw) in enumerate(ranges):
+                if aw >= bw:
+                    continue
+                t_first = aw // SS
+                cur = set()
+                for u in range(aw, bw):
+                    t, s = divmod(u, SS)
+                    key = (kb, t, s)
+                    assert key not in seen, f"unit {key} computed twice"
+                    seen.add(key)
+                    cur.add(key)
+                    if s == SS - 1 or u + 1 == bw:
+                        whole = t * SS >= aw and (t + 1) * SS <= bw
+                        if whole and nkb == 1:
+                            finalize(t, cur)
+                        elif whole:
+                            publish(t, kb, kb * nslot, cur)
+                        else:
+                            sidx = 0 if t == t_first else 1
+                            assert (w, sidx) not in wslot
+                            wslot[(w, sidx)] = (t, cur)
+                        cur = set()
+            for w, (aw, bw) in enumerate(ranges):
+                if aw >= bw:
+                    continue
+                t_first, t_last = aw // SS, (bw - 1) // SS
+                for which in (0, 1):
+                    t = t_last if which else t_first
+                    if which and t_last == t_first:
+                        break
+                    if t * SS >= aw and (t + 1) * SS <= bw:
+                        continue
+                    if max(t * SS, a) < aw:
+                        continue
+                    tt, units = wslot[(w, which)]
+                    assert tt == t
+                    units = set(units)
+                    for w2 in range(w + 1, WAVES):
+                        a2, b2 = ranges[w2]
+                        if a2 >= (t + 1) * SS:
+                            break
+                        if a2 == b2:
+                            continue
+                        t2, u2 = wslot[(w2, 0)]
+                        assert t2 == t
+                        units |= u2
+                    if t * SS >= a and (t + 1) * SS <= b and nkb == 1:
+                        finalize(t, units)
+                    else:
+                        first = owner_wg(t * SS, U, G)
+                        publish(t, kb, kb * nslot + (cl - first), units)
+    assert len(seen) == nkb * U
+    assert sorted(y_writes) == list(range(T))
+    need_ws = nkb > 1 or nslot > 1
+    assert p["need_ws"] == int(need_ws)
+    if not need_ws:
+        assert not ws_slots
+
+
+SHAPES = [
+    (8, 17408, 5120, 4, 64), (1, 17408, 5120, 4, 64), (8, 5120, 17408, 4, 64),
+    (8, 7168, 5120, 8, 64), (8, 5120, 5120, 8, 64), (8, 7168, 5120, 4, 32),
+    (1, 4096, 4096, 4, 64), (8, 1024, 5120, 4, 64), (8, 16, 128, 4, 64), (3, 40, 256, 4, 64),
+    (8, 257, 640, 4, 64), (8, 48, 16384, 4, 64), (4, 5000, 12288, 4, 64), (8, 17, 8192, 8, 64),
+    (8, 333, 768, 4, 128), (8, 130, 1024, 8, 128), (8, 200, 512, 8, 32), (2, 3, 2560, 4, 64),
+    (8, 100000, 256, 4, 64), (5, 999, 3072, 8, 64),
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_split_covers_every_unit_once(shape):
+    p = make_plan(*shape)
+    assert p is not None, shape
+    replay(p)
+
+
+@pytest.mark.parametrize("cus", [1, 7, 80, 256, 304])
+def test_split_for_other_cu_counts(cus):
+    for shape in [(8, 17408, 5120, 4, 64), (8, 48, 16384, 4, 64), (1, 300, 1024, 8, 32)]:
+        replay(make_plan(*shape, cus=cus))
+
+
+def test_planner_respects_lds_and_staging_limits():
+    for (M, N, K, bits, gs) in [(8, 5120, 17408, 4, 64), (1, 5120, 17408, 4, 64),
+                                (8, 64, 65536, 4, 128)]:
+        p = make_plan(M, N, K, bits, gs)
+        assert M * p["kr"] // 8 <= 12 * 512
+        assert p["lds_bytes"] <= 163840
+        assert K % p["kr"] == 0 and K // p["kr"] == p["nkb"]
+
+
+def test_planner_rejects_unsupported_shapes():
+    assert make_plan(9, 64, 512, 4, 64) is None     # more than 8 rows per launch
+    assert make_plan(8, 64, 500, 4, 64) is None     # K not a multiple of the super-step
+    assert make_plan(8, 64, 192, 4, 128) is None
