@@ -14,7 +14,8 @@ namespace dfq {
 struct Plan {
     int kss = 0;        /* k per super-step                                  */
     int T = 0;          /* column tiles of 16                                */
-    int SS = 0;         /* super-steps per k-block                           */
+    int ch = 0;         /* super-steps per chunk (1, or 8 groups' worth)     */
+    int SS = 0;         /* chunks per tile per k-block                       */
     int nkb = 0;        /* k-blocks                                          */
     int Gkb = 0;        /* workgroups per k-block                            */
     int nslot_kb = 0;   /* partial slots per tile per k-block                */

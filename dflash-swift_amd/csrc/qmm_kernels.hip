@@ -52,6 +52,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "qmm_params.h"
 
 namespace {
@@ -280,7 +282,13 @@ __device__ __forceinline__ void store_y(const QmmParams& p, int t, int lane, f32
 }
 
 /* Contribute a partial tile to the workspace; the last contributor sums all slots of the
- * tile in a fixed order, writes y and re-arms the counter. */
+ * tile in a fixed order, writes y, zeroes the slots and re-arms the counter, so the whole
+ * workspace is zero again when the kernel ends.
+ *
+ * Workgroups on different XCDs exchange these partials.  Every access to a slot or a
+ * counter is an agent-scope atomic (coherent across the XCDs' L2s without a whole-cache
+ * write-back or invalidate); the slot stores are waited for before the counter increment,
+ * and the last contributor only reads slots after its own increment has returned. */
 template <bool F16>
 __device__ void publish(const QmmParams& p, int t, int slot, int lane, f32x4_t v) {
     const int q = lane >> 4, n = lane & 15;
@@ -288,23 +296,30 @@ __device__ void publish(const QmmParams& p, int t, int slot, int lane, f32x4_t v
     const int U = p.T * SS;
     const int nwg = owner_wg(t * SS + SS - 1, U, p.Gkb) - owner_wg(t * SS, U, p.Gkb) + 1;
     const uint32_t total = (uint32_t)(p.nkb * nwg);
-    float* base = p.slots + (size_t)t * p.nkb * p.nslot_kb * 128;
-    if (lane < 32) *(f32x4_t*)(base + (size_t)slot * 128 + n * 8 + q * 4) = v;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    uint32_t* base = (uint32_t*)p.slots + (size_t)t * p.nkb * p.nslot_kb * 128;
+    if (lane < 32) {
+        uint32_t* sl = base + (size_t)slot * 128 + n * 8 + q * 4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            __hip_atomic_store(sl + r, __float_as_uint(v[r]), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     uint32_t old = 0;
     if (lane == 0)
-        old = __hip_atomic_fetch_add(p.counters + t, 1u, __ATOMIC_ACQ_REL,
+        old = __hip_atomic_fetch_add(p.counters + t, 1u, __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_AGENT);
     old = __builtin_amdgcn_readfirstlane(old);
     if (old + 1 != total) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
     if (lane < 32) {
         for (int kb = 0; kb < p.nkb; ++kb)
             for (int j = 0; j < nwg; ++j) {
-                const float* s = base + ((size_t)kb * p.nslot_kb + j) * 128 + n * 8 + q * 4;
-                f32x4_t w = __builtin_nontemporal_load((const f32x4_t*)s);
-                sum += w;
+                uint32_t* sl = base + ((size_t)kb * p.nslot_kb + j) * 128 + n * 8 + q * 4;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    sum[r] += __uint_as_float(__hip_atomic_exchange(
+                        sl + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
             }
     }
     store_y<F16>(p, t, lane, sum);
@@ -316,9 +331,13 @@ __device__ void publish(const QmmParams& p, int t, int slot, int lane, f32x4_t v
 /* The fast kernel                                                                      */
 /* ---------------------------------------------------------------------------------- */
 
-template <int BITS, int GS, bool F16, int PF>
+/* CH super-steps form one work unit ("chunk").  With CH = 8 / GPS a chunk spans exactly 8
+ * quantisation groups, so each lane fetches the chunk's scales (and biases) of its row as
+ * one 16-byte load; CH = 1 is the general form (one 4-byte scale load per super-step). */
+template <int BITS, int GS, bool F16, int CH, int PF>
 __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     using C = Cfg<BITS, GS>;
+    static_assert(CH == 1 || CH * C::GPS == 8, "chunk = one super-step or 8 groups");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
     const int tid = threadIdx.x;
@@ -329,7 +348,7 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
 
     const int kb = blockIdx.x / p.Gkb;
     const int cl = blockIdx.x - kb * p.Gkb;
-    const int SS = p.SS;
+    const int SS = p.SS;      // chunks per tile per k-block
     const int U = p.T * SS;
     const int a = (int)((int64_t)U * cl / p.Gkb);
     const int b = (int)((int64_t)U * (cl + 1) / p.Gkb);
@@ -353,14 +372,17 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
         const int r = it / CPR, c = it - r * CPR;
         xv[i] = *(const u32x4_t*)(xg + (size_t)r * p.K + k0 + c * 8);
     }
+    __builtin_amdgcn_sched_barrier(0);
 
-    /* ---- weight / scale / bias prefetch ring */
+    /* ---- weight / scale / bias prefetch ring, one chunk per slot */
     const uint32_t lane_w = (uint32_t)n * RB + (uint32_t)q * 16u;
-    const uint32_t lane_s = ((uint32_t)n * GPR + (C::GPS == 4 ? 2u * (q >> 1) : 0u)) * 2u;
-    u32x4_t rw[PF][C::NS];
-    uint32_t rs[PF], rb[PF];
+    const uint32_t lane_s = (CH > 1) ? (uint32_t)n * GPR * 2u
+                                     : ((uint32_t)n * GPR + (C::GPS == 4 ? 2u * (q >> 1) : 0u)) * 2u;
+    using SV = typename std::conditional<(CH > 1), u32x4_t, uint32_t>::type;
+    u32x4_t rw[PF][CH][C::NS];
+    SV rs[PF], rb[PF];
 
-    int pt = aw / SS, pss = aw - (aw / SS) * SS;  // prefetch stream position
+    int pt = aw / SS, pc = aw - (aw / SS) * SS;  // prefetch stream position (tile, chunk)
     auto issue = [&](int slot, int u) {
         const bool valid = u < bw;
         const int row0 = pt * 16;
@@ -371,16 +393,26 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
             make_rsrc((const uint16_t*)p.scales + (size_t)row0 * GPR, srec);
         __amdgpu_buffer_rsrc_t rsb =
             make_rsrc((const uint16_t*)p.biases + (size_t)row0 * GPR, srec);
-        const int kss = k0 + pss * C::KSS;
-        const int soff_w = kss * BITS / 8;
-        const int soff_s = (kss / GS) * 2;
+        const int kc = k0 + pc * (CH * C::KSS);  // first k of the chunk
+        const int soff_w = kc * BITS / 8;
+        const int soff_s = (kc / GS) * 2;
 #pragma unroll
-        for (int s = 0; s < C::NS; ++s)
-            rw[slot][s] = __builtin_bit_cast(
-                u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rsw, lane_w, soff_w + s * 64, 0));
-        rs[slot] = __builtin_amdgcn_raw_buffer_load_b32(rss, lane_s, soff_s, 0);
-        rb[slot] = __builtin_amdgcn_raw_buffer_load_b32(rsb, lane_s, soff_s, 0);
-        if (++pss == SS) { pss = 0; ++pt; }
+        for (int j = 0; j < CH; ++j)
+#pragma unroll
+            for (int s = 0; s < C::NS; ++s)
+                rw[slot][j][s] = __builtin_bit_cast(
+                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                 rsw, lane_w, soff_w + (j * C::NS + s) * 64, 0));
+        if constexpr (CH > 1) {
+            rs[slot] = __builtin_bit_cast(
+                u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rss, lane_s, soff_s, 0));
+            rb[slot] = __builtin_bit_cast(
+                u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rsb, lane_s, soff_s, 0));
+        } else {
+            rs[slot] = __builtin_amdgcn_raw_buffer_load_b32(rss, lane_s, soff_s, 0);
+            rb[slot] = __builtin_amdgcn_raw_buffer_load_b32(rsb, lane_s, soff_s, 0);
+        }
+        if (++pc == SS) { pc = 0; ++pt; }
     };
 #pragma unroll
     for (int i = 0; i < PF; ++i) issue(i, aw + i);
@@ -421,44 +453,63 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
 
     const int t_first = aw / SS;
     f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    int ct = t_first, css = aw - t_first * SS;
+    int ct = t_first, cc = aw - t_first * SS;
 
     for (int u0 = aw; u0 < bw; u0 += PF) {
 #pragma unroll
         for (int i = 0; i < PF; ++i) {
             const int u = u0 + i;
             if (u < bw) {
-                uint32_t OW[C::NOW];
-                build_operand_words<BITS, GS>(rw[i], OW);
-                const uint32_t aoff = abase + (uint32_t)css * (C::CPS * 16);
-                f32x4_t P[C::NP];
 #pragma unroll
-                for (int pp = 0; pp < C::NP; ++pp) P[pp] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                for (int j = 0; j < CH; ++j) {
+                    const int css = cc * CH + j;  // super-step within the k-block
+                    uint32_t OW[C::NOW];
+                    build_operand_words<BITS, GS>(rw[i][j], OW);
+                    const uint32_t aoff = abase + (uint32_t)css * (C::CPS * 16);
+                    f32x4_t P[C::NP];
 #pragma unroll
-                for (int o = 0; o < C::NOPS; ++o) {
-                    const u32x4_t A =
-                        *(const u32x4_t*)(lds + aoff + C::delta_chunk(o) * 16);
-                    u32x4_t B;
-                    if constexpr (BITS == 4) B = nibble_operand<F16>(OW[o]);
-                    else B = byte_operand<F16>(OW[2 * o], OW[2 * o + 1]);
-                    P[C::partial_of(o)] = mfma<F16>(A, B, P[C::partial_of(o)]);
-                }
-                const uint32_t xo = xbase + (uint32_t)css * (C::GPS * 32);
+                    for (int pp = 0; pp < C::NP; ++pp) P[pp] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int pp = 0; pp < C::NP; ++pp) {
-                    const uint32_t sh = (C::GPS == 4) ? (pp ? 0u : 16u) : sh_half;
-                    const float s = half_of<F16>(rs[i], sh);
-                    const float bb = half_of<F16>(rb[i], sh);
-                    const float bp = (kOff != 0.0f) ? __builtin_fmaf(-kOff, s, bb) : bb;
-                    const f32x4_t X = *(const f32x4_t*)(lds + xo + pp * 32);
+                    for (int o = 0; o < C::NOPS; ++o) {
+                        const u32x4_t A =
+                            *(const u32x4_t*)(lds + aoff + C::delta_chunk(o) * 16);
+                        u32x4_t B;
+                        if constexpr (BITS == 4) B = nibble_operand<F16>(OW[o]);
+                        else B = byte_operand<F16>(OW[2 * o], OW[2 * o + 1]);
+                        P[C::partial_of(o)] = mfma<F16>(A, B, P[C::partial_of(o)]);
+                    }
+                    const uint32_t xo = xbase + (uint32_t)css * (C::GPS * 32);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        acc[r] = __builtin_fmaf(s, P[pp][r], acc[r]);
-                        acc[r] = __builtin_fmaf(bp, X[r], acc[r]);
+                    for (int pp = 0; pp < C::NP; ++pp) {
+                        uint32_t sw, bw2, sh;
+                        if constexpr (CH > 1) {
+                            if constexpr (C::GPS == 4) {
+                                sw = (q >> 1) ? rs[i][2 * j + 1] : rs[i][2 * j];
+                                bw2 = (q >> 1) ? rb[i][2 * j + 1] : rb[i][2 * j];
+                                sh = pp ? 0u : 16u;
+                            } else {
+                                sw = rs[i][j];
+                                bw2 = rb[i][j];
+                                sh = sh_half;
+                            }
+                        } else {
+                            sw = rs[i];
+                            bw2 = rb[i];
+                            sh = (C::GPS == 4) ? (pp ? 0u : 16u) : sh_half;
+                        }
+                        const float s = half_of<F16>(sw, sh);
+                        const float bb = half_of<F16>(bw2, sh);
+                        const float bp = (kOff != 0.0f) ? __builtin_fmaf(-kOff, s, bb) : bb;
+                        const f32x4_t X = *(const f32x4_t*)(lds + xo + pp * 32);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            acc[r] = __builtin_fmaf(s, P[pp][r], acc[r]);
+                            acc[r] = __builtin_fmaf(bp, X[r], acc[r]);
+                        }
                     }
                 }
                 /* end of this wave's part of tile ct? */
-                if (css == SS - 1 || u + 1 == bw) {
+                if (cc == SS - 1 || u + 1 == bw) {
                     f32x4_t v;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
@@ -480,7 +531,7 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
                     }
                     acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
                 }
-                if (++css == SS) { css = 0; ++ct; }
+                if (++cc == SS) { cc = 0; ++ct; }
             }
             issue(i, u + PF);
         }
@@ -495,8 +546,8 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
         const int t = which ? t_last : t_first;
         if (which && t_last == t_first) break;
         const bool whole = t * SS >= aw && (t + 1) * SS <= bw;
-        if (whole) continue;                       // written in the main loop
-        if ((t * SS > a ? t * SS : a) < aw) continue;  // an earlier wave combines it
+        if (whole) continue;                             // written in the main loop
+        if ((t * SS > a ? t * SS : a) < aw) continue;    // an earlier wave combines it
         f32x4_t v = {0.0f, 0.0f, 0.0f, 0.0f};
         if (lane < 32) {
             v = *(const f32x4_t*)(wslot + (wave * 2 + which) * 128 + n * 8 + q * 4);
@@ -571,21 +622,24 @@ extern "C" __global__ void __launch_bounds__(256) dfq_fill_u32(uint32_t* ptr, ui
         ptr[i] = v;
 }
 
-#define DFQ_MT8_KERNEL(BITS, GS, F16, NAME)                                                 \
-    extern "C" __global__ void __launch_bounds__(kThreads) dfq_qmm_mt8_b##BITS##_g##GS##_##NAME( \
-        QmmParams p) {                                                                      \
-        qmm_mt8<BITS, GS, F16, 8>(p);                                                       \
+#define DFQ_MT8_KERNEL(BITS, GS, F16, NAME, CHN, CH)                                        \
+    extern "C" __global__ void __launch_bounds__(kThreads)                                   \
+        dfq_qmm_mt8_b##BITS##_g##GS##_##NAME##_##CHN(QmmParams p) {                           \
+        qmm_mt8<BITS, GS, F16, CH, (CH > 1 ? 2 : 8)>(p);                                      \
     }
+#define DFQ_MT8_FORMAT(BITS, GS, F16, NAME)                                                    \
+    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c1, 1)                                                \
+    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS))
 
-DFQ_MT8_KERNEL(4, 32, false, bf16)
-DFQ_MT8_KERNEL(4, 64, false, bf16)
-DFQ_MT8_KERNEL(4, 128, false, bf16)
-DFQ_MT8_KERNEL(8, 32, false, bf16)
-DFQ_MT8_KERNEL(8, 64, false, bf16)
-DFQ_MT8_KERNEL(8, 128, false, bf16)
-DFQ_MT8_KERNEL(4, 32, true, f16)
-DFQ_MT8_KERNEL(4, 64, true, f16)
-DFQ_MT8_KERNEL(4, 128, true, f16)
-DFQ_MT8_KERNEL(8, 32, true, f16)
-DFQ_MT8_KERNEL(8, 64, true, f16)
-DFQ_MT8_KERNEL(8, 128, true, f16)
+DFQ_MT8_FORMAT(4, 32, false, bf16)
+DFQ_MT8_FORMAT(4, 64, false, bf16)
+DFQ_MT8_FORMAT(4, 128, false, bf16)
+DFQ_MT8_FORMAT(8, 32, false, bf16)
+DFQ_MT8_FORMAT(8, 64, false, bf16)
+DFQ_MT8_FORMAT(8, 128, false, bf16)
+DFQ_MT8_FORMAT(4, 32, true, f16)
+DFQ_MT8_FORMAT(4, 64, true, f16)
+DFQ_MT8_FORMAT(4, 128, true, f16)
+DFQ_MT8_FORMAT(8, 32, true, f16)
+DFQ_MT8_FORMAT(8, 64, true, f16)
+DFQ_MT8_FORMAT(8, 128, true, f16)

@@ -12,10 +12,11 @@
  *
  *  - output features are cut into T column tiles of 16 (the MFMA N dimension);
  *  - K is cut into nkb k-blocks of kr elements (kr * rows of x must fit in LDS), and each
- *    k-block into SS super-steps (one super-step = the k span that holds exactly two
- *    quantisation groups per lane half, 64..256 elements);
- *  - the T*SS units of one k-block are split into Gkb equal contiguous ranges, one per
- *    workgroup, and each workgroup's range into one contiguous range per wave;
+ *    k-block into SS chunks of CH super-steps (one super-step = the k span that holds
+ *    exactly two quantisation groups per lane half, 64..256 elements; a chunk is one
+ *    super-step or the 8 groups whose scales one 16-byte load fetches);
+ *  - the T*SS units (tile, chunk) of one k-block are split into Gkb equal contiguous
+ *    ranges, one per workgroup, and each workgroup's range into one range per wave;
  *  - a tile covered by one wave is written straight to y; a tile shared between waves is
  *    summed in LDS in wave order; a tile shared between workgroups (or k-blocks) is summed
  *    through workspace slots in a fixed order by whichever workgroup arrives last.
@@ -31,7 +32,7 @@ typedef struct QmmParams {
     uint32_t* counters;     /* workspace: per-tile arrival counters (zero at rest)    */
     int32_t M, N, K;
     int32_t T;              /* column tiles of 16                                     */
-    int32_t SS;             /* super-steps per k-block                                */
+    int32_t SS;             /* chunks per tile per k-block                            */
     int32_t nkb;            /* k-blocks                                               */
     int32_t Gkb;            /* workgroups per k-block                                 */
     int32_t nslot_kb;       /* partial slots per tile per k-block                     */

@@ -70,7 +70,7 @@ struct dfq_ctx {
     int num_cus = 0;
     size_t lds_max = 0;
     hipModule_t module = nullptr;
-    hipFunction_t mt8[2][3][2] = {};  // [bits 4/8][gs 32/64/128][bf16/f16]
+    hipFunction_t mt8[2][3][2][2] = {};  // [bits 4/8][gs 32/64/128][bf16/f16][chunk 1/8 groups]
     hipFunction_t generic = nullptr;
     hipFunction_t fill = nullptr;
     std::mutex mu;
@@ -124,11 +124,15 @@ static int64_t owner_wg(int64_t u, int64_t U, int64_t G) { return (G * (u + 1) -
 bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_max, Plan* pl) {
     const int kss = kss_for(bits, gs);
     if (M < 1 || M > 8 || N < 1 || K < kss || K % kss) return false;
-    const int ss_total = K / kss;
+    /* A chunk of 8 groups lets each lane fetch its row's scales with one 16-byte load. */
+    const int gps = kss / gs;
+    const int ch = (K % (kss * (8 / gps)) == 0) ? 8 / gps : 1;
+    const int kch = kss * ch;
+    const int chunks = K / kch;
     int nkb = 0, kr = 0;
     size_t lds = 0;
-    for (int d = 1; d <= ss_total; ++d) {
-        if (ss_total % d) continue;
+    for (int d = 1; d <= chunks; ++d) {
+        if (chunks % d) continue;
         const int k = K / d;
         if ((int64_t)M * (k / 8) > (int64_t)kMaxStageItems * kThreads) continue;
         const size_t rs = (size_t)2 * k + 16;
@@ -142,10 +146,11 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
     if (!nkb) return false;
     Plan p{};
     p.kss = kss;
+    p.ch = ch;
     p.T = (N + 15) / 16;
     p.nkb = nkb;
     p.kr = kr;
-    p.SS = ss_total / nkb;
+    p.SS = chunks / nkb;
     const int64_t U = (int64_t)p.T * p.SS;
     int64_t G = std::max(1, num_cus / nkb);
     if (G > U) G = U;
@@ -256,18 +261,21 @@ dfq_status dfq_init(int device, dfq_ctx** out) {
     static const int kBits[2] = {4, 8};
     static const int kGs[3] = {32, 64, 128};
     static const char* kDt[2] = {"bf16", "f16"};
+    static const char* kCh[2] = {"c1", "c8"};
     for (int b = 0; b < 2; ++b)
         for (int g2 = 0; g2 < 3; ++g2)
-            for (int d = 0; d < 2; ++d) {
-                char name[64];
-                snprintf(name, sizeof name, "dfq_qmm_mt8_b%d_g%d_%s", kBits[b], kGs[g2], kDt[d]);
-                if ((e = hipModuleGetFunction(&ctx->mt8[b][g2][d], ctx->module, name)) !=
-                    hipSuccess) {
-                    (void)hipModuleUnload(ctx->module);
-                    delete ctx;
-                    return hip_fail(e, name);
+            for (int d = 0; d < 2; ++d)
+                for (int c = 0; c < 2; ++c) {
+                    char name[64];
+                    snprintf(name, sizeof name, "dfq_qmm_mt8_b%d_g%d_%s_%s", kBits[b], kGs[g2],
+                             kDt[d], kCh[c]);
+                    if ((e = hipModuleGetFunction(&ctx->mt8[b][g2][d][c], ctx->module, name)) !=
+                        hipSuccess) {
+                        (void)hipModuleUnload(ctx->module);
+                        delete ctx;
+                        return hip_fail(e, name);
+                    }
                 }
-            }
     if ((e = hipModuleGetFunction(&ctx->generic, ctx->module, "dfq_qmm_generic")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->fill, ctx->module, "dfq_fill_u32")) != hipSuccess) {
         (void)hipModuleUnload(ctx->module);
@@ -449,7 +457,8 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
     const int gi = gs == 32 ? 0 : gs == 64 ? 1 : 2;
     const int di = dt == DFQ_BF16 ? 0 : 1;
     void* args[] = {&p};
-    hipError_t e = hipModuleLaunchKernel(ctx->mt8[bi][gi][di], (unsigned)(pl.nkb * pl.Gkb), 1, 1,
+    const int ci = pl.ch > 1 ? 1 : 0;
+    hipError_t e = hipModuleLaunchKernel(ctx->mt8[bi][gi][di][ci], (unsigned)(pl.nkb * pl.Gkb), 1, 1,
                                          kThreads, 1, 1, (unsigned)pl.lds_bytes, stream, args,
                                          nullptr);
     return e == hipSuccess ? DFQ_OK : hip_fail(e, "launch dfq_qmm_mt8");
@@ -572,26 +581,26 @@ dfq_status dfq_graph_destroy(dfq_graph* gr) {
 /* ---- introspection used by tests and the benchmark (not part of the drop-in surface) -- */
 
 /* Fills the work split the fast kernel uses for a shape: {T, SS, nkb, Gkb, nslot_kb, kr,
- * lds_bytes, need_ws}. */
-dfq_status dfq_debug_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, int* out8) {
-    if (!out8) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
+ * lds_bytes, need_ws, ch}. */
+dfq_status dfq_debug_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, int* out9) {
+    if (!out9) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
     Plan p;
     dfq_status s = get_plan(ctx, M, N, K, bits, gs, &p);
     if (s) return s;
-    int v[8] = {p.T, p.SS, p.nkb, p.Gkb, p.nslot_kb, p.kr, p.lds_bytes, p.need_ws ? 1 : 0};
-    std::memcpy(out8, v, sizeof v);
+    int v[9] = {p.T, p.SS, p.nkb, p.Gkb, p.nslot_kb, p.kr, p.lds_bytes, p.need_ws ? 1 : 0, p.ch};
+    std::memcpy(out9, v, sizeof v);
     return DFQ_OK;
 }
 
 /* The same split computed without a device, for a given CU count and LDS limit. */
 dfq_status dfq_debug_make_plan(int M, int N, int K, int bits, int gs, int num_cus,
-                               size_t lds_max, int* out8) {
-    if (!out8) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
+                               size_t lds_max, int* out9) {
+    if (!out9) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
     Plan p;
     if (!make_plan(M, N, K, bits, gs, num_cus, lds_max, &p))
         return fail(DFQ_ERR_UNSUPPORTED, "no work split");
-    int v[8] = {p.T, p.SS, p.nkb, p.Gkb, p.nslot_kb, p.kr, p.lds_bytes, p.need_ws ? 1 : 0};
-    std::memcpy(out8, v, sizeof v);
+    int v[9] = {p.T, p.SS, p.nkb, p.Gkb, p.nslot_kb, p.kr, p.lds_bytes, p.need_ws ? 1 : 0, p.ch};
+    std::memcpy(out9, v, sizeof v);
     return DFQ_OK;
 }
 

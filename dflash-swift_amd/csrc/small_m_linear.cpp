@@ -133,7 +133,8 @@ struct dfq_model {
 extern "C" {
 
 dfq_status dfq_linear_create(dfq_ctx* ctx, const dfq_linear_desc* desc, dfq_linear** out) {
-    if (!ctx || !desc || !out) return dfq::fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
+    /* ctx may be NULL: such a layer can be inspected and swapped but not called. */
+    if (!desc || !out) return dfq::fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
     *out = nullptr;
     const dfq_linear_desc& d = *desc;
     if (!d.weight || !d.scales)
@@ -171,12 +172,14 @@ dfq_dtype dfq_linear_output_dtype(const dfq_linear* lin, dfq_dtype x_dtype) {
 dfq_status dfq_linear_forward(dfq_linear* lin, const void* x, dfq_dtype x_dtype, int rows,
                               void* y, void* ws, size_t wsb, void* stream, int* took_kernel) {
     if (!lin) return dfq::fail(DFQ_ERR_INVALID_ARGUMENT, "null layer");
+    if (!lin->impl->ctx()) return dfq::fail(DFQ_ERR_STATE, "layer was created without a context");
     if (rows < 1) return dfq::fail(DFQ_ERR_INVALID_ARGUMENT, "rows must be >= 1");
     return lin->impl->callAsFunction(x, x_dtype, rows, y, ws, wsb, stream, took_kernel);
 }
 
 dfq_status dfq_linear_workspace_bytes(dfq_linear* lin, int rows, size_t* bytes) {
     if (!lin || !bytes) return dfq::fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
+    if (!lin->impl->ctx()) return dfq::fail(DFQ_ERR_STATE, "layer was created without a context");
     return lin->impl->workspaceBytes(rows, bytes);
 }
 

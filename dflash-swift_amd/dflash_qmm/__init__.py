@@ -146,8 +146,8 @@ def dtype_code(t) -> int:
 class Context:
     """A dfq_ctx: the gfx950 code object loaded on one device."""
 
-    def __init__(self, device: int = 0):
-        self.lib = load_library()
+    def __init__(self, device: int = 0, lib_path: str | None = None):
+        self.lib = load_library(lib_path)
         h = ctypes.c_void_p()
         _check(self.lib.dfq_init(device, ctypes.byref(h)), "dfq_init")
         self.handle = h
@@ -186,9 +186,9 @@ class Context:
                "dfq_workspace_clear")
 
     def plan(self, M, N, K, bits, gs) -> dict:
-        out = (ctypes.c_int * 8)()
+        out = (ctypes.c_int * 9)()
         _check(self.lib.dfq_debug_plan(self.handle, M, N, K, bits, gs, out), "dfq_debug_plan")
-        keys = ["T", "SS", "nkb", "Gkb", "nslot_kb", "kr", "lds_bytes", "need_ws"]
+        keys = ["T", "SS", "nkb", "Gkb", "nslot_kb", "kr", "lds_bytes", "need_ws", "ch"]
         return dict(zip(keys, list(out)))
 
     def qmm_raw(self, x, w, scales, biases, y, M, N, K, bits, gs, xdt, sdt, ydt, lbias=None,
@@ -300,9 +300,11 @@ class SmallMQuantizedMatmul:
 class QuantizedLinear:
     """MLX's QuantizedLinear over device arrays (weight, scales, biases, bias)."""
 
-    def __init__(self, ctx: Context, weight, scales, biases, bias=None, group_size=64, bits=4,
-                 mode="affine", _handle=None):
+    def __init__(self, ctx: Context | None, weight, scales, biases, bias=None, group_size=64,
+                 bits=4, mode="affine", _handle=None):
+        """ctx None gives a layer that can be inspected and swapped but not called."""
         self.ctx = ctx
+        self.lib = load_library()
         self.weight, self.scales, self.biases, self.bias = weight, scales, biases, bias
         self.group_size, self.bits, self.mode = group_size, bits, mode
         self.out_features = weight.shape[0]
@@ -310,21 +312,23 @@ class QuantizedLinear:
         if _handle is not None:
             self._h = _handle
             return
-        d = _LinearDesc(_ptr(weight), _ptr(scales), _ptr(biases), _ptr(bias),
-                        self.out_features, self.in_features, bits, group_size,
-                        int(mode == "affine"), dtype_code(scales))
+        d = _desc(self)
         h = ctypes.c_void_p()
-        _check(ctx.lib.dfq_linear_create(ctx.handle, ctypes.byref(d), ctypes.byref(h)),
-               "dfq_linear_create")
+        _check(self.lib.dfq_linear_create(ctx.handle if ctx else None, ctypes.byref(d),
+                                          ctypes.byref(h)), "dfq_linear_create")
         self._h = h
 
     def __del__(self):
         try:
             if self._h:
-                self.ctx.lib.dfq_linear_destroy(self._h)
+                self.lib.dfq_linear_destroy(self._h)
                 self._h = None
         except Exception:
             pass
+
+    @property
+    def is_small_m(self) -> bool:
+        return bool(self.lib.dfq_linear_is_small_m(self._h))
 
     @property
     def shape(self):
@@ -332,7 +336,7 @@ class QuantizedLinear:
 
     def output_dtype(self, x):
         import torch
-        code = self.ctx.lib.dfq_linear_output_dtype(self._h, dtype_code(x))
+        code = self.lib.dfq_linear_output_dtype(self._h, dtype_code(x))
         return {BF16: torch.bfloat16, F16: torch.float16, F32: torch.float32}[code]
 
     def __call__(self, x, stream=None):
@@ -345,11 +349,11 @@ class QuantizedLinear:
         flat = x.reshape(rows, x.shape[-1]).contiguous()
         y = torch.empty((rows, self.out_features), dtype=self.output_dtype(x), device=x.device)
         nb = ctypes.c_size_t()
-        _check(self.ctx.lib.dfq_linear_workspace_bytes(self._h, rows, ctypes.byref(nb)),
+        _check(self.lib.dfq_linear_workspace_bytes(self._h, rows, ctypes.byref(nb)),
                "dfq_linear_workspace_bytes")
         ws = self.ctx.workspace(nb.value)
         took = ctypes.c_int(0)
-        _check(self.ctx.lib.dfq_linear_forward(
+        _check(self.lib.dfq_linear_forward(
             self._h, _ptr(flat), dtype_code(x), rows, _ptr(y), _ptr(ws),
             ws.numel() if ws is not None else 0, _stream(stream), ctypes.byref(took)),
             "dfq_linear_forward")
@@ -357,65 +361,73 @@ class QuantizedLinear:
         return y.reshape(*lead, self.out_features)
 
 
+def _desc(layer) -> _LinearDesc:
+    return _LinearDesc(_ptr(layer.weight), _ptr(layer.scales), _ptr(layer.biases),
+                       _ptr(layer.bias), layer.out_features, layer.in_features, layer.bits,
+                       layer.group_size, int(layer.mode == "affine"), dtype_code(layer.scales))
+
+
 class SmallMQuantizedLinear(QuantizedLinear):
     """SmallMQuantizedLinear(other): shares other's arrays (SmallMQuantizedMatmul.swift:243-252)."""
 
     def __init__(self, other: QuantizedLinear):
         h = ctypes.c_void_p()
-        _check(other.ctx.lib.dfq_small_m_linear_create(other._h, ctypes.byref(h)),
+        _check(other.lib.dfq_small_m_linear_create(other._h, ctypes.byref(h)),
                "dfq_small_m_linear_create")
         super().__init__(other.ctx, other.weight, other.scales, other.biases, other.bias,
                          other.group_size, other.bits, other.mode, _handle=h)
 
 
 class Model:
-    """A module tree reduced to named leaf layers."""
+    """A module tree reduced to named leaf layers (the model owns its own layer handles)."""
 
-    def __init__(self, ctx: Context, **leaves: QuantizedLinear):
-        self.ctx = ctx
+    def __init__(self, **leaves: QuantizedLinear):
+        self.lib = load_library()
         h = ctypes.c_void_p()
-        _check(ctx.lib.dfq_model_create(ctypes.byref(h)), "dfq_model_create")
+        _check(self.lib.dfq_model_create(ctypes.byref(h)), "dfq_model_create")
         self._h = h
-        self._py = {}
+        self._src = {}
         for name, leaf in leaves.items():
             self.set_leaf(name, leaf)
 
     def set_leaf(self, path: str, leaf: QuantizedLinear):
-        # the model owns a handle of its own on the same layer object
-        if isinstance(leaf, SmallMQuantizedLinear):
-            h = ctypes.c_void_p()
-            _check(self.ctx.lib.dfq_small_m_linear_create(leaf._h, ctypes.byref(h)),
+        h = ctypes.c_void_p()
+        if leaf.is_small_m:
+            _check(self.lib.dfq_small_m_linear_create(leaf._h, ctypes.byref(h)),
                    "dfq_small_m_linear_create")
         else:
-            d = _LinearDesc(_ptr(leaf.weight), _ptr(leaf.scales), _ptr(leaf.biases),
-                            _ptr(leaf.bias), leaf.out_features, leaf.in_features, leaf.bits,
-                            leaf.group_size, int(leaf.mode == "affine"), dtype_code(leaf.scales))
-            h = ctypes.c_void_p()
-            _check(self.ctx.lib.dfq_linear_create(self.ctx.handle, ctypes.byref(d),
-                                                  ctypes.byref(h)), "dfq_linear_create")
-        _check(self.ctx.lib.dfq_model_set_leaf(self._h, path.encode(), h), "dfq_model_set_leaf")
-        self._py[path] = leaf
+            d = _desc(leaf)
+            _check(self.lib.dfq_linear_create(leaf.ctx.handle if leaf.ctx else None,
+                                              ctypes.byref(d), ctypes.byref(h)),
+                   "dfq_linear_create")
+        _check(self.lib.dfq_model_set_leaf(self._h, path.encode(), h), "dfq_model_set_leaf")
+        self._src[path] = leaf
+
+    def __getattr__(self, path: str) -> QuantizedLinear:
+        if path.startswith("_") or path in ("lib",):
+            raise AttributeError(path)
+        return self.leaf(path)
 
     def leaf(self, path: str) -> QuantizedLinear:
-        """The current leaf at `path`, as a Python layer sharing the model's layer object."""
-        h = self.ctx.lib.dfq_model_leaf(self._h, path.encode())
+        """The current leaf at `path`: a SmallMQuantizedLinear once it has been swapped."""
+        h = self.lib.dfq_model_leaf(self._h, path.encode())
         if not h:
             raise KeyError(path)
         h = ctypes.c_void_p(h)
-        src = self._py[path]
-        cls = SmallMQuantizedLinear if self.ctx.lib.dfq_linear_is_small_m(h) else QuantizedLinear
+        src = self._src[path]
+        cls = SmallMQuantizedLinear if self.lib.dfq_linear_is_small_m(h) else QuantizedLinear
         obj = cls.__new__(cls)
-        QuantizedLinear.__init__(obj, self.ctx, src.weight, src.scales, src.biases, src.bias,
+        QuantizedLinear.__init__(obj, src.ctx, src.weight, src.scales, src.biases, src.bias,
                                  src.group_size, src.bits, src.mode, _handle=h)
         return obj
 
     def __len__(self):
-        return self.ctx.lib.dfq_model_leaf_count(self._h)
+        return self.lib.dfq_model_leaf_count(self._h)
 
     def __del__(self):
         try:
             if self._h:
-                self.ctx.lib.dfq_model_destroy(self._h)
+                self.lib.dfq_model_destroy(self._h)
                 self._h = None
         except Exception:
             pass
@@ -423,7 +435,7 @@ class Model:
 
 def enable_small_m_quantized_matmul(model: Model) -> int:
     """Swap every eligible leaf for a SmallMQuantizedLinear; return how many were swapped."""
-    n = model.ctx.lib.dfq_enable_small_m_quantized_matmul(model._h)
+    n = model.lib.dfq_enable_small_m_quantized_matmul(model._h)
     if n < 0:
         _check(2, "dfq_enable_small_m_quantized_matmul")
     return n

@@ -101,7 +101,8 @@ int dfq_qmm_supported(const dfq_ctx* ctx, int M, int N, int K, int bits, int gro
 /* ---- the matmul ------------------------------------------------------------------- */
 
 /* Workspace dfq_qmm needs for this shape (0 if none).  The workspace must be zero-filled
- * once before its first use (dfq_workspace_clear); every call leaves it zeroed again. */
+ * once before its first use (dfq_workspace_clear); every call leaves all of it zero again,
+ * so one workspace serves calls of any shape in stream order. */
 dfq_status dfq_qmm_workspace_bytes(dfq_ctx* ctx, int M, int N, int K, int bits,
                                    int group_size, size_t* bytes);
 dfq_status dfq_workspace_clear(dfq_ctx* ctx, void* workspace, size_t bytes, void* stream);
@@ -154,7 +155,8 @@ typedef struct dfq_linear_desc {
     dfq_dtype dtype;          /* dtype of scales / biases / bias                     */
 } dfq_linear_desc;
 
-/* A stock QuantizedLinear: every call goes to the generic path. */
+/* A stock QuantizedLinear: every call goes to the generic path.  ctx may be NULL for a
+ * layer that is only inspected or swapped (its forward then returns DFQ_ERR_STATE). */
 dfq_status dfq_linear_create(dfq_ctx* ctx, const dfq_linear_desc* desc, dfq_linear** out);
 /* SmallMQuantizedLinear(other): wraps `other`, sharing its arrays (:243-252). */
 dfq_status dfq_small_m_linear_create(dfq_linear* other, dfq_linear** out);

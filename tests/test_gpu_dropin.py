@@ -1,0 +1,117 @@
+"""The drop-in layer on the GPU, mirroring the reference's kernel tests.
+
+Reference: Tests/DFlashKitTests/SmallMQuantizedMatmulTests.swift.  `stock` is a plain
+QuantizedLinear (the generic path), `fast` is SmallMQuantizedLinear(stock) sharing its
+arrays.  The reference builds its layer with MLX's quantiser from normal(scale 0.05) weights
+(:47-55); MLX is not available here, so codes, scales and biases are drawn directly with the
+same layer shape (out 4096, in 1024, group 64).
+"""
+import numpy as np
+import pytest
+import torch
+
+from dflash_qmm import QuantizedLinear, SmallMQuantizedLinear
+from gpu_util import announce, upload
+from oracle.qmm_oracle import BF16, make_case
+
+pytestmark = pytest.mark.gpu
+
+OUT, IN, TOL = 4096, 1024, 0.02
+
+
+def make_layer(ctx, bits, out_features=OUT, in_features=IN, group_size=64, seed=7):
+    c = make_case(1, out_features, in_features, bits=bits, gs=group_size, seed=seed)
+    _, w, s, b, _ = upload(c)
+    return QuantizedLinear(ctx, w, s, b, None, group_size=group_size, bits=bits)
+
+
+def make_input(rows, in_features=IN, seed=11):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    return (torch.randn(rows, in_features, device="cuda", generator=g) * 0.1).to(torch.bfloat16)
+
+
+def assert_agrees(ctx, bits, rows):
+    stock = make_layer(ctx, bits)
+    fast = SmallMQuantizedLinear(stock)
+    x = make_input(rows)
+    announce(f"dropin agrees bits={bits} rows={rows}")
+    ref = stock(x).float()
+    assert not stock.last_took_kernel
+    got = fast(x)
+    assert fast.last_took_kernel
+    assert got.shape == (rows, OUT)
+    diff = (ref - got.float()).abs().max().item()
+    mag = ref.abs().max().item()
+    assert diff <= TOL * max(mag, 1.0), f"{bits}-bit M={rows}: {diff} at {mag}"
+
+
+@pytest.mark.parametrize("rows", range(6, 17))
+def test_4bit_matches_stock(ctx, rows):
+    assert_agrees(ctx, 4, rows)
+
+
+@pytest.mark.parametrize("rows", range(6, 17))
+def test_8bit_matches_stock(ctx, rows):
+    assert_agrees(ctx, 8, rows)
+
+
+def test_kernel_output_is_not_bit_identical(ctx):
+    stock = make_layer(ctx, 4)
+    fast = SmallMQuantizedLinear(stock)
+    x = make_input(8)
+    announce("dropin not bit identical")
+    assert (stock(x) != fast(x)).any().item()
+
+
+def test_ineligible_shape_returns_the_stock_result(ctx):
+    stock = make_layer(ctx, 4, out_features=2048)
+    fast = SmallMQuantizedLinear(stock)
+    x = make_input(8)
+    announce("dropin ineligible shape")
+    assert torch.equal(stock(x), fast(x))
+    assert not fast.last_took_kernel
+
+
+def test_row_counts_outside_the_window_return_the_stock_result(ctx):
+    stock = make_layer(ctx, 4)
+    fast = SmallMQuantizedLinear(stock)
+    for rows in [1, 3, 5, 17, 24, 32]:
+        x = make_input(rows)
+        announce(f"dropin rows outside window {rows}")
+        assert torch.equal(stock(x), fast(x)), f"M={rows}"
+        assert not fast.last_took_kernel
+
+
+def test_float16_input_falls_through_to_stock(ctx):
+    stock = make_layer(ctx, 4)
+    fast = SmallMQuantizedLinear(stock)
+    x = make_input(8).to(torch.float16)
+    announce("dropin fp16 falls through")
+    ref = stock(x)
+    y = fast(x)
+    assert y.dtype == ref.dtype == torch.float32
+    assert torch.equal(ref, y)
+
+
+def test_leading_dimensions_are_flattened(ctx):
+    """callAsFunction multiplies out the leading dimensions (:255-256, :287)."""
+    stock = make_layer(ctx, 4)
+    fast = SmallMQuantizedLinear(stock)
+    x = make_input(8).reshape(1, 8, IN)
+    announce("dropin leading dims")
+    y = fast(x)
+    assert y.shape == (1, 8, OUT) and fast.last_took_kernel
+    assert torch.equal(y.reshape(8, OUT), fast(x.reshape(8, IN)))
+
+
+def test_linear_bias_is_added(ctx):
+    c = make_case(1, OUT, IN, bits=4, gs=64, seed=3, lbias=True)
+    _, w, s, b, lb = upload(c)
+    stock = QuantizedLinear(ctx, w, s, b, lb, group_size=64, bits=4)
+    nob = QuantizedLinear(ctx, w, s, b, None, group_size=64, bits=4)
+    fast = SmallMQuantizedLinear(stock)
+    x = make_input(8)
+    announce("dropin linear bias")
+    d = (fast(x).float() - (nob(x).float() + lb.float()[None, :])).abs().max().item()
+    assert d <= TOL * max(nob(x).float().abs().max().item(), 1.0)

@@ -3,7 +3,7 @@
 The runtime's planner (dfq_debug_make_plan, the same code dfq_qmm uses) is run for many
 shapes; the kernel's split and fix-up rules (qmm_kernels.hip: unit ranges per workgroup and
 wave, wave-level LDS slots, workgroup combine, workspace publish with a last-arriver sum)
-are replayed here unit by unit.  Every (k-block, tile, super-step) unit must be computed
+are replayed here unit by unit.  Every (k-block, tile, chunk) unit must be computed
 exactly once, every tile must be written exactly once with all of its units, and every
 workspace / LDS slot index must stay inside what the planner sized.
 """
@@ -18,11 +18,11 @@ WAVES = 8
 
 def make_plan(M, N, K, bits, gs, cus=256, lds=163840):
     lib = dflash_qmm.load_library()
-    out = (ctypes.c_int * 8)()
+    out = (ctypes.c_int * 9)()
     rc = lib.dfq_debug_make_plan(M, N, K, bits, gs, cus, lds, out)
     if rc:
         return None
-    keys = ["T", "SS", "nkb", "Gkb", "nslot_kb", "kr", "lds_bytes", "need_ws"]
+    keys = ["T", "SS", "nkb", "Gkb", "nslot_kb", "kr", "lds_bytes", "need_ws", "ch"]
     return dict(zip(keys, list(out)))
 
 
