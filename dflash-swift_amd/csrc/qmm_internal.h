@@ -18,6 +18,8 @@ struct Plan {
     int SS = 0;         /* chunks per tile per k-block                       */
     int nkb = 0;        /* k-blocks                                          */
     int Gkb = 0;        /* workgroups per k-block                            */
+    int wg_base = 0;    /* units per workgroup, rounded down                 */
+    int wg_rem = 0;     /* workgroups holding one extra unit                 */
     int nslot_kb = 0;   /* partial slots per tile per k-block                */
     int kr = 0;         /* k elements per k-block                            */
     int rs = 0;         /* LDS bytes per staged x row                        */

@@ -36,9 +36,8 @@
  *
  * x (M rows of the k-block) is staged once per workgroup in LDS, pre-permuted into the MFMA
  * k order, with the per-group sums sum_{k in g} x[m,k] next to it.  Weights, scales and
- * biases stream straight from HBM into VGPRs through raw buffer loads with a software
- * prefetch ring; out-of-range prefetches use the buffer's bounds check (num_records) so
- * they cost no memory traffic and need no branch.
+ * biases stream straight from HBM into VGPRs through global loads (a scalar base plus a
+ * 32-bit lane offset) with a software prefetch ring over work chunks.
  *
  * Work decomposition: see qmm_params.h.  One 512-thread workgroup per CU (the LDS request
  * keeps two from sharing a CU); units of (16-column tile, super-step) are split evenly over
@@ -64,15 +63,16 @@ typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 8;
+#ifndef DFQ_WAVES
+#define DFQ_WAVES 8        /* waves per workgroup; the host is built with the same value */
+#endif
+#ifndef DFQ_PF_CHUNKS
+#define DFQ_PF_CHUNKS 2    /* 8-group chunks in flight per wave */
+#endif
+constexpr int kWaves = DFQ_WAVES;
 constexpr int kThreads = kWaves * 64;
-constexpr int kMaxStageItems = 12;  // x chunks of 16 bytes staged per thread (M*kr/8 <= 6144)
-constexpr uint32_t kRsrcWord3 = 0x00020000u;  // gfx9 raw buffer descriptor, dword 3
+constexpr int kMaxStageItems = 96 / DFQ_WAVES;  // 16-byte x chunks staged per thread
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
-                                             (int)kRsrcWord3);
-}
 
 /* ---------------------------------------------------------------------------------- */
 /* Per-format constants                                                                */
@@ -253,10 +253,18 @@ __device__ __forceinline__ u32x4_t nibble_permute(u32x4_t v) {
     return o;
 }
 
-/* Index of the workgroup (within the k-block) whose range holds unit u:
- * the largest c with floor(U*c/G) <= u. */
-__device__ __forceinline__ int owner_wg(int u, int U, int G) {
-    return (int)(((int64_t)G * (u + 1) - 1) / U);
+/* The split of the U units of a k-block over G workgroups: workgroup c owns
+ * [c*base + min(c, rem), +base + (c < rem)), with base = U / G and rem = U % G computed on
+ * the host.  Within a workgroup, wave w owns [w*lb + min(w, lr), +lb + (w < lr)) of its L
+ * units, lb = L / kWaves, lr = L % kWaves. */
+__device__ __forceinline__ int wg_start(int c, int base, int rem) {
+    return c * base + (c < rem ? c : rem);
+}
+
+/* Index of the workgroup (within the k-block) whose range holds unit u. */
+__device__ __forceinline__ int owner_wg(int u, int base, int rem) {
+    const int big = rem * (base + 1);
+    return u < big ? u / (base + 1) : rem + (u - big) / base;
 }
 
 /* One partial tile (8 rows x 16 columns, fp32) as held by lanes 0-31: lane (q, n) holds
@@ -293,8 +301,8 @@ template <bool F16>
 __device__ void publish(const QmmParams& p, int t, int slot, int lane, f32x4_t v) {
     const int q = lane >> 4, n = lane & 15;
     const int SS = p.SS;
-    const int U = p.T * SS;
-    const int nwg = owner_wg(t * SS + SS - 1, U, p.Gkb) - owner_wg(t * SS, U, p.Gkb) + 1;
+    const int nwg = owner_wg(t * SS + SS - 1, p.wg_base, p.wg_rem) -
+                    owner_wg(t * SS, p.wg_base, p.wg_rem) + 1;
     const uint32_t total = (uint32_t)(p.nkb * nwg);
     uint32_t* base = (uint32_t*)p.slots + (size_t)t * p.nkb * p.nslot_kb * 128;
     if (lane < 32) {
@@ -349,12 +357,12 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     const int kb = blockIdx.x / p.Gkb;
     const int cl = blockIdx.x - kb * p.Gkb;
     const int SS = p.SS;      // chunks per tile per k-block
-    const int U = p.T * SS;
-    const int a = (int)((int64_t)U * cl / p.Gkb);
-    const int b = (int)((int64_t)U * (cl + 1) / p.Gkb);
+    const int a = wg_start(cl, p.wg_base, p.wg_rem);
+    const int b = wg_start(cl + 1, p.wg_base, p.wg_rem);
     const int L = b - a;
-    const int aw = a + (int)((int64_t)L * wave / kWaves);
-    const int bw = a + (int)((int64_t)L * (wave + 1) / kWaves);
+    const int lb = L / kWaves, lr = L % kWaves;  // power-of-two divisions
+    const int aw = a + wave * lb + (wave < lr ? wave : lr);
+    const int bw = aw + lb + (wave < lr ? 1 : 0);
 
     const int RB = p.K * BITS / 8;        // bytes per weight row
     const int GPR = p.K / GS;             // groups per row
@@ -365,52 +373,55 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     const int items = p.M * CPR;
     const uint16_t* xg = (const uint16_t*)p.x;
     u32x4_t xv[kMaxStageItems];
+    int xr[kMaxStageItems], xc[kMaxStageItems];
+    {
+        int r = tid / CPR, c = tid - (tid / CPR) * CPR;  // item tid + i*kThreads -> (row, chunk)
+#pragma unroll
+        for (int i = 0; i < kMaxStageItems; ++i) {
+            xr[i] = r;
+            xc[i] = c;
+            c += kThreads;
+            while (c >= CPR) { c -= CPR; ++r; }
+        }
+    }
 #pragma unroll
     for (int i = 0; i < kMaxStageItems; ++i) {
-        int it = tid + i * kThreads;
-        it = it < items ? it : items - 1;
-        const int r = it / CPR, c = it - r * CPR;
+        const bool act = tid + i * kThreads < items;
+        const int r = act ? xr[i] : p.M - 1, c = act ? xc[i] : CPR - 1;
         xv[i] = *(const u32x4_t*)(xg + (size_t)r * p.K + k0 + c * 8);
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    /* ---- weight / scale / bias prefetch ring, one chunk per slot */
-    const uint32_t lane_w = (uint32_t)n * RB + (uint32_t)q * 16u;
-    const uint32_t lane_s = (CH > 1) ? (uint32_t)n * GPR * 2u
-                                     : ((uint32_t)n * GPR + (C::GPS == 4 ? 2u * (q >> 1) : 0u)) * 2u;
+    /* ---- weight / scale / bias prefetch ring, one chunk per slot.  Loads take a scalar
+     * base (tile row 0, chunk k) plus a per-lane 32-bit offset; a lane whose row is past N
+     * re-reads row N-1 (its result is never stored); slots past the wave's range load
+     * nothing. */
+    const uint32_t lane_w = (uint32_t)q * 16u;
+    const uint32_t lane_s = (CH > 1) ? 0u : (C::GPS == 4 ? 4u * (q >> 1) : 0u);
     using SV = typename std::conditional<(CH > 1), u32x4_t, uint32_t>::type;
     u32x4_t rw[PF][CH][C::NS];
     SV rs[PF], rb[PF];
+    const uint8_t* wbytes = (const uint8_t*)p.w;
+    const uint8_t* sbytes = (const uint8_t*)p.scales;
+    const uint8_t* bbytes = (const uint8_t*)p.biases;
 
     int pt = aw / SS, pc = aw - (aw / SS) * SS;  // prefetch stream position (tile, chunk)
     auto issue = [&](int slot, int u) {
-        const bool valid = u < bw;
-        const int row0 = pt * 16;
-        const uint32_t wrec = valid ? (uint32_t)(p.N - row0) * RB : 0u;
-        const uint32_t srec = valid ? (uint32_t)(p.N - row0) * GPR * 2u : 0u;
-        __amdgpu_buffer_rsrc_t rsw = make_rsrc(p.w + (size_t)row0 * (RB / 4), wrec);
-        __amdgpu_buffer_rsrc_t rss =
-            make_rsrc((const uint16_t*)p.scales + (size_t)row0 * GPR, srec);
-        __amdgpu_buffer_rsrc_t rsb =
-            make_rsrc((const uint16_t*)p.biases + (size_t)row0 * GPR, srec);
-        const int kc = k0 + pc * (CH * C::KSS);  // first k of the chunk
-        const int soff_w = kc * BITS / 8;
-        const int soff_s = (kc / GS) * 2;
+        if (u < bw) {
+            const int row0 = pt * 16;
+            const int rl = (row0 + 16 <= p.N) ? n : min(n, p.N - 1 - row0);
+            const uint32_t vw = (uint32_t)rl * RB + lane_w;
+            const uint32_t vs = (uint32_t)rl * GPR * 2u + lane_s;
+            const int kc = k0 + pc * (CH * C::KSS);  // first k of the chunk
+            const uint8_t* wb = wbytes + (size_t)row0 * RB + kc * BITS / 8;
+            const size_t so = ((size_t)row0 * GPR + kc / GS) * 2;
 #pragma unroll
-        for (int j = 0; j < CH; ++j)
+            for (int j = 0; j < CH; ++j)
 #pragma unroll
-            for (int s = 0; s < C::NS; ++s)
-                rw[slot][j][s] = __builtin_bit_cast(
-                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                 rsw, lane_w, soff_w + (j * C::NS + s) * 64, 0));
-        if constexpr (CH > 1) {
-            rs[slot] = __builtin_bit_cast(
-                u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rss, lane_s, soff_s, 0));
-            rb[slot] = __builtin_bit_cast(
-                u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rsb, lane_s, soff_s, 0));
-        } else {
-            rs[slot] = __builtin_amdgcn_raw_buffer_load_b32(rss, lane_s, soff_s, 0);
-            rb[slot] = __builtin_amdgcn_raw_buffer_load_b32(rsb, lane_s, soff_s, 0);
+                for (int s = 0; s < C::NS; ++s)
+                    rw[slot][j][s] = *(const u32x4_t*)(wb + vw + (j * C::NS + s) * 64);
+            rs[slot] = *(const SV*)(sbytes + so + vs);
+            rb[slot] = *(const SV*)(bbytes + so + vs);
         }
         if (++pc == SS) { pc = 0; ++pt; }
     };
@@ -424,10 +435,8 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     const int GK = p.kr / GS;  // groups in the k-block
 #pragma unroll
     for (int i = 0; i < kMaxStageItems; ++i) {
-        const int it0 = tid + i * kThreads;
-        const bool act = it0 < items;
-        const int it = act ? it0 : items - 1;
-        const int r = it / CPR, c = it - r * CPR;
+        const bool act = tid + i * kThreads < items;
+        const int r = xr[i], c = xc[i];
         float s = act ? chunk_sum<F16>(xv[i]) : 0.0f;
 #pragma unroll
         for (int off = 1; off < GS / 8; off <<= 1) s += __shfl_xor(s, off);
@@ -552,8 +561,8 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
         if (lane < 32) {
             v = *(const f32x4_t*)(wslot + (wave * 2 + which) * 128 + n * 8 + q * 4);
             for (int w2 = wave + 1; w2 < kWaves; ++w2) {
-                const int a2 = a + (int)((int64_t)L * w2 / kWaves);
-                const int b2 = a + (int)((int64_t)L * (w2 + 1) / kWaves);
+                const int a2 = a + w2 * lb + (w2 < lr ? w2 : lr);
+                const int b2 = a2 + lb + (w2 < lr ? 1 : 0);
                 if (a2 >= (t + 1) * SS) break;
                 if (a2 == b2) continue;
                 v += *(const f32x4_t*)(wslot + (w2 * 2 + 0) * 128 + n * 8 + q * 4);
@@ -563,7 +572,7 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
         if (wg_whole && p.nkb == 1) {
             store_y<F16>(p, t, lane, v);
         } else {
-            const int first = owner_wg(t * SS, U, p.Gkb);
+            const int first = owner_wg(t * SS, p.wg_base, p.wg_rem);
             publish<F16>(p, t, kb * p.nslot_kb + (cl - first), lane, v);
         }
     }
@@ -625,7 +634,7 @@ extern "C" __global__ void __launch_bounds__(256) dfq_fill_u32(uint32_t* ptr, ui
 #define DFQ_MT8_KERNEL(BITS, GS, F16, NAME, CHN, CH)                                        \
     extern "C" __global__ void __launch_bounds__(kThreads)                                   \
         dfq_qmm_mt8_b##BITS##_g##GS##_##NAME##_##CHN(QmmParams p) {                           \
-        qmm_mt8<BITS, GS, F16, CH, (CH > 1 ? 2 : 8)>(p);                                      \
+        qmm_mt8<BITS, GS, F16, CH, (CH > 1 ? DFQ_PF_CHUNKS : 8)>(p);                                      \
     }
 #define DFQ_MT8_FORMAT(BITS, GS, F16, NAME)                                                    \
     DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c1, 1)                                                \

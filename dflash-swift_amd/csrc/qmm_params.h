@@ -15,8 +15,9 @@
  *    k-block into SS chunks of CH super-steps (one super-step = the k span that holds
  *    exactly two quantisation groups per lane half, 64..256 elements; a chunk is one
  *    super-step or the 8 groups whose scales one 16-byte load fetches);
- *  - the T*SS units (tile, chunk) of one k-block are split into Gkb equal contiguous
- *    ranges, one per workgroup, and each workgroup's range into one range per wave;
+ *  - the U = T*SS units (tile, chunk) of one k-block are split into Gkb contiguous ranges
+ *    whose sizes differ by at most one (the first U % Gkb get one more), and each
+ *    workgroup's range likewise into one range per wave;
  *  - a tile covered by one wave is written straight to y; a tile shared between waves is
  *    summed in LDS in wave order; a tile shared between workgroups (or k-blocks) is summed
  *    through workspace slots in a fixed order by whichever workgroup arrives last.
@@ -40,6 +41,8 @@ typedef struct QmmParams {
     int32_t lds_row_stride; /* bytes per staged x row in LDS                          */
     int32_t lds_xsum_off;   /* byte offset of the per-group x sums in LDS             */
     int32_t lds_slot_off;   /* byte offset of the per-wave partial slots in LDS       */
+    int32_t wg_base;        /* units per workgroup, rounded down (U / Gkb)            */
+    int32_t wg_rem;         /* workgroups with one extra unit (U % Gkb)               */
     uint32_t w_bytes;       /* size of w in bytes (< 2^31)                            */
     uint32_t s_bytes;       /* size of scales (= size of biases) in bytes             */
 } QmmParams;

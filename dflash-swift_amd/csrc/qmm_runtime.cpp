@@ -42,9 +42,12 @@ namespace {
 
 thread_local std::string g_last_error;
 
-constexpr int kThreads = 512;         // qmm_mt8 workgroup size (8 waves)
-constexpr int kMaxStageItems = 12;    // must match qmm_kernels.hip
-constexpr int kWaveSlotsBytes = 8 * 2 * 512;
+#ifndef DFQ_WAVES
+#define DFQ_WAVES 8                    // must match the kernels' build
+#endif
+constexpr int kThreads = DFQ_WAVES * 64;          // qmm_mt8 workgroup size
+constexpr int kMaxStageItems = 96 / DFQ_WAVES;    // must match qmm_kernels.hip
+constexpr int kWaveSlotsBytes = DFQ_WAVES * 2 * 512;
 
 struct PlanKey {
     int M, N, K, bits, gs;
@@ -119,7 +122,11 @@ int kss_for(int bits, int gs) {
     return kstep * ns;
 }
 
-static int64_t owner_wg(int64_t u, int64_t U, int64_t G) { return (G * (u + 1) - 1) / U; }
+/* Workgroup c owns units [c*base + min(c, rem), +base + (c < rem)); same rule as the kernel. */
+static int64_t owner_wg(int64_t u, int64_t base, int64_t rem) {
+    const int64_t big = rem * (base + 1);
+    return u < big ? u / (base + 1) : rem + (u - big) / base;
+}
 
 bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_max, Plan* pl) {
     const int kss = kss_for(bits, gs);
@@ -155,9 +162,12 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
     int64_t G = std::max(1, num_cus / nkb);
     if (G > U) G = U;
     p.Gkb = (int)G;
+    p.wg_base = (int)(U / G);
+    p.wg_rem = (int)(U % G);
     int nslot = 1;
     for (int64_t t = 0; t < p.T; ++t) {
-        const int64_t c0 = owner_wg(t * p.SS, U, G), c1 = owner_wg(t * p.SS + p.SS - 1, U, G);
+        const int64_t c0 = owner_wg(t * p.SS, p.wg_base, p.wg_rem);
+        const int64_t c1 = owner_wg(t * p.SS + p.SS - 1, p.wg_base, p.wg_rem);
         nslot = std::max<int>(nslot, (int)(c1 - c0 + 1));
     }
     p.nslot_kb = nslot;
@@ -451,6 +461,8 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
     p.lds_row_stride = pl.rs;
     p.lds_xsum_off = pl.xsum_off;
     p.lds_slot_off = pl.slot_off;
+    p.wg_base = pl.wg_base;
+    p.wg_rem = pl.wg_rem;
     p.w_bytes = (uint32_t)((int64_t)N * K * bits / 8);
     p.s_bytes = (uint32_t)((int64_t)N * (K / gs) * 2);
     const int bi = bits == 4 ? 0 : 1;

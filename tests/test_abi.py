@@ -1,0 +1,77 @@
+"""The C-ABI library on the CPU: it loads, exports every function include/dflash_qmm.h
+declares, and its host-side checks and error paths behave without a GPU (no kernel is
+launched here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import dflash_qmm
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dflash_qmm.h")
+
+
+def declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(dfq_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_function():
+    lib = dflash_qmm.load_library()
+    names = declared_functions()
+    assert len(names) >= 35
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_abi_version_and_status_strings():
+    lib = dflash_qmm.load_library()
+    assert lib.dfq_abi_version() == 1
+    assert lib.dfq_status_string(0) == b"ok"
+    assert lib.dfq_status_string(2) == b"unsupported"
+
+
+def test_init_without_a_device_fails_cleanly():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    lib = dflash_qmm.load_library()
+    h = ctypes.c_void_p()
+    assert lib.dfq_init(0, ctypes.byref(h)) == 5          # DFQ_ERR_NO_DEVICE
+    assert not h.value
+    assert b"device" in lib.dfq_last_error()
+    with pytest.raises(dflash_qmm.DfqError):
+        dflash_qmm.Context(0)
+
+
+def test_null_arguments_are_rejected():
+    lib = dflash_qmm.load_library()
+    assert lib.dfq_init(0, None) == 1
+    assert lib.dfq_qmm(None, None, None, None, None, None, None, 8, 64, 128, 4, 64, 0, 0, 0,
+                       None, 0, None) == 1
+    assert lib.dfq_qmm_fallback(None, None, None, None, None, None, None, 1, 1, 64, 4, 64, 0,
+                                0, 0, None) == 1
+    assert lib.dfq_graph_launch(None, None) == 1
+    assert lib.dfq_enable_small_m_quantized_matmul(None) == -1
+
+
+def test_eligibility_gate_matches_the_reference():
+    """SmallMQuantizedMatmul.isEligible (SmallMQuantizedMatmul.swift:193-201)."""
+    e = dflash_qmm.load_library().dfq_is_eligible
+    assert e(4096, 1024, 4, 64, 1, 1) == 1
+    assert e(17408, 5120, 8, 64, 1, 1) == 1
+    assert e(4095, 1024, 4, 64, 1, 1) == 0       # N below 4096
+    assert e(4096, 1024 + 64, 4, 64, 1, 1) == 0  # K not a multiple of 512
+    assert e(4096, 1024, 4, 32, 1, 1) == 0       # group size 32
+    assert e(4096, 1024, 3, 64, 1, 1) == 0       # 3-bit
+    assert e(4096, 1024, 4, 64, 0, 1) == 0       # not affine
+    assert e(4096, 1024, 4, 64, 1, 0) == 0       # no biases
+
+
+def test_fast_path_shape_checks_need_no_device():
+    """dfq_qmm_supported's argument checks run on the host; without a context it says no."""
+    lib = dflash_qmm.load_library()
+    assert lib.dfq_qmm_supported(None, 8, 17408, 5120, 4, 64, 0, 0, 0) == 0

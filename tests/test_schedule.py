@@ -26,13 +26,29 @@ def make_plan(M, N, K, bits, gs, cus=256, lds=163840):
     return dict(zip(keys, list(out)))
 
 
-def owner_wg(u, U, G):
-    return (G * (u + 1) - 1) // U
+def wg_start(c, base, rem):
+    return c * base + min(c, rem)
+
+
+def owner_wg(u, base, rem):
+    big = rem * (base + 1)
+    return u // (base + 1) if u < big else rem + (u - big) // base
+
+
+def wave_ranges(a, b):
+    L = b - a
+    lb, lr = divmod(L, WAVES)
+    out = []
+    for w in range(WAVES):
+        aw = a + w * lb + min(w, lr)
+        out.append((aw, aw + lb + (1 if w < lr else 0)))
+    return out
 
 
 def replay(p):
     T, SS, nkb, G, nslot = p["T"], p["SS"], p["nkb"], p["Gkb"], p["nslot_kb"]
     U = T * SS
+    base, rem = divmod(U, G)
     seen = set()
     y_writes = {}
     ws_slots = {}
@@ -47,7 +63,7 @@ def replay(p):
         assert 0 <= j < nkb * nslot, (t, j, nslot)
         assert (t, j) not in ws_slots, f"slot {(t, j)} written twice"
         ws_slots[(t, j)] = units
-        nwg = owner_wg(t * SS + SS - 1, U, G) - owner_wg(t * SS, U, G) + 1
+        nwg = owner_wg(t * SS + SS - 1, base, rem) - owner_wg(t * SS, base, rem) + 1
         arrivals[t] = arrivals.get(t, 0) + 1
         if arrivals[t] == nkb * nwg:
             allu = set()
@@ -58,9 +74,8 @@ def replay(p):
 
     for kb in range(nkb):
         for cl in range(G):
-            a, b = U * cl // G, U * (cl + 1) // G
-            L = b - a
-            ranges = [(a + L * w // WAVES, a + L * (w + 1) // WAVES) for w in range(WAVES)]
+            a, b = wg_start(cl, base, rem), wg_start(cl + 1, base, rem)
+            ranges = wave_ranges(a, b)
             wslot = {}
             for w, (aw, bw) in enumerate(ranges):
                 if aw >= bw:
@@ -111,7 +126,7 @@ def replay(p):
                     if t * SS >= a and (t + 1) * SS <= b and nkb == 1:
                         finalize(t, units)
                     else:
-                        first = owner_wg(t * SS, U, G)
+                        first = owner_wg(t * SS, base, rem)
                         publish(t, kb, kb * nslot + (cl - first), units)
     assert len(seen) == nkb * U
     assert sorted(y_writes) == list(range(T))
