@@ -120,6 +120,9 @@ def main():
     ap.add_argument("--ms", default="1,2,4,6,8")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="only run 20 plain device copies of this many MiB (the reference "
+                         "point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -132,6 +135,15 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
+    if args.copy_mib:
+        n = args.copy_mib << 20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_per_launch": n, "launches": 20}), flush=True)
+        return
     ctx = dflash_qmm.Context(0)
     stream = torch.cuda.Stream(device=dev)
     sets = make_sets(torch, args.sets, N_OUT, K_IN, BITS, GS, dev)
