@@ -66,12 +66,13 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 #ifndef DFQ_WAVES
 #define DFQ_WAVES 8        /* waves per workgroup; the host is built with the same value */
 #endif
-#ifndef DFQ_PF_CHUNKS
-#define DFQ_PF_CHUNKS 2    /* 8-group chunks in flight per wave */
+#ifndef DFQ_PF_LOADS
+#define DFQ_PF_LOADS 8     /* 16-byte weight loads in flight per lane (8 KB per wave) */
 #endif
 constexpr int kWaves = DFQ_WAVES;
 constexpr int kThreads = kWaves * 64;
 constexpr int kMaxStageItems = 96 / DFQ_WAVES;  // 16-byte x chunks staged per thread
+constexpr int kStageTasks = (kMaxStageItems + 7) / 8;  // 64-k staging tasks per thread
 
 
 /* ---------------------------------------------------------------------------------- */
@@ -159,15 +160,25 @@ __device__ __forceinline__ void build_operand_words(const u32x4_t (&R)[Cfg<BITS,
     }
 }
 
-/* 8 nibbles of a word -> bf16/fp16 (MAGIC + q) pairs (q_i, q_{i+4}) in VGPR i. */
+/* (a & m) | c in one VOP3 op.  gfx9 VOP3 takes no literal constants, so without this the
+ * compiler emits a v_and_b32 and a v_or_b32 with literals; here the mask sits in an SGPR
+ * and the magic in a VGPR, both loop-invariant. */
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
+    uint32_t r;
+    __asm__("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(c));
+    return r;
+}
+
+/* 8 nibbles of a word -> bf16/fp16 (MAGIC + q) pairs (q_i, q_{i+4}) in VGPR i: seven VALU
+ * ops per word (three shifts, four and-ors). */
 template <bool F16>
-__device__ __forceinline__ u32x4_t nibble_operand(uint32_t p) {
-    constexpr uint32_t kMagic = F16 ? 0x64006400u : 0x43004300u;
+__device__ __forceinline__ u32x4_t nibble_operand(uint32_t p, uint32_t magic) {
+    constexpr uint32_t kMask = 0x000F000Fu;
     u32x4_t v;
-    v[0] = (p & 0x000F000Fu) | kMagic;
-    v[1] = ((p >> 4) & 0x000F000Fu) | kMagic;
-    v[2] = ((p >> 8) & 0x000F000Fu) | kMagic;
-    v[3] = ((p >> 12) & 0x000F000Fu) | kMagic;
+    v[0] = and_or(p, kMask, magic);
+    v[1] = and_or(p >> 4, kMask, magic);
+    v[2] = and_or(p >> 8, kMask, magic);
+    v[3] = and_or(p >> 12, kMask, magic);
     return v;
 }
 
@@ -213,6 +224,20 @@ __device__ __forceinline__ float half_of(uint32_t w, uint32_t sh_lo16) {
     }
 }
 
+/* Byte selectors for v_perm_b32(0, w, sel) that move the low (kSelLo) or high (kSelHi)
+ * 16-bit half of w into the high half of the result, zeroing the low half: a bf16 half
+ * becomes its fp32 value in one op even when the half is chosen per lane. */
+constexpr uint32_t kSelLo = 0x01000c0cu;
+constexpr uint32_t kSelHi = 0x03020c0cu;
+
+/* 16-bit float in the half of w that `sel` (kSelLo / kSelHi) picks -> fp32. */
+template <bool F16>
+__device__ __forceinline__ float half_sel(uint32_t w, uint32_t sel) {
+    const uint32_t h = __builtin_amdgcn_perm(0u, w, sel);
+    if constexpr (F16) return (float)__builtin_bit_cast(_Float16, (uint16_t)(h >> 16));
+    else return __uint_as_float(h);
+}
+
 template <bool F16>
 __device__ __forceinline__ float elem_to_f32(uint32_t bits16) {
     if constexpr (F16) return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
@@ -231,14 +256,20 @@ __device__ __forceinline__ uint16_t f32_to_out(float f) {
     }
 }
 
-/* Sum of the 8 elements of a 16-byte chunk, in k order. */
+/* s + the 8 elements of a 16-byte chunk, added pairwise in k order with v_dot2c against
+ * (1, 1): four VALU ops per chunk.  Written as inline asm on one 32-bit register at a time:
+ * the builtin form, applied to elements of a 128-bit vector, has been compiled (ROCm 7.2)
+ * to read the vector's first register for every element. */
 template <bool F16>
-__device__ __forceinline__ float chunk_sum(u32x4_t v) {
-    float s = 0.0f;
+__device__ __forceinline__ float chunk_dot(u32x4_t v, float s) {
+    const uint32_t ones = F16 ? 0x3c003c00u : 0x3f803f80u;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        s += elem_to_f32<F16>(v[i] & 0xffffu);
-        s += elem_to_f32<F16>(v[i] >> 16);
+        const uint32_t e = v[i];
+        if constexpr (F16)
+            __asm__("v_dot2c_f32_f16 %0, %1, %2" : "+v"(s) : "v"(e), "v"(ones));
+        else
+            __asm__("v_dot2c_f32_bf16 %0, %1, %2" : "+v"(s) : "v"(e), "v"(ones));
     }
     return s;
 }
@@ -289,14 +320,22 @@ __device__ __forceinline__ void store_y(const QmmParams& p, int t, int lane, f32
     }
 }
 
-/* Contribute a partial tile to the workspace; the last contributor sums all slots of the
- * tile in a fixed order, writes y, zeroes the slots and re-arms the counter, so the whole
- * workspace is zero again when the kernel ends.
+/* Contribute a partial tile to the workspace.
  *
- * Workgroups on different XCDs exchange these partials.  Every access to a slot or a
- * counter is an agent-scope atomic (coherent across the XCDs' L2s without a whole-cache
- * write-back or invalidate); the slot stores are waited for before the counter increment,
- * and the last contributor only reads slots after its own increment has returned. */
+ * Two contributors (the usual case: a tile split between two workgroups): every element of
+ * the tile's slot is a 64-bit word (tag << 32 | fp32 bits), zero at rest.  Each contributor
+ * swaps its value in with one atomic exchange per element; whoever gets back a tagged word
+ * arrived second, adds the two values (fp32 addition of two terms does not depend on their
+ * order), writes that y element and zeroes the word.  One round trip, no counter.
+ *
+ * More contributors: the last contributor (found with a per-tile arrival counter) sums all
+ * slots of the tile in a fixed order, writes y, zeroes the slots and re-arms the counter.
+ *
+ * Either way the workspace is zero again when the kernel ends.  Workgroups on different
+ * XCDs exchange these partials: every access to a slot or a counter is an agent-scope
+ * atomic (coherent across the XCDs' L2s without a whole-cache write-back or invalidate);
+ * in the counter scheme the slot stores are waited for before the counter increment, and
+ * the last contributor only reads slots after its own increment has returned. */
 template <bool F16>
 __device__ void publish(const QmmParams& p, int t, int slot, int lane, f32x4_t v) {
     const int q = lane >> 4, n = lane & 15;
@@ -305,6 +344,29 @@ __device__ void publish(const QmmParams& p, int t, int slot, int lane, f32x4_t v
                     owner_wg(t * SS, p.wg_base, p.wg_rem) + 1;
     const uint32_t total = (uint32_t)(p.nkb * nwg);
     uint32_t* base = (uint32_t*)p.slots + (size_t)t * p.nkb * p.nslot_kb * 128;
+    if (total == 2) {
+        const int col = t * 16 + n;
+        if (lane < 32) {
+            uint64_t* sl = (uint64_t*)base + n * 8 + q * 4;
+            uint64_t old[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                old[r] = __hip_atomic_exchange(sl + r, (1ull << 32) | __float_as_uint(v[r]),
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            float lb = 0.0f;
+            if (p.lbias && col < p.N) lb = elem_to_f32<F16>(((const uint16_t*)p.lbias)[col]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (!(old[r] >> 32)) continue;
+                const int m = 4 * q + r;
+                const float sum = v[r] + __uint_as_float((uint32_t)old[r]);
+                if (m < p.M && col < p.N)
+                    ((uint16_t*)p.y)[(size_t)m * p.N + col] = f32_to_out<F16>(sum + lb);
+                __hip_atomic_store(sl + r, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        return;
+    }
     if (lane < 32) {
         uint32_t* sl = base + (size_t)slot * 128 + n * 8 + q * 4;
 #pragma unroll
@@ -368,34 +430,35 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     const int GPR = p.K / GS;             // groups per row
     const int k0 = kb * p.kr;             // first k of this k-block
 
-    /* ---- x staging loads go out first (their wait must not cover the weight prefetch) */
-    const int CPR = p.kr / 8;
-    const int items = p.M * CPR;
+    /* ---- x staging loads go out first (their wait must not cover the weight prefetch).
+     * A task is 64 consecutive k of one row: eight 16-byte chunks, summed in-thread into
+     * the group sums and written to LDS.  Tasks are dealt round-robin over the threads;
+     * threads past the last task load nothing (x is a sizeable share of what the CU's
+     * memory pipeline carries at the start of the kernel). */
+    const int TPR = p.kr / 64;  // tasks per row
+    const int ntask = p.M * TPR;
     const uint16_t* xg = (const uint16_t*)p.x;
-    u32x4_t xv[kMaxStageItems];
-    int xr[kMaxStageItems], xc[kMaxStageItems];
-    {
-        int r = tid / CPR, c = tid - (tid / CPR) * CPR;  // item tid + i*kThreads -> (row, chunk)
+    u32x4_t xv[kStageTasks][8];
 #pragma unroll
-        for (int i = 0; i < kMaxStageItems; ++i) {
-            xr[i] = r;
-            xc[i] = c;
-            c += kThreads;
-            while (c >= CPR) { c -= CPR; ++r; }
+    for (int i = 0; i < kStageTasks; ++i) {
+        const int task = min(tid + i * kThreads, ntask - 1);
+        const int r = task / TPR, j = task - r * TPR;
+        const uint16_t* src = xg + (size_t)r * p.K + k0 + j * 64;
+        if (tid + i * kThreads < ntask) {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) xv[i][c] = *(const u32x4_t*)(src + c * 8);
         }
-    }
-#pragma unroll
-    for (int i = 0; i < kMaxStageItems; ++i) {
-        const bool act = tid + i * kThreads < items;
-        const int r = act ? xr[i] : p.M - 1, c = act ? xc[i] : CPR - 1;
-        xv[i] = *(const u32x4_t*)(xg + (size_t)r * p.K + k0 + c * 8);
     }
     __builtin_amdgcn_sched_barrier(0);
 
     /* ---- weight / scale / bias prefetch ring, one chunk per slot.  Loads take a scalar
      * base (tile row 0, chunk k) plus a per-lane 32-bit offset; a lane whose row is past N
-     * re-reads row N-1 (its result is never stored); slots past the wave's range load
-     * nothing. */
+     * re-reads row N-1 (its result is never stored).  Every issue loads its slot: once the
+     * wave's range is exhausted it fetches the range's last unit again (an L2 hit).  The
+     * number of loads in flight is then the same on every path through the loop, so the
+     * compiler's vmcnt waits name exactly the slot being consumed; a load skipped on one
+     * path would make it wait for every load in flight. */
+    const bool has_work = aw < bw;
     const uint32_t lane_w = (uint32_t)q * 16u;
     const uint32_t lane_s = (CH > 1) ? 0u : (C::GPS == 4 ? 4u * (q >> 1) : 0u);
     using SV = typename std::conditional<(CH > 1), u32x4_t, uint32_t>::type;
@@ -405,47 +468,77 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     const uint8_t* sbytes = (const uint8_t*)p.scales;
     const uint8_t* bbytes = (const uint8_t*)p.biases;
 
-    int pt = aw / SS, pc = aw - (aw / SS) * SS;  // prefetch stream position (tile, chunk)
+    /* a wave without work fetches unit 0 of the k-block (never used): the prefetch is then
+     * unconditional too, and the x-staging waits below do not drain it */
+    const int a0 = has_work ? aw : 0;
+    int pt = a0 / SS, pc = a0 - (a0 / SS) * SS;  // next unit of the range to fetch
+    int lt = pt, lc = pc;                        // last unit of the range fetched
     auto issue = [&](int slot, int u) {
-        if (u < bw) {
-            const int row0 = pt * 16;
-            const int rl = (row0 + 16 <= p.N) ? n : min(n, p.N - 1 - row0);
-            const uint32_t vw = (uint32_t)rl * RB + lane_w;
-            const uint32_t vs = (uint32_t)rl * GPR * 2u + lane_s;
-            const int kc = k0 + pc * (CH * C::KSS);  // first k of the chunk
-            const uint8_t* wb = wbytes + (size_t)row0 * RB + kc * BITS / 8;
-            const size_t so = ((size_t)row0 * GPR + kc / GS) * 2;
+        const bool in = u < bw;
+        const int t = in ? pt : lt, c = in ? pc : lc;
+        lt = t;
+        lc = c;
+        if (in && ++pc == SS) { pc = 0; ++pt; }
+        const int row0 = t * 16;
+        const int rl = (row0 + 16 <= p.N) ? n : min(n, p.N - 1 - row0);
+        const uint32_t vw = (uint32_t)rl * RB + lane_w;
+        const uint32_t vs = (uint32_t)rl * GPR * 2u + lane_s;
+        const int kc = k0 + c * (CH * C::KSS);  // first k of the chunk
+        const uint8_t* wb = wbytes + (size_t)row0 * RB + kc * BITS / 8;
+        const size_t so = ((size_t)row0 * GPR + kc / GS) * 2;
 #pragma unroll
-            for (int j = 0; j < CH; ++j)
+        for (int j = 0; j < CH; ++j)
 #pragma unroll
-                for (int s = 0; s < C::NS; ++s)
-                    rw[slot][j][s] = *(const u32x4_t*)(wb + vw + (j * C::NS + s) * 64);
-            rs[slot] = *(const SV*)(sbytes + so + vs);
-            rb[slot] = *(const SV*)(bbytes + so + vs);
-        }
-        if (++pc == SS) { pc = 0; ++pt; }
+            for (int s = 0; s < C::NS; ++s)
+                rw[slot][j][s] = *(const u32x4_t*)(wb + vw + (j * C::NS + s) * 64);
+        rs[slot] = *(const SV*)(sbytes + so + vs);
+        rb[slot] = *(const SV*)(bbytes + so + vs);
     };
+    /* the loads go out in slot order, here and in the loop, so the queue the loop waits
+     * on has the same layout on entry as on every back edge */
 #pragma unroll
-    for (int i = 0; i < PF; ++i) issue(i, aw + i);
+    for (int i = 0; i < PF; ++i) {
+        issue(i, aw + i);
+        __builtin_amdgcn_sched_barrier(0);
+    }
 
-    /* ---- LDS layout: row 0 zeros, rows 1..M x; then per-group x sums; then wave slots */
+    /* ---- LDS layout: row 0 zeros, rows 1..M x; then per-group x sums; then per-wave
+     * slots for partial tiles; then per-wave result tiles */
     const int RS = p.lds_row_stride;
     float* xsum = (float*)(lds + p.lds_xsum_off);
     float* wslot = (float*)(lds + p.lds_slot_off);
+    float* ytile = (float*)(lds + p.lds_ytile_off) + wave * p.ytw * 128;
     const int GK = p.kr / GS;  // groups in the k-block
 #pragma unroll
-    for (int i = 0; i < kMaxStageItems; ++i) {
-        const bool act = tid + i * kThreads < items;
-        const int r = xr[i], c = xc[i];
-        float s = act ? chunk_sum<F16>(xv[i]) : 0.0f;
+    for (int i = 0; i < kStageTasks; ++i) {
+        const int task = tid + i * kThreads;
+        const bool act = task < ntask;
+        const int tc = min(task, ntask - 1);
+        const int r = tc / TPR, j = tc - r * TPR;
+        float s0 = 0.0f, s1 = 0.0f;  // group sums (two groups per task at GS = 32)
 #pragma unroll
-        for (int off = 1; off < GS / 8; off <<= 1) s += __shfl_xor(s, off);
+        for (int c = 0; c < 8; ++c) {
+            if (GS == 32 && c >= 4) s1 = chunk_dot<F16>(xv[i][c], s1);
+            else s0 = chunk_dot<F16>(xv[i][c], s0);
+        }
+        /* GS = 128: tasks 2g and 2g+1 of a row sit in neighbouring lanes */
+        if constexpr (GS == 128) s0 += __shfl_xor(s0, 1);
         if (act) {
-            const u32x4_t v = (BITS == 4) ? nibble_permute(xv[i]) : xv[i];
-            *(u32x4_t*)(lds + (size_t)(1 + r) * RS + c * 16) = v;
-            if ((c & (GS / 8 - 1)) == 0) xsum[(c / (GS / 8)) * 8 + r] = s;
+            uint8_t* dst = lds + (size_t)(1 + r) * RS + j * 128;
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+                *(u32x4_t*)(dst + c * 16) = (BITS == 4) ? nibble_permute(xv[i][c]) : xv[i][c];
+            if constexpr (GS == 32) {
+                xsum[(2 * j) * 8 + r] = s0;
+                xsum[(2 * j + 1) * 8 + r] = s1;
+            } else if constexpr (GS == 64) {
+                xsum[j * 8 + r] = s0;
+            } else {
+                if ((j & 1) == 0) xsum[(j >> 1) * 8 + r] = s0;
+            }
         }
     }
+    const int CPR = p.kr / 8;
     for (int c = tid; c < CPR; c += kThreads) *(u32x4_t*)(lds + c * 16) = u32x4_t{0, 0, 0, 0};
     for (int i = tid; i < GK * 8; i += kThreads)
         if ((i & 7) >= p.M) xsum[i] = 0.0f;
@@ -457,10 +550,12 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     const uint32_t abase = (uint32_t)arow * RS + (uint32_t)C::base_chunk(q) * 16u;
     const uint32_t xbase =
         (uint32_t)p.lds_xsum_off + (uint32_t)C::group_of(0, q) * 32u + (uint32_t)(q & 1) * 16u;
-    const uint32_t sh_half = (C::GPS == 4) ? 0u : ((q >> 1) ? 0u : 16u);
+    const uint32_t sel_half = (q >> 1) ? kSelHi : kSelLo;
     constexpr float kOff = (BITS == 4) ? (F16 ? 1024.0f : 128.0f) : 0.0f;
+    const uint32_t magic = F16 ? 0x64006400u : 0x43004300u;
 
     const int t_first = aw / SS;
+    const int tw0 = (aw + SS - 1) / SS;  // first tile lying wholly inside the wave's range
     f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
     int ct = t_first, cc = aw - t_first * SS;
 
@@ -468,94 +563,101 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
 #pragma unroll
         for (int i = 0; i < PF; ++i) {
             const int u = u0 + i;
+            /* no early exit: every pass issues all PF slots (see the prefetch ring) */
             if (u < bw) {
 #pragma unroll
-                for (int j = 0; j < CH; ++j) {
-                    const int css = cc * CH + j;  // super-step within the k-block
-                    uint32_t OW[C::NOW];
-                    build_operand_words<BITS, GS>(rw[i][j], OW);
-                    const uint32_t aoff = abase + (uint32_t)css * (C::CPS * 16);
-                    f32x4_t P[C::NP];
+            for (int j = 0; j < CH; ++j) {
+                const int css = cc * CH + j;  // super-step within the k-block
+                uint32_t OW[C::NOW];
+                build_operand_words<BITS, GS>(rw[i][j], OW);
+                const uint32_t aoff = abase + (uint32_t)css * (C::CPS * 16);
+                f32x4_t P[C::NP];
 #pragma unroll
-                    for (int pp = 0; pp < C::NP; ++pp) P[pp] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                for (int pp = 0; pp < C::NP; ++pp) P[pp] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                    for (int o = 0; o < C::NOPS; ++o) {
-                        const u32x4_t A =
-                            *(const u32x4_t*)(lds + aoff + C::delta_chunk(o) * 16);
-                        u32x4_t B;
-                        if constexpr (BITS == 4) B = nibble_operand<F16>(OW[o]);
-                        else B = byte_operand<F16>(OW[2 * o], OW[2 * o + 1]);
-                        P[C::partial_of(o)] = mfma<F16>(A, B, P[C::partial_of(o)]);
-                    }
-                    const uint32_t xo = xbase + (uint32_t)css * (C::GPS * 32);
-#pragma unroll
-                    for (int pp = 0; pp < C::NP; ++pp) {
-                        uint32_t sw, bw2, sh;
-                        if constexpr (CH > 1) {
-                            if constexpr (C::GPS == 4) {
-                                sw = (q >> 1) ? rs[i][2 * j + 1] : rs[i][2 * j];
-                                bw2 = (q >> 1) ? rb[i][2 * j + 1] : rb[i][2 * j];
-                                sh = pp ? 0u : 16u;
-                            } else {
-                                sw = rs[i][j];
-                                bw2 = rb[i][j];
-                                sh = sh_half;
-                            }
-                        } else {
-                            sw = rs[i];
-                            bw2 = rb[i];
-                            sh = (C::GPS == 4) ? (pp ? 0u : 16u) : sh_half;
-                        }
-                        const float s = half_of<F16>(sw, sh);
-                        const float bb = half_of<F16>(bw2, sh);
-                        const float bp = (kOff != 0.0f) ? __builtin_fmaf(-kOff, s, bb) : bb;
-                        const f32x4_t X = *(const f32x4_t*)(lds + xo + pp * 32);
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            acc[r] = __builtin_fmaf(s, P[pp][r], acc[r]);
-                            acc[r] = __builtin_fmaf(bp, X[r], acc[r]);
-                        }
-                    }
+                for (int o = 0; o < C::NOPS; ++o) {
+                    const u32x4_t A = *(const u32x4_t*)(lds + aoff + C::delta_chunk(o) * 16);
+                    u32x4_t B;
+                    if constexpr (BITS == 4) B = nibble_operand<F16>(OW[o], magic);
+                    else B = byte_operand<F16>(OW[2 * o], OW[2 * o + 1]);
+                    P[C::partial_of(o)] = mfma<F16>(A, B, P[C::partial_of(o)]);
                 }
-                /* end of this wave's part of tile ct? */
-                if (cc == SS - 1 || u + 1 == bw) {
-                    f32x4_t v;
+                const uint32_t xo = xbase + (uint32_t)css * (C::GPS * 32);
+#pragma unroll
+                for (int pp = 0; pp < C::NP; ++pp) {
+                    uint32_t sw, bw2, sel;
+                    if constexpr (CH > 1) {
+                        if constexpr (C::GPS == 4) {
+                            sw = (q >> 1) ? rs[i][2 * j + 1] : rs[i][2 * j];
+                            bw2 = (q >> 1) ? rb[i][2 * j + 1] : rb[i][2 * j];
+                            sel = pp ? kSelHi : kSelLo;
+                        } else {
+                            sw = rs[i][j];
+                            bw2 = rb[i][j];
+                            sel = sel_half;
+                        }
+                    } else {
+                        sw = rs[i];
+                        bw2 = rb[i];
+                        sel = (C::GPS == 4) ? (pp ? kSelHi : kSelLo) : sel_half;
+                    }
+                    const float s = half_sel<F16>(sw, sel);
+                    const float bb = half_sel<F16>(bw2, sel);
+                    const float bp = (kOff != 0.0f) ? __builtin_fmaf(-kOff, s, bb) : bb;
+                    const f32x4_t X = *(const f32x4_t*)(lds + xo + pp * 32);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[r]),
-                                                                   __float_as_uint(acc[r]),
-                                                                   false, false);
-                        /* lanes 0-31 of the two halves: own value + lanes 32-63 */
-                        v[r] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+                        acc[r] = __builtin_fmaf(s, P[pp][r], acc[r]);
+                        acc[r] = __builtin_fmaf(bp, X[r], acc[r]);
                     }
-                    const bool whole = ct * SS >= aw && (ct + 1) * SS <= bw;
-                    if (whole && p.nkb == 1) {
-                        store_y<F16>(p, ct, lane, v);
-                    } else if (whole) {
-                        publish<F16>(p, ct, kb * p.nslot_kb, lane, v);
-                    } else {
-                        const int sidx = (ct == t_first) ? 0 : 1;
-                        if (lane < 32)
-                            *(f32x4_t*)(wslot + (wave * 2 + sidx) * 128 + n * 8 + q * 4) = v;
-                    }
-                    acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
                 }
-                if (++cc == SS) { cc = 0; ++ct; }
             }
+            /* end of this wave's part of tile ct: fold the two group halves and park the
+             * tile in LDS (no global store inside the loop) */
+            if (cc == SS - 1 || u + 1 == bw) {
+                f32x4_t v;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[r]),
+                                                               __float_as_uint(acc[r]),
+                                                               false, false);
+                    /* lanes 0-31 of the two halves: own value + lanes 32-63 */
+                    v[r] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+                }
+                const bool whole = ct * SS >= aw && (ct + 1) * SS <= bw;
+                float* dst = whole ? ytile + (ct - tw0) * 128
+                                   : wslot + (wave * 2 + (ct == t_first ? 0 : 1)) * 128;
+                if (lane < 32) *(f32x4_t*)(dst + n * 8 + q * 4) = v;
+                acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+            if (++cc == SS) { cc = 0; ++ct; }
+            }
+            __builtin_amdgcn_sched_barrier(0);
             issue(i, u + PF);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 
-    /* ---- combine tiles shared between waves of this workgroup */
     __syncthreads();
-    if (aw >= bw) return;
+    if (!has_work) return;
+
+    /* ---- tiles that lie wholly inside this wave's range */
+    const int nwhole = bw / SS - tw0;
+    for (int e = 0; e < nwhole; ++e) {
+        f32x4_t v = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (lane < 32) v = *(const f32x4_t*)(ytile + e * 128 + n * 8 + q * 4);
+        if (p.nkb == 1) store_y<F16>(p, tw0 + e, lane, v);
+        else publish<F16>(p, tw0 + e, kb * p.nslot_kb, lane, v);
+    }
+
+    /* ---- combine tiles shared between waves of this workgroup */
     const int t_last = (bw - 1) / SS;
 #pragma unroll
     for (int which = 0; which < 2; ++which) {
         const int t = which ? t_last : t_first;
         if (which && t_last == t_first) break;
         const bool whole = t * SS >= aw && (t + 1) * SS <= bw;
-        if (whole) continue;                             // written in the main loop
+        if (whole) continue;                             // stored above
         if ((t * SS > a ? t * SS : a) < aw) continue;    // an earlier wave combines it
         f32x4_t v = {0.0f, 0.0f, 0.0f, 0.0f};
         if (lane < 32) {
@@ -631,10 +733,19 @@ extern "C" __global__ void __launch_bounds__(256) dfq_fill_u32(uint32_t* ptr, ui
         ptr[i] = v;
 }
 
+/* Chunks in flight per wave: enough to keep DFQ_PF_LOADS weight loads per lane
+ * outstanding, at least 2 and at most 8. */
+template <int BITS, int GS, int CH>
+constexpr int prefetch_depth() {
+    constexpr int loads = CH * Cfg<BITS, GS>::NS;
+    constexpr int d = DFQ_PF_LOADS / loads;
+    return d < 2 ? 2 : (d > 8 ? 8 : d);
+}
+
 #define DFQ_MT8_KERNEL(BITS, GS, F16, NAME, CHN, CH)                                        \
     extern "C" __global__ void __launch_bounds__(kThreads)                                   \
         dfq_qmm_mt8_b##BITS##_g##GS##_##NAME##_##CHN(QmmParams p) {                           \
-        qmm_mt8<BITS, GS, F16, CH, (CH > 1 ? DFQ_PF_CHUNKS : 8)>(p);                                      \
+        qmm_mt8<BITS, GS, F16, CH, prefetch_depth<BITS, GS, CH>()>(p);                        \
     }
 #define DFQ_MT8_FORMAT(BITS, GS, F16, NAME)                                                    \
     DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c1, 1)                                                \

@@ -18,7 +18,8 @@
  *  - the U = T*SS units (tile, chunk) of one k-block are split into Gkb contiguous ranges
  *    whose sizes differ by at most one (the first U % Gkb get one more), and each
  *    workgroup's range likewise into one range per wave;
- *  - a tile covered by one wave is written straight to y; a tile shared between waves is
+ *  - a tile covered by one wave is parked in LDS during the main loop and written to y
+ *    after it (the loop itself issues no global stores); a tile shared between waves is
  *    summed in LDS in wave order; a tile shared between workgroups (or k-blocks) is summed
  *    through workspace slots in a fixed order by whichever workgroup arrives last.
  */
@@ -41,6 +42,8 @@ typedef struct QmmParams {
     int32_t lds_row_stride; /* bytes per staged x row in LDS                          */
     int32_t lds_xsum_off;   /* byte offset of the per-group x sums in LDS             */
     int32_t lds_slot_off;   /* byte offset of the per-wave partial slots in LDS       */
+    int32_t lds_ytile_off;  /* byte offset of the per-wave result tiles in LDS        */
+    int32_t ytw;            /* result tiles per wave (tiles wholly inside its range)  */
     int32_t wg_base;        /* units per workgroup, rounded down (U / Gkb)            */
     int32_t wg_rem;         /* workgroups with one extra unit (U % Gkb)               */
     uint32_t w_bytes;       /* size of w in bytes (< 2^31)                            */

@@ -45,7 +45,11 @@ thread_local std::string g_last_error;
 #ifndef DFQ_WAVES
 #define DFQ_WAVES 8                    // must match the kernels' build
 #endif
-constexpr int kThreads = DFQ_WAVES * 64;          // qmm_mt8 workgroup size
+#ifndef DFQ_MIN_KBLOCKS
+#define DFQ_MIN_KBLOCKS 1              // k-blocks the planner starts from
+#endif
+constexpr int kWaves = DFQ_WAVES;
+constexpr int kThreads = kWaves * 64;             // qmm_mt8 workgroup size
 constexpr int kMaxStageItems = 96 / DFQ_WAVES;    // must match qmm_kernels.hip
 constexpr int kWaveSlotsBytes = DFQ_WAVES * 2 * 512;
 
@@ -136,53 +140,58 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
     const int ch = (K % (kss * (8 / gps)) == 0) ? 8 / gps : 1;
     const int kch = kss * ch;
     const int chunks = K / kch;
-    int nkb = 0, kr = 0;
-    size_t lds = 0;
-    for (int d = 1; d <= chunks; ++d) {
+    const int T = (N + 15) / 16;
+    /* Fewest k-blocks (at least DFQ_MIN_KBLOCKS) whose x slice (plus the per-wave tiles
+     * the split leaves) fits in LDS. */
+    for (int d = std::min(DFQ_MIN_KBLOCKS, chunks); d <= chunks; ++d) {
         if (chunks % d) continue;
-        const int k = K / d;
-        if ((int64_t)M * (k / 8) > (int64_t)kMaxStageItems * kThreads) continue;
-        const size_t rs = (size_t)2 * k + 16;
-        const size_t need = (size_t)(M + 1) * rs + (size_t)(k / gs) * 32 + kWaveSlotsBytes;
+        const int kr = K / d;
+        if ((int64_t)M * (kr / 8) > (int64_t)kMaxStageItems * kThreads) continue;
+        Plan p{};
+        p.kss = kss;
+        p.ch = ch;
+        p.T = T;
+        p.nkb = d;
+        p.kr = kr;
+        p.SS = chunks / d;
+        p.rs = 2 * kr + 16;
+        p.xsum_off = ((M + 1) * p.rs + 15) & ~15;
+        p.slot_off = p.xsum_off + (kr / gs) * 32;
+        p.ytile_off = p.slot_off + kWaveSlotsBytes;
+        if ((size_t)p.ytile_off + (size_t)kWaves * 512 > lds_max) continue;
+        /* result tiles a wave may park in LDS; more workgroups (beyond one per CU) shorten
+         * the ranges when the tiles would not fit */
+        const int64_t ytw_cap = (int64_t)(lds_max - p.ytile_off) / ((int64_t)kWaves * 512);
+        const int64_t U = (int64_t)T * p.SS;
+        int64_t G = std::max(1, num_cus / d);
+        G = std::max<int64_t>(G, (U + kWaves * ytw_cap * p.SS - 1) / (kWaves * ytw_cap * p.SS));
+        if (G > U) G = U;
+        p.Gkb = (int)G;
+        p.wg_base = (int)(U / G);
+        p.wg_rem = (int)(U % G);
+        /* a wave holds at most ceil(L / waves) units, so at most that / SS whole tiles */
+        const int64_t Lmax = p.wg_base + (p.wg_rem ? 1 : 0);
+        const int64_t umax = (Lmax + kWaves - 1) / kWaves;
+        p.ytw = (int)std::max<int64_t>(1, umax / p.SS);
+        const size_t need = (size_t)p.ytile_off + (size_t)kWaves * p.ytw * 512;
         if (need > lds_max) continue;
-        nkb = d;
-        kr = k;
-        lds = need;
-        break;
+        int nslot = 1;
+        for (int64_t t = 0; t < T; ++t) {
+            const int64_t c0 = owner_wg(t * p.SS, p.wg_base, p.wg_rem);
+            const int64_t c1 = owner_wg(t * p.SS + p.SS - 1, p.wg_base, p.wg_rem);
+            nslot = std::max<int>(nslot, (int)(c1 - c0 + 1));
+        }
+        p.nslot_kb = nslot;
+        /* Ask for more than half the CU's LDS so that exactly one workgroup lands per CU. */
+        const size_t want = std::max(need, lds_max / 2 + 256);
+        p.lds_bytes = (int)std::min(want, lds_max);
+        p.need_ws = d > 1 || nslot > 1;
+        p.ws_counter_bytes = ((size_t)T * 4 + 255) & ~(size_t)255;
+        p.ws_bytes = p.need_ws ? p.ws_counter_bytes + (size_t)T * d * nslot * 128 * 4 : 0;
+        *pl = p;
+        return true;
     }
-    if (!nkb) return false;
-    Plan p{};
-    p.kss = kss;
-    p.ch = ch;
-    p.T = (N + 15) / 16;
-    p.nkb = nkb;
-    p.kr = kr;
-    p.SS = chunks / nkb;
-    const int64_t U = (int64_t)p.T * p.SS;
-    int64_t G = std::max(1, num_cus / nkb);
-    if (G > U) G = U;
-    p.Gkb = (int)G;
-    p.wg_base = (int)(U / G);
-    p.wg_rem = (int)(U % G);
-    int nslot = 1;
-    for (int64_t t = 0; t < p.T; ++t) {
-        const int64_t c0 = owner_wg(t * p.SS, p.wg_base, p.wg_rem);
-        const int64_t c1 = owner_wg(t * p.SS + p.SS - 1, p.wg_base, p.wg_rem);
-        nslot = std::max<int>(nslot, (int)(c1 - c0 + 1));
-    }
-    p.nslot_kb = nslot;
-    p.rs = 2 * kr + 16;
-    p.xsum_off = (M + 1) * p.rs;
-    p.xsum_off = (p.xsum_off + 15) & ~15;
-    p.slot_off = p.xsum_off + (kr / gs) * 32;
-    /* Ask for more than half the CU's LDS so that exactly one workgroup lands per CU. */
-    size_t want = std::max(lds, lds_max / 2 + 256);
-    p.lds_bytes = (int)std::min(want, lds_max);
-    p.need_ws = nkb > 1 || nslot > 1;
-    p.ws_counter_bytes = ((size_t)p.T * 4 + 255) & ~(size_t)255;
-    p.ws_bytes = p.need_ws ? p.ws_counter_bytes + (size_t)p.T * nkb * nslot * 128 * 4 : 0;
-    *pl = p;
-    return true;
+    return false;
 }
 
 static dfq_status get_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, Plan* out) {
@@ -461,6 +470,8 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
     p.lds_row_stride = pl.rs;
     p.lds_xsum_off = pl.xsum_off;
     p.lds_slot_off = pl.slot_off;
+    p.lds_ytile_off = pl.ytile_off;
+    p.ytw = pl.ytw;
     p.wg_base = pl.wg_base;
     p.wg_rem = pl.wg_rem;
     p.w_bytes = (uint32_t)((int64_t)N * K * bits / 8);
@@ -593,26 +604,28 @@ dfq_status dfq_graph_destroy(dfq_graph* gr) {
 /* ---- introspection used by tests and the benchmark (not part of the drop-in surface) -- */
 
 /* Fills the work split the fast kernel uses for a shape: {T, SS, nkb, Gkb, nslot_kb, kr,
- * lds_bytes, need_ws, ch}. */
-dfq_status dfq_debug_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, int* out9) {
-    if (!out9) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
+ * lds_bytes, need_ws, ch, ytw}. */
+dfq_status dfq_debug_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, int* out10) {
+    if (!out10) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
     Plan p;
     dfq_status s = get_plan(ctx, M, N, K, bits, gs, &p);
     if (s) return s;
-    int v[9] = {p.T, p.SS, p.nkb, p.Gkb, p.nslot_kb, p.kr, p.lds_bytes, p.need_ws ? 1 : 0, p.ch};
-    std::memcpy(out9, v, sizeof v);
+    int v[10] = {p.T,  p.SS,        p.nkb,          p.Gkb, p.nslot_kb,
+                 p.kr, p.lds_bytes, p.need_ws ? 1 : 0, p.ch, p.ytw};
+    std::memcpy(out10, v, sizeof v);
     return DFQ_OK;
 }
 
 /* The same split computed without a device, for a given CU count and LDS limit. */
 dfq_status dfq_debug_make_plan(int M, int N, int K, int bits, int gs, int num_cus,
-                               size_t lds_max, int* out9) {
-    if (!out9) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
+                               size_t lds_max, int* out10) {
+    if (!out10) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
     Plan p;
     if (!make_plan(M, N, K, bits, gs, num_cus, lds_max, &p))
         return fail(DFQ_ERR_UNSUPPORTED, "no work split");
-    int v[9] = {p.T, p.SS, p.nkb, p.Gkb, p.nslot_kb, p.kr, p.lds_bytes, p.need_ws ? 1 : 0, p.ch};
-    std::memcpy(out9, v, sizeof v);
+    int v[10] = {p.T,  p.SS,        p.nkb,          p.Gkb, p.nslot_kb,
+                 p.kr, p.lds_bytes, p.need_ws ? 1 : 0, p.ch, p.ytw};
+    std::memcpy(out10, v, sizeof v);
     return DFQ_OK;
 }
 

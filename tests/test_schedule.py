@@ -2,7 +2,8 @@
 
 The runtime's planner (dfq_debug_make_plan, the same code dfq_qmm uses) is run for many
 shapes; the kernel's split and fix-up rules (qmm_kernels.hip: unit ranges per workgroup and
-wave, wave-level LDS slots, workgroup combine, workspace publish with a last-arriver sum)
+wave, wave-level LDS slots and result tiles, workgroup combine, workspace publish with a
+last-arriver sum)
 are replayed here unit by unit.  Every (k-block, tile, chunk) unit must be computed
 exactly once, every tile must be written exactly once with all of its units, and every
 workspace / LDS slot index must stay inside what the planner sized.
@@ -18,11 +19,11 @@ WAVES = 8
 
 def make_plan(M, N, K, bits, gs, cus=256, lds=163840):
     lib = dflash_qmm.load_library()
-    out = (ctypes.c_int * 9)()
+    out = (ctypes.c_int * 10)()
     rc = lib.dfq_debug_make_plan(M, N, K, bits, gs, cus, lds, out)
     if rc:
         return None
-    keys = ["T", "SS", "nkb", "Gkb", "nslot_kb", "kr", "lds_bytes", "need_ws", "ch"]
+    keys = ["T", "SS", "nkb", "Gkb", "nslot_kb", "kr", "lds_bytes", "need_ws", "ch", "ytw"]
     return dict(zip(keys, list(out)))
 
 
@@ -81,6 +82,7 @@ def replay(p):
                 if aw >= bw:
                     continue
                 t_first = aw // SS
+                tw0 = -(-aw // SS)  # first tile wholly inside the wave's range
                 cur = set()
                 for u in range(aw, bw):
                     t, s = divmod(u, SS)
@@ -90,6 +92,8 @@ def replay(p):
                     cur.add(key)
                     if s == SS - 1 or u + 1 == bw:
                         whole = t * SS >= aw and (t + 1) * SS <= bw
+                        if whole:  # parked in the wave's LDS result tiles
+                            assert 0 <= t - tw0 < p["ytw"], (t, tw0, p["ytw"])
                         if whole and nkb == 1:
                             finalize(t, cur)
                         elif whole:
