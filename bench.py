@@ -29,6 +29,21 @@ sys.path.insert(0, os.path.join(ROOT, "dflash-swift_amd"))
 
 N_OUT, K_IN, BITS, GS = 17408, 5120, 4, 64
 HBM_PEAK_GBS = 8000.0
+# rocprofv3 summary of the M=8 launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated); the
+# roofline's measured-traffic figure is read from its "traffic_bytes_per_launch:" line.
+PROFILE = os.path.join(ROOT, "profiles", "qmm_mt8_b4g64_bf16_k5120_n17408.md")
+
+
+def measured_traffic():
+    """HBM bytes per M=8 launch from the committed rocprofv3 summary, or None."""
+    try:
+        with open(PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
 
 
 def algorithmic_bytes(M, N=N_OUT, K=K_IN, bits=BITS, gs=GS):
@@ -190,7 +205,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
         },
     }
     if not args.no_cpu_baseline:

@@ -309,6 +309,7 @@ class QuantizedLinear:
         self.group_size, self.bits, self.mode = group_size, bits, mode
         self.out_features = weight.shape[0]
         self.in_features = weight.shape[1] * 32 // bits
+        self._owned = True
         if _handle is not None:
             self._h = _handle
             return
@@ -320,9 +321,9 @@ class QuantizedLinear:
 
     def __del__(self):
         try:
-            if self._h:
+            if self._h and self._owned:
                 self.lib.dfq_linear_destroy(self._h)
-                self._h = None
+            self._h = None
         except Exception:
             pass
 
@@ -419,6 +420,8 @@ class Model:
         obj = cls.__new__(cls)
         QuantizedLinear.__init__(obj, src.ctx, src.weight, src.scales, src.biases, src.bias,
                                  src.group_size, src.bits, src.mode, _handle=h)
+        obj._owned = False  # the model owns the leaf; the view must not destroy it
+        obj._model = self   # and keeps the model alive while the view exists
         return obj
 
     def __len__(self):

@@ -104,3 +104,20 @@ def test_context_free_layer_cannot_be_called():
         rc = lay.lib.dfq_linear_forward(lay._h, None, 0, 8, None, None, 0, None, None)
         dflash_qmm._check(rc, "dfq_linear_forward")
     assert e.value.status == 6
+
+
+def test_leaf_views_do_not_own_the_model_leaves():
+    """A leaf fetched from the model is a view: dropping it must not destroy the leaf."""
+    import gc
+    model = Model(projection=layer(bits=4), other=layer(bits=8))
+    for _ in range(50):
+        v = model.projection
+        assert v.shape == (4096, 1024) and not v.is_small_m
+        del v
+        gc.collect()
+    assert len(model) == 2
+    assert enable_small_m_quantized_matmul(model) == 2
+    for _ in range(50):
+        assert model.projection.is_small_m and model.other.is_small_m
+        gc.collect()
+    assert enable_small_m_quantized_matmul(model) == 0
