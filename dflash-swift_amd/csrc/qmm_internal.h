@@ -24,9 +24,9 @@ struct Plan {
     int kr = 0;         /* k elements per k-block                            */
     int rs = 0;         /* LDS bytes per staged x row                        */
     int xsum_off = 0;   /* LDS offset of the per-group x sums                */
-    int slot_off = 0;   /* LDS offset of the wave partial slots              */
-    int ytile_off = 0;  /* LDS offset of the per-wave result tiles           */
-    int ytw = 0;        /* result tiles per wave                             */
+    int part_off = 0;   /* LDS offset of the per-unit partial tiles          */
+    int cnt_off = 0;    /* LDS offset of the tile arrival counters           */
+    int umax = 0;       /* most units per workgroup                          */
     int lds_bytes = 0;  /* dynamic LDS requested per workgroup               */
     bool need_ws = false;
     size_t ws_counter_bytes = 0;

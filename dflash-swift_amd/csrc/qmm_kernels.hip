@@ -122,6 +122,18 @@ struct Cfg {
     }
 };
 
+/* v_permlane16_swap / v_permlane32_swap with explicit wait states on both sides.  The
+ * compiler (ROCm 7.2) pads the VALU-write -> swap-read side but not the swap-write ->
+ * VALU-read side; a VALU op issued right after the swap has been seen to read the swapped
+ * register's old contents on gfx950.  Semantics as the builtins: a is VDST, b is VSRC;
+ * the 16-lane (32-lane) rows are exchanged between the two registers. */
+__device__ __forceinline__ void permlane16_swap(uint32_t& a, uint32_t& b) {
+    __asm__ volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 4" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void permlane32_swap(uint32_t& a, uint32_t& b) {
+    __asm__ volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 4" : "+v"(a), "+v"(b));
+}
+
 /* Rearrange the raw words of one super-step (R[step][word], word j of lane group q covering
  * k chunk 4q+j (4-bit) / 2q+j/2 (8-bit)) so that lanes 0-31 of every operand hold one
  * quantisation group and lanes 32-63 another. */
@@ -129,17 +141,17 @@ template <int BITS, int GS>
 __device__ __forceinline__ void build_operand_words(const u32x4_t (&R)[Cfg<BITS, GS>::NS],
                                                     uint32_t (&OW)[Cfg<BITS, GS>::NOW]) {
     if constexpr (BITS == 4 && GS == 32) {
-        auto s01 = __builtin_amdgcn_permlane16_swap(R[0][0], R[0][1], false, false);
-        auto s23 = __builtin_amdgcn_permlane16_swap(R[0][2], R[0][3], false, false);
-        OW[0] = s01[0]; OW[1] = s01[1]; OW[2] = s23[0]; OW[3] = s23[1];
+        OW[0] = R[0][0]; OW[1] = R[0][1]; OW[2] = R[0][2]; OW[3] = R[0][3];
+        permlane16_swap(OW[0], OW[1]);
+        permlane16_swap(OW[2], OW[3]);
     } else if constexpr (BITS == 4 && GS == 64) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) OW[j] = R[0][j];
     } else if constexpr (BITS == 4 && GS == 128) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            auto s = __builtin_amdgcn_permlane32_swap(R[0][j], R[1][j], false, false);
-            OW[j] = s[0]; OW[4 + j] = s[1];
+            OW[j] = R[0][j]; OW[4 + j] = R[1][j];
+            permlane32_swap(OW[j], OW[4 + j]);
         }
     } else if constexpr (BITS == 8 && GS == 32) {
 #pragma unroll
@@ -147,38 +159,33 @@ __device__ __forceinline__ void build_operand_words(const u32x4_t (&R)[Cfg<BITS,
     } else if constexpr (BITS == 8 && GS == 64) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            auto s = __builtin_amdgcn_permlane32_swap(R[0][j], R[1][j], false, false);
-            OW[j] = s[0]; OW[4 + j] = s[1];
+            OW[j] = R[0][j]; OW[4 + j] = R[1][j];
+            permlane32_swap(OW[j], OW[4 + j]);
         }
     } else {  // 8-bit, group 128
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            auto s02 = __builtin_amdgcn_permlane32_swap(R[0][j], R[2][j], false, false);
-            auto s13 = __builtin_amdgcn_permlane32_swap(R[1][j], R[3][j], false, false);
-            OW[j] = s02[0]; OW[4 + j] = s02[1]; OW[8 + j] = s13[0]; OW[12 + j] = s13[1];
+            OW[j] = R[0][j]; OW[4 + j] = R[2][j]; OW[8 + j] = R[1][j]; OW[12 + j] = R[3][j];
+            permlane32_swap(OW[j], OW[4 + j]);
+            permlane32_swap(OW[8 + j], OW[12 + j]);
         }
     }
 }
 
-/* (a & m) | c in one VOP3 op.  gfx9 VOP3 takes no literal constants, so without this the
- * compiler emits a v_and_b32 and a v_or_b32 with literals; here the mask sits in an SGPR
- * and the magic in a VGPR, both loop-invariant. */
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
-    uint32_t r;
-    __asm__("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(c));
-    return r;
-}
-
 /* 8 nibbles of a word -> bf16/fp16 (MAGIC + q) pairs (q_i, q_{i+4}) in VGPR i: seven VALU
- * ops per word (three shifts, four and-ors). */
+ * ops per word (three shifts, four v_and_or_b32).  gfx9 VOP3 takes no literal constant, so
+ * with constant mask and magic the compiler would split each and-or into a v_and_b32 and a
+ * v_or_b32 with literals; the caller passes both as opaque register values (mask in an SGPR,
+ * magic in a VGPR, loop-invariant) and the compiler forms v_and_or_b32 itself.  It has to
+ * be the compiler's instruction, not inline asm: the MFMA that reads the result needs wait
+ * states after a VALU write, and the compiler only pads hazards it can see. */
 template <bool F16>
-__device__ __forceinline__ u32x4_t nibble_operand(uint32_t p, uint32_t magic) {
-    constexpr uint32_t kMask = 0x000F000Fu;
+__device__ __forceinline__ u32x4_t nibble_operand(uint32_t p, uint32_t mask, uint32_t magic) {
     u32x4_t v;
-    v[0] = and_or(p, kMask, magic);
-    v[1] = and_or(p >> 4, kMask, magic);
-    v[2] = and_or(p >> 8, kMask, magic);
-    v[3] = and_or(p >> 12, kMask, magic);
+    v[0] = (p & mask) | magic;
+    v[1] = ((p >> 4) & mask) | magic;
+    v[2] = ((p >> 8) & mask) | magic;
+    v[3] = ((p >> 12) & mask) | magic;
     return v;
 }
 
@@ -421,10 +428,6 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     const int SS = p.SS;      // chunks per tile per k-block
     const int a = wg_start(cl, p.wg_base, p.wg_rem);
     const int b = wg_start(cl + 1, p.wg_base, p.wg_rem);
-    const int L = b - a;
-    const int lb = L / kWaves, lr = L % kWaves;  // power-of-two divisions
-    const int aw = a + wave * lb + (wave < lr ? wave : lr);
-    const int bw = aw + lb + (wave < lr ? 1 : 0);
 
     const int RB = p.K * BITS / 8;        // bytes per weight row
     const int GPR = p.K / GS;             // groups per row
@@ -451,34 +454,38 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    /* ---- weight / scale / bias prefetch ring, one chunk per slot.  Loads take a scalar
+    /* ---- units of this workgroup, in the order its waves take them: the tile it shares
+     * with the next workgroup first ([s1, b)), then the rest from a (which starts with the
+     * tile shared with the previous one), so that cross-workgroup fix-ups happen early.
+     * Waves take the first kWaves*PF units by index and the rest from an LDS counter. */
+    const int L = b - a;
+    const int tlast = (b - 1) / SS;
+    const int s1 = max(a, tlast * SS);
+    const int nrot = b - s1;
+    auto unit_of = [&](int g) { return g < nrot ? s1 + g : a + (g - nrot); };
+
+    /* ---- weight / scale / bias prefetch ring, one unit per slot.  Loads take a scalar
      * base (tile row 0, chunk k) plus a per-lane 32-bit offset; a lane whose row is past N
-     * re-reads row N-1 (its result is never stored).  Every issue loads its slot: once the
-     * wave's range is exhausted it fetches the range's last unit again (an L2 hit).  The
-     * number of loads in flight is then the same on every path through the loop, so the
-     * compiler's vmcnt waits name exactly the slot being consumed; a load skipped on one
-     * path would make it wait for every load in flight. */
-    const bool has_work = aw < bw;
+     * re-reads row N-1 (its result is never stored).  Every issue loads its slot: past the
+     * end of the range it fetches the last unit it had again (an L2 hit), so the number of
+     * loads in flight is the same on every path through the loop and the compiler's vmcnt
+     * waits name exactly the slot being consumed. */
     const uint32_t lane_w = (uint32_t)q * 16u;
     const uint32_t lane_s = (CH > 1) ? 0u : (C::GPS == 4 ? 4u * (q >> 1) : 0u);
     using SV = typename std::conditional<(CH > 1), u32x4_t, uint32_t>::type;
     u32x4_t rw[PF][CH][C::NS];
     SV rs[PF], rb[PF];
+    int sg[PF];  // the unit (as a take index) each slot holds; >= L: none
     const uint8_t* wbytes = (const uint8_t*)p.w;
     const uint8_t* sbytes = (const uint8_t*)p.scales;
     const uint8_t* bbytes = (const uint8_t*)p.biases;
 
-    /* a wave without work fetches unit 0 of the k-block (never used): the prefetch is then
-     * unconditional too, and the x-staging waits below do not drain it */
-    const int a0 = has_work ? aw : 0;
-    int pt = a0 / SS, pc = a0 - (a0 / SS) * SS;  // next unit of the range to fetch
-    int lt = pt, lc = pc;                        // last unit of the range fetched
-    auto issue = [&](int slot, int u) {
-        const bool in = u < bw;
-        const int t = in ? pt : lt, c = in ? pc : lc;
-        lt = t;
-        lc = c;
-        if (in && ++pc == SS) { pc = 0; ++pt; }
+    int lu = a;  // last unit fetched (a wave that gets none fetches unit a, never used)
+    auto issue = [&](int slot, int g) {
+        sg[slot] = g;
+        const int u = g < L ? unit_of(g) : lu;
+        lu = u;
+        const int t = u / SS, c = u - t * SS;
         const int row0 = t * 16;
         const int rl = (row0 + 16 <= p.N) ? n : min(n, p.N - 1 - row0);
         const uint32_t vw = (uint32_t)rl * RB + lane_w;
@@ -498,16 +505,19 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
      * on has the same layout on entry as on every back edge */
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
-        issue(i, aw + i);
+        issue(i, wave * PF + i);
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    /* ---- LDS layout: row 0 zeros, rows 1..M x; then per-group x sums; then per-wave
-     * slots for partial tiles; then per-wave result tiles */
+    /* ---- LDS layout: row 0 zeros, rows 1..M x; per-group x sums; per-unit partial tiles
+     * ([n][8] fp32, 512 bytes each); tile arrival counters; the take counter */
     const int RS = p.lds_row_stride;
     float* xsum = (float*)(lds + p.lds_xsum_off);
-    float* wslot = (float*)(lds + p.lds_slot_off);
-    float* ytile = (float*)(lds + p.lds_ytile_off) + wave * p.ytw * 128;
+    float* part = (float*)(lds + p.lds_part_off);
+    uint32_t* tcnt = (uint32_t*)(lds + p.lds_cnt_off);
+    const int ta = a / SS;               // first tile touched by this workgroup
+    const int ntl = tlast - ta + 1;      // tiles touched
+    uint32_t* gcnt = tcnt + ntl;
     const int GK = p.kr / GS;  // groups in the k-block
 #pragma unroll
     for (int i = 0; i < kStageTasks; ++i) {
@@ -515,10 +525,10 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
         const bool act = task < ntask;
         const int tc = min(task, ntask - 1);
         const int r = tc / TPR, j = tc - r * TPR;
-        float s0 = 0.0f, s1 = 0.0f;  // group sums (two groups per task at GS = 32)
+        float s0 = 0.0f, s1s = 0.0f;  // group sums (two groups per task at GS = 32)
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-            if (GS == 32 && c >= 4) s1 = chunk_dot<F16>(xv[i][c], s1);
+            if (GS == 32 && c >= 4) s1s = chunk_dot<F16>(xv[i][c], s1s);
             else s0 = chunk_dot<F16>(xv[i][c], s0);
         }
         /* GS = 128: tasks 2g and 2g+1 of a row sit in neighbouring lanes */
@@ -530,7 +540,7 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
                 *(u32x4_t*)(dst + c * 16) = (BITS == 4) ? nibble_permute(xv[i][c]) : xv[i][c];
             if constexpr (GS == 32) {
                 xsum[(2 * j) * 8 + r] = s0;
-                xsum[(2 * j + 1) * 8 + r] = s1;
+                xsum[(2 * j + 1) * 8 + r] = s1s;
             } else if constexpr (GS == 64) {
                 xsum[j * 8 + r] = s0;
             } else {
@@ -542,6 +552,8 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     for (int c = tid; c < CPR; c += kThreads) *(u32x4_t*)(lds + c * 16) = u32x4_t{0, 0, 0, 0};
     for (int i = tid; i < GK * 8; i += kThreads)
         if ((i & 7) >= p.M) xsum[i] = 0.0f;
+    for (int i = tid; i < ntl; i += kThreads) tcnt[i] = 0u;
+    if (tid == 0) *gcnt = (uint32_t)(kWaves * PF);
     __syncthreads();
 
     /* ---- per-lane A / x-sum addresses */
@@ -552,19 +564,27 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
         (uint32_t)p.lds_xsum_off + (uint32_t)C::group_of(0, q) * 32u + (uint32_t)(q & 1) * 16u;
     const uint32_t sel_half = (q >> 1) ? kSelHi : kSelLo;
     constexpr float kOff = (BITS == 4) ? (F16 ? 1024.0f : 128.0f) : 0.0f;
-    const uint32_t magic = F16 ? 0x64006400u : 0x43004300u;
+    uint32_t magic = F16 ? 0x64006400u : 0x43004300u;
+    uint32_t nmask = 0x000F000Fu;
+    __asm__ volatile("" : "+v"(magic));  // opaque: keep in a VGPR (see nibble_operand)
+    __asm__ volatile("" : "+s"(nmask));  // opaque: keep in an SGPR
 
-    const int t_first = aw / SS;
-    const int tw0 = (aw + SS - 1) / SS;  // first tile lying wholly inside the wave's range
-    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    int ct = t_first, cc = aw - t_first * SS;
-
-    for (int u0 = aw; u0 < bw; u0 += PF) {
+    /* The only exit is at the top: takes grow monotonically, so once slot 0 holds no unit no
+     * slot does.  Every pass refills every slot (past the end with a clamped reload), so no
+     * path reaches the back edge with fewer loads in flight. */
+    while (sg[0] < L) {
 #pragma unroll
         for (int i = 0; i < PF; ++i) {
-            const int u = u0 + i;
-            /* no early exit: every pass issues all PF slots (see the prefetch ring) */
-            if (u < bw) {
+            const int g = sg[i];
+            /* take the next unit now; its index is needed when slot i is refilled */
+            uint32_t gn = 0;
+            if (lane == 0)
+                gn = __hip_atomic_fetch_add(gcnt, 1u, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (g < L) {
+            const int u = unit_of(g);
+            const int t = u / SS, cc = u - t * SS;
+            f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int j = 0; j < CH; ++j) {
                 const int css = cc * CH + j;  // super-step within the k-block
@@ -578,7 +598,7 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
                 for (int o = 0; o < C::NOPS; ++o) {
                     const u32x4_t A = *(const u32x4_t*)(lds + aoff + C::delta_chunk(o) * 16);
                     u32x4_t B;
-                    if constexpr (BITS == 4) B = nibble_operand<F16>(OW[o], magic);
+                    if constexpr (BITS == 4) B = nibble_operand<F16>(OW[o], nmask, magic);
                     else B = byte_operand<F16>(OW[2 * o], OW[2 * o + 1]);
                     P[C::partial_of(o)] = mfma<F16>(A, B, P[C::partial_of(o)]);
                 }
@@ -612,73 +632,44 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
                     }
                 }
             }
-            /* end of this wave's part of tile ct: fold the two group halves and park the
-             * tile in LDS (no global store inside the loop) */
-            if (cc == SS - 1 || u + 1 == bw) {
-                f32x4_t v;
+            /* fold the two group halves (lanes 0-31 hold the 8x16 partial) and park it */
+            f32x4_t v;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[r]),
-                                                               __float_as_uint(acc[r]),
-                                                               false, false);
-                    /* lanes 0-31 of the two halves: own value + lanes 32-63 */
-                    v[r] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+            for (int r = 0; r < 4; ++r) {
+                uint32_t lo = __float_as_uint(acc[r]), hi = lo;
+                permlane32_swap(lo, hi);
+                /* lanes 0-31: own value + the value of lane + 32 */
+                v[r] = __uint_as_float(lo) + __uint_as_float(hi);
+            }
+            if (lane < 32) *(f32x4_t*)(part + (u - a) * 128 + n * 8 + q * 4) = v;
+            /* arrive at tile t; the wave that completes its units here finishes it */
+            const int u0 = max(a, t * SS), u1 = min(b, (t + 1) * SS);
+            uint32_t old = 0;
+            if (lane == 0)
+                old = __hip_atomic_fetch_add(tcnt + (t - ta), 1u, __ATOMIC_ACQ_REL,
+                                             __HIP_MEMORY_SCOPE_WORKGROUP);
+            old = __builtin_amdgcn_readfirstlane(old);
+            if ((int)old + 1 == u1 - u0) {
+                f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (lane < 32)
+                    for (int uu = u0; uu < u1; ++uu)
+                        sum += *(const f32x4_t*)(part + (uu - a) * 128 + n * 8 + q * 4);
+                if (u0 == t * SS && u1 == (t + 1) * SS && p.nkb == 1) {
+                    store_y<F16>(p, t, lane, sum);
+                } else {
+                    const int first = owner_wg(t * SS, p.wg_base, p.wg_rem);
+                    publish<F16>(p, t, kb * p.nslot_kb + (cl - first), lane, sum);
                 }
-                const bool whole = ct * SS >= aw && (ct + 1) * SS <= bw;
-                float* dst = whole ? ytile + (ct - tw0) * 128
-                                   : wslot + (wave * 2 + (ct == t_first ? 0 : 1)) * 128;
-                if (lane < 32) *(f32x4_t*)(dst + n * 8 + q * 4) = v;
-                acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
             }
-            if (++cc == SS) { cc = 0; ++ct; }
             }
+            gn = __builtin_amdgcn_readfirstlane(gn);
             __builtin_amdgcn_sched_barrier(0);
-            issue(i, u + PF);
+            issue(i, (int)gn);
             __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-
-    __syncthreads();
-    if (!has_work) return;
-
-    /* ---- tiles that lie wholly inside this wave's range */
-    const int nwhole = bw / SS - tw0;
-    for (int e = 0; e < nwhole; ++e) {
-        f32x4_t v = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (lane < 32) v = *(const f32x4_t*)(ytile + e * 128 + n * 8 + q * 4);
-        if (p.nkb == 1) store_y<F16>(p, tw0 + e, lane, v);
-        else publish<F16>(p, tw0 + e, kb * p.nslot_kb, lane, v);
-    }
-
-    /* ---- combine tiles shared between waves of this workgroup */
-    const int t_last = (bw - 1) / SS;
-#pragma unroll
-    for (int which = 0; which < 2; ++which) {
-        const int t = which ? t_last : t_first;
-        if (which && t_last == t_first) break;
-        const bool whole = t * SS >= aw && (t + 1) * SS <= bw;
-        if (whole) continue;                             // stored above
-        if ((t * SS > a ? t * SS : a) < aw) continue;    // an earlier wave combines it
-        f32x4_t v = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (lane < 32) {
-            v = *(const f32x4_t*)(wslot + (wave * 2 + which) * 128 + n * 8 + q * 4);
-            for (int w2 = wave + 1; w2 < kWaves; ++w2) {
-                const int a2 = a + w2 * lb + (w2 < lr ? w2 : lr);
-                const int b2 = a2 + lb + (w2 < lr ? 1 : 0);
-                if (a2 >= (t + 1) * SS) break;
-                if (a2 == b2) continue;
-                v += *(const f32x4_t*)(wslot + (w2 * 2 + 0) * 128 + n * 8 + q * 4);
-            }
-        }
-        const bool wg_whole = t * SS >= a && (t + 1) * SS <= b;
-        if (wg_whole && p.nkb == 1) {
-            store_y<F16>(p, t, lane, v);
-        } else {
-            const int first = owner_wg(t * SS, p.wg_base, p.wg_rem);
-            publish<F16>(p, t, kb * p.nslot_kb + (cl - first), lane, v);
         }
     }
 }
+
 
 /* ---------------------------------------------------------------------------------- */
 /* Generic kernel: the stock-op stand-in                                                */

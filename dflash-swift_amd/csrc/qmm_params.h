@@ -16,12 +16,16 @@
  *    exactly two quantisation groups per lane half, 64..256 elements; a chunk is one
  *    super-step or the 8 groups whose scales one 16-byte load fetches);
  *  - the U = T*SS units (tile, chunk) of one k-block are split into Gkb contiguous ranges
- *    whose sizes differ by at most one (the first U % Gkb get one more), and each
- *    workgroup's range likewise into one range per wave;
- *  - a tile covered by one wave is parked in LDS during the main loop and written to y
- *    after it (the loop itself issues no global stores); a tile shared between waves is
- *    summed in LDS in wave order; a tile shared between workgroups (or k-blocks) is summed
- *    through workspace slots in a fixed order by whichever workgroup arrives last.
+ *    whose sizes differ by at most one (the first U % Gkb get one more);
+ *  - inside a workgroup the waves take units of its range one at a time from a counter in
+ *    LDS (the first ones by wave index), in a rotated order that starts with the tile shared
+ *    with the next workgroup and continues with the one shared with the previous, so that
+ *    cross-workgroup fix-ups happen early;
+ *  - every unit's partial tile goes to its own LDS slot; the wave that completes a tile's
+ *    units in this workgroup (an LDS arrival counter) sums the slots in unit order and writes
+ *    y, or, for a tile shared with other workgroups (or k-blocks), hands the sum to the
+ *    workspace fix-up: one 64-bit atomic exchange per element when exactly two parts exist,
+ *    else per-part slots summed in a fixed order by whichever part arrives last.
  */
 typedef struct QmmParams {
     const void* x;          /* [M][K] activations, bf16 or fp16                      */
@@ -41,9 +45,9 @@ typedef struct QmmParams {
     int32_t kr;             /* k elements per k-block                                 */
     int32_t lds_row_stride; /* bytes per staged x row in LDS                          */
     int32_t lds_xsum_off;   /* byte offset of the per-group x sums in LDS             */
-    int32_t lds_slot_off;   /* byte offset of the per-wave partial slots in LDS       */
-    int32_t lds_ytile_off;  /* byte offset of the per-wave result tiles in LDS        */
-    int32_t ytw;            /* result tiles per wave (tiles wholly inside its range)  */
+    int32_t lds_part_off;   /* byte offset of the per-unit partial tiles in LDS       */
+    int32_t lds_cnt_off;    /* byte offset of the per-tile arrival counters in LDS    */
+    int32_t umax;           /* most units one workgroup holds (partial slots sized)  */
     int32_t wg_base;        /* units per workgroup, rounded down (U / Gkb)            */
     int32_t wg_rem;         /* workgroups with one extra unit (U % Gkb)               */
     uint32_t w_bytes;       /* size of w in bytes (< 2^31)                            */

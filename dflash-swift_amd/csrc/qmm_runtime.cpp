@@ -51,7 +51,6 @@ thread_local std::string g_last_error;
 constexpr int kWaves = DFQ_WAVES;
 constexpr int kThreads = kWaves * 64;             // qmm_mt8 workgroup size
 constexpr int kMaxStageItems = 96 / DFQ_WAVES;    // must match qmm_kernels.hip
-constexpr int kWaveSlotsBytes = DFQ_WAVES * 2 * 512;
 
 struct PlanKey {
     int M, N, K, bits, gs;
@@ -141,8 +140,8 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
     const int kch = kss * ch;
     const int chunks = K / kch;
     const int T = (N + 15) / 16;
-    /* Fewest k-blocks (at least DFQ_MIN_KBLOCKS) whose x slice (plus the per-wave tiles
-     * the split leaves) fits in LDS. */
+    /* Fewest k-blocks (at least DFQ_MIN_KBLOCKS) whose x slice, plus the per-unit partial
+     * slots of the split, fits in LDS. */
     for (int d = std::min(DFQ_MIN_KBLOCKS, chunks); d <= chunks; ++d) {
         if (chunks % d) continue;
         const int kr = K / d;
@@ -156,24 +155,23 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
         p.SS = chunks / d;
         p.rs = 2 * kr + 16;
         p.xsum_off = ((M + 1) * p.rs + 15) & ~15;
-        p.slot_off = p.xsum_off + (kr / gs) * 32;
-        p.ytile_off = p.slot_off + kWaveSlotsBytes;
-        if ((size_t)p.ytile_off + (size_t)kWaves * 512 > lds_max) continue;
-        /* result tiles a wave may park in LDS; more workgroups (beyond one per CU) shorten
-         * the ranges when the tiles would not fit */
-        const int64_t ytw_cap = (int64_t)(lds_max - p.ytile_off) / ((int64_t)kWaves * 512);
+        p.part_off = p.xsum_off + (kr / gs) * 32;
+        /* each unit of a workgroup owns a 512-byte partial slot (plus at most one 4-byte
+         * tile counter); more workgroups (beyond one per CU) shorten the ranges when the
+         * slots would not fit */
+        if ((size_t)p.part_off + 512 + 256 > lds_max) continue;
+        const int64_t cap = (int64_t)(lds_max - p.part_off - 256) / 516;
         const int64_t U = (int64_t)T * p.SS;
         int64_t G = std::max(1, num_cus / d);
-        G = std::max<int64_t>(G, (U + kWaves * ytw_cap * p.SS - 1) / (kWaves * ytw_cap * p.SS));
+        G = std::max<int64_t>(G, (U + cap - 1) / cap);
         if (G > U) G = U;
         p.Gkb = (int)G;
         p.wg_base = (int)(U / G);
         p.wg_rem = (int)(U % G);
-        /* a wave holds at most ceil(L / waves) units, so at most that / SS whole tiles */
-        const int64_t Lmax = p.wg_base + (p.wg_rem ? 1 : 0);
-        const int64_t umax = (Lmax + kWaves - 1) / kWaves;
-        p.ytw = (int)std::max<int64_t>(1, umax / p.SS);
-        const size_t need = (size_t)p.ytile_off + (size_t)kWaves * p.ytw * 512;
+        p.umax = p.wg_base + (p.wg_rem ? 1 : 0);
+        p.cnt_off = p.part_off + p.umax * 512;
+        const int ntl_max = (p.umax + p.SS - 1) / p.SS + 1;  // tiles a range can touch
+        const size_t need = (size_t)p.cnt_off + (size_t)(ntl_max + 1) * 4;
         if (need > lds_max) continue;
         int nslot = 1;
         for (int64_t t = 0; t < T; ++t) {
@@ -469,9 +467,9 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
     p.kr = pl.kr;
     p.lds_row_stride = pl.rs;
     p.lds_xsum_off = pl.xsum_off;
-    p.lds_slot_off = pl.slot_off;
-    p.lds_ytile_off = pl.ytile_off;
-    p.ytw = pl.ytw;
+    p.lds_part_off = pl.part_off;
+    p.lds_cnt_off = pl.cnt_off;
+    p.umax = pl.umax;
     p.wg_base = pl.wg_base;
     p.wg_rem = pl.wg_rem;
     p.w_bytes = (uint32_t)((int64_t)N * K * bits / 8);
@@ -604,14 +602,14 @@ dfq_status dfq_graph_destroy(dfq_graph* gr) {
 /* ---- introspection used by tests and the benchmark (not part of the drop-in surface) -- */
 
 /* Fills the work split the fast kernel uses for a shape: {T, SS, nkb, Gkb, nslot_kb, kr,
- * lds_bytes, need_ws, ch, ytw}. */
+ * lds_bytes, need_ws, ch, umax}. */
 dfq_status dfq_debug_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, int* out10) {
     if (!out10) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
     Plan p;
     dfq_status s = get_plan(ctx, M, N, K, bits, gs, &p);
     if (s) return s;
     int v[10] = {p.T,  p.SS,        p.nkb,          p.Gkb, p.nslot_kb,
-                 p.kr, p.lds_bytes, p.need_ws ? 1 : 0, p.ch, p.ytw};
+                 p.kr, p.lds_bytes, p.need_ws ? 1 : 0, p.ch, p.umax};
     std::memcpy(out10, v, sizeof v);
     return DFQ_OK;
 }
@@ -624,7 +622,7 @@ dfq_status dfq_debug_make_plan(int M, int N, int K, int bits, int gs, int num_cu
     if (!make_plan(M, N, K, bits, gs, num_cus, lds_max, &p))
         return fail(DFQ_ERR_UNSUPPORTED, "no work split");
     int v[10] = {p.T,  p.SS,        p.nkb,          p.Gkb, p.nslot_kb,
-                 p.kr, p.lds_bytes, p.need_ws ? 1 : 0, p.ch, p.ytw};
+                 p.kr, p.lds_bytes, p.need_ws ? 1 : 0, p.ch, p.umax};
     std::memcpy(out10, v, sizeof v);
     return DFQ_OK;
 }

@@ -2,11 +2,13 @@
 
 The runtime's planner (dfq_debug_make_plan, the same code dfq_qmm uses) is run for many
 shapes; the kernel's split and fix-up rules (qmm_kernels.hip: unit ranges per workgroup and
-wave, wave-level LDS slots and result tiles, workgroup combine, workspace publish with a
+wave, per-unit LDS partial slots, per-tile arrival counters, workspace publish with a
 last-arriver sum)
 are replayed here unit by unit.  Every (k-block, tile, chunk) unit must be computed
 exactly once, every tile must be written exactly once with all of its units, and every
-workspace / LDS slot index must stay inside what the planner sized.
+workspace / LDS slot index must stay inside what the planner sized.  The order in which a
+workgroup's waves take its units does not change which arrival completes a tile's count, so
+replaying the workgroup's take order covers every interleaving of its waves.
 """
 import ctypes
 
@@ -14,7 +16,6 @@ import pytest
 
 import dflash_qmm
 
-WAVES = 8
 
 
 def make_plan(M, N, K, bits, gs, cus=256, lds=163840):
@@ -23,7 +24,7 @@ def make_plan(M, N, K, bits, gs, cus=256, lds=163840):
     rc = lib.dfq_debug_make_plan(M, N, K, bits, gs, cus, lds, out)
     if rc:
         return None
-    keys = ["T", "SS", "nkb", "Gkb", "nslot_kb", "kr", "lds_bytes", "need_ws", "ch", "ytw"]
+    keys = ["T", "SS", "nkb", "Gkb", "nslot_kb", "kr", "lds_bytes", "need_ws", "ch", "umax"]
     return dict(zip(keys, list(out)))
 
 
@@ -36,20 +37,19 @@ def owner_wg(u, base, rem):
     return u // (base + 1) if u < big else rem + (u - big) // base
 
 
-def wave_ranges(a, b):
-    L = b - a
-    lb, lr = divmod(L, WAVES)
-    out = []
-    for w in range(WAVES):
-        aw = a + w * lb + min(w, lr)
-        out.append((aw, aw + lb + (1 if w < lr else 0)))
-    return out
+def take_order(a, b, SS):
+    """Units of a workgroup range in the order its waves take them (the kernel's unit_of):
+    the tile shared with the next workgroup first, then the rest from a."""
+    s1 = max(a, ((b - 1) // SS) * SS)
+    return list(range(s1, b)) + list(range(a, s1))
 
 
 def replay(p):
     T, SS, nkb, G, nslot = p["T"], p["SS"], p["nkb"], p["Gkb"], p["nslot_kb"]
     U = T * SS
     base, rem = divmod(U, G)
+    umax = base + (1 if rem else 0)
+    assert p["umax"] == umax
     seen = set()
     y_writes = {}
     ws_slots = {}
@@ -76,62 +76,31 @@ def replay(p):
     for kb in range(nkb):
         for cl in range(G):
             a, b = wg_start(cl, base, rem), wg_start(cl + 1, base, rem)
-            ranges = wave_ranges(a, b)
-            wslot = {}
-            for w, (aw, bw) in enumerate(ranges):
-                if aw >= bw:
-                    continue
-                t_first = aw // SS
-                tw0 = -(-aw // SS)  # first tile wholly inside the wave's range
-                cur = set()
-                for u in range(aw, bw):
-                    t, s = divmod(u, SS)
-                    key = (kb, t, s)
-                    assert key not in seen, f"unit {key} computed twice"
-                    seen.add(key)
-                    cur.add(key)
-                    if s == SS - 1 or u + 1 == bw:
-                        whole = t * SS >= aw and (t + 1) * SS <= bw
-                        if whole:  # parked in the wave's LDS result tiles
-                            assert 0 <= t - tw0 < p["ytw"], (t, tw0, p["ytw"])
-                        if whole and nkb == 1:
-                            finalize(t, cur)
-                        elif whole:
-                            publish(t, kb, kb * nslot, cur)
-                        else:
-                            sidx = 0 if t == t_first else 1
-                            assert (w, sidx) not in wslot
-                            wslot[(w, sidx)] = (t, cur)
-                        cur = set()
-            for w, (aw, bw) in enumerate(ranges):
-                if aw >= bw:
-                    continue
-                t_first, t_last = aw // SS, (bw - 1) // SS
-                for which in (0, 1):
-                    t = t_last if which else t_first
-                    if which and t_last == t_first:
-                        break
-                    if t * SS >= aw and (t + 1) * SS <= bw:
-                        continue
-                    if max(t * SS, a) < aw:
-                        continue
-                    tt, units = wslot[(w, which)]
-                    assert tt == t
-                    units = set(units)
-                    for w2 in range(w + 1, WAVES):
-                        a2, b2 = ranges[w2]
-                        if a2 >= (t + 1) * SS:
-                            break
-                        if a2 == b2:
-                            continue
-                        t2, u2 = wslot[(w2, 0)]
-                        assert t2 == t
-                        units |= u2
-                    if t * SS >= a and (t + 1) * SS <= b and nkb == 1:
+            order = take_order(a, b, SS)
+            assert sorted(order) == list(range(a, b))
+            ta, tlast = a // SS, (b - 1) // SS
+            ntl = tlast - ta + 1
+            assert ntl <= (umax + SS - 1) // SS + 1          # LDS counters sized for this
+            part = {}
+            tcnt = [0] * ntl
+            for u in order:                                   # any wave, one unit at a time
+                key = (kb, u // SS, u % SS)
+                assert key not in seen, f"unit {key} computed twice"
+                seen.add(key)
+                assert 0 <= u - a < umax                      # its LDS partial slot
+                part[u - a] = key
+                t = u // SS
+                u0, u1 = max(a, t * SS), min(b, (t + 1) * SS)
+                tcnt[t - ta] += 1
+                if tcnt[t - ta] == u1 - u0:                   # the arrival that completes t
+                    units = {part[uu - a] for uu in range(u0, u1)}
+                    if u0 == t * SS and u1 == (t + 1) * SS and nkb == 1:
                         finalize(t, units)
                     else:
                         first = owner_wg(t * SS, base, rem)
                         publish(t, kb, kb * nslot + (cl - first), units)
+            assert all(c == min(b, (t + 1) * SS) - max(a, t * SS)
+                       for c, t in zip(tcnt, range(ta, tlast + 1)))
     assert len(seen) == nkb * U
     assert sorted(y_writes) == list(range(T))
     need_ws = nkb > 1 or nslot > 1
