@@ -60,6 +60,7 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -70,9 +71,9 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 #define DFQ_PF_LOADS 8     /* 16-byte weight loads in flight per lane (8 KB per wave) */
 #endif
 constexpr int kWaves = DFQ_WAVES;
+constexpr uint32_t kTileDone = 0x80000000u;  // tile counter value once a wave finished it
 constexpr int kThreads = kWaves * 64;
 constexpr int kMaxStageItems = 96 / DFQ_WAVES;  // 16-byte x chunks staged per thread
-constexpr int kStageTasks = (kMaxStageItems + 7) / 8;  // 64-k staging tasks per thread
 
 
 /* ---------------------------------------------------------------------------------- */
@@ -264,21 +265,33 @@ __device__ __forceinline__ uint16_t f32_to_out(float f) {
 }
 
 /* s + the 8 elements of a 16-byte chunk, added pairwise in k order with v_dot2c against
- * (1, 1): four VALU ops per chunk.  Written as inline asm on one 32-bit register at a time:
- * the builtin form, applied to elements of a 128-bit vector, has been compiled (ROCm 7.2)
- * to read the vector's first register for every element. */
+ * (1, 1): four VALU ops per chunk.  Each element goes through a plain 32-bit temporary: the
+ * builtin applied directly to an element of a 128-bit vector has been compiled (ROCm 7.2)
+ * to read the vector's first register for every element.  It stays the compiler's own
+ * instruction (not inline asm) so that the wait states a following DPP or MFMA read needs
+ * are inserted. */
 template <bool F16>
 __device__ __forceinline__ float chunk_dot(u32x4_t v, float s) {
-    const uint32_t ones = F16 ? 0x3c003c00u : 0x3f803f80u;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t e = v[i];
         if constexpr (F16)
-            __asm__("v_dot2c_f32_f16 %0, %1, %2" : "+v"(s) : "v"(e), "v"(ones));
+            s = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, e),
+                                       __builtin_bit_cast(f16x2_t, 0x3c003c00u), s, false);
         else
-            __asm__("v_dot2c_f32_bf16 %0, %1, %2" : "+v"(s) : "v"(e), "v"(ones));
+            s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, e),
+                                                __builtin_bit_cast(bf16x2_t, 0x3f803f80u), s,
+                                                false);
     }
     return s;
+}
+
+/* v from another lane of the same 16-lane row (DPP control CTRL; lanes whose source is
+ * outside the row read 0). */
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 
 /* (x0..x7) -> (x0,x4, x1,x5, x2,x6, x3,x7): the k order of a nibble operand. */
@@ -434,22 +447,19 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     const int k0 = kb * p.kr;             // first k of this k-block
 
     /* ---- x staging loads go out first (their wait must not cover the weight prefetch).
-     * A task is 64 consecutive k of one row: eight 16-byte chunks, summed in-thread into
-     * the group sums and written to LDS.  Tasks are dealt round-robin over the threads;
-     * threads past the last task load nothing (x is a sizeable share of what the CU's
-     * memory pipeline carries at the start of the kernel). */
-    const int TPR = p.kr / 64;  // tasks per row
-    const int ntask = p.M * TPR;
+     * Item c (16 bytes, 8 elements) of the M x kr block goes to thread c % kThreads, so each
+     * load instruction reads 1 KB of consecutive x; rounds past the last item are skipped
+     * and lanes past it reload the last one. */
+    const int CPR = p.kr / 8;  // 16-byte chunks per row of the k-block
+    const int items = p.M * CPR;
     const uint16_t* xg = (const uint16_t*)p.x;
-    u32x4_t xv[kStageTasks][8];
+    u32x4_t xv[kMaxStageItems];
 #pragma unroll
-    for (int i = 0; i < kStageTasks; ++i) {
-        const int task = min(tid + i * kThreads, ntask - 1);
-        const int r = task / TPR, j = task - r * TPR;
-        const uint16_t* src = xg + (size_t)r * p.K + k0 + j * 64;
-        if (tid + i * kThreads < ntask) {
-#pragma unroll
-            for (int c = 0; c < 8; ++c) xv[i][c] = *(const u32x4_t*)(src + c * 8);
+    for (int i = 0; i < kMaxStageItems; ++i) {
+        if (i * kThreads < items) {
+            const int c = min(tid + i * kThreads, items - 1);
+            const int r = c / CPR, cc = c - r * CPR;
+            xv[i] = *(const u32x4_t*)(xg + (size_t)r * p.K + k0 + cc * 8);
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -519,36 +529,26 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     const int ntl = tlast - ta + 1;      // tiles touched
     uint32_t* gcnt = tcnt + ntl;
     const int GK = p.kr / GS;  // groups in the k-block
+    /* per item: pre-permute into the MFMA k order, and sum its 8 elements; the GS/8 items
+     * of a group sit in aligned neighbouring lanes and are summed with DPP */
 #pragma unroll
-    for (int i = 0; i < kStageTasks; ++i) {
-        const int task = tid + i * kThreads;
-        const bool act = task < ntask;
-        const int tc = min(task, ntask - 1);
-        const int r = tc / TPR, j = tc - r * TPR;
-        float s0 = 0.0f, s1s = 0.0f;  // group sums (two groups per task at GS = 32)
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            if (GS == 32 && c >= 4) s1s = chunk_dot<F16>(xv[i][c], s1s);
-            else s0 = chunk_dot<F16>(xv[i][c], s0);
-        }
-        /* GS = 128: tasks 2g and 2g+1 of a row sit in neighbouring lanes */
-        if constexpr (GS == 128) s0 += __shfl_xor(s0, 1);
-        if (act) {
-            uint8_t* dst = lds + (size_t)(1 + r) * RS + j * 128;
-#pragma unroll
-            for (int c = 0; c < 8; ++c)
-                *(u32x4_t*)(dst + c * 16) = (BITS == 4) ? nibble_permute(xv[i][c]) : xv[i][c];
-            if constexpr (GS == 32) {
-                xsum[(2 * j) * 8 + r] = s0;
-                xsum[(2 * j + 1) * 8 + r] = s1s;
-            } else if constexpr (GS == 64) {
-                xsum[j * 8 + r] = s0;
-            } else {
-                if ((j & 1) == 0) xsum[(j >> 1) * 8 + r] = s0;
+    for (int i = 0; i < kMaxStageItems; ++i) {
+        if (i * kThreads < items) {
+            const int c = tid + i * kThreads;
+            const bool act = c < items;
+            const int r = c / CPR, cc = c - r * CPR;
+            float sm = act ? chunk_dot<F16>(xv[i], 0.0f) : 0.0f;
+            sm += dpp_f32<0xB1>(sm);             // lanes ^1 (quad_perm 1,0,3,2)
+            sm += dpp_f32<0x4E>(sm);             // lanes ^2 (quad_perm 2,3,0,1)
+            if constexpr (GS >= 64) sm += dpp_f32<0x104>(sm);   // + lane+4 (row_shl:4)
+            if constexpr (GS >= 128) sm += dpp_f32<0x108>(sm);  // + lane+8 (row_shl:8)
+            if (act) {
+                const u32x4_t v = (BITS == 4) ? nibble_permute(xv[i]) : xv[i];
+                *(u32x4_t*)(lds + (size_t)(1 + r) * RS + cc * 16) = v;
+                if ((cc & (GS / 8 - 1)) == 0) xsum[(cc / (GS / 8)) * 8 + r] = sm;
             }
         }
     }
-    const int CPR = p.kr / 8;
     for (int c = tid; c < CPR; c += kThreads) *(u32x4_t*)(lds + c * 16) = u32x4_t{0, 0, 0, 0};
     for (int i = tid; i < GK * 8; i += kThreads)
         if ((i & 7) >= p.M) xsum[i] = 0.0f;
@@ -642,7 +642,10 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
                 v[r] = __uint_as_float(lo) + __uint_as_float(hi);
             }
             if (lane < 32) *(f32x4_t*)(part + (u - a) * 128 + n * 8 + q * 4) = v;
-            /* arrive at tile t; the wave that completes its units here finishes it */
+            /* arrive at tile t; the wave that completes its units here sums them into the slot
+             * of the tile's first unit and marks the tile as its own (written after the loop:
+             * a global store or atomic inside the loop would make the next slot's wait cover
+             * it, since the compiler must also allow for the path without it) */
             const int u0 = max(a, t * SS), u1 = min(b, (t + 1) * SS);
             uint32_t old = 0;
             if (lane == 0)
@@ -650,22 +653,35 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
                                              __HIP_MEMORY_SCOPE_WORKGROUP);
             old = __builtin_amdgcn_readfirstlane(old);
             if ((int)old + 1 == u1 - u0) {
-                f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (lane < 32)
+                if (lane < 32) {
+                    f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
                     for (int uu = u0; uu < u1; ++uu)
                         sum += *(const f32x4_t*)(part + (uu - a) * 128 + n * 8 + q * 4);
-                if (u0 == t * SS && u1 == (t + 1) * SS && p.nkb == 1) {
-                    store_y<F16>(p, t, lane, sum);
-                } else {
-                    const int first = owner_wg(t * SS, p.wg_base, p.wg_rem);
-                    publish<F16>(p, t, kb * p.nslot_kb + (cl - first), lane, sum);
+                    *(f32x4_t*)(part + (u0 - a) * 128 + n * 8 + q * 4) = sum;
                 }
+                if (lane == 0) tcnt[t - ta] = kTileDone | (uint32_t)wave;
             }
             }
             gn = __builtin_amdgcn_readfirstlane(gn);
             __builtin_amdgcn_sched_barrier(0);
             issue(i, (int)gn);
             __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    /* ---- write the tiles this wave finished: y, or the workspace fix-up for tiles shared
+     * with other workgroups or k-blocks */
+    for (int tl = 0; tl < ntl; ++tl) {
+        if (tcnt[tl] != (kTileDone | (uint32_t)wave)) continue;
+        const int t = ta + tl;
+        const int u0 = max(a, t * SS), u1 = min(b, (t + 1) * SS);
+        f32x4_t v = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (lane < 32) v = *(const f32x4_t*)(part + (u0 - a) * 128 + n * 8 + q * 4);
+        if (u0 == t * SS && u1 == (t + 1) * SS && p.nkb == 1) {
+            store_y<F16>(p, t, lane, v);
+        } else {
+            const int first = owner_wg(t * SS, p.wg_base, p.wg_rem);
+            publish<F16>(p, t, kb * p.nslot_kb + (cl - first), lane, v);
         }
     }
 }
