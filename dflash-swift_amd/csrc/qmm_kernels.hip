@@ -65,15 +65,23 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 #ifndef DFQ_WAVES
-#define DFQ_WAVES 8        /* waves per workgroup; the host is built with the same value */
+#define DFQ_WAVES 12       /* streaming waves per workgroup; the host is built with the same value */
 #endif
 #ifndef DFQ_PF_LOADS
-#define DFQ_PF_LOADS 8     /* 16-byte weight loads in flight per lane (8 KB per wave) */
+#define DFQ_PF_LOADS 4     /* 16-byte weight loads in flight per lane (4 KB per wave) */
 #endif
 constexpr int kWaves = DFQ_WAVES;
-constexpr uint32_t kTileDone = 0x80000000u;  // tile counter value once a wave finished it
-constexpr int kThreads = kWaves * 64;
+constexpr uint32_t kTileDone = 0x80000000u;  // tile counter value once its units are summed
+constexpr uint32_t kTileOut = 0x80000001u;   // ... and once the publisher wave wrote it
+constexpr int kThreads = kWaves * 64;        // streaming threads
+constexpr int kBlock = kThreads + 64;        // + the publisher wave
 constexpr int kMaxStageItems = 96 / DFQ_WAVES;  // 16-byte x chunks staged per thread
+
+/* The dynamic LDS block of a qmm_mt8 workgroup (its layout is fixed by the host plan). */
+__device__ __forceinline__ uint8_t* lds_base() {
+    extern __shared__ __attribute__((aligned(16))) uint8_t dfq_lds[];
+    return dfq_lds;
+}
 
 
 /* ---------------------------------------------------------------------------------- */
@@ -417,6 +425,56 @@ __device__ void publish(const QmmParams& p, int t, int slot, int lane, f32x4_t v
         __hip_atomic_store(p.counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+/* The publisher wave of a qmm_mt8 workgroup.  The streaming waves only sum a finished tile
+ * into LDS and mark it kTileDone; this wave, which issues no weight loads, writes it out (y,
+ * or the workspace fix-up of a tile shared with other workgroups or k-blocks) while the
+ * streaming continues.  Global stores and atomics in the streaming waves would sit in the
+ * same in-order vmcnt queue as their prefetch and make every later wait cover them.
+ *
+ * It polls the tile counters of its workgroup (one lane per tile, sleeping between empty
+ * polls) until each of the ntl tiles has been written.  Every unit of [a, b) is taken by
+ * exactly one streaming wave, so every tile reaches kTileDone and the loop ends. */
+template <bool F16>
+__device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b, int lane) {
+    const int SS = p.SS;
+    const int q = lane >> 4, n = lane & 15;
+    const int ta = a / SS;
+    const int ntl = (b > a) ? (b - 1) / SS - ta + 1 : 0;
+    uint32_t* tcnt = (uint32_t*)(lds_base() + p.lds_cnt_off);
+    const float* part = (const float*)(lds_base() + p.lds_part_off);
+    __syncthreads();  // the staging barrier of the streaming waves (tile counters zeroed)
+    int remaining = ntl;
+    while (remaining > 0) {
+        int found = 0;
+        for (int base = 0; base < ntl; base += 64) {
+            const int tl = base + lane;
+            bool ready = false;
+            if (tl < ntl)
+                ready = __hip_atomic_load(tcnt + tl, __ATOMIC_ACQUIRE,
+                                          __HIP_MEMORY_SCOPE_WORKGROUP) == kTileDone;
+            uint64_t m = __builtin_amdgcn_ballot_w64(ready);
+            while (m) {
+                const int bit = __builtin_ctzll(m);
+                m &= m - 1;
+                const int t = ta + base + bit;
+                const int u0 = max(a, t * SS), u1 = min(b, (t + 1) * SS);
+                f32x4_t v = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (lane < 32) v = *(const f32x4_t*)(part + (u0 - a) * 128 + n * 8 + q * 4);
+                if (u0 == t * SS && u1 == (t + 1) * SS && p.nkb == 1) {
+                    store_y<F16>(p, t, lane, v);
+                } else {
+                    const int first = owner_wg(t * SS, p.wg_base, p.wg_rem);
+                    publish<F16>(p, t, kb * p.nslot_kb + (cl - first), lane, v);
+                }
+                if (lane == 0) tcnt[base + bit] = kTileOut;
+                ++found;
+            }
+        }
+        remaining -= found;
+        if (!found) __builtin_amdgcn_s_sleep(1);
+    }
+}
+
 /* ---------------------------------------------------------------------------------- */
 /* The fast kernel                                                                      */
 /* ---------------------------------------------------------------------------------- */
@@ -428,7 +486,7 @@ template <int BITS, int GS, bool F16, int CH, int PF>
 __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     using C = Cfg<BITS, GS>;
     static_assert(CH == 1 || CH * C::GPS == 8, "chunk = one super-step or 8 groups");
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    uint8_t* lds = lds_base();
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -441,6 +499,11 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     const int SS = p.SS;      // chunks per tile per k-block
     const int a = wg_start(cl, p.wg_base, p.wg_rem);
     const int b = wg_start(cl + 1, p.wg_base, p.wg_rem);
+
+    if (wave == kWaves) {
+        publisher_wave<F16>(p, kb, cl, a, b, lane);
+        return;
+    }
 
     const int RB = p.K * BITS / 8;        // bytes per weight row
     const int GPR = p.K / GS;             // groups per row
@@ -643,9 +706,7 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
             }
             if (lane < 32) *(f32x4_t*)(part + (u - a) * 128 + n * 8 + q * 4) = v;
             /* arrive at tile t; the wave that completes its units here sums them into the slot
-             * of the tile's first unit and marks the tile as its own (written after the loop:
-             * a global store or atomic inside the loop would make the next slot's wait cover
-             * it, since the compiler must also allow for the path without it) */
+             * of the tile's first unit and hands the tile to the publisher wave */
             const int u0 = max(a, t * SS), u1 = min(b, (t + 1) * SS);
             uint32_t old = 0;
             if (lane == 0)
@@ -659,29 +720,15 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
                         sum += *(const f32x4_t*)(part + (uu - a) * 128 + n * 8 + q * 4);
                     *(f32x4_t*)(part + (u0 - a) * 128 + n * 8 + q * 4) = sum;
                 }
-                if (lane == 0) tcnt[t - ta] = kTileDone | (uint32_t)wave;
+                if (lane == 0)
+                    __hip_atomic_store(tcnt + (t - ta), kTileDone, __ATOMIC_RELEASE,
+                                       __HIP_MEMORY_SCOPE_WORKGROUP);
             }
             }
             gn = __builtin_amdgcn_readfirstlane(gn);
             __builtin_amdgcn_sched_barrier(0);
             issue(i, (int)gn);
             __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-
-    /* ---- write the tiles this wave finished: y, or the workspace fix-up for tiles shared
-     * with other workgroups or k-blocks */
-    for (int tl = 0; tl < ntl; ++tl) {
-        if (tcnt[tl] != (kTileDone | (uint32_t)wave)) continue;
-        const int t = ta + tl;
-        const int u0 = max(a, t * SS), u1 = min(b, (t + 1) * SS);
-        f32x4_t v = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (lane < 32) v = *(const f32x4_t*)(part + (u0 - a) * 128 + n * 8 + q * 4);
-        if (u0 == t * SS && u1 == (t + 1) * SS && p.nkb == 1) {
-            store_y<F16>(p, t, lane, v);
-        } else {
-            const int first = owner_wg(t * SS, p.wg_base, p.wg_rem);
-            publish<F16>(p, t, kb * p.nslot_kb + (cl - first), lane, v);
         }
     }
 }
@@ -741,16 +788,18 @@ extern "C" __global__ void __launch_bounds__(256) dfq_fill_u32(uint32_t* ptr, ui
 }
 
 /* Chunks in flight per wave: enough to keep DFQ_PF_LOADS weight loads per lane
- * outstanding, at least 2 and at most 8. */
+ * outstanding, at least 1 and at most 8.  Measured on the headline shape, one 4 KB chunk per
+ * wave (about 48 KB per CU with scales and biases) streams faster than two or more: deeper
+ * queues only add latency. */
 template <int BITS, int GS, int CH>
 constexpr int prefetch_depth() {
     constexpr int loads = CH * Cfg<BITS, GS>::NS;
     constexpr int d = DFQ_PF_LOADS / loads;
-    return d < 2 ? 2 : (d > 8 ? 8 : d);
+    return d < 1 ? 1 : (d > 8 ? 8 : d);
 }
 
 #define DFQ_MT8_KERNEL(BITS, GS, F16, NAME, CHN, CH)                                        \
-    extern "C" __global__ void __launch_bounds__(kThreads)                                   \
+    extern "C" __global__ void __launch_bounds__(kBlock)                                     \
         dfq_qmm_mt8_b##BITS##_g##GS##_##NAME##_##CHN(QmmParams p) {                           \
         qmm_mt8<BITS, GS, F16, CH, prefetch_depth<BITS, GS, CH>()>(p);                        \
     }

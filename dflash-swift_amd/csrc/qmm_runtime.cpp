@@ -43,13 +43,14 @@ namespace {
 thread_local std::string g_last_error;
 
 #ifndef DFQ_WAVES
-#define DFQ_WAVES 8                    // must match the kernels' build
+#define DFQ_WAVES 12                   // must match the kernels' build
 #endif
 #ifndef DFQ_MIN_KBLOCKS
 #define DFQ_MIN_KBLOCKS 1              // k-blocks the planner starts from
 #endif
 constexpr int kWaves = DFQ_WAVES;
-constexpr int kThreads = kWaves * 64;             // qmm_mt8 workgroup size
+constexpr int kThreads = kWaves * 64;             // qmm_mt8 streaming threads
+constexpr int kBlockThreads = kThreads + 64;      // + the publisher wave: the workgroup size
 constexpr int kMaxStageItems = 96 / DFQ_WAVES;    // must match qmm_kernels.hip
 
 struct PlanKey {
@@ -480,7 +481,7 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
     void* args[] = {&p};
     const int ci = pl.ch > 1 ? 1 : 0;
     hipError_t e = hipModuleLaunchKernel(ctx->mt8[bi][gi][di][ci], (unsigned)(pl.nkb * pl.Gkb), 1, 1,
-                                         kThreads, 1, 1, (unsigned)pl.lds_bytes, stream, args,
+                                         kBlockThreads, 1, 1, (unsigned)pl.lds_bytes, stream, args,
                                          nullptr);
     return e == hipSuccess ? DFQ_OK : hip_fail(e, "launch dfq_qmm_mt8");
 }
