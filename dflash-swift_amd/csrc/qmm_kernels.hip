@@ -632,6 +632,109 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     __asm__ volatile("" : "+v"(magic));  // opaque: keep in a VGPR (see nibble_operand)
     __asm__ volatile("" : "+s"(nmask));  // opaque: keep in an SGPR
 
+    /* One unit: CH super-steps of MFMA on the operands in slot i, the scale / bias epilogue,
+     * the fold of the two group halves, and the arrival at the unit's tile. */
+    auto process = [&](const int i, const int g) {
+        const int u = unit_of(g);
+        const int t = u / SS, cc = u - t * SS;
+        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const int css = cc * CH + j;  // super-step within the k-block
+            uint32_t OW[C::NOW];
+            build_operand_words<BITS, GS>(rw[i][j], OW);
+            const uint32_t aoff = abase + (uint32_t)css * (C::CPS * 16);
+            f32x4_t P[C::NP];
+#pragma unroll
+            for (int pp = 0; pp < C::NP; ++pp) P[pp] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int o = 0; o < C::NOPS; ++o) {
+                const u32x4_t A = *(const u32x4_t*)(lds + aoff + C::delta_chunk(o) * 16);
+                u32x4_t B;
+                if constexpr (BITS == 4) B = nibble_operand<F16>(OW[o], nmask, magic);
+                else B = byte_operand<F16>(OW[2 * o], OW[2 * o + 1]);
+                P[C::partial_of(o)] = mfma<F16>(A, B, P[C::partial_of(o)]);
+            }
+            const uint32_t xo = xbase + (uint32_t)css * (C::GPS * 32);
+#pragma unroll
+            for (int pp = 0; pp < C::NP; ++pp) {
+                uint32_t sw, bw2, sel;
+                if constexpr (CH > 1) {
+                    if constexpr (C::GPS == 4) {
+                        sw = (q >> 1) ? rs[i][2 * j + 1] : rs[i][2 * j];
+                        bw2 = (q >> 1) ? rb[i][2 * j + 1] : rb[i][2 * j];
+                        sel = pp ? kSelHi : kSelLo;
+                    } else {
+                        sw = rs[i][j];
+                        bw2 = rb[i][j];
+                        sel = sel_half;
+                    }
+                } else {
+                    sw = rs[i];
+                    bw2 = rb[i];
+                    sel = (C::GPS == 4) ? (pp ? kSelHi : kSelLo) : sel_half;
+                }
+                const float s = half_sel<F16>(sw, sel);
+                const float bb = half_sel<F16>(bw2, sel);
+                const float bp = (kOff != 0.0f) ? __builtin_fmaf(-kOff, s, bb) : bb;
+                const f32x4_t X = *(const f32x4_t*)(lds + xo + pp * 32);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    acc[r] = __builtin_fmaf(s, P[pp][r], acc[r]);
+                    acc[r] = __builtin_fmaf(bp, X[r], acc[r]);
+                }
+            }
+        }
+        /* fold the two group halves (lanes 0-31 hold the 8x16 partial) and park it */
+        f32x4_t v;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            uint32_t lo = __float_as_uint(acc[r]), hi = lo;
+            permlane32_swap(lo, hi);
+            /* lanes 0-31: own value + the value of lane + 32 */
+            v[r] = __uint_as_float(lo) + __uint_as_float(hi);
+        }
+        if (lane < 32) *(f32x4_t*)(part + (u - a) * 128 + n * 8 + q * 4) = v;
+        /* arrive at tile t; the wave that completes its units here sums them into the slot
+         * of the tile's first unit and hands the tile to the publisher wave */
+        const int u0 = max(a, t * SS), u1 = min(b, (t + 1) * SS);
+        uint32_t old = 0;
+        if (lane == 0)
+            old = __hip_atomic_fetch_add(tcnt + (t - ta), 1u, __ATOMIC_ACQ_REL,
+                                         __HIP_MEMORY_SCOPE_WORKGROUP);
+        old = __builtin_amdgcn_readfirstlane(old);
+        if ((int)old + 1 == u1 - u0) {
+            if (lane < 32) {
+                f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
+                for (int uu = u0; uu < u1; ++uu)
+                    sum += *(const f32x4_t*)(part + (uu - a) * 128 + n * 8 + q * 4);
+                *(f32x4_t*)(part + (u0 - a) * 128 + n * 8 + q * 4) = sum;
+            }
+            if (lane == 0)
+                __hip_atomic_store(tcnt + (t - ta), kTileDone, __ATOMIC_RELEASE,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+    };
+
+    if constexpr (PF == 1) {
+        /* One slot: take the next unit, compute this one, and refill the slot only if there
+         * is a next unit.  Both edges into the loop header carry exactly the slot's loads,
+         * and the last pass issues nothing (no reload past the end to drain before exit). */
+        int g = sg[0];
+        while (g < L) {
+            uint32_t gn = 0;
+            if (lane == 0)
+                gn = __hip_atomic_fetch_add(gcnt, 1u, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_WORKGROUP);
+            process(0, g);
+            gn = __builtin_amdgcn_readfirstlane(gn);
+            if ((int)gn >= L) break;
+            __builtin_amdgcn_sched_barrier(0);
+            issue(0, (int)gn);
+            __builtin_amdgcn_sched_barrier(0);
+            g = (int)gn;
+        }
+    } else {
     /* The only exit is at the top: takes grow monotonically, so once slot 0 holds no unit no
      * slot does.  Every pass refills every slot (past the end with a clamped reload), so no
      * path reaches the back edge with fewer loads in flight. */
@@ -644,92 +747,13 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
             if (lane == 0)
                 gn = __hip_atomic_fetch_add(gcnt, 1u, __ATOMIC_RELAXED,
                                             __HIP_MEMORY_SCOPE_WORKGROUP);
-            if (g < L) {
-            const int u = unit_of(g);
-            const int t = u / SS, cc = u - t * SS;
-            f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int j = 0; j < CH; ++j) {
-                const int css = cc * CH + j;  // super-step within the k-block
-                uint32_t OW[C::NOW];
-                build_operand_words<BITS, GS>(rw[i][j], OW);
-                const uint32_t aoff = abase + (uint32_t)css * (C::CPS * 16);
-                f32x4_t P[C::NP];
-#pragma unroll
-                for (int pp = 0; pp < C::NP; ++pp) P[pp] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int o = 0; o < C::NOPS; ++o) {
-                    const u32x4_t A = *(const u32x4_t*)(lds + aoff + C::delta_chunk(o) * 16);
-                    u32x4_t B;
-                    if constexpr (BITS == 4) B = nibble_operand<F16>(OW[o], nmask, magic);
-                    else B = byte_operand<F16>(OW[2 * o], OW[2 * o + 1]);
-                    P[C::partial_of(o)] = mfma<F16>(A, B, P[C::partial_of(o)]);
-                }
-                const uint32_t xo = xbase + (uint32_t)css * (C::GPS * 32);
-#pragma unroll
-                for (int pp = 0; pp < C::NP; ++pp) {
-                    uint32_t sw, bw2, sel;
-                    if constexpr (CH > 1) {
-                        if constexpr (C::GPS == 4) {
-                            sw = (q >> 1) ? rs[i][2 * j + 1] : rs[i][2 * j];
-                            bw2 = (q >> 1) ? rb[i][2 * j + 1] : rb[i][2 * j];
-                            sel = pp ? kSelHi : kSelLo;
-                        } else {
-                            sw = rs[i][j];
-                            bw2 = rb[i][j];
-                            sel = sel_half;
-                        }
-                    } else {
-                        sw = rs[i];
-                        bw2 = rb[i];
-                        sel = (C::GPS == 4) ? (pp ? kSelHi : kSelLo) : sel_half;
-                    }
-                    const float s = half_sel<F16>(sw, sel);
-                    const float bb = half_sel<F16>(bw2, sel);
-                    const float bp = (kOff != 0.0f) ? __builtin_fmaf(-kOff, s, bb) : bb;
-                    const f32x4_t X = *(const f32x4_t*)(lds + xo + pp * 32);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        acc[r] = __builtin_fmaf(s, P[pp][r], acc[r]);
-                        acc[r] = __builtin_fmaf(bp, X[r], acc[r]);
-                    }
-                }
-            }
-            /* fold the two group halves (lanes 0-31 hold the 8x16 partial) and park it */
-            f32x4_t v;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                uint32_t lo = __float_as_uint(acc[r]), hi = lo;
-                permlane32_swap(lo, hi);
-                /* lanes 0-31: own value + the value of lane + 32 */
-                v[r] = __uint_as_float(lo) + __uint_as_float(hi);
-            }
-            if (lane < 32) *(f32x4_t*)(part + (u - a) * 128 + n * 8 + q * 4) = v;
-            /* arrive at tile t; the wave that completes its units here sums them into the slot
-             * of the tile's first unit and hands the tile to the publisher wave */
-            const int u0 = max(a, t * SS), u1 = min(b, (t + 1) * SS);
-            uint32_t old = 0;
-            if (lane == 0)
-                old = __hip_atomic_fetch_add(tcnt + (t - ta), 1u, __ATOMIC_ACQ_REL,
-                                             __HIP_MEMORY_SCOPE_WORKGROUP);
-            old = __builtin_amdgcn_readfirstlane(old);
-            if ((int)old + 1 == u1 - u0) {
-                if (lane < 32) {
-                    f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
-                    for (int uu = u0; uu < u1; ++uu)
-                        sum += *(const f32x4_t*)(part + (uu - a) * 128 + n * 8 + q * 4);
-                    *(f32x4_t*)(part + (u0 - a) * 128 + n * 8 + q * 4) = sum;
-                }
-                if (lane == 0)
-                    __hip_atomic_store(tcnt + (t - ta), kTileDone, __ATOMIC_RELEASE,
-                                       __HIP_MEMORY_SCOPE_WORKGROUP);
-            }
-            }
+            if (g < L) process(i, g);
             gn = __builtin_amdgcn_readfirstlane(gn);
             __builtin_amdgcn_sched_barrier(0);
             issue(i, (int)gn);
             __builtin_amdgcn_sched_barrier(0);
         }
+    }
     }
 }
 
