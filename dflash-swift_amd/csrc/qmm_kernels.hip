@@ -143,6 +143,31 @@ __device__ __forceinline__ void permlane32_swap(uint32_t& a, uint32_t& b) {
     __asm__ volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 4" : "+v"(a), "+v"(b));
 }
 
+/* Scales and biases arrive in one load: lane rows 0 and 2 (lane groups q = 0, 2) hold the
+ * scale words, rows 1 and 3 the bias words of the same lane positions.  v_permlane16_swap of
+ * the loaded value with a copy of itself exchanges the odd rows of the first with the even
+ * rows of the second, leaving scales in every row of one and biases in every row of the
+ * other.  All swaps share one wait-state pad on each side. */
+__device__ __forceinline__ void split_scale_bias(uint32_t w, uint32_t& sw, uint32_t& bw) {
+    sw = w;
+    bw = w;
+    __asm__ volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 4" : "+v"(sw), "+v"(bw));
+}
+__device__ __forceinline__ void split_scale_bias(u32x4_t w, u32x4_t& sv, u32x4_t& bv) {
+    uint32_t s0 = w[0], s1 = w[1], s2 = w[2], s3 = w[3];
+    uint32_t b0 = w[0], b1 = w[1], b2 = w[2], b3 = w[3];
+    __asm__ volatile(
+        "s_nop 1\n\t"
+        "v_permlane16_swap_b32 %0, %4\n\t"
+        "v_permlane16_swap_b32 %1, %5\n\t"
+        "v_permlane16_swap_b32 %2, %6\n\t"
+        "v_permlane16_swap_b32 %3, %7\n\t"
+        "s_nop 4"
+        : "+v"(s0), "+v"(s1), "+v"(s2), "+v"(s3), "+v"(b0), "+v"(b1), "+v"(b2), "+v"(b3));
+    sv = u32x4_t{s0, s1, s2, s3};
+    bv = u32x4_t{b0, b1, b2, b3};
+}
+
 /* Rearrange the raw words of one super-step (R[step][word], word j of lane group q covering
  * k chunk 4q+j (4-bit) / 2q+j/2 (8-bit)) so that lanes 0-31 of every operand hold one
  * quantisation group and lanes 32-63 another. */
@@ -547,7 +572,7 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     const uint32_t lane_s = (CH > 1) ? 0u : (C::GPS == 4 ? 4u * (q >> 1) : 0u);
     using SV = typename std::conditional<(CH > 1), u32x4_t, uint32_t>::type;
     u32x4_t rw[PF][CH][C::NS];
-    SV rs[PF], rb[PF];
+    SV rsb[PF];  // scale words (lane rows 0, 2) or bias words (rows 1, 3) of the slot's unit
     int sg[PF];  // the unit (as a take index) each slot holds; >= L: none
     const uint8_t* wbytes = (const uint8_t*)p.w;
     const uint8_t* sbytes = (const uint8_t*)p.scales;
@@ -563,16 +588,17 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
         const int rl = (row0 + 16 <= p.N) ? n : min(n, p.N - 1 - row0);
         const uint32_t vw = (uint32_t)rl * RB + lane_w;
         const uint32_t vs = (uint32_t)rl * GPR * 2u + lane_s;
+        const uint8_t* sbb = (q & 1) ? bbytes : sbytes;
         const int kc = k0 + c * (CH * C::KSS);  // first k of the chunk
         const uint8_t* wb = wbytes + (size_t)row0 * RB + kc * BITS / 8;
         const size_t so = ((size_t)row0 * GPR + kc / GS) * 2;
+        /* scales / biases first: they are split (a cross-lane swap) before the first MFMA */
+        rsb[slot] = *(const SV*)(sbb + so + vs);
 #pragma unroll
         for (int j = 0; j < CH; ++j)
 #pragma unroll
             for (int s = 0; s < C::NS; ++s)
                 rw[slot][j][s] = *(const u32x4_t*)(wb + vw + (j * C::NS + s) * 64);
-        rs[slot] = *(const SV*)(sbytes + so + vs);
-        rb[slot] = *(const SV*)(bbytes + so + vs);
     };
     /* the loads go out in slot order, here and in the loop, so the queue the loop waits
      * on has the same layout on entry as on every back edge */
@@ -637,6 +663,8 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     auto process = [&](const int i, const int g) {
         const int u = unit_of(g);
         const int t = u / SS, cc = u - t * SS;
+        SV rs_i, rb_i;
+        split_scale_bias(rsb[i], rs_i, rb_i);
         f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int j = 0; j < CH; ++j) {
@@ -661,17 +689,17 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
                 uint32_t sw, bw2, sel;
                 if constexpr (CH > 1) {
                     if constexpr (C::GPS == 4) {
-                        sw = (q >> 1) ? rs[i][2 * j + 1] : rs[i][2 * j];
-                        bw2 = (q >> 1) ? rb[i][2 * j + 1] : rb[i][2 * j];
+                        sw = (q >> 1) ? rs_i[2 * j + 1] : rs_i[2 * j];
+                        bw2 = (q >> 1) ? rb_i[2 * j + 1] : rb_i[2 * j];
                         sel = pp ? kSelHi : kSelLo;
                     } else {
-                        sw = rs[i][j];
-                        bw2 = rb[i][j];
+                        sw = rs_i[j];
+                        bw2 = rb_i[j];
                         sel = sel_half;
                     }
                 } else {
-                    sw = rs[i];
-                    bw2 = rb[i];
+                    sw = rs_i;
+                    bw2 = rb_i;
                     sel = (C::GPS == 4) ? (pp ? kSelHi : kSelLo) : sel_half;
                 }
                 const float s = half_sel<F16>(sw, sel);
