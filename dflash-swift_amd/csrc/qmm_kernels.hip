@@ -541,13 +541,27 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     const int CPR = p.kr / 8;  // 16-byte chunks per row of the k-block
     const int items = p.M * CPR;
     const uint16_t* xg = (const uint16_t*)p.x;
+    /* (row, chunk) of item tid + i * kThreads, stepped without a per-item division */
+    const int dr = kThreads / CPR, dcc = kThreads - dr * CPR;  // wave-uniform
+    int xr[kMaxStageItems], xc[kMaxStageItems];
     u32x4_t xv[kMaxStageItems];
+    {
+        int r = tid / CPR, cc = tid - r * CPR;
 #pragma unroll
-    for (int i = 0; i < kMaxStageItems; ++i) {
-        if (i * kThreads < items) {
-            const int c = min(tid + i * kThreads, items - 1);
-            const int r = c / CPR, cc = c - r * CPR;
-            xv[i] = *(const u32x4_t*)(xg + (size_t)r * p.K + k0 + cc * 8);
+        for (int i = 0; i < kMaxStageItems; ++i) {
+            xr[i] = r;
+            xc[i] = cc;
+            if (i * kThreads < items) {
+                const bool in = r < p.M;
+                const int rr = in ? r : p.M - 1, c2 = in ? cc : CPR - 1;
+                xv[i] = *(const u32x4_t*)(xg + (size_t)rr * p.K + k0 + c2 * 8);
+            }
+            r += dr;
+            cc += dcc;
+            if (cc >= CPR) {
+                cc -= CPR;
+                ++r;
+            }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -623,9 +637,8 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
 #pragma unroll
     for (int i = 0; i < kMaxStageItems; ++i) {
         if (i * kThreads < items) {
-            const int c = tid + i * kThreads;
-            const bool act = c < items;
-            const int r = c / CPR, cc = c - r * CPR;
+            const int r = xr[i], cc = xc[i];
+            const bool act = r < p.M;
             float sm = act ? chunk_dot<F16>(xv[i], 0.0f) : 0.0f;
             sm += dpp_f32<0xB1>(sm);             // lanes ^1 (quad_perm 1,0,3,2)
             sm += dpp_f32<0x4E>(sm);             // lanes ^2 (quad_perm 2,3,0,1)
