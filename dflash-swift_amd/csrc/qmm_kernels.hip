@@ -614,13 +614,6 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
             for (int s = 0; s < C::NS; ++s)
                 rw[slot][j][s] = *(const u32x4_t*)(wb + vw + (j * C::NS + s) * 64);
     };
-    /* the loads go out in slot order, here and in the loop, so the queue the loop waits
-     * on has the same layout on entry as on every back edge */
-#pragma unroll
-    for (int i = 0; i < PF; ++i) {
-        issue(i, wave * PF + i);
-        __builtin_amdgcn_sched_barrier(0);
-    }
 
     /* ---- LDS layout: row 0 zeros, rows 1..M x; per-group x sums; per-unit partial tiles
      * ([n][8] fp32, 512 bytes each); tile arrival counters; the take counter */
@@ -656,6 +649,12 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
         if ((i & 7) >= p.M) xsum[i] = 0.0f;
     for (int i = tid; i < ntl; i += kThreads) tcnt[i] = 0u;
     if (tid == 0) *gcnt = (uint32_t)(kWaves * PF);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+        issue(i, wave * PF + i);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     __syncthreads();
 
     /* ---- per-lane A / x-sum addresses */
