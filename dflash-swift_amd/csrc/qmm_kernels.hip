@@ -37,11 +37,11 @@
  * x (M rows of the k-block) is staged once per workgroup in LDS, pre-permuted into the MFMA
  * k order, with the per-group sums sum_{k in g} x[m,k] next to it.  Weights, scales and
  * biases stream straight from HBM into VGPRs through global loads (a scalar base plus a
- * 32-bit lane offset) with a software prefetch ring over work chunks.
+ * 32-bit lane offset), one work unit in flight per wave at 4-bit g64.
  *
- * Work decomposition: see qmm_params.h.  One 512-thread workgroup per CU (the LDS request
- * keeps two from sharing a CU); units of (16-column tile, super-step) are split evenly over
- * workgroups and waves, so every SIMD streams the same number of bytes.
+ * Work decomposition: see qmm_params.h.  One workgroup per CU (the LDS request keeps two
+ * from sharing a CU) of 12 streaming waves, which take units of (16-column tile, chunk) from
+ * an LDS counter, and one publisher wave, which writes finished tiles.
  *
  * Generic path (qmm_generic): the stock-op stand-in -- one wave per output element, plain
  * per-element dequantisation, W re-read for every row.  It exists so that the drop-in layer
@@ -339,8 +339,7 @@ __device__ __forceinline__ u32x4_t nibble_permute(u32x4_t v) {
 
 /* The split of the U units of a k-block over G workgroups: workgroup c owns
  * [c*base + min(c, rem), +base + (c < rem)), with base = U / G and rem = U % G computed on
- * the host.  Within a workgroup, wave w owns [w*lb + min(w, lr), +lb + (w < lr)) of its L
- * units, lb = L / kWaves, lr = L % kWaves. */
+ * the host. */
 __device__ __forceinline__ int wg_start(int c, int base, int rem) {
     return c * base + (c < rem ? c : rem);
 }

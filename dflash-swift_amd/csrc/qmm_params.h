@@ -22,10 +22,11 @@
  *    with the next workgroup and continues with the one shared with the previous, so that
  *    cross-workgroup fix-ups happen early;
  *  - every unit's partial tile goes to its own LDS slot; the wave that completes a tile's
- *    units in this workgroup (an LDS arrival counter) sums the slots in unit order and writes
- *    y, or, for a tile shared with other workgroups (or k-blocks), hands the sum to the
- *    workspace fix-up: one 64-bit atomic exchange per element when exactly two parts exist,
- *    else per-part slots summed in a fixed order by whichever part arrives last.
+ *    units in this workgroup (an LDS arrival counter) sums the slots in unit order and marks
+ *    the tile done; the workgroup's publisher wave then writes y, or, for a tile shared with
+ *    other workgroups (or k-blocks), does the workspace fix-up: one 64-bit atomic exchange
+ *    per element when exactly two parts exist, else per-part slots summed in a fixed order
+ *    by whichever part arrives last.
  */
 typedef struct QmmParams {
     const void* x;          /* [M][K] activations, bf16 or fp16                      */
