@@ -15,13 +15,13 @@ struct Plan {
     int kss = 0;        /* k per super-step                                  */
     int T = 0;          /* column tiles of 16                                */
     int ch = 0;         /* super-steps per chunk (1, or 8 groups' worth)     */
-    int SS = 0;         /* chunks per tile per k-block                       */
-    int nkb = 0;        /* k-blocks                                          */
+    int chunks = 0;     /* chunks of K                                       */
+    int SS = 0;         /* chunks in the largest k-block                     */
+    int nkb = 0;        /* k-blocks (sizes differ by at most one chunk)      */
     int Gkb = 0;        /* workgroups per k-block                            */
-    int wg_base = 0;    /* units per workgroup, rounded down                 */
-    int wg_rem = 0;     /* workgroups holding one extra unit                 */
     int nslot_kb = 0;   /* partial slots per tile per k-block                */
-    int kr = 0;         /* k elements per k-block                            */
+    int kr = 0;         /* k elements in the largest k-block                 */
+    bool reduce = false; /* shared tiles summed by the second kernel         */
     int rs = 0;         /* LDS bytes per staged x row                        */
     int xsum_off = 0;   /* LDS offset of the per-group x sums                */
     int part_off = 0;   /* LDS offset of the per-unit partial tiles          */

@@ -350,6 +350,24 @@ __device__ __forceinline__ int owner_wg(int u, int base, int rem) {
     return u < big ? u / (base + 1) : rem + (u - big) / base;
 }
 
+/* k-block kb holds chunks [c0, c0 + SS) of K (the chunks spread over the k-blocks with
+ * sizes differing by at most one); its T*SS units go to the Gkb workgroups as above. */
+struct KBlock {
+    int c0, SS, base, rem;
+};
+__device__ __forceinline__ KBlock kblock(const QmmParams& p, int kb) {
+    const int c0 = kb * p.chunks / p.nkb, c1 = (kb + 1) * p.chunks / p.nkb;
+    const int SS = c1 - c0, U = p.T * SS;
+    return KBlock{c0, SS, U / p.Gkb, U % p.Gkb};
+}
+
+/* Partial-tile slot j of k-block kb for tile t in the workspace: [T][nkb][nslot_kb][128]
+ * fp32, lane (q, n) of lanes 0-31 owning floats n*8 + q*4 .. +3. */
+__device__ __forceinline__ float* tile_slot(const QmmParams& p, int t, int kb, int j, int lane) {
+    return p.slots + ((size_t)(t * p.nkb + kb) * p.nslot_kb + j) * 128 + (lane & 15) * 8 +
+           (lane >> 4) * 4;
+}
+
 /* One partial tile (8 rows x 16 columns, fp32) as held by lanes 0-31: lane (q, n) holds
  * rows 4q..4q+3 of column n.  Layout in LDS / workspace slots: [n][8]. */
 struct Tile {
@@ -389,11 +407,10 @@ __device__ __forceinline__ void store_y(const QmmParams& p, int t, int lane, f32
  * in the counter scheme the slot stores are waited for before the counter increment, and
  * the last contributor only reads slots after its own increment has returned. */
 template <bool F16>
-__device__ void publish(const QmmParams& p, int t, int slot, int lane, f32x4_t v) {
+__device__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t, int slot,
+                        int lane, f32x4_t v) {
     const int q = lane >> 4, n = lane & 15;
-    const int SS = p.SS;
-    const int nwg = owner_wg(t * SS + SS - 1, p.wg_base, p.wg_rem) -
-                    owner_wg(t * SS, p.wg_base, p.wg_rem) + 1;
+    const int nwg = owner_wg(t * SS + SS - 1, base_u, rem_u) - owner_wg(t * SS, base_u, rem_u) + 1;
     const uint32_t total = (uint32_t)(p.nkb * nwg);
     uint32_t* base = (uint32_t*)p.slots + (size_t)t * p.nkb * p.nslot_kb * 128;
     if (total == 2) {
@@ -459,8 +476,8 @@ __device__ void publish(const QmmParams& p, int t, int slot, int lane, f32x4_t v
  * polls) until each of the ntl tiles has been written.  Every unit of [a, b) is taken by
  * exactly one streaming wave, so every tile reaches kTileDone and the loop ends. */
 template <bool F16>
-__device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b, int lane) {
-    const int SS = p.SS;
+__device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b, int SS,
+                               int base_u, int rem_u, int lane) {
     const int q = lane >> 4, n = lane & 15;
     const int ta = a / SS;
     const int ntl = (b > a) ? (b - 1) / SS - ta + 1 : 0;
@@ -484,11 +501,15 @@ __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
                 const int u0 = max(a, t * SS), u1 = min(b, (t + 1) * SS);
                 f32x4_t v = {0.0f, 0.0f, 0.0f, 0.0f};
                 if (lane < 32) v = *(const f32x4_t*)(part + (u0 - a) * 128 + n * 8 + q * 4);
+                const int first = owner_wg(t * SS, base_u, rem_u);
                 if (u0 == t * SS && u1 == (t + 1) * SS && p.nkb == 1) {
                     store_y<F16>(p, t, lane, v);
+                } else if (p.reduce) {
+                    /* summed by dfq_qmm_reduce after this kernel: no round trip here */
+                    if (lane < 32) *(f32x4_t*)tile_slot(p, t, kb, cl - first, lane) = v;
                 } else {
-                    const int first = owner_wg(t * SS, p.wg_base, p.wg_rem);
-                    publish<F16>(p, t, kb * p.nslot_kb + (cl - first), lane, v);
+                    publish<F16>(p, SS, base_u, rem_u, t, kb * p.nslot_kb + (cl - first), lane,
+                                 v);
                 }
                 if (lane == 0) tcnt[base + bit] = kTileOut;
                 ++found;
@@ -520,24 +541,26 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
 
     const int kb = blockIdx.x / p.Gkb;
     const int cl = blockIdx.x - kb * p.Gkb;
-    const int SS = p.SS;      // chunks per tile per k-block
-    const int a = wg_start(cl, p.wg_base, p.wg_rem);
-    const int b = wg_start(cl + 1, p.wg_base, p.wg_rem);
+    const KBlock kbk = kblock(p, kb);
+    const int SS = kbk.SS;    // chunks per tile in this k-block
+    const int a = wg_start(cl, kbk.base, kbk.rem);
+    const int b = wg_start(cl + 1, kbk.base, kbk.rem);
 
     if (wave == kWaves) {
-        publisher_wave<F16>(p, kb, cl, a, b, lane);
+        publisher_wave<F16>(p, kb, cl, a, b, SS, kbk.base, kbk.rem, lane);
         return;
     }
 
     const int RB = p.K * BITS / 8;        // bytes per weight row
     const int GPR = p.K / GS;             // groups per row
-    const int k0 = kb * p.kr;             // first k of this k-block
+    const int kr = SS * (CH * C::KSS);    // k elements in this k-block
+    const int k0 = kbk.c0 * (CH * C::KSS);  // first k of this k-block
 
     /* ---- x staging loads go out first (their wait must not cover the weight prefetch).
      * Item c (16 bytes, 8 elements) of the M x kr block goes to thread c % kThreads, so each
      * load instruction reads 1 KB of consecutive x; rounds past the last item are skipped
      * and lanes past it reload the last one. */
-    const int CPR = p.kr / 8;  // 16-byte chunks per row of the k-block
+    const int CPR = kr / 8;  // 16-byte chunks per row of the k-block
     const int items = p.M * CPR;
     const uint16_t* xg = (const uint16_t*)p.x;
     /* (row, chunk) of item tid + i * kThreads, stepped without a per-item division */
@@ -591,7 +614,10 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     const uint8_t* sbytes = (const uint8_t*)p.scales;
     const uint8_t* bbytes = (const uint8_t*)p.biases;
 
-    int lu = a;  // last unit fetched (a wave that gets none fetches unit a, never used)
+    /* last unit fetched.  A wave that gets no unit still fetches one, never used: the first
+     * unit of the range, or the k-block's last unit for an empty range (which can sit past
+     * the last unit when a small k-block has fewer units than workgroups). */
+    int lu = min(a, p.T * SS - 1);
     auto issue = [&](int slot, int g) {
         sg[slot] = g;
         const int u = g < L ? unit_of(g) : lu;
@@ -623,7 +649,7 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     const int ta = a / SS;               // first tile touched by this workgroup
     const int ntl = tlast - ta + 1;      // tiles touched
     uint32_t* gcnt = tcnt + ntl;
-    const int GK = p.kr / GS;  // groups in the k-block
+    const int GK = kr / GS;  // groups in the k-block
     /* per item: pre-permute into the MFMA k order, and sum its 8 elements; the GS/8 items
      * of a group sit in aligned neighbouring lanes and are summed with DPP */
 #pragma unroll
@@ -848,6 +874,38 @@ extern "C" __global__ void __launch_bounds__(256) dfq_fill_u32(uint32_t* ptr, ui
     for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < count;
          i += (uint64_t)gridDim.x * 256)
         ptr[i] = v;
+}
+
+/* The second pass of a split whose tiles can have more than two contributors (several
+ * k-blocks, or tiles spread over three or more workgroups): one wave per 16-column tile sums
+ * the tile's partial slots in (k-block, workgroup) order -- a fixed order, so the result does
+ * not depend on timing -- adds the linear bias, writes y and zeroes the slots, which leaves
+ * the workspace zero at rest.  Tiles with one contributor were written by qmm_mt8. */
+template <bool F16>
+__device__ __forceinline__ void qmm_reduce(const QmmParams& p) {
+    const int t = blockIdx.x, lane = threadIdx.x;
+    f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
+    int parts = 0;
+    for (int kb = 0; kb < p.nkb; ++kb) {
+        const KBlock k = kblock(p, kb);
+        const int first = owner_wg(t * k.SS, k.base, k.rem);
+        const int nwg = owner_wg(t * k.SS + k.SS - 1, k.base, k.rem) - first + 1;
+        for (int j = 0; j < nwg; ++j, ++parts) {
+            if (lane < 32) {
+                f32x4_t* sl = (f32x4_t*)tile_slot(p, t, kb, j, lane);
+                sum += *sl;
+                *sl = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+        }
+    }
+    if (parts > 1) store_y<F16>(p, t, lane, sum);
+}
+
+extern "C" __global__ void __launch_bounds__(64) dfq_qmm_reduce_bf16(QmmParams p) {
+    qmm_reduce<false>(p);
+}
+extern "C" __global__ void __launch_bounds__(64) dfq_qmm_reduce_f16(QmmParams p) {
+    qmm_reduce<true>(p);
 }
 
 /* Chunks in flight per wave: enough to keep DFQ_PF_LOADS weight loads per lane

@@ -11,12 +11,13 @@
 /* Work decomposition of the fast kernel (a "stream-K" split with a deterministic fix-up):
  *
  *  - output features are cut into T column tiles of 16 (the MFMA N dimension);
- *  - K is cut into nkb k-blocks of kr elements (kr * rows of x must fit in LDS), and each
- *    k-block into SS chunks of CH super-steps (one super-step = the k span that holds
- *    exactly two quantisation groups per lane half, 64..256 elements; a chunk is one
- *    super-step or the 8 groups whose scales one 16-byte load fetches);
- *  - the U = T*SS units (tile, chunk) of one k-block are split into Gkb contiguous ranges
- *    whose sizes differ by at most one (the first U % Gkb get one more);
+ *  - K is cut into chunks of CH super-steps (one super-step = the k span that holds exactly
+ *    two quantisation groups per lane half, 64..256 elements; a chunk is one super-step or
+ *    the 8 groups whose scales one 16-byte load fetches), and the chunks into nkb k-blocks
+ *    whose sizes differ by at most one (k-block kb holds chunks [kb*chunks/nkb,
+ *    (kb+1)*chunks/nkb); its x slice must fit in LDS);
+ *  - the U = T*SS units (tile, chunk) of a k-block of SS chunks are split into Gkb
+ *    contiguous ranges whose sizes differ by at most one (the first U % Gkb get one more);
  *  - inside a workgroup the waves take units of its range one at a time from a counter in
  *    LDS (the first ones by wave index), in a rotated order that starts with the tile shared
  *    with the next workgroup and continues with the one shared with the previous, so that
@@ -24,9 +25,10 @@
  *  - every unit's partial tile goes to its own LDS slot; the wave that completes a tile's
  *    units in this workgroup (an LDS arrival counter) sums the slots in unit order and marks
  *    the tile done; the workgroup's publisher wave then writes y, or, for a tile shared with
- *    other workgroups (or k-blocks), does the workspace fix-up: one 64-bit atomic exchange
- *    per element when exactly two parts exist, else per-part slots summed in a fixed order
- *    by whichever part arrives last.
+ *    other workgroups (or k-blocks), its part: with at most two parts per tile anywhere in
+ *    the split, one 64-bit atomic exchange per element (the second arriver writes y);
+ *    otherwise ("reduce" splits) a plain store into the tile's workspace slot, and a second
+ *    kernel sums every tile's slots in a fixed order.
  */
 typedef struct QmmParams {
     const void* x;          /* [M][K] activations, bf16 or fp16                      */
@@ -39,18 +41,16 @@ typedef struct QmmParams {
     uint32_t* counters;     /* workspace: per-tile arrival counters (zero at rest)    */
     int32_t M, N, K;
     int32_t T;              /* column tiles of 16                                     */
-    int32_t SS;             /* chunks per tile per k-block                            */
+    int32_t chunks;         /* chunks of K                                            */
     int32_t nkb;            /* k-blocks                                               */
     int32_t Gkb;            /* workgroups per k-block                                 */
     int32_t nslot_kb;       /* partial slots per tile per k-block                     */
-    int32_t kr;             /* k elements per k-block                                 */
+    int32_t reduce;         /* 1: shared tiles go to slots summed by dfq_qmm_reduce   */
     int32_t lds_row_stride; /* bytes per staged x row in LDS                          */
     int32_t lds_xsum_off;   /* byte offset of the per-group x sums in LDS             */
     int32_t lds_part_off;   /* byte offset of the per-unit partial tiles in LDS       */
     int32_t lds_cnt_off;    /* byte offset of the per-tile arrival counters in LDS    */
     int32_t umax;           /* most units one workgroup holds (partial slots sized)  */
-    int32_t wg_base;        /* units per workgroup, rounded down (U / Gkb)            */
-    int32_t wg_rem;         /* workgroups with one extra unit (U % Gkb)               */
     uint32_t w_bytes;       /* size of w in bytes (< 2^31)                            */
     uint32_t s_bytes;       /* size of scales (= size of biases) in bytes             */
 } QmmParams;

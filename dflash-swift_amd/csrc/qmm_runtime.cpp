@@ -78,6 +78,7 @@ struct dfq_ctx {
     size_t lds_max = 0;
     hipModule_t module = nullptr;
     hipFunction_t mt8[2][3][2][2] = {};  // [bits 4/8][gs 32/64/128][bf16/f16][chunk 1/8 groups]
+    hipFunction_t reduce[2] = {};        // second pass of reduce splits [bf16/f16]
     hipFunction_t generic = nullptr;
     hipFunction_t fill = nullptr;
     std::mutex mu;
@@ -132,6 +133,13 @@ static int64_t owner_wg(int64_t u, int64_t base, int64_t rem) {
     return u < big ? u / (base + 1) : rem + (u - big) / base;
 }
 
+/* Workgroups of k-block range [a, b) that share tile t's units, for a k-block of SS chunks
+ * split over G workgroups. */
+static int tile_owners(int64_t t, int64_t SS, int64_t G, int64_t T) {
+    const int64_t U = T * SS, base = U / G, rem = U % G;
+    return (int)(owner_wg(t * SS + SS - 1, base, rem) - owner_wg(t * SS, base, rem) + 1);
+}
+
 bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_max, Plan* pl) {
     const int kss = kss_for(bits, gs);
     if (M < 1 || M > 8 || N < 1 || K < kss || K % kss) return false;
@@ -141,19 +149,21 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
     const int kch = kss * ch;
     const int chunks = K / kch;
     const int T = (N + 15) / 16;
-    /* Fewest k-blocks (at least DFQ_MIN_KBLOCKS) whose x slice, plus the per-unit partial
-     * slots of the split, fits in LDS. */
+    /* Fewest k-blocks (at least DFQ_MIN_KBLOCKS) whose largest x slice, plus the per-unit
+     * partial slots of the split, fits in LDS.  The chunks spread over the k-blocks with
+     * sizes differing by at most one. */
     for (int d = std::min(DFQ_MIN_KBLOCKS, chunks); d <= chunks; ++d) {
-        if (chunks % d) continue;
-        const int kr = K / d;
+        const int ss_max = (chunks + d - 1) / d, ss_min = chunks / d;
+        const int kr = ss_max * kch;
         if ((int64_t)M * (kr / 8) > (int64_t)kMaxStageItems * kThreads) continue;
         Plan p{};
         p.kss = kss;
         p.ch = ch;
         p.T = T;
+        p.chunks = chunks;
         p.nkb = d;
         p.kr = kr;
-        p.SS = chunks / d;
+        p.SS = ss_max;
         p.rs = 2 * kr + 16;
         p.xsum_off = ((M + 1) * p.rs + 15) & ~15;
         p.part_off = p.xsum_off + (kr / gs) * 32;
@@ -162,25 +172,23 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
          * slots would not fit */
         if ((size_t)p.part_off + 512 + 256 > lds_max) continue;
         const int64_t cap = (int64_t)(lds_max - p.part_off - 256) / 516;
-        const int64_t U = (int64_t)T * p.SS;
+        const int64_t U = (int64_t)T * ss_max;
         int64_t G = std::max(1, num_cus / d);
         G = std::max<int64_t>(G, (U + cap - 1) / cap);
         if (G > U) G = U;
         p.Gkb = (int)G;
-        p.wg_base = (int)(U / G);
-        p.wg_rem = (int)(U % G);
-        p.umax = p.wg_base + (p.wg_rem ? 1 : 0);
+        p.umax = (int)(U / G + ((U % G) ? 1 : 0));
         p.cnt_off = p.part_off + p.umax * 512;
-        const int ntl_max = (p.umax + p.SS - 1) / p.SS + 1;  // tiles a range can touch
+        const int ntl_max = (p.umax + ss_min - 1) / ss_min + 1;  // tiles a range can touch
         const size_t need = (size_t)p.cnt_off + (size_t)(ntl_max + 1) * 4;
         if (need > lds_max) continue;
         int nslot = 1;
-        for (int64_t t = 0; t < T; ++t) {
-            const int64_t c0 = owner_wg(t * p.SS, p.wg_base, p.wg_rem);
-            const int64_t c1 = owner_wg(t * p.SS + p.SS - 1, p.wg_base, p.wg_rem);
-            nslot = std::max<int>(nslot, (int)(c1 - c0 + 1));
-        }
+        for (int ss : {ss_min, ss_max})
+            for (int64_t t = 0; t < T; ++t) nslot = std::max(nslot, tile_owners(t, ss, G, T));
         p.nslot_kb = nslot;
+        /* At most two parts per tile: the pair exchange inside the kernel.  More: plain slot
+         * stores and the fixed-order second kernel. */
+        p.reduce = d > 1 ? (d > 2 || nslot > 1) : nslot > 2;
         /* Ask for more than half the CU's LDS so that exactly one workgroup lands per CU. */
         const size_t want = std::max(need, lds_max / 2 + 256);
         p.lds_bytes = (int)std::min(want, lds_max);
@@ -295,6 +303,8 @@ dfq_status dfq_init(int device, dfq_ctx** out) {
                     }
                 }
     if ((e = hipModuleGetFunction(&ctx->generic, ctx->module, "dfq_qmm_generic")) != hipSuccess ||
+        (e = hipModuleGetFunction(&ctx->reduce[0], ctx->module, "dfq_qmm_reduce_bf16")) != hipSuccess ||
+        (e = hipModuleGetFunction(&ctx->reduce[1], ctx->module, "dfq_qmm_reduce_f16")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->fill, ctx->module, "dfq_fill_u32")) != hipSuccess) {
         (void)hipModuleUnload(ctx->module);
         delete ctx;
@@ -461,18 +471,16 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
     p.N = N;
     p.K = K;
     p.T = pl.T;
-    p.SS = pl.SS;
+    p.chunks = pl.chunks;
     p.nkb = pl.nkb;
     p.Gkb = pl.Gkb;
     p.nslot_kb = pl.nslot_kb;
-    p.kr = pl.kr;
+    p.reduce = pl.reduce ? 1 : 0;
     p.lds_row_stride = pl.rs;
     p.lds_xsum_off = pl.xsum_off;
     p.lds_part_off = pl.part_off;
     p.lds_cnt_off = pl.cnt_off;
     p.umax = pl.umax;
-    p.wg_base = pl.wg_base;
-    p.wg_rem = pl.wg_rem;
     p.w_bytes = (uint32_t)((int64_t)N * K * bits / 8);
     p.s_bytes = (uint32_t)((int64_t)N * (K / gs) * 2);
     const int bi = bits == 4 ? 0 : 1;
@@ -483,7 +491,13 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
     hipError_t e = hipModuleLaunchKernel(ctx->mt8[bi][gi][di][ci], (unsigned)(pl.nkb * pl.Gkb), 1, 1,
                                          kBlockThreads, 1, 1, (unsigned)pl.lds_bytes, stream, args,
                                          nullptr);
-    return e == hipSuccess ? DFQ_OK : hip_fail(e, "launch dfq_qmm_mt8");
+    if (e != hipSuccess) return hip_fail(e, "launch dfq_qmm_mt8");
+    if (pl.reduce) {
+        e = hipModuleLaunchKernel(ctx->reduce[di], (unsigned)pl.T, 1, 1, 64, 1, 1, 0, stream, args,
+                                  nullptr);
+        if (e != hipSuccess) return hip_fail(e, "launch dfq_qmm_reduce");
+    }
+    return DFQ_OK;
 }
 
 dfq_status dfq_qmm(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
@@ -603,28 +617,28 @@ dfq_status dfq_graph_destroy(dfq_graph* gr) {
 /* ---- introspection used by tests and the benchmark (not part of the drop-in surface) -- */
 
 /* Fills the work split the fast kernel uses for a shape: {T, SS, nkb, Gkb, nslot_kb, kr,
- * lds_bytes, need_ws, ch, umax}. */
-dfq_status dfq_debug_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, int* out10) {
-    if (!out10) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
+ * lds_bytes, need_ws, ch, umax, chunks, reduce} (SS and kr of the largest k-block). */
+dfq_status dfq_debug_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, int* out12) {
+    if (!out12) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
     Plan p;
     dfq_status s = get_plan(ctx, M, N, K, bits, gs, &p);
     if (s) return s;
-    int v[10] = {p.T,  p.SS,        p.nkb,          p.Gkb, p.nslot_kb,
-                 p.kr, p.lds_bytes, p.need_ws ? 1 : 0, p.ch, p.umax};
-    std::memcpy(out10, v, sizeof v);
+    const int v[12] = {p.T,  p.SS,        p.nkb,            p.Gkb, p.nslot_kb, p.kr,
+                       p.lds_bytes, p.need_ws ? 1 : 0, p.ch, p.umax, p.chunks, p.reduce ? 1 : 0};
+    std::memcpy(out12, v, sizeof v);
     return DFQ_OK;
 }
 
 /* The same split computed without a device, for a given CU count and LDS limit. */
 dfq_status dfq_debug_make_plan(int M, int N, int K, int bits, int gs, int num_cus,
-                               size_t lds_max, int* out10) {
-    if (!out10) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
+                               size_t lds_max, int* out12) {
+    if (!out12) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
     Plan p;
     if (!make_plan(M, N, K, bits, gs, num_cus, lds_max, &p))
         return fail(DFQ_ERR_UNSUPPORTED, "no work split");
-    int v[10] = {p.T,  p.SS,        p.nkb,          p.Gkb, p.nslot_kb,
-                 p.kr, p.lds_bytes, p.need_ws ? 1 : 0, p.ch, p.umax};
-    std::memcpy(out10, v, sizeof v);
+    const int v[12] = {p.T,  p.SS,        p.nkb,            p.Gkb, p.nslot_kb, p.kr,
+                       p.lds_bytes, p.need_ws ? 1 : 0, p.ch, p.umax, p.chunks, p.reduce ? 1 : 0};
+    std::memcpy(out12, v, sizeof v);
     return DFQ_OK;
 }
 

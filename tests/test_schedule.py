@@ -20,11 +20,12 @@ import dflash_qmm
 
 def make_plan(M, N, K, bits, gs, cus=256, lds=163840):
     lib = dflash_qmm.load_library()
-    out = (ctypes.c_int * 10)()
+    out = (ctypes.c_int * 12)()
     rc = lib.dfq_debug_make_plan(M, N, K, bits, gs, cus, lds, out)
     if rc:
         return None
-    keys = ["T", "SS", "nkb", "Gkb", "nslot_kb", "kr", "lds_bytes", "need_ws", "ch", "umax"]
+    keys = ["T", "SS", "nkb", "Gkb", "nslot_kb", "kr", "lds_bytes", "need_ws", "ch", "umax",
+            "chunks", "reduce"]
     return dict(zip(keys, list(out)))
 
 
@@ -37,6 +38,14 @@ def owner_wg(u, base, rem):
     return u // (base + 1) if u < big else rem + (u - big) // base
 
 
+def kblock(p, kb):
+    """Chunks [c0, c0 + SS) of k-block kb and its workgroup split (the kernel's kblock)."""
+    c0 = kb * p["chunks"] // p["nkb"]
+    SS = (kb + 1) * p["chunks"] // p["nkb"] - c0
+    base, rem = divmod(p["T"] * SS, p["Gkb"])
+    return c0, SS, base, rem
+
+
 def take_order(a, b, SS):
     """Units of a workgroup range in the order its waves take them (the kernel's unit_of):
     the tile shared with the next workgroup first, then the rest from a."""
@@ -45,42 +54,54 @@ def take_order(a, b, SS):
 
 
 def replay(p):
-    T, SS, nkb, G, nslot = p["T"], p["SS"], p["nkb"], p["Gkb"], p["nslot_kb"]
-    U = T * SS
-    base, rem = divmod(U, G)
-    umax = base + (1 if rem else 0)
-    assert p["umax"] == umax
+    T, nkb, G, nslot = p["T"], p["nkb"], p["Gkb"], p["nslot_kb"]
+    chunks, umax = p["chunks"], p["umax"]
     seen = set()
     y_writes = {}
     ws_slots = {}
     arrivals = {}
+    parts_of = {}        # tile -> number of parts anywhere in the split
+
+    for kb in range(nkb):
+        c0, SS, base, rem = kblock(p, kb)
+        assert SS in (chunks // nkb, -(-chunks // nkb)) and SS <= p["SS"]
+        assert p["kr"] == p["SS"] * (p["kr"] // p["SS"])
+        assert base + (1 if rem else 0) <= umax
+        for t in range(T):
+            parts_of[t] = parts_of.get(t, 0) + (owner_wg(t * SS + SS - 1, base, rem)
+                                                - owner_wg(t * SS, base, rem) + 1)
+    max_parts = max(parts_of.values())
+    assert p["reduce"] == int(max_parts > 2), (max_parts, p["reduce"])
 
     def finalize(t, units):
         assert t not in y_writes, f"tile {t} written twice"
-        assert units == {(kb, t, s) for kb in range(nkb) for s in range(SS)}, f"tile {t} units"
+        assert units == {(kb, t, c) for kb in range(nkb) for c in range(kblock(p, kb)[1])}, t
         y_writes[t] = True
 
     def publish(t, kb, j, units):
-        assert 0 <= j < nkb * nslot, (t, j, nslot)
-        assert (t, j) not in ws_slots, f"slot {(t, j)} written twice"
-        ws_slots[(t, j)] = units
-        nwg = owner_wg(t * SS + SS - 1, base, rem) - owner_wg(t * SS, base, rem) + 1
+        """pair exchange (two parts) or a reduce slot; the tile is final once all parts are in"""
+        assert 0 <= j < nslot, (t, j, nslot)
+        assert (t, kb, j) not in ws_slots, f"slot {(t, kb, j)} written twice"
+        ws_slots[(t, kb, j)] = units
         arrivals[t] = arrivals.get(t, 0) + 1
-        if arrivals[t] == nkb * nwg:
+        if arrivals[t] == parts_of[t]:
             allu = set()
-            for kb2 in range(nkb):
-                for j2 in range(nwg):
-                    allu |= ws_slots[(t, kb2 * nslot + j2)]
+            for (t2, kb2, j2), uu in ws_slots.items():
+                if t2 == t:
+                    allu |= uu
             finalize(t, allu)
 
     for kb in range(nkb):
+        c0, SS, base, rem = kblock(p, kb)
         for cl in range(G):
             a, b = wg_start(cl, base, rem), wg_start(cl + 1, base, rem)
-            order = take_order(a, b, SS)
+            order = take_order(a, b, SS) if b > a else []
             assert sorted(order) == list(range(a, b))
+            if b <= a:
+                continue
             ta, tlast = a // SS, (b - 1) // SS
             ntl = tlast - ta + 1
-            assert ntl <= (umax + SS - 1) // SS + 1          # LDS counters sized for this
+            assert ntl <= (umax + (chunks // nkb) - 1) // (chunks // nkb) + 1  # LDS counters
             part = {}
             tcnt = [0] * ntl
             for u in order:                                   # any wave, one unit at a time
@@ -97,11 +118,10 @@ def replay(p):
                     if u0 == t * SS and u1 == (t + 1) * SS and nkb == 1:
                         finalize(t, units)
                     else:
-                        first = owner_wg(t * SS, base, rem)
-                        publish(t, kb, kb * nslot + (cl - first), units)
+                        publish(t, kb, cl - owner_wg(t * SS, base, rem), units)
             assert all(c == min(b, (t + 1) * SS) - max(a, t * SS)
                        for c, t in zip(tcnt, range(ta, tlast + 1)))
-    assert len(seen) == nkb * U
+    assert len(seen) == sum(T * kblock(p, kb)[1] for kb in range(nkb))
     assert sorted(y_writes) == list(range(T))
     need_ws = nkb > 1 or nslot > 1
     assert p["need_ws"] == int(need_ws)
@@ -136,12 +156,90 @@ def test_planner_respects_lds_and_staging_limits():
     for (M, N, K, bits, gs) in [(8, 5120, 17408, 4, 64), (1, 5120, 17408, 4, 64),
                                 (8, 64, 65536, 4, 128)]:
         p = make_plan(M, N, K, bits, gs)
-        assert M * p["kr"] // 8 <= 12 * 512
+        assert M * p["kr"] // 8 <= 8 * 12 * 64          # x items a workgroup stages
         assert p["lds_bytes"] <= 163840
-        assert K % p["kr"] == 0 and K // p["kr"] == p["nkb"]
+        assert p["SS"] == -(-p["chunks"] // p["nkb"]) and p["kr"] * p["chunks"] == K * p["SS"]
+
+
+def test_long_k_uses_few_uneven_k_blocks():
+    # K = 17408 at M = 8: 34 chunks of 512 k; three k-blocks of 11-12 chunks fit LDS
+    p = make_plan(8, 5120, 17408, 4, 64)
+    assert p["nkb"] == 3 and p["chunks"] == 34 and p["reduce"] == 1
 
 
 def test_planner_rejects_unsupported_shapes():
     assert make_plan(9, 64, 512, 4, 64) is None     # more than 8 rows per launch
     assert make_plan(8, 64, 500, 4, 64) is None     # K not a multiple of the super-step
     assert make_plan(8, 64, 192, 4, 128) is None
+
+
+WAVES = 12          # streaming waves per workgroup (DFQ_WAVES)
+PF_LOADS = 4        # 16-byte weight loads in flight per lane (DFQ_PF_LOADS)
+
+
+def fmt_consts(bits, gs, ch):
+    """Per-format constants of the kernel (Cfg): steps per super-step, k per super-step,
+    groups per super-step, and the prefetch depth for chunks of ch super-steps."""
+    kstep = 512 // bits
+    ns = (2 if gs == 128 else 1) if bits == 4 else gs // 32
+    kss = kstep * ns
+    gps = kss // gs
+    pf = max(1, min(8, PF_LOADS // (ch * ns)))
+    return ns, kss, gps, pf
+
+
+def fetched_units(a, b, SS, U, wave, pf):
+    """Every unit a wave may load (the kernel's issue): its initial take indices (the unused
+    fetch of a wave with none goes to the range's first unit, clamped to the k-block's last),
+    and any unit of the range a later take can return."""
+    L = b - a
+    s1 = max(a, ((b - 1) // SS) * SS) if L > 0 else a
+    nrot = b - s1
+
+    def unit_of(g):
+        return s1 + g if g < nrot else a + (g - nrot)
+
+    lu = min(a, U - 1)
+    out = []
+    for i in range(pf):
+        g = wave * pf + i
+        u = unit_of(g) if g < L else lu
+        lu = u
+        out.append(u)
+    return out + [unit_of(g) for g in range(L)]
+
+
+@pytest.mark.parametrize("shape", SHAPES + [(8, 1024, 5120, 4, 64), (8, 151936, 5120, 4, 64)])
+def test_prefetch_addresses_stay_in_bounds(shape):
+    M, N, K, bits, gs = shape
+    p = make_plan(*shape)
+    ns, kss, gps, pf = fmt_consts(bits, gs, p["ch"])
+    ch = p["ch"]
+    kch = kss * ch
+    RB = K * bits // 8                      # bytes per weight row
+    GPR = K // gs                           # groups per row
+    T, G = p["T"], p["Gkb"]
+    sv = 16 if ch > 1 else 4                # bytes of one scale/bias load per lane
+    for kb in range(p["nkb"]):
+        c0, SS, base, rem = kblock(p, kb)
+        U = T * SS
+        kr = SS * kch
+        k0 = c0 * kch
+        assert k0 + kr <= K and M * (kr // 8) <= WAVES * 64 * (96 // WAVES)
+        for cl in range(G):
+            a, b = wg_start(cl, base, rem), wg_start(cl + 1, base, rem)
+            units = set()
+            for wave in range(WAVES):
+                units.update(fetched_units(a, b, SS, U, wave, pf))
+            for u in units:
+                assert 0 <= u < U, (kb, cl, u, U)
+                t, c = divmod(u, SS)
+                row0 = t * 16
+                rmax = 15 if row0 + 16 <= N else N - 1 - row0     # the kernel's row clamp
+                assert 0 <= rmax <= 15
+                kc = k0 + c * kch
+                last_w = (row0 + rmax) * RB + kc * bits // 8 + 3 * 16 + (ch * ns - 1) * 64 + 16
+                assert last_w <= N * RB, (kb, cl, u)
+                lane_s = 0 if ch > 1 else (4 if gps == 4 else 0)
+                last_s = ((row0 + rmax) * GPR + kc // gs) * 2 + lane_s + sv
+                assert last_s <= N * GPR * 2, (kb, cl, u)
