@@ -97,6 +97,96 @@ def time_m(torch, ctx, stream, sets, M, steps, warmup, N, K, bits, gs, ws, wsb):
     return e0.elapsed_time(e1) * 1000.0 / steps
 
 
+# One verify-pass layer of the C5 chain (N, K): q, k, v, o, gate, up, down; then the lm_head.
+C5_LAYER = [(5120, 5120), (1024, 5120), (1024, 5120), (5120, 5120), (17408, 5120),
+            (17408, 5120), (5120, 17408)]
+C5_LM_HEAD = (151936, 5120)
+
+
+def chain_c5(torch, ctx, dev, layers=64, reps=5):
+    """The C5 verify forward at M=8: `layers` layers of seven 4-bit g64 matmuls, each layer
+    captured as one HIP graph, then the lm_head; distinct random weights per layer (about
+    11.6 GiB, so every layer streams from HBM).  Returns microseconds per forward."""
+    import dflash_qmm
+    M = 8
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+
+    def weights(N, K):
+        w = torch.randint(-(2 ** 31), 2 ** 31 - 1, (N, K // 8), dtype=torch.int32, device=dev,
+                          generator=g)
+        s = (torch.randn(N, K // 64, device=dev, generator=g) * 0.02).abs().to(torch.bfloat16)
+        b = (torch.randn(N, K // 64, device=dev, generator=g) * 0.01).to(torch.bfloat16)
+        return w, s, b
+
+    shapes = C5_LAYER + [C5_LM_HEAD]
+    wsb = max(ctx.workspace_bytes(M, N, K, 4, 64) for (N, K) in shapes)
+    ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
+    x = torch.randn(M, 5120, device=dev, generator=g).to(torch.bfloat16)
+    outs = [torch.empty(M, N, device=dev, dtype=torch.bfloat16) for (N, K) in C5_LAYER]
+    # inputs: q, k, v, gate, up read x (the layer input); o reads q; down reads gate
+    srcs = [None, None, None, 0, None, None, 4]
+    lm_out = torch.empty(M, C5_LM_HEAD[0], device=dev, dtype=torch.bfloat16)
+    stream = torch.cuda.Stream(device=dev)
+    B = dflash_qmm.BF16
+    graphs, lw = [], []
+    for li in range(layers):
+        wl = [weights(N, K) for (N, K) in C5_LAYER]
+        lw.append(wl)
+        layer_in = x if li == 0 else outs[6]
+        ctx.graph_begin(stream)
+        for j, (N, K) in enumerate(C5_LAYER):
+            inp = layer_in if srcs[j] is None else outs[srcs[j]]
+            w, s, b = wl[j]
+            ctx.qmm_raw(inp, w, s, b, outs[j], M, N, K, 4, 64, B, B, B, ws=ws,
+                        ws_bytes=ws.numel(), stream=stream)
+        graphs.append(ctx.graph_end(stream))
+    wlm, slm, blm = weights(*C5_LM_HEAD)
+
+    def forward():
+        for gr in graphs:
+            gr.launch(stream)
+        ctx.qmm_raw(outs[6], wlm, slm, blm, lm_out, M, C5_LM_HEAD[0], C5_LM_HEAD[1], 4, 64,
+                    B, B, B, ws=ws, ws_bytes=ws.numel(), stream=stream)
+
+    def lm_only():
+        ctx.qmm_raw(outs[6], wlm, slm, blm, lm_out, M, C5_LM_HEAD[0], C5_LM_HEAD[1], 4, 64,
+                    B, B, B, ws=ws, ws_bytes=ws.numel(), stream=stream)
+
+    def timed(fn, n):
+        with torch.cuda.stream(stream):
+            fn()
+            torch.cuda.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(n):
+                fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / n
+
+    total = timed(forward, reps)
+    lm = timed(lm_only, 20)
+    for gr in graphs:
+        gr.close()
+    layer_bytes = sum(algorithmic_bytes(M, N, K) for (N, K) in C5_LAYER)
+    total_bytes = layers * layer_bytes + algorithmic_bytes(M, *C5_LM_HEAD)
+    ideal = total_bytes / (HBM_PEAK_GBS * 1e3)
+    return {
+        "workload": f"M=8 verify forward: {layers} layers x (q,k,v,o,gate,up,down) + lm_head, "
+                    "4-bit g64 bf16, one HIP graph per layer",
+        "us_per_forward": round(total, 1),
+        "ideal_us_at_8TBs": round(ideal, 1),
+        "frac_of_ideal": round(ideal / total, 4),
+        "bytes_per_forward": total_bytes,
+        "layer_us": round((total - lm) / layers, 2),
+        "layer_ideal_us": round(layer_bytes / (HBM_PEAK_GBS * 1e3), 2),
+        "lm_head_us": round(lm, 2),
+        "lm_head_ideal_us": round(algorithmic_bytes(M, *C5_LM_HEAD) / (HBM_PEAK_GBS * 1e3), 2),
+    }
+
+
 def cpu_baseline(seconds):
     """The oracle's OpenMP fp32 restatement on a bounded sample of the M=8 workload."""
     import numpy as np
@@ -135,6 +225,8 @@ def main():
     ap.add_argument("--ms", default="1,2,4,6,8")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-chain", action="store_true",
+                    help="skip the 64-layer verify-forward measurement (c5_chain)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run 20 plain device copies of this many MiB (the reference "
                          "point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -208,6 +300,12 @@ def main():
             "traffic": measured_traffic(),
         },
     }
+    if not args.no_chain:
+        del sets
+        torch.cuda.empty_cache()
+        out["c5_chain"] = chain_c5(torch, ctx, dev)
+        print(f"[bench] C5 chain: {out['c5_chain']['us_per_forward']} us/forward "
+              f"(ideal {out['c5_chain']['ideal_us_at_8TBs']})", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)
