@@ -100,13 +100,17 @@ def time_m(torch, ctx, stream, sets, M, steps, warmup, N, K, bits, gs, ws, wsb):
 # One verify-pass layer of the C5 chain (N, K): q, k, v, o, gate, up, down; then the lm_head.
 C5_LAYER = [(5120, 5120), (1024, 5120), (1024, 5120), (5120, 5120), (17408, 5120),
             (17408, 5120), (5120, 17408)]
+# The same layer with the projections that read one input fused (weights concatenated at
+# load): q|k|v, o, gate|up (then SiLU-mul on the device), down.
+C5_FUSED = [(7168, 5120), (5120, 5120), (34816, 5120), (5120, 17408)]
 C5_LM_HEAD = (151936, 5120)
 
 
-def chain_c5(torch, ctx, dev, layers=64, reps=5):
-    """The C5 verify forward at M=8: `layers` layers of seven 4-bit g64 matmuls, each layer
-    captured as one HIP graph, then the lm_head; distinct random weights per layer (about
-    11.6 GiB, so every layer streams from HBM).  Returns microseconds per forward."""
+def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False):
+    """The C5 verify forward at M=8: `layers` layers of seven 4-bit g64 matmuls (or, fused,
+    q|k|v, o, gate|up + SiLU-mul, down), each layer captured as one HIP graph, then the
+    lm_head; distinct random weights per layer (about 11.6 GiB, so every layer streams from
+    HBM).  Returns microseconds per forward."""
     import dflash_qmm
     M = 8
     g = torch.Generator(device=dev)
@@ -119,24 +123,35 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5):
         b = (torch.randn(N, K // 64, device=dev, generator=g) * 0.01).to(torch.bfloat16)
         return w, s, b
 
-    shapes = C5_LAYER + [C5_LM_HEAD]
+    layer = C5_FUSED if fused else C5_LAYER
+    shapes = layer + [C5_LM_HEAD]
     wsb = max(ctx.workspace_bytes(M, N, K, 4, 64) for (N, K) in shapes)
     ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
     x = torch.randn(M, 5120, device=dev, generator=g).to(torch.bfloat16)
-    outs = [torch.empty(M, N, device=dev, dtype=torch.bfloat16) for (N, K) in C5_LAYER]
-    # inputs: q, k, v, gate, up read x (the layer input); o reads q; down reads gate
-    srcs = [None, None, None, 0, None, None, 4]
+    outs = [torch.empty(M, N, device=dev, dtype=torch.bfloat16) for (N, K) in layer]
+    if fused:
+        # q|k|v, o and gate|up read the layer input (o stands in for attention's output);
+        # down reads the SiLU-mul of gate|up
+        srcs = [None, None, None, "h"]
+        h = torch.empty(M, C5_FUSED[3][1], device=dev, dtype=torch.bfloat16)
+    else:
+        # q, k, v, gate, up read x (the layer input); o reads q; down reads gate
+        srcs = [None, None, None, 0, None, None, 4]
     lm_out = torch.empty(M, C5_LM_HEAD[0], device=dev, dtype=torch.bfloat16)
     stream = torch.cuda.Stream(device=dev)
     B = dflash_qmm.BF16
     graphs, lw = [], []
     for li in range(layers):
-        wl = [weights(N, K) for (N, K) in C5_LAYER]
+        wl = [weights(N, K) for (N, K) in layer]
         lw.append(wl)
-        layer_in = x if li == 0 else outs[6]
+        layer_in = x if li == 0 else outs[-1]
         ctx.graph_begin(stream)
-        for j, (N, K) in enumerate(C5_LAYER):
-            inp = layer_in if srcs[j] is None else outs[srcs[j]]
+        for j, (N, K) in enumerate(layer):
+            if srcs[j] == "h":
+                ctx.silu_mul(outs[2], h, stream=stream)
+                inp = h
+            else:
+                inp = layer_in if srcs[j] is None else outs[srcs[j]]
             w, s, b = wl[j]
             ctx.qmm_raw(inp, w, s, b, outs[j], M, N, K, 4, 64, B, B, B, ws=ws,
                         ws_bytes=ws.numel(), stream=stream)
@@ -146,11 +161,11 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5):
     def forward():
         for gr in graphs:
             gr.launch(stream)
-        ctx.qmm_raw(outs[6], wlm, slm, blm, lm_out, M, C5_LM_HEAD[0], C5_LM_HEAD[1], 4, 64,
+        ctx.qmm_raw(outs[-1], wlm, slm, blm, lm_out, M, C5_LM_HEAD[0], C5_LM_HEAD[1], 4, 64,
                     B, B, B, ws=ws, ws_bytes=ws.numel(), stream=stream)
 
     def lm_only():
-        ctx.qmm_raw(outs[6], wlm, slm, blm, lm_out, M, C5_LM_HEAD[0], C5_LM_HEAD[1], 4, 64,
+        ctx.qmm_raw(outs[-1], wlm, slm, blm, lm_out, M, C5_LM_HEAD[0], C5_LM_HEAD[1], 4, 64,
                     B, B, B, ws=ws, ws_bytes=ws.numel(), stream=stream)
 
     def timed(fn, n):
@@ -170,12 +185,14 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5):
     lm = timed(lm_only, 20)
     for gr in graphs:
         gr.close()
-    layer_bytes = sum(algorithmic_bytes(M, N, K) for (N, K) in C5_LAYER)
+    layer_bytes = sum(algorithmic_bytes(M, N, K) for (N, K) in C5_LAYER)   # the same fused
     total_bytes = layers * layer_bytes + algorithmic_bytes(M, *C5_LM_HEAD)
     ideal = total_bytes / (HBM_PEAK_GBS * 1e3)
     return {
-        "workload": f"M=8 verify forward: {layers} layers x (q,k,v,o,gate,up,down) + lm_head, "
-                    "4-bit g64 bf16, one HIP graph per layer",
+        "workload": (f"M=8 verify forward: {layers} layers x "
+                     + ("(q|k|v, o, gate|up, silu*up, down)" if fused
+                        else "(q,k,v,o,gate,up,down)")
+                     + " + lm_head, 4-bit g64 bf16, one HIP graph per layer"),
         "us_per_forward": round(total, 1),
         "ideal_us_at_8TBs": round(ideal, 1),
         "frac_of_ideal": round(ideal / total, 4),
@@ -304,8 +321,11 @@ def main():
         del sets
         torch.cuda.empty_cache()
         out["c5_chain"] = chain_c5(torch, ctx, dev)
-        print(f"[bench] C5 chain: {out['c5_chain']['us_per_forward']} us/forward "
-              f"(ideal {out['c5_chain']['ideal_us_at_8TBs']})", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+        out["c5_chain_fused"] = chain_c5(torch, ctx, dev, fused=True)
+        for key in ("c5_chain", "c5_chain_fused"):
+            print(f"[bench] {key}: {out[key]['us_per_forward']} us/forward "
+                  f"(ideal {out[key]['ideal_us_at_8TBs']})", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -876,6 +876,28 @@ extern "C" __global__ void __launch_bounds__(256) dfq_fill_u32(uint32_t* ptr, ui
         ptr[i] = v;
 }
 
+/* h[m][n] = silu(g) * u with g = gu[m][n], u = gu[m][N + n] (gu row pitch 2N), in fp32,
+ * rounded once to the output dtype. */
+template <bool F16>
+__device__ __forceinline__ void silu_mul(const uint16_t* gu, uint16_t* h, int M, int N) {
+    const int64_t total = (int64_t)M * N;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * 256) {
+        const int64_t m = i / N, n = i - m * N;
+        const float g = elem_to_f32<F16>(gu[m * 2 * N + n]);
+        const float u = elem_to_f32<F16>(gu[m * 2 * N + N + n]);
+        h[i] = f32_to_out<F16>(g / (1.0f + __expf(-g)) * u);
+    }
+}
+extern "C" __global__ void __launch_bounds__(256) dfq_silu_mul_bf16(const uint16_t* gu,
+                                                                    uint16_t* h, int M, int N) {
+    silu_mul<false>(gu, h, M, N);
+}
+extern "C" __global__ void __launch_bounds__(256) dfq_silu_mul_f16(const uint16_t* gu,
+                                                                   uint16_t* h, int M, int N) {
+    silu_mul<true>(gu, h, M, N);
+}
+
 /* The second pass of a split whose tiles can have more than two contributors (several
  * k-blocks, or tiles spread over three or more workgroups): one wave per 16-column tile sums
  * the tile's partial slots in (k-block, workgroup) order -- a fixed order, so the result does

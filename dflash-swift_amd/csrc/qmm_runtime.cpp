@@ -79,6 +79,7 @@ struct dfq_ctx {
     hipModule_t module = nullptr;
     hipFunction_t mt8[2][3][2][2] = {};  // [bits 4/8][gs 32/64/128][bf16/f16][chunk 1/8 groups]
     hipFunction_t reduce[2] = {};        // second pass of reduce splits [bf16/f16]
+    hipFunction_t silu_mul[2] = {};      // SiLU-mul of a fused gate||up output [bf16/f16]
     hipFunction_t generic = nullptr;
     hipFunction_t fill = nullptr;
     std::mutex mu;
@@ -305,6 +306,8 @@ dfq_status dfq_init(int device, dfq_ctx** out) {
     if ((e = hipModuleGetFunction(&ctx->generic, ctx->module, "dfq_qmm_generic")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->reduce[0], ctx->module, "dfq_qmm_reduce_bf16")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->reduce[1], ctx->module, "dfq_qmm_reduce_f16")) != hipSuccess ||
+        (e = hipModuleGetFunction(&ctx->silu_mul[0], ctx->module, "dfq_silu_mul_bf16")) != hipSuccess ||
+        (e = hipModuleGetFunction(&ctx->silu_mul[1], ctx->module, "dfq_silu_mul_f16")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->fill, ctx->module, "dfq_fill_u32")) != hipSuccess) {
         (void)hipModuleUnload(ctx->module);
         delete ctx;
@@ -523,6 +526,24 @@ dfq_status dfq_qmm(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* s
         if (s) return s;
     }
     return DFQ_OK;
+}
+
+dfq_status dfq_silu_mul(dfq_ctx* ctx, const void* gu, void* h, int M, int N, dfq_dtype dtype,
+                        void* stream) {
+    if (!ctx) return fail(DFQ_ERR_INVALID_ARGUMENT, "null context");
+    if (!gu || !h) return fail(DFQ_ERR_INVALID_ARGUMENT, "null gu or h");
+    if (M < 1 || N < 1) return fail(DFQ_ERR_INVALID_ARGUMENT, "M and N must be positive");
+    if (dtype != DFQ_BF16 && dtype != DFQ_F16)
+        return fail(DFQ_ERR_UNSUPPORTED, "silu_mul takes bf16 or fp16");
+    if (!aligned(gu, 2) || !aligned(h, 2))
+        return fail(DFQ_ERR_INVALID_ARGUMENT, "gu and h must be 2-byte aligned");
+    DeviceGuard g(ctx->device);
+    const uint64_t total = (uint64_t)M * N;
+    unsigned grid = (unsigned)std::min<uint64_t>((total + 255) / 256, 8192);
+    void* args[] = {(void*)&gu, &h, &M, &N};
+    hipError_t e = hipModuleLaunchKernel(ctx->silu_mul[dtype == DFQ_BF16 ? 0 : 1], grid, 1, 1,
+                                         256, 1, 1, 0, (hipStream_t)stream, args, nullptr);
+    return e == hipSuccess ? DFQ_OK : hip_fail(e, "launch dfq_silu_mul");
 }
 
 dfq_status dfq_qmm_fallback(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,

@@ -83,6 +83,7 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         "dfq_qmm": ([P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, P, S, P], I),
         "dfq_qmm_fallback": ([P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, P], I),
         "dfq_graph_begin": ([P, P], I), "dfq_graph_end": ([P, P, PP], I),
+        "dfq_silu_mul": ([P, P, P, I, I, I, P], I),
         "dfq_graph_launch": ([P, P], I), "dfq_graph_destroy": ([P], I),
         "dfq_linear_create": ([P, ctypes.POINTER(_LinearDesc), PP], I),
         "dfq_small_m_linear_create": ([P, PP], I), "dfq_linear_destroy": ([P], I),
@@ -246,6 +247,17 @@ class Context:
         self.fallback_raw(x, w, scales, biases, out, M, N, K, bits, gs, xdt, sdt,
                           dtype_code(out), lbias=lbias, stream=stream)
         return out
+
+    def silu_mul(self, gu, h=None, stream=None):
+        """h[m, n] = silu(gu[m, n]) * gu[m, N + n] for a fused gate||up output gu [M, 2N]."""
+        import torch
+        M, N2 = gu.shape
+        N = N2 // 2
+        if h is None:
+            h = torch.empty((M, N), dtype=gu.dtype, device=gu.device)
+        _check(self.lib.dfq_silu_mul(self.handle, _ptr(gu), _ptr(h), M, N, dtype_code(gu),
+                                     _stream(stream)), "dfq_silu_mul")
+        return h
 
     # ---- graphs ---------------------------------------------------------------------------
     def graph_begin(self, stream):

@@ -138,6 +138,14 @@ dfq_status dfq_graph_end(dfq_ctx* ctx, void* stream, dfq_graph** out);
 dfq_status dfq_graph_launch(dfq_graph* graph, void* stream);
 dfq_status dfq_graph_destroy(dfq_graph* graph);
 
+/* h[m][n] = silu(gu[m][n]) * gu[m][N + n] for the fused gate||up projection's output
+ * gu[M][2N] (row pitch 2N elements): the activation between gate||up and down in a layer
+ * chain.  bf16 or fp16, computed in fp32 (silu(g) = g / (1 + e^-g)) and rounded once.  No
+ * counterpart on the reference's path: MLX runs SiLU and the product as its own ops in the
+ * model's MLP, around the swapped projections (SmallMQuantizedMatmul.swift:303-317). */
+dfq_status dfq_silu_mul(dfq_ctx* ctx, const void* gu, void* h, int M, int N, dfq_dtype dtype,
+                        void* stream);
+
 /* ---- the drop-in layer (SmallMQuantizedMatmul.swift:227-317) -------------------------- */
 
 typedef struct dfq_linear dfq_linear;

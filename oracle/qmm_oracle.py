@@ -17,6 +17,8 @@ seeded input generators for the benchmark configurations.  Reference behaviour f
 * ``Sources/DFlashKit/SmallMQuantizedMatmul.swift:59, 69`` -- ``w = float(code) * s + b``.
 * ``Sources/DFlashKit/SmallMQuantizedMatmul.swift:209, 288-290`` --
   ``y = x @ dequant(W).T`` (+ optional linear bias).
+* ``Sources/DFlashKit/DFlashDecoderLayer.swift:26`` -- the MLP between the swapped
+  projections: ``down(silu(gate(x)) * up(x))`` with ``silu(g) = g * sigmoid(g)``.
 """
 from __future__ import annotations
 
@@ -121,6 +123,16 @@ def qmm_f64(x, xdt, w, scales, biases, sdt, bits, gs, lbias=None, lbdt=BF16) -> 
     if lbias is not None:
         y = y + from_bits(lbias, lbdt).astype(np.float64)[None, :]
     return y
+
+
+def silu_mul_f64(gu, dt: int) -> np.ndarray:
+    """fp64 ``silu(g) * u`` for a fused gate||up output ``gu`` [M, 2N] (bits of dtype dt):
+    g = gu[:, :N], u = gu[:, N:], silu(g) = g / (1 + exp(-g))
+    (Sources/DFlashKit/DFlashDecoderLayer.swift:26)."""
+    a = from_bits(np.asarray(gu), dt).astype(np.float64)
+    n = a.shape[1] // 2
+    g, u = a[:, :n], a[:, n:]
+    return g / (1.0 + np.exp(-g)) * u
 
 
 def out_dtype(xdt: int, sdt: int) -> int:

@@ -240,3 +240,23 @@ def test_planted_transposed_operand_is_caught(oracle):
     y_t = wd[:, :16] @ x[:, :16].T       # a transposed-operand slip on a square corner
     rel, _ = Q.tolerance_check(y_t, oracle.qmm_f64(c))
     assert rel > 1e-2
+
+
+def test_silu_mul_closed_forms():
+    """silu(0) = 0; silu(g) - silu(-g) = g (g*sigmoid(g) + g*sigmoid(-g) = g); silu(g) -> g
+    for large g and -> 0 for very negative g; u = 0 or u = 1 isolate each factor."""
+    from oracle.qmm_oracle import silu_mul_f64, to_bits, from_bits
+    g = np.array([[0.0, 1.0, -1.0, 2.5, -2.5, 40.0, -40.0, 0.5]], dtype=np.float32)
+    g = from_bits(to_bits(g, BF16), BF16)
+    ones = np.ones_like(g)
+    h = silu_mul_f64(to_bits(np.concatenate([g, ones], axis=1), BF16), BF16)[0]
+    hn = silu_mul_f64(to_bits(np.concatenate([-g, ones], axis=1), BF16), BF16)[0]
+    assert h[0] == 0.0
+    np.testing.assert_allclose(h - hn, g[0], rtol=1e-12, atol=1e-12)
+    assert abs(h[5] - 40.0) < 1e-12 and abs(h[6]) < 1e-15
+    np.testing.assert_allclose(h[1], 1.0 / (1.0 + np.exp(-1.0)), rtol=1e-15)
+    zero = silu_mul_f64(to_bits(np.concatenate([g, 0 * ones], axis=1), BF16), BF16)
+    assert not zero.any()
+    u = np.array([[3.0, -2.0, 0.25, 1.0, 1.0, 1.0, 1.0, 1.0]], dtype=np.float32)
+    hu = silu_mul_f64(to_bits(np.concatenate([g, u], axis=1), BF16), BF16)[0]
+    np.testing.assert_allclose(hu, h * from_bits(to_bits(u, BF16), BF16)[0], rtol=1e-15)
