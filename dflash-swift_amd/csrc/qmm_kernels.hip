@@ -898,6 +898,82 @@ extern "C" __global__ void __launch_bounds__(256) dfq_silu_mul_f16(const uint16_
     silu_mul<true>(gu, h, M, N);
 }
 
+/* Greedy accept of a verify pass (the reference's acceptedPrefix).  Blocks of one row cover
+ * chunks of its V logits; each folds its chunk's maximum into the row's 64-bit key with an
+ * agent-scope atomic max: the high word is the logit's bits made order-preserving (sign flip
+ * or full flip for negatives), the low word is ~index, so the largest key is the largest
+ * logit and, among equal logits, the first index (MLX's argMax).  NaN logits are skipped.
+ * The last block to arrive (counter) turns the keys into tokens, counts the leading run of
+ * tokens[i] == proposals[i] (i < M-1), writes both, and re-arms keys and counter to zero. */
+__device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
+    const uint32_t b = __float_as_uint(v);
+    const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((uint64_t)o << 32) | (uint32_t)~(uint32_t)idx;
+}
+
+template <bool F16>
+__device__ __forceinline__ void argmax_accept(const uint16_t* logits, int M, int V, int chunk,
+                                              const int32_t* proposals, int32_t* tokens,
+                                              int32_t* accepted, uint64_t* keys,
+                                              uint32_t* counter) {
+    const int per_row = (V + chunk - 1) / chunk;
+    const int row = blockIdx.x / per_row, c = blockIdx.x - row * per_row;
+    const int lo = c * chunk, hi = min(V, lo + chunk);
+    const uint16_t* lr = logits + (size_t)row * V;
+    uint64_t best = 0;
+    for (int i = lo + (int)threadIdx.x; i < hi; i += 256) {
+        const float v = elem_to_f32<F16>(lr[i]);
+        if (v != v) continue;
+        const uint64_t k = argmax_key(v, i);
+        best = k > best ? k : best;
+    }
+    /* tree reduction of the block's keys through LDS */
+    __shared__ uint64_t red[256];
+    red[threadIdx.x] = best;
+    __syncthreads();
+    for (int s2 = 128; s2 > 0; s2 >>= 1) {
+        if ((int)threadIdx.x < s2) {
+            const uint64_t o = red[threadIdx.x + s2];
+            if (o > red[threadIdx.x]) red[threadIdx.x] = o;
+        }
+        __syncthreads();
+    }
+    __shared__ uint32_t last;
+    if (threadIdx.x == 0) {
+        if (red[0]) __hip_atomic_fetch_max(keys + row, red[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t n = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+        last = (n + 1 == gridDim.x) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!last || threadIdx.x != 0) return;
+    int run = 0;
+    bool agree = true;
+    for (int m = 0; m < M; ++m) {
+        const uint64_t k = __hip_atomic_exchange(keys + m, 0ull, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+        const int32_t tok = k ? (int32_t)~(uint32_t)k : -1;
+        if (tokens) tokens[m] = tok;
+        if (m < M - 1) {
+            agree = agree && proposals && proposals[m] == tok;
+            run += agree ? 1 : 0;
+        }
+    }
+    if (accepted) *accepted = run;
+    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+extern "C" __global__ void __launch_bounds__(256) dfq_argmax_accept_bf16(
+    const uint16_t* logits, int M, int V, int chunk, const int32_t* proposals, int32_t* tokens,
+    int32_t* accepted, uint64_t* keys, uint32_t* counter) {
+    argmax_accept<false>(logits, M, V, chunk, proposals, tokens, accepted, keys, counter);
+}
+extern "C" __global__ void __launch_bounds__(256) dfq_argmax_accept_f16(
+    const uint16_t* logits, int M, int V, int chunk, const int32_t* proposals, int32_t* tokens,
+    int32_t* accepted, uint64_t* keys, uint32_t* counter) {
+    argmax_accept<true>(logits, M, V, chunk, proposals, tokens, accepted, keys, counter);
+}
+
 /* The second pass of a split whose tiles can have more than two contributors (several
  * k-blocks, or tiles spread over three or more workgroups): one wave per 16-column tile sums
  * the tile's partial slots in (k-block, workgroup) order -- a fixed order, so the result does

@@ -80,6 +80,7 @@ struct dfq_ctx {
     hipFunction_t mt8[2][3][2][2] = {};  // [bits 4/8][gs 32/64/128][bf16/f16][chunk 1/8 groups]
     hipFunction_t reduce[2] = {};        // second pass of reduce splits [bf16/f16]
     hipFunction_t silu_mul[2] = {};      // SiLU-mul of a fused gate||up output [bf16/f16]
+    hipFunction_t argmax_accept[2] = {}; // greedy accept of a verify pass [bf16/f16]
     hipFunction_t generic = nullptr;
     hipFunction_t fill = nullptr;
     std::mutex mu;
@@ -308,6 +309,8 @@ dfq_status dfq_init(int device, dfq_ctx** out) {
         (e = hipModuleGetFunction(&ctx->reduce[1], ctx->module, "dfq_qmm_reduce_f16")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->silu_mul[0], ctx->module, "dfq_silu_mul_bf16")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->silu_mul[1], ctx->module, "dfq_silu_mul_f16")) != hipSuccess ||
+        (e = hipModuleGetFunction(&ctx->argmax_accept[0], ctx->module, "dfq_argmax_accept_bf16")) != hipSuccess ||
+        (e = hipModuleGetFunction(&ctx->argmax_accept[1], ctx->module, "dfq_argmax_accept_f16")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->fill, ctx->module, "dfq_fill_u32")) != hipSuccess) {
         (void)hipModuleUnload(ctx->module);
         delete ctx;
@@ -544,6 +547,44 @@ dfq_status dfq_silu_mul(dfq_ctx* ctx, const void* gu, void* h, int M, int N, dfq
     hipError_t e = hipModuleLaunchKernel(ctx->silu_mul[dtype == DFQ_BF16 ? 0 : 1], grid, 1, 1,
                                          256, 1, 1, 0, (hipStream_t)stream, args, nullptr);
     return e == hipSuccess ? DFQ_OK : hip_fail(e, "launch dfq_silu_mul");
+}
+
+dfq_status dfq_argmax_accept_workspace_bytes(int M, size_t* bytes) {
+    if (!bytes) return fail(DFQ_ERR_INVALID_ARGUMENT, "null bytes");
+    if (M < 1) return fail(DFQ_ERR_INVALID_ARGUMENT, "M must be positive");
+    /* one 64-bit key per row, then the arrival counter */
+    *bytes = ((size_t)M * 8 + 4 + 255) & ~(size_t)255;
+    return DFQ_OK;
+}
+
+dfq_status dfq_argmax_accept(dfq_ctx* ctx, const void* logits, int M, int V, dfq_dtype dtype,
+                             const int32_t* proposals, int32_t* tokens, int32_t* accepted,
+                             void* ws, size_t wsb, void* stream) {
+    if (!ctx) return fail(DFQ_ERR_INVALID_ARGUMENT, "null context");
+    if (!logits) return fail(DFQ_ERR_INVALID_ARGUMENT, "null logits");
+    if (M < 1 || V < 1) return fail(DFQ_ERR_INVALID_ARGUMENT, "M and V must be positive");
+    if ((int64_t)V > 0x7fffffff / 2) return fail(DFQ_ERR_UNSUPPORTED, "V too large");
+    if (dtype != DFQ_BF16 && dtype != DFQ_F16)
+        return fail(DFQ_ERR_UNSUPPORTED, "argmax_accept takes bf16 or fp16 logits");
+    size_t need = 0;
+    dfq_argmax_accept_workspace_bytes(M, &need);
+    if (!ws || wsb < need)
+        return fail(DFQ_ERR_WORKSPACE, "workspace of %zu bytes needed (got %zu)", need,
+                    ws ? wsb : (size_t)0);
+    if (!aligned(ws, 8) || !aligned(logits, 2))
+        return fail(DFQ_ERR_INVALID_ARGUMENT, "workspace must be 8-byte aligned");
+    DeviceGuard g(ctx->device);
+    int chunk = 4096;
+    const int64_t per_row = ((int64_t)V + chunk - 1) / chunk;
+    if ((int64_t)M * per_row > 0x7fffffff) return fail(DFQ_ERR_UNSUPPORTED, "grid too large");
+    uint64_t* keys = (uint64_t*)ws;
+    uint32_t* counter = (uint32_t*)((char*)ws + (size_t)M * 8);
+    void* args[] = {(void*)&logits, &M, &V, &chunk, (void*)&proposals, &tokens, &accepted,
+                    &keys, &counter};
+    hipError_t e = hipModuleLaunchKernel(ctx->argmax_accept[dtype == DFQ_BF16 ? 0 : 1],
+                                         (unsigned)(M * per_row), 1, 1, 256, 1, 1, 0,
+                                         (hipStream_t)stream, args, nullptr);
+    return e == hipSuccess ? DFQ_OK : hip_fail(e, "launch dfq_argmax_accept");
 }
 
 dfq_status dfq_qmm_fallback(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,

@@ -84,6 +84,8 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         "dfq_qmm_fallback": ([P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, P], I),
         "dfq_graph_begin": ([P, P], I), "dfq_graph_end": ([P, P, PP], I),
         "dfq_silu_mul": ([P, P, P, I, I, I, P], I),
+        "dfq_argmax_accept_workspace_bytes": ([I, ctypes.POINTER(S)], I),
+        "dfq_argmax_accept": ([P, P, I, I, I, P, P, P, P, S, P], I),
         "dfq_graph_launch": ([P, P], I), "dfq_graph_destroy": ([P], I),
         "dfq_linear_create": ([P, ctypes.POINTER(_LinearDesc), PP], I),
         "dfq_small_m_linear_create": ([P, PP], I), "dfq_linear_destroy": ([P], I),
@@ -258,6 +260,28 @@ class Context:
         _check(self.lib.dfq_silu_mul(self.handle, _ptr(gu), _ptr(h), M, N, dtype_code(gu),
                                      _stream(stream)), "dfq_silu_mul")
         return h
+
+    def argmax_accept(self, logits, proposals=None, tokens=None, accepted=None, ws=None,
+                      stream=None):
+        """Greedy accept on the device: (tokens [M] int32, accepted [1] int32) for logits
+        [M, V] (M = 1 + drafts) and proposals [M-1] int32 (acceptedPrefix)."""
+        import torch
+        M, V = logits.shape
+        dev = logits.device
+        if tokens is None:
+            tokens = torch.empty(M, dtype=torch.int32, device=dev)
+        if accepted is None:
+            accepted = torch.empty(1, dtype=torch.int32, device=dev)
+        if ws is None:
+            b = ctypes.c_size_t()
+            _check(self.lib.dfq_argmax_accept_workspace_bytes(M, ctypes.byref(b)),
+                   "dfq_argmax_accept_workspace_bytes")
+            ws = torch.zeros(b.value, dtype=torch.uint8, device=dev)
+        _check(self.lib.dfq_argmax_accept(self.handle, _ptr(logits), M, V, dtype_code(logits),
+                                          _ptr(proposals), _ptr(tokens), _ptr(accepted),
+                                          _ptr(ws), ws.numel(), _stream(stream)),
+               "dfq_argmax_accept")
+        return tokens, accepted
 
     # ---- graphs ---------------------------------------------------------------------------
     def graph_begin(self, stream):

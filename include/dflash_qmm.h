@@ -146,6 +146,21 @@ dfq_status dfq_graph_destroy(dfq_graph* graph);
 dfq_status dfq_silu_mul(dfq_ctx* ctx, const void* gu, void* h, int M, int N, dfq_dtype dtype,
                         void* stream);
 
+/* ---- greedy accept of a verify pass ---------------------------------------------------- */
+/* tokens[m] = argmax over V of logits[m][*] (first index among equal maxima, NaN skipped;
+ * -1 for a row with no number) for the M = 1 + drafts verify positions, and
+ * *accepted = the leading run of proposals[i] == tokens[i], i < M - 1 (the sum of the
+ * cumulative product of the matches).  On the device: only these M + 1 ints need to reach
+ * the host.  proposals, tokens or accepted may be NULL (no proposals: accepted = 0).
+ * Replaces acceptedPrefix(targetLogits:proposals:) (DFlashSpeculativeGenerator.swift:555-571,
+ * argMax / == / cumprod / sum at :562-564).  The workspace (dfq_argmax_accept_workspace_bytes,
+ * 8-byte aligned) must be zero before the first call (dfq_workspace_clear); every call
+ * leaves it zero. */
+dfq_status dfq_argmax_accept_workspace_bytes(int M, size_t* bytes);
+dfq_status dfq_argmax_accept(dfq_ctx* ctx, const void* logits, int M, int V, dfq_dtype dtype,
+                             const int32_t* proposals, int32_t* tokens, int32_t* accepted,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- the drop-in layer (SmallMQuantizedMatmul.swift:227-317) -------------------------- */
 
 typedef struct dfq_linear dfq_linear;

@@ -19,6 +19,9 @@ seeded input generators for the benchmark configurations.  Reference behaviour f
   ``y = x @ dequant(W).T`` (+ optional linear bias).
 * ``Sources/DFlashKit/DFlashDecoderLayer.swift:26`` -- the MLP between the swapped
   projections: ``down(silu(gate(x)) * up(x))`` with ``silu(g) = g * sigmoid(g)``.
+* ``Sources/DFlashKit/DFlashSpeculativeGenerator.swift:555-571`` -- greedy accept: per-row
+  ``argMax`` of the verify logits, ``proposals == targetTokens[..<drafts]``, and the sum of
+  the cumulative product of the matches.
 """
 from __future__ import annotations
 
@@ -133,6 +136,23 @@ def silu_mul_f64(gu, dt: int) -> np.ndarray:
     n = a.shape[1] // 2
     g, u = a[:, :n], a[:, n:]
     return g / (1.0 + np.exp(-g)) * u
+
+
+def argmax_accept(logits, dt: int, proposals=None):
+    """(tokens, accepted) for verify logits [M, V] (bits of dtype dt): tokens[m] is the first
+    index of the largest non-NaN logit of row m (-1 if none), accepted the leading run of
+    proposals[i] == tokens[i] over i < M-1 (acceptedPrefix,
+    Sources/DFlashKit/DFlashSpeculativeGenerator.swift:555-571)."""
+    a = from_bits(np.asarray(logits), dt).astype(np.float64)
+    tokens = []
+    for row in a:
+        idx = np.flatnonzero(~np.isnan(row))
+        tokens.append(int(idx[np.argmax(row[idx])]) if idx.size else -1)
+    tokens = np.array(tokens, dtype=np.int32)
+    if proposals is None:
+        return tokens, 0
+    match = (np.asarray(proposals, dtype=np.int32) == tokens[: len(proposals)]).astype(np.int32)
+    return tokens, int(np.cumprod(match).sum())
 
 
 def out_dtype(xdt: int, sdt: int) -> int:

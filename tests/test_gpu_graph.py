@@ -135,3 +135,33 @@ def test_fused_mlp_chain_matches_oracle(ctx):
         torch.cuda.synchronize()
         assert torch.equal(eager.view(torch.int16), y.view(torch.int16))
     gr.close()
+
+
+@pytest.mark.parametrize("dt,M,V", [("bf16", 8, 151936), ("f16", 3, 1000), ("bf16", 1, 4097)])
+def test_argmax_accept_matches_oracle(ctx, dt, M, V):
+    import numpy as np
+    from gpu_util import to_dev16
+    from oracle.qmm_oracle import BF16, F16, argmax_accept, to_bits
+    code = BF16 if dt == "bf16" else F16
+    rng = np.random.default_rng(M * 7 + V)
+    a = rng.normal(0.0, 3.0, size=(M, V)).astype(np.float32)
+    a[0, V // 3] = a[0, (2 * V) // 3] = 50.0            # a tie: the first index wins
+    if M > 2:
+        a[2, :] = np.nan
+        a[2, V - 1] = -7.0                               # one number among NaNs
+    bits = to_bits(a, code)
+    logits = to_dev16(bits, code)
+    want_tokens, _ = argmax_accept(bits, code)
+    ws = torch.zeros(256, dtype=torch.uint8, device="cuda")
+    for agree in range(M):                               # proposals matching the first `agree`
+        props = want_tokens[: M - 1].copy()
+        if agree < M - 1:
+            props[agree] = (props[agree] + 1) % V
+        _, want_acc = argmax_accept(bits, code, props)
+        announce(f"argmax_accept {dt} M={M} V={V} agree={agree}")
+        p_dev = torch.from_numpy(props.astype(np.int32)).cuda() if M > 1 else None
+        tokens, acc = ctx.argmax_accept(logits, p_dev, ws=ws)
+        torch.cuda.synchronize()
+        assert tokens.cpu().numpy().tolist() == want_tokens.tolist()
+        assert int(acc.item()) == want_acc == min(agree, M - 1)
+        assert int(ws.count_nonzero().item()) == 0       # the workspace is zero again

@@ -260,3 +260,30 @@ def test_silu_mul_closed_forms():
     u = np.array([[3.0, -2.0, 0.25, 1.0, 1.0, 1.0, 1.0, 1.0]], dtype=np.float32)
     hu = silu_mul_f64(to_bits(np.concatenate([g, u], axis=1), BF16), BF16)[0]
     np.testing.assert_allclose(hu, h * from_bits(to_bits(u, BF16), BF16)[0], rtol=1e-15)
+
+
+def test_argmax_accept_closed_forms():
+    """First index among equal maxima, NaN skipped (an all-NaN row gives -1), -inf rows give
+    index 0, and the accepted count is the run of leading matches, checked against a plain
+    loop over the same tokens."""
+    from oracle.qmm_oracle import argmax_accept, to_bits
+    nan, inf = float("nan"), float("inf")
+    rows = np.array([[1.0, 3.0, 3.0, 2.0],          # tie -> 1
+                     [nan, 0.5, nan, 0.25],         # NaN skipped -> 1
+                     [-inf, -inf, -inf, -inf],      # all -inf -> 0
+                     [nan, nan, nan, nan],          # no number -> -1
+                     [-1.0, -2.0, -0.5, -0.5]],     # negative tie -> 2
+                    dtype=np.float32)
+    bits = to_bits(rows, BF16)
+    tokens, acc = argmax_accept(bits, BF16, proposals=[1, 1, 0, 5])
+    assert tokens.tolist() == [1, 1, 0, -1, 2]
+    assert acc == 3                                   # 1==1, 1==1, 0==0, 5!=-1
+    for props in ([0, 1, 0, -1], [1, 2, 0, -1], [1, 1, 0, -1], []):
+        _, acc = argmax_accept(bits, BF16, proposals=props)
+        run = 0
+        for p_, t in zip(props, tokens):
+            if p_ != t:
+                break
+            run += 1
+        assert acc == run
+    assert argmax_accept(bits[:1], BF16, proposals=[])[1] == 0
