@@ -157,16 +157,21 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False):
                         ws_bytes=ws.numel(), stream=stream)
         graphs.append(ctx.graph_end(stream))
     wlm, slm, blm = weights(*C5_LM_HEAD)
+    proposals = torch.zeros(M - 1, dtype=torch.int32, device=dev)
+    tokens = torch.empty(M, dtype=torch.int32, device=dev)
+    accepted = torch.empty(1, dtype=torch.int32, device=dev)
+    acc_ws = torch.zeros(256, dtype=torch.uint8, device=dev)
+
+    def lm_only():
+        """the lm_head and the greedy accept: only M + 1 ints leave the device"""
+        ctx.qmm_raw(outs[-1], wlm, slm, blm, lm_out, M, C5_LM_HEAD[0], C5_LM_HEAD[1], 4, 64,
+                    B, B, B, ws=ws, ws_bytes=ws.numel(), stream=stream)
+        ctx.argmax_accept(lm_out, proposals, tokens, accepted, ws=acc_ws, stream=stream)
 
     def forward():
         for gr in graphs:
             gr.launch(stream)
-        ctx.qmm_raw(outs[-1], wlm, slm, blm, lm_out, M, C5_LM_HEAD[0], C5_LM_HEAD[1], 4, 64,
-                    B, B, B, ws=ws, ws_bytes=ws.numel(), stream=stream)
-
-    def lm_only():
-        ctx.qmm_raw(outs[-1], wlm, slm, blm, lm_out, M, C5_LM_HEAD[0], C5_LM_HEAD[1], 4, 64,
-                    B, B, B, ws=ws, ws_bytes=ws.numel(), stream=stream)
+        lm_only()
 
     def timed(fn, n):
         with torch.cuda.stream(stream):
@@ -192,14 +197,14 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False):
         "workload": (f"M=8 verify forward: {layers} layers x "
                      + ("(q|k|v, o, gate|up, silu*up, down)" if fused
                         else "(q,k,v,o,gate,up,down)")
-                     + " + lm_head, 4-bit g64 bf16, one HIP graph per layer"),
+                     + " + lm_head + greedy accept, 4-bit g64 bf16, one HIP graph per layer"),
         "us_per_forward": round(total, 1),
         "ideal_us_at_8TBs": round(ideal, 1),
         "frac_of_ideal": round(ideal / total, 4),
         "bytes_per_forward": total_bytes,
         "layer_us": round((total - lm) / layers, 2),
         "layer_ideal_us": round(layer_bytes / (HBM_PEAK_GBS * 1e3), 2),
-        "lm_head_us": round(lm, 2),
+        "lm_head_accept_us": round(lm, 2),
         "lm_head_ideal_us": round(algorithmic_bytes(M, *C5_LM_HEAD) / (HBM_PEAK_GBS * 1e3), 2),
     }
 

@@ -26,6 +26,8 @@ struct Plan {
     int xsum_off = 0;   /* LDS offset of the per-group x sums                */
     int part_off = 0;   /* LDS offset of the per-unit partial tiles          */
     int cnt_off = 0;    /* LDS offset of the tile arrival counters           */
+    int gen_off = 0;    /* LDS offset of the partial slots' generations      */
+    int ring = 0;       /* partial-tile slots (a ring over the take order)   */
     int umax = 0;       /* most units per workgroup                          */
     int lds_bytes = 0;  /* dynamic LDS requested per workgroup               */
     bool need_ws = false;

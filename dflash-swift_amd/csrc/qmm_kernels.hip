@@ -482,7 +482,9 @@ __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
     const int ta = a / SS;
     const int ntl = (b > a) ? (b - 1) / SS - ta + 1 : 0;
     uint32_t* tcnt = (uint32_t*)(lds_base() + p.lds_cnt_off);
+    uint32_t* gen = (uint32_t*)(lds_base() + p.lds_gen_off);
     const float* part = (const float*)(lds_base() + p.lds_part_off);
+    const int s1 = max(a, ((b - 1) / SS) * SS), nrot = b - s1;  // the take order (unit_of)
     __syncthreads();  // the staging barrier of the streaming waves (tile counters zeroed)
     int remaining = ntl;
     while (remaining > 0) {
@@ -499,8 +501,15 @@ __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
                 m &= m - 1;
                 const int t = ta + base + bit;
                 const int u0 = max(a, t * SS), u1 = min(b, (t + 1) * SS);
+                const int g0 = u0 >= s1 ? u0 - s1 : nrot + (u0 - a);  // take index of u0
+                const int sl0 = g0 % p.ring;
                 f32x4_t v = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (lane < 32) v = *(const f32x4_t*)(part + (u0 - a) * 128 + n * 8 + q * 4);
+                if (lane < 32) v = *(const f32x4_t*)(part + sl0 * 128 + n * 8 + q * 4);
+                /* the tile's sum is read: its slot may take the unit p.ring takes later (LDS
+                 * operations of a wave complete in order, so the read precedes the release) */
+                if (lane == 0)
+                    __hip_atomic_store(gen + sl0, (uint32_t)(g0 + p.ring), __ATOMIC_RELEASE,
+                                       __HIP_MEMORY_SCOPE_WORKGROUP);
                 const int first = owner_wg(t * SS, base_u, rem_u);
                 if (u0 == t * SS && u1 == (t + 1) * SS && p.nkb == 1) {
                     store_y<F16>(p, t, lane, v);
@@ -640,11 +649,15 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
                 rw[slot][j][s] = *(const u32x4_t*)(wb + vw + (j * C::NS + s) * 64);
     };
 
-    /* ---- LDS layout: row 0 zeros, rows 1..M x; per-group x sums; per-unit partial tiles
-     * ([n][8] fp32, 512 bytes each); tile arrival counters; the take counter */
+    /* ---- LDS layout: row 0 zeros, rows 1..M x; per-group x sums; a ring of p.ring partial
+     * tiles ([n][8] fp32, 512 bytes each), the unit with take index g using slot g % ring,
+     * and each slot's generation (the take index allowed to write it next); tile arrival
+     * counters; the take counter */
     const int RS = p.lds_row_stride;
+    const int R = p.ring;
     float* xsum = (float*)(lds + p.lds_xsum_off);
     float* part = (float*)(lds + p.lds_part_off);
+    uint32_t* gen = (uint32_t*)(lds + p.lds_gen_off);
     uint32_t* tcnt = (uint32_t*)(lds + p.lds_cnt_off);
     const int ta = a / SS;               // first tile touched by this workgroup
     const int ntl = tlast - ta + 1;      // tiles touched
@@ -673,6 +686,7 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     for (int i = tid; i < GK * 8; i += kThreads)
         if ((i & 7) >= p.M) xsum[i] = 0.0f;
     for (int i = tid; i < ntl; i += kThreads) tcnt[i] = 0u;
+    for (int i = tid; i < R; i += kThreads) gen[i] = (uint32_t)i;
     if (tid == 0) *gcnt = (uint32_t)(kWaves * PF);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -759,9 +773,18 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
             /* lanes 0-31: own value + the value of lane + 32 */
             v[r] = __uint_as_float(lo) + __uint_as_float(hi);
         }
-        if (lane < 32) *(f32x4_t*)(part + (u - a) * 128 + n * 8 + q * 4) = v;
-        /* arrive at tile t; the wave that completes its units here sums them into the slot
-         * of the tile's first unit and hands the tile to the publisher wave */
+        /* the slot of take g: wait until the unit that held it last (take g - R) is
+         * released (never, when the range fits the ring) */
+        const int sl = g % R;
+        if (L > R) {
+            while ((int)__hip_atomic_load(gen + sl, __ATOMIC_ACQUIRE,
+                                          __HIP_MEMORY_SCOPE_WORKGROUP) != g)
+                __builtin_amdgcn_s_sleep(1);
+        }
+        if (lane < 32) *(f32x4_t*)(part + sl * 128 + n * 8 + q * 4) = v;
+        /* arrive at tile t; the wave that completes its units here sums them (in unit order)
+         * into the slot of the tile's first unit, releases the other slots, and hands the
+         * tile to the publisher wave */
         const int u0 = max(a, t * SS), u1 = min(b, (t + 1) * SS);
         uint32_t old = 0;
         if (lane == 0)
@@ -769,15 +792,21 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
                                          __HIP_MEMORY_SCOPE_WORKGROUP);
         old = __builtin_amdgcn_readfirstlane(old);
         if ((int)old + 1 == u1 - u0) {
+            const int g0 = u0 >= s1 ? u0 - s1 : nrot + (u0 - a);  // the tile's takes: g0..
+            const int sl0 = g0 % R;
             if (lane < 32) {
                 f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
-                for (int uu = u0; uu < u1; ++uu)
-                    sum += *(const f32x4_t*)(part + (uu - a) * 128 + n * 8 + q * 4);
-                *(f32x4_t*)(part + (u0 - a) * 128 + n * 8 + q * 4) = sum;
+                for (int i = 0, s2 = sl0; i < u1 - u0; ++i, s2 = (s2 + 1 == R) ? 0 : s2 + 1)
+                    sum += *(const f32x4_t*)(part + s2 * 128 + n * 8 + q * 4);
+                *(f32x4_t*)(part + sl0 * 128 + n * 8 + q * 4) = sum;
             }
-            if (lane == 0)
+            if (lane == 0) {
+                for (int i = 1; i < u1 - u0; ++i)
+                    __hip_atomic_store(gen + (g0 + i) % R, (uint32_t)(g0 + i + R),
+                                       __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
                 __hip_atomic_store(tcnt + (t - ta), kTileDone, __ATOMIC_RELEASE,
                                    __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
         }
     };
 

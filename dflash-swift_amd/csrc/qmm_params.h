@@ -50,7 +50,9 @@ typedef struct QmmParams {
     int32_t lds_xsum_off;   /* byte offset of the per-group x sums in LDS             */
     int32_t lds_part_off;   /* byte offset of the per-unit partial tiles in LDS       */
     int32_t lds_cnt_off;    /* byte offset of the per-tile arrival counters in LDS    */
-    int32_t umax;           /* most units one workgroup holds (partial slots sized)  */
+    int32_t lds_gen_off;    /* byte offset of the partial slots' generations in LDS   */
+    int32_t umax;           /* most units one workgroup holds                         */
+    int32_t ring;           /* partial-tile slots in LDS (a ring over the take order) */
     uint32_t w_bytes;       /* size of w in bytes (< 2^31)                            */
     uint32_t s_bytes;       /* size of scales (= size of biases) in bytes             */
 } QmmParams;

@@ -169,21 +169,28 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
         p.rs = 2 * kr + 16;
         p.xsum_off = ((M + 1) * p.rs + 15) & ~15;
         p.part_off = p.xsum_off + (kr / gs) * 32;
-        /* each unit of a workgroup owns a 512-byte partial slot (plus at most one 4-byte
-         * tile counter); more workgroups (beyond one per CU) shorten the ranges when the
-         * slots would not fit */
-        if ((size_t)p.part_off + 512 + 256 > lds_max) continue;
-        const int64_t cap = (int64_t)(lds_max - p.part_off - 256) / 516;
+        /* Partial tiles live in a ring of 512-byte LDS slots over the take order: a range's
+         * whole length when it is short, else enough for the units in flight plus a few
+         * tiles waiting for their sum (at least the units one tile can have in a range, which
+         * keeps the ring free of deadlock), plus a 4-byte generation per slot and a counter
+         * per tile.  More workgroups than one per CU shorten the ranges when even that would
+         * not fit. */
         const int64_t U = (int64_t)T * ss_max;
-        int64_t G = std::max(1, num_cus / d);
-        G = std::max<int64_t>(G, (U + cap - 1) / cap);
-        if (G > U) G = U;
-        p.Gkb = (int)G;
-        p.umax = (int)(U / G + ((U % G) ? 1 : 0));
-        p.cnt_off = p.part_off + p.umax * 512;
-        const int ntl_max = (p.umax + ss_min - 1) / ss_min + 1;  // tiles a range can touch
-        const size_t need = (size_t)p.cnt_off + (size_t)(ntl_max + 1) * 4;
+        int64_t G = std::min<int64_t>(std::max(1, num_cus / d), U);
+        size_t need = 0;
+        for (;; G = std::min<int64_t>(U, G + std::max<int64_t>(1, G / 8))) {
+            const int64_t umax = U / G + ((U % G) ? 1 : 0);
+            const int64_t ring = std::min<int64_t>(umax, 4 * ss_max + 24);
+            const int64_t ntl_max = (umax + ss_min - 1) / ss_min + 1;  // tiles a range touches
+            p.umax = (int)umax;
+            p.ring = (int)ring;
+            p.gen_off = p.part_off + (int)ring * 512;
+            p.cnt_off = p.gen_off + (int)ring * 4;
+            need = (size_t)p.cnt_off + (size_t)(ntl_max + 1) * 4;
+            if (need <= lds_max || G == U) break;
+        }
         if (need > lds_max) continue;
+        p.Gkb = (int)G;
         int nslot = 1;
         for (int ss : {ss_min, ss_max})
             for (int64_t t = 0; t < T; ++t) nslot = std::max(nslot, tile_owners(t, ss, G, T));
@@ -486,7 +493,9 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
     p.lds_xsum_off = pl.xsum_off;
     p.lds_part_off = pl.part_off;
     p.lds_cnt_off = pl.cnt_off;
+    p.lds_gen_off = pl.gen_off;
     p.umax = pl.umax;
+    p.ring = pl.ring;
     p.w_bytes = (uint32_t)((int64_t)N * K * bits / 8);
     p.s_bytes = (uint32_t)((int64_t)N * (K / gs) * 2);
     const int bi = bits == 4 ? 0 : 1;
@@ -679,28 +688,30 @@ dfq_status dfq_graph_destroy(dfq_graph* gr) {
 /* ---- introspection used by tests and the benchmark (not part of the drop-in surface) -- */
 
 /* Fills the work split the fast kernel uses for a shape: {T, SS, nkb, Gkb, nslot_kb, kr,
- * lds_bytes, need_ws, ch, umax, chunks, reduce} (SS and kr of the largest k-block). */
-dfq_status dfq_debug_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, int* out12) {
-    if (!out12) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
+ * lds_bytes, need_ws, ch, umax, chunks, reduce, ring} (SS and kr of the largest k-block). */
+dfq_status dfq_debug_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, int* out13) {
+    if (!out13) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
     Plan p;
     dfq_status s = get_plan(ctx, M, N, K, bits, gs, &p);
     if (s) return s;
-    const int v[12] = {p.T,  p.SS,        p.nkb,            p.Gkb, p.nslot_kb, p.kr,
-                       p.lds_bytes, p.need_ws ? 1 : 0, p.ch, p.umax, p.chunks, p.reduce ? 1 : 0};
-    std::memcpy(out12, v, sizeof v);
+    const int v[13] = {p.T,  p.SS,        p.nkb,            p.Gkb, p.nslot_kb, p.kr,
+                       p.lds_bytes, p.need_ws ? 1 : 0, p.ch, p.umax, p.chunks, p.reduce ? 1 : 0,
+                       p.ring};
+    std::memcpy(out13, v, sizeof v);
     return DFQ_OK;
 }
 
 /* The same split computed without a device, for a given CU count and LDS limit. */
 dfq_status dfq_debug_make_plan(int M, int N, int K, int bits, int gs, int num_cus,
-                               size_t lds_max, int* out12) {
-    if (!out12) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
+                               size_t lds_max, int* out13) {
+    if (!out13) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
     Plan p;
     if (!make_plan(M, N, K, bits, gs, num_cus, lds_max, &p))
         return fail(DFQ_ERR_UNSUPPORTED, "no work split");
-    const int v[12] = {p.T,  p.SS,        p.nkb,            p.Gkb, p.nslot_kb, p.kr,
-                       p.lds_bytes, p.need_ws ? 1 : 0, p.ch, p.umax, p.chunks, p.reduce ? 1 : 0};
-    std::memcpy(out12, v, sizeof v);
+    const int v[13] = {p.T,  p.SS,        p.nkb,            p.Gkb, p.nslot_kb, p.kr,
+                       p.lds_bytes, p.need_ws ? 1 : 0, p.ch, p.umax, p.chunks, p.reduce ? 1 : 0,
+                       p.ring};
+    std::memcpy(out13, v, sizeof v);
     return DFQ_OK;
 }
 

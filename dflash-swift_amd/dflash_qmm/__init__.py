@@ -189,10 +189,10 @@ class Context:
                "dfq_workspace_clear")
 
     def plan(self, M, N, K, bits, gs) -> dict:
-        out = (ctypes.c_int * 12)()
+        out = (ctypes.c_int * 13)()
         _check(self.lib.dfq_debug_plan(self.handle, M, N, K, bits, gs, out), "dfq_debug_plan")
         keys = ["T", "SS", "nkb", "Gkb", "nslot_kb", "kr", "lds_bytes", "need_ws", "ch", "umax",
-                "chunks", "reduce"]
+                "chunks", "reduce", "ring"]
         return dict(zip(keys, list(out)))
 
     def qmm_raw(self, x, w, scales, biases, y, M, N, K, bits, gs, xdt, sdt, ydt, lbias=None,

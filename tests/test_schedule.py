@@ -20,12 +20,12 @@ import dflash_qmm
 
 def make_plan(M, N, K, bits, gs, cus=256, lds=163840):
     lib = dflash_qmm.load_library()
-    out = (ctypes.c_int * 12)()
+    out = (ctypes.c_int * 13)()
     rc = lib.dfq_debug_make_plan(M, N, K, bits, gs, cus, lds, out)
     if rc:
         return None
     keys = ["T", "SS", "nkb", "Gkb", "nslot_kb", "kr", "lds_bytes", "need_ws", "ch", "umax",
-            "chunks", "reduce"]
+            "chunks", "reduce", "ring"]
     return dict(zip(keys, list(out)))
 
 
@@ -55,7 +55,9 @@ def take_order(a, b, SS):
 
 def replay(p):
     T, nkb, G, nslot = p["T"], p["nkb"], p["Gkb"], p["nslot_kb"]
-    chunks, umax = p["chunks"], p["umax"]
+    chunks, umax, R = p["chunks"], p["umax"], p["ring"]
+    # the ring of partial slots holds at least every unit one tile can have in a range
+    assert R <= umax and R >= min(-(-chunks // nkb), umax), (R, umax)
     seen = set()
     y_writes = {}
     ws_slots = {}
@@ -104,17 +106,25 @@ def replay(p):
             assert ntl <= (umax + (chunks // nkb) - 1) // (chunks // nkb) + 1  # LDS counters
             part = {}
             tcnt = [0] * ntl
-            for u in order:                                   # any wave, one unit at a time
+            gen = list(range(R))                              # slot generations
+            g_of = {u: g for g, u in enumerate(order)}
+            for g, u in enumerate(order):                     # any wave, one unit at a time
                 key = (kb, u // SS, u % SS)
                 assert key not in seen, f"unit {key} computed twice"
                 seen.add(key)
-                assert 0 <= u - a < umax                      # its LDS partial slot
-                part[u - a] = key
+                assert 0 <= u - a < umax
+                assert gen[g % R] == g, (kb, cl, g)           # its ring slot is released
+                part[g % R] = key
                 t = u // SS
                 u0, u1 = max(a, t * SS), min(b, (t + 1) * SS)
                 tcnt[t - ta] += 1
                 if tcnt[t - ta] == u1 - u0:                   # the arrival that completes t
-                    units = {part[uu - a] for uu in range(u0, u1)}
+                    g0 = g_of[u0]
+                    assert [g_of[uu] for uu in range(u0, u1)] == list(range(g0, g0 + u1 - u0))
+                    units = {part[(g0 + i) % R] for i in range(u1 - u0)}
+                    for i in range(1, u1 - u0):               # the summing wave releases
+                        gen[(g0 + i) % R] = g0 + i + R
+                    gen[g0 % R] = g0 + R                      # the publisher, after reading
                     if u0 == t * SS and u1 == (t + 1) * SS and nkb == 1:
                         finalize(t, units)
                     else:
