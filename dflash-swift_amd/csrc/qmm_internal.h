@@ -13,6 +13,7 @@ namespace dfq {
 /* The fast kernel's work split for one problem shape (see qmm_params.h). */
 struct Plan {
     int kss = 0;        /* k per super-step                                  */
+    int mt = 0;         /* row tiles of 8 (2 for 9..16 rows)                 */
     int T = 0;          /* column tiles of 16                                */
     int ch = 0;         /* super-steps per chunk (1, or 8 groups' worth)     */
     int chunks = 0;     /* chunks of K                                       */

@@ -361,11 +361,13 @@ __device__ __forceinline__ KBlock kblock(const QmmParams& p, int kb) {
     return KBlock{c0, SS, U / p.Gkb, U % p.Gkb};
 }
 
-/* Partial-tile slot j of k-block kb for tile t in the workspace: [T][nkb][nslot_kb][128]
- * fp32, lane (q, n) of lanes 0-31 owning floats n*8 + q*4 .. +3. */
-__device__ __forceinline__ float* tile_slot(const QmmParams& p, int t, int kb, int j, int lane) {
-    return p.slots + ((size_t)(t * p.nkb + kb) * p.nslot_kb + j) * 128 + (lane & 15) * 8 +
-           (lane >> 4) * 4;
+/* Partial-tile slot j of k-block kb for tile t in the workspace: [T][nkb][nslot_kb][MT][128]
+ * fp32 (MT row tiles of 8), lane (q, n) of lanes 0-31 owning floats n*8 + q*4 .. +3 of each
+ * row tile. */
+__device__ __forceinline__ float* tile_slot(const QmmParams& p, int t, int kb, int j, int mt,
+                                            int lane) {
+    return p.slots + (((size_t)(t * p.nkb + kb) * p.nslot_kb + j) * p.mt + mt) * 128 +
+           (lane & 15) * 8 + (lane >> 4) * 4;
 }
 
 /* One partial tile (8 rows x 16 columns, fp32) as held by lanes 0-31: lane (q, n) holds
@@ -375,8 +377,9 @@ struct Tile {
     int lane;
 };
 
+/* Row tile mt (rows 8*mt ..) of tile t, as held by lanes 0-31, plus the linear bias, to y. */
 template <bool F16>
-__device__ __forceinline__ void store_y(const QmmParams& p, int t, int lane, f32x4_t v) {
+__device__ __forceinline__ void store_y(const QmmParams& p, int t, int mt, int lane, f32x4_t v) {
     const int q = lane >> 4, n = lane & 15;
     const int col = t * 16 + n;
     if (lane >= 32 || col >= p.N) return;
@@ -385,7 +388,7 @@ __device__ __forceinline__ void store_y(const QmmParams& p, int t, int lane, f32
     uint16_t* y = (uint16_t*)p.y;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        const int m = 4 * q + r;
+        const int m = 8 * mt + 4 * q + r;
         if (m < p.M) y[(size_t)m * p.N + col] = f32_to_out<F16>(v[r] + lb);
     }
 }
@@ -407,16 +410,17 @@ __device__ __forceinline__ void store_y(const QmmParams& p, int t, int lane, f32
  * in the counter scheme the slot stores are waited for before the counter increment, and
  * the last contributor only reads slots after its own increment has returned. */
 template <bool F16>
-__device__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t, int slot,
-                        int lane, f32x4_t v) {
+__device__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t, int mt,
+                        int slot, int lane, f32x4_t v) {
     const int q = lane >> 4, n = lane & 15;
     const int nwg = owner_wg(t * SS + SS - 1, base_u, rem_u) - owner_wg(t * SS, base_u, rem_u) + 1;
     const uint32_t total = (uint32_t)(p.nkb * nwg);
-    uint32_t* base = (uint32_t*)p.slots + (size_t)t * p.nkb * p.nslot_kb * 128;
+    /* the tile's workspace area: nkb*nslot_kb slots of MT*128 floats */
+    uint32_t* base = (uint32_t*)p.slots + (size_t)t * p.nkb * p.nslot_kb * p.mt * 128;
     if (total == 2) {
         const int col = t * 16 + n;
         if (lane < 32) {
-            uint64_t* sl = (uint64_t*)base + n * 8 + q * 4;
+            uint64_t* sl = (uint64_t*)base + mt * 128 + n * 8 + q * 4;
             uint64_t old[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r)
@@ -427,7 +431,7 @@ __device__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 if (!(old[r] >> 32)) continue;
-                const int m = 4 * q + r;
+                const int m = 8 * mt + 4 * q + r;
                 const float sum = v[r] + __uint_as_float((uint32_t)old[r]);
                 if (m < p.M && col < p.N)
                     ((uint16_t*)p.y)[(size_t)m * p.N + col] = f32_to_out<F16>(sum + lb);
@@ -436,8 +440,10 @@ __device__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t
         }
         return;
     }
+    /* more than two parts: unused when the split runs in reduce mode (the planner's choice
+     * whenever a tile can have more than two parts); kept for one row tile */
     if (lane < 32) {
-        uint32_t* sl = base + (size_t)slot * 128 + n * 8 + q * 4;
+        uint32_t* sl = base + ((size_t)slot * p.mt + mt) * 128 + n * 8 + q * 4;
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             __hip_atomic_store(sl + r, __float_as_uint(v[r]), __ATOMIC_RELAXED,
@@ -446,7 +452,7 @@ __device__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     uint32_t old = 0;
     if (lane == 0)
-        old = __hip_atomic_fetch_add(p.counters + t, 1u, __ATOMIC_RELAXED,
+        old = __hip_atomic_fetch_add(p.counters + t * p.mt + mt, 1u, __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_AGENT);
     old = __builtin_amdgcn_readfirstlane(old);
     if (old + 1 != total) return;
@@ -454,16 +460,18 @@ __device__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t
     if (lane < 32) {
         for (int kb = 0; kb < p.nkb; ++kb)
             for (int j = 0; j < nwg; ++j) {
-                uint32_t* sl = base + ((size_t)kb * p.nslot_kb + j) * 128 + n * 8 + q * 4;
+                uint32_t* sl = base + (((size_t)kb * p.nslot_kb + j) * p.mt + mt) * 128 +
+                               n * 8 + q * 4;
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     sum[r] += __uint_as_float(__hip_atomic_exchange(
                         sl + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
             }
     }
-    store_y<F16>(p, t, lane, sum);
+    store_y<F16>(p, t, mt, lane, sum);
     if (lane == 0)
-        __hip_atomic_store(p.counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.counters + t * p.mt + mt, 0u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
 }
 
 /* The publisher wave of a qmm_mt8 workgroup.  The streaming waves only sum a finished tile
@@ -475,7 +483,7 @@ __device__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t
  * It polls the tile counters of its workgroup (one lane per tile, sleeping between empty
  * polls) until each of the ntl tiles has been written.  Every unit of [a, b) is taken by
  * exactly one streaming wave, so every tile reaches kTileDone and the loop ends. */
-template <bool F16>
+template <bool F16, int MT>
 __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b, int SS,
                                int base_u, int rem_u, int lane) {
     const int q = lane >> 4, n = lane & 15;
@@ -503,22 +511,30 @@ __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
                 const int u0 = max(a, t * SS), u1 = min(b, (t + 1) * SS);
                 const int g0 = u0 >= s1 ? u0 - s1 : nrot + (u0 - a);  // take index of u0
                 const int sl0 = g0 % p.ring;
-                f32x4_t v = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (lane < 32) v = *(const f32x4_t*)(part + sl0 * 128 + n * 8 + q * 4);
+                f32x4_t v[MT];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    v[mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                    if (lane < 32)
+                        v[mt] = *(const f32x4_t*)(part + (sl0 * MT + mt) * 128 + n * 8 + q * 4);
+                }
                 /* the tile's sum is read: its slot may take the unit p.ring takes later (LDS
                  * operations of a wave complete in order, so the read precedes the release) */
                 if (lane == 0)
                     __hip_atomic_store(gen + sl0, (uint32_t)(g0 + p.ring), __ATOMIC_RELEASE,
                                        __HIP_MEMORY_SCOPE_WORKGROUP);
                 const int first = owner_wg(t * SS, base_u, rem_u);
-                if (u0 == t * SS && u1 == (t + 1) * SS && p.nkb == 1) {
-                    store_y<F16>(p, t, lane, v);
-                } else if (p.reduce) {
-                    /* summed by dfq_qmm_reduce after this kernel: no round trip here */
-                    if (lane < 32) *(f32x4_t*)tile_slot(p, t, kb, cl - first, lane) = v;
-                } else {
-                    publish<F16>(p, SS, base_u, rem_u, t, kb * p.nslot_kb + (cl - first), lane,
-                                 v);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    if (u0 == t * SS && u1 == (t + 1) * SS && p.nkb == 1) {
+                        store_y<F16>(p, t, mt, lane, v[mt]);
+                    } else if (p.reduce) {
+                        /* summed by dfq_qmm_reduce after this kernel: no round trip here */
+                        if (lane < 32) *(f32x4_t*)tile_slot(p, t, kb, cl - first, mt, lane) = v[mt];
+                    } else {
+                        publish<F16>(p, SS, base_u, rem_u, t, mt, kb * p.nslot_kb + (cl - first),
+                                     lane, v[mt]);
+                    }
                 }
                 if (lane == 0) tcnt[base + bit] = kTileOut;
                 ++found;
@@ -536,9 +552,10 @@ __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
 /* CH super-steps form one work unit ("chunk").  With CH = 8 / GPS a chunk spans exactly 8
  * quantisation groups, so each lane fetches the chunk's scales (and biases) of its row as
  * one 16-byte load; CH = 1 is the general form (one 4-byte scale load per super-step). */
-template <int BITS, int GS, bool F16, int CH, int PF>
+template <int BITS, int GS, bool F16, int CH, int PF, int MT>
 __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     using C = Cfg<BITS, GS>;
+    constexpr int XR = 8 * MT;  // rows of x sums per group in LDS
     static_assert(CH == 1 || CH * C::GPS == 8, "chunk = one super-step or 8 groups");
     uint8_t* lds = lds_base();
 
@@ -556,7 +573,7 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     const int b = wg_start(cl + 1, kbk.base, kbk.rem);
 
     if (wave == kWaves) {
-        publisher_wave<F16>(p, kb, cl, a, b, SS, kbk.base, kbk.rem, lane);
+        publisher_wave<F16, MT>(p, kb, cl, a, b, SS, kbk.base, kbk.rem, lane);
         return;
     }
 
@@ -678,13 +695,13 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
             if (act) {
                 const u32x4_t v = (BITS == 4) ? nibble_permute(xv[i]) : xv[i];
                 *(u32x4_t*)(lds + (size_t)(1 + r) * RS + cc * 16) = v;
-                if ((cc & (GS / 8 - 1)) == 0) xsum[(cc / (GS / 8)) * 8 + r] = sm;
+                if ((cc & (GS / 8 - 1)) == 0) xsum[(cc / (GS / 8)) * XR + r] = sm;
             }
         }
     }
     for (int c = tid; c < CPR; c += kThreads) *(u32x4_t*)(lds + c * 16) = u32x4_t{0, 0, 0, 0};
-    for (int i = tid; i < GK * 8; i += kThreads)
-        if ((i & 7) >= p.M) xsum[i] = 0.0f;
+    for (int i = tid; i < GK * XR; i += kThreads)
+        if ((i & (XR - 1)) >= p.M) xsum[i] = 0.0f;
     for (int i = tid; i < ntl; i += kThreads) tcnt[i] = 0u;
     for (int i = tid; i < R; i += kThreads) gen[i] = (uint32_t)i;
     if (tid == 0) *gcnt = (uint32_t)(kWaves * PF);
@@ -698,10 +715,14 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
 
     /* ---- per-lane A / x-sum addresses */
     const bool diag = (n < 8) == (q < 2);
-    const int arow = (diag && (n & 7) < p.M) ? 1 + (n & 7) : 0;
-    const uint32_t abase = (uint32_t)arow * RS + (uint32_t)C::base_chunk(q) * 16u;
-    const uint32_t xbase =
-        (uint32_t)p.lds_xsum_off + (uint32_t)C::group_of(0, q) * 32u + (uint32_t)(q & 1) * 16u;
+    uint32_t abase[MT];  // row tile mt reads x rows 8*mt + (n & 7) (row 0 of LDS is zeros)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int arow = (diag && 8 * mt + (n & 7) < p.M) ? 1 + 8 * mt + (n & 7) : 0;
+        abase[mt] = (uint32_t)arow * RS + (uint32_t)C::base_chunk(q) * 16u;
+    }
+    const uint32_t xbase = (uint32_t)p.lds_xsum_off + (uint32_t)C::group_of(0, q) * (XR * 4u) +
+                           (uint32_t)(q & 1) * 16u;
     const uint32_t sel_half = (q >> 1) ? kSelHi : kSelLo;
     constexpr float kOff = (BITS == 4) ? (F16 ? 1024.0f : 128.0f) : 0.0f;
     uint32_t magic = F16 ? 0x64006400u : 0x43004300u;
@@ -716,25 +737,33 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
         const int t = u / SS, cc = u - t * SS;
         SV rs_i, rb_i;
         split_scale_bias(rsb[i], rs_i, rb_i);
-        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        f32x4_t acc[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int j = 0; j < CH; ++j) {
             const int css = cc * CH + j;  // super-step within the k-block
             uint32_t OW[C::NOW];
             build_operand_words<BITS, GS>(rw[i][j], OW);
-            const uint32_t aoff = abase + (uint32_t)css * (C::CPS * 16);
-            f32x4_t P[C::NP];
+            f32x4_t P[MT][C::NP];
 #pragma unroll
-            for (int pp = 0; pp < C::NP; ++pp) P[pp] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int pp = 0; pp < C::NP; ++pp) P[mt][pp] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int o = 0; o < C::NOPS; ++o) {
-                const u32x4_t A = *(const u32x4_t*)(lds + aoff + C::delta_chunk(o) * 16);
                 u32x4_t B;
                 if constexpr (BITS == 4) B = nibble_operand<F16>(OW[o], nmask, magic);
                 else B = byte_operand<F16>(OW[2 * o], OW[2 * o + 1]);
-                P[C::partial_of(o)] = mfma<F16>(A, B, P[C::partial_of(o)]);
+                /* one decoded B operand serves every row tile */
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const uint32_t aoff = abase[mt] + (uint32_t)css * (C::CPS * 16);
+                    const u32x4_t A = *(const u32x4_t*)(lds + aoff + C::delta_chunk(o) * 16);
+                    P[mt][C::partial_of(o)] = mfma<F16>(A, B, P[mt][C::partial_of(o)]);
+                }
             }
-            const uint32_t xo = xbase + (uint32_t)css * (C::GPS * 32);
+            const uint32_t xo = xbase + (uint32_t)css * (C::GPS * XR * 4);
 #pragma unroll
             for (int pp = 0; pp < C::NP; ++pp) {
                 uint32_t sw, bw2, sel;
@@ -756,23 +785,28 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
                 const float s = half_sel<F16>(sw, sel);
                 const float bb = half_sel<F16>(bw2, sel);
                 const float bp = (kOff != 0.0f) ? __builtin_fmaf(-kOff, s, bb) : bb;
-                const f32x4_t X = *(const f32x4_t*)(lds + xo + pp * 32);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    acc[r] = __builtin_fmaf(s, P[pp][r], acc[r]);
-                    acc[r] = __builtin_fmaf(bp, X[r], acc[r]);
+                for (int mt = 0; mt < MT; ++mt) {
+                    const f32x4_t X = *(const f32x4_t*)(lds + xo + pp * (XR * 4) + mt * 32);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        acc[mt][r] = __builtin_fmaf(s, P[mt][pp][r], acc[mt][r]);
+                        acc[mt][r] = __builtin_fmaf(bp, X[r], acc[mt][r]);
+                    }
                 }
             }
         }
-        /* fold the two group halves (lanes 0-31 hold the 8x16 partial) and park it */
-        f32x4_t v;
+        /* fold the two group halves (lanes 0-31 hold each 8x16 partial) and park them */
+        f32x4_t v[MT];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            uint32_t lo = __float_as_uint(acc[r]), hi = lo;
-            permlane32_swap(lo, hi);
-            /* lanes 0-31: own value + the value of lane + 32 */
-            v[r] = __uint_as_float(lo) + __uint_as_float(hi);
-        }
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                uint32_t lo = __float_as_uint(acc[mt][r]), hi = lo;
+                permlane32_swap(lo, hi);
+                /* lanes 0-31: own value + the value of lane + 32 */
+                v[mt][r] = __uint_as_float(lo) + __uint_as_float(hi);
+            }
         /* the slot of take g: wait until the unit that held it last (take g - R) is
          * released (never, when the range fits the ring) */
         const int sl = g % R;
@@ -781,7 +815,11 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
                                           __HIP_MEMORY_SCOPE_WORKGROUP) != g)
                 __builtin_amdgcn_s_sleep(1);
         }
-        if (lane < 32) *(f32x4_t*)(part + sl * 128 + n * 8 + q * 4) = v;
+        if (lane < 32) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+                *(f32x4_t*)(part + (sl * MT + mt) * 128 + n * 8 + q * 4) = v[mt];
+        }
         /* arrive at tile t; the wave that completes its units here sums them (in unit order)
          * into the slot of the tile's first unit, releases the other slots, and hands the
          * tile to the publisher wave */
@@ -795,10 +833,13 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
             const int g0 = u0 >= s1 ? u0 - s1 : nrot + (u0 - a);  // the tile's takes: g0..
             const int sl0 = g0 % R;
             if (lane < 32) {
-                f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
-                for (int i = 0, s2 = sl0; i < u1 - u0; ++i, s2 = (s2 + 1 == R) ? 0 : s2 + 1)
-                    sum += *(const f32x4_t*)(part + s2 * 128 + n * 8 + q * 4);
-                *(f32x4_t*)(part + sl0 * 128 + n * 8 + q * 4) = sum;
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
+                    for (int i = 0, s2 = sl0; i < u1 - u0; ++i, s2 = (s2 + 1 == R) ? 0 : s2 + 1)
+                        sum += *(const f32x4_t*)(part + (s2 * MT + mt) * 128 + n * 8 + q * 4);
+                    *(f32x4_t*)(part + (sl0 * MT + mt) * 128 + n * 8 + q * 4) = sum;
+                }
             }
             if (lane == 0) {
                 for (int i = 1; i < u1 - u0; ++i)
@@ -1010,7 +1051,7 @@ extern "C" __global__ void __launch_bounds__(256) dfq_argmax_accept_f16(
  * the workspace zero at rest.  Tiles with one contributor were written by qmm_mt8. */
 template <bool F16>
 __device__ __forceinline__ void qmm_reduce(const QmmParams& p) {
-    const int t = blockIdx.x, lane = threadIdx.x;
+    const int t = blockIdx.x / p.mt, mt = blockIdx.x - t * p.mt, lane = threadIdx.x;
     f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
     int parts = 0;
     for (int kb = 0; kb < p.nkb; ++kb) {
@@ -1019,13 +1060,13 @@ __device__ __forceinline__ void qmm_reduce(const QmmParams& p) {
         const int nwg = owner_wg(t * k.SS + k.SS - 1, k.base, k.rem) - first + 1;
         for (int j = 0; j < nwg; ++j, ++parts) {
             if (lane < 32) {
-                f32x4_t* sl = (f32x4_t*)tile_slot(p, t, kb, j, lane);
+                f32x4_t* sl = (f32x4_t*)tile_slot(p, t, kb, j, mt, lane);
                 sum += *sl;
                 *sl = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
             }
         }
     }
-    if (parts > 1) store_y<F16>(p, t, lane, sum);
+    if (parts > 1) store_y<F16>(p, t, mt, lane, sum);
 }
 
 extern "C" __global__ void __launch_bounds__(64) dfq_qmm_reduce_bf16(QmmParams p) {
@@ -1046,14 +1087,16 @@ constexpr int prefetch_depth() {
     return d < 1 ? 1 : (d > 8 ? 8 : d);
 }
 
-#define DFQ_MT8_KERNEL(BITS, GS, F16, NAME, CHN, CH)                                        \
+#define DFQ_MT8_KERNEL(BITS, GS, F16, NAME, CHN, CH, MTN, MT)                               \
     extern "C" __global__ void __launch_bounds__(kBlock)                                     \
-        dfq_qmm_mt8_b##BITS##_g##GS##_##NAME##_##CHN(QmmParams p) {                           \
-        qmm_mt8<BITS, GS, F16, CH, prefetch_depth<BITS, GS, CH>()>(p);                        \
+        dfq_qmm_##MTN##_b##BITS##_g##GS##_##NAME##_##CHN(QmmParams p) {                       \
+        qmm_mt8<BITS, GS, F16, CH, prefetch_depth<BITS, GS, CH>(), MT>(p);                    \
     }
+/* per format: one super-step or 8-group chunks at up to 8 rows; 8-group chunks at up to 16 */
 #define DFQ_MT8_FORMAT(BITS, GS, F16, NAME)                                                    \
-    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c1, 1)                                                \
-    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS))
+    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c1, 1, mt8, 1)                                        \
+    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt8, 1)                 \
+    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt16, 2)
 
 DFQ_MT8_FORMAT(4, 32, false, bf16)
 DFQ_MT8_FORMAT(4, 64, false, bf16)

@@ -40,6 +40,7 @@ typedef struct QmmParams {
     float* slots;           /* workspace: per-tile partial sums                       */
     uint32_t* counters;     /* workspace: per-tile arrival counters (zero at rest)    */
     int32_t M, N, K;
+    int32_t mt;             /* row tiles of 8 the launch computes (1: M<=8, 2: M<=16) */
     int32_t T;              /* column tiles of 16                                     */
     int32_t chunks;         /* chunks of K                                            */
     int32_t nkb;            /* k-blocks                                               */

@@ -78,6 +78,7 @@ struct dfq_ctx {
     size_t lds_max = 0;
     hipModule_t module = nullptr;
     hipFunction_t mt8[2][3][2][2] = {};  // [bits 4/8][gs 32/64/128][bf16/f16][chunk 1/8 groups]
+    hipFunction_t mt16[2][3][2] = {};    // up to 16 rows, 8-group chunks [bits][gs][bf16/f16]
     hipFunction_t reduce[2] = {};        // second pass of reduce splits [bf16/f16]
     hipFunction_t silu_mul[2] = {};      // SiLU-mul of a fused gate||up output [bf16/f16]
     hipFunction_t argmax_accept[2] = {}; // greedy accept of a verify pass [bf16/f16]
@@ -144,10 +145,13 @@ static int tile_owners(int64_t t, int64_t SS, int64_t G, int64_t T) {
 
 bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_max, Plan* pl) {
     const int kss = kss_for(bits, gs);
-    if (M < 1 || M > 8 || N < 1 || K < kss || K % kss) return false;
+    if (M < 1 || M > 16 || N < 1 || K < kss || K % kss) return false;
     /* A chunk of 8 groups lets each lane fetch its row's scales with one 16-byte load. */
     const int gps = kss / gs;
     const int ch = (K % (kss * (8 / gps)) == 0) ? 8 / gps : 1;
+    /* 9..16 rows: two row tiles per weight tile, built for 8-group chunks only */
+    const int mt = M > 8 ? 2 : 1;
+    if (mt == 2 && ch == 1) return false;
     const int kch = kss * ch;
     const int chunks = K / kch;
     const int T = (N + 15) / 16;
@@ -160,6 +164,7 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
         if ((int64_t)M * (kr / 8) > (int64_t)kMaxStageItems * kThreads) continue;
         Plan p{};
         p.kss = kss;
+        p.mt = mt;
         p.ch = ch;
         p.T = T;
         p.chunks = chunks;
@@ -168,8 +173,8 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
         p.SS = ss_max;
         p.rs = 2 * kr + 16;
         p.xsum_off = ((M + 1) * p.rs + 15) & ~15;
-        p.part_off = p.xsum_off + (kr / gs) * 32;
-        /* Partial tiles live in a ring of 512-byte LDS slots over the take order: a range's
+        p.part_off = p.xsum_off + (kr / gs) * 32 * mt;
+        /* Partial tiles live in a ring of 512*mt-byte LDS slots over the take order: a range's
          * whole length when it is short, else enough for the units in flight plus a few
          * tiles waiting for their sum (at least the units one tile can have in a range, which
          * keeps the ring free of deadlock), plus a 4-byte generation per slot and a counter
@@ -184,7 +189,7 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
             const int64_t ntl_max = (umax + ss_min - 1) / ss_min + 1;  // tiles a range touches
             p.umax = (int)umax;
             p.ring = (int)ring;
-            p.gen_off = p.part_off + (int)ring * 512;
+            p.gen_off = p.part_off + (int)ring * 512 * mt;
             p.cnt_off = p.gen_off + (int)ring * 4;
             need = (size_t)p.cnt_off + (size_t)(ntl_max + 1) * 4;
             if (need <= lds_max || G == U) break;
@@ -202,29 +207,40 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
         const size_t want = std::max(need, lds_max / 2 + 256);
         p.lds_bytes = (int)std::min(want, lds_max);
         p.need_ws = d > 1 || nslot > 1;
-        p.ws_counter_bytes = ((size_t)T * 4 + 255) & ~(size_t)255;
-        p.ws_bytes = p.need_ws ? p.ws_counter_bytes + (size_t)T * d * nslot * 128 * 4 : 0;
+        p.ws_counter_bytes = ((size_t)T * mt * 4 + 255) & ~(size_t)255;
+        p.ws_bytes = p.need_ws ? p.ws_counter_bytes + (size_t)T * d * nslot * mt * 128 * 4 : 0;
         *pl = p;
         return true;
     }
     return false;
 }
 
-static dfq_status get_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, Plan* out) {
+/* The cached split for a shape; a shape with none is cached too (T == 0). */
+static bool find_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, Plan* out) {
     PlanKey key{M, N, K, bits, gs};
     std::lock_guard<std::mutex> lk(ctx->mu);
     auto it = ctx->plans.find(key);
-    if (it != ctx->plans.end()) {
-        *out = it->second;
-        return DFQ_OK;
+    if (it == ctx->plans.end()) {
+        Plan p;
+        if (!make_plan(M, N, K, bits, gs, ctx->num_cus, ctx->lds_max, &p)) p = Plan{};
+        it = ctx->plans.emplace(key, p).first;
     }
-    Plan p;
-    if (!make_plan(M, N, K, bits, gs, ctx->num_cus, ctx->lds_max, &p))
+    *out = it->second;
+    return out->T > 0;
+}
+
+static dfq_status get_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, Plan* out) {
+    if (!find_plan(ctx, M, N, K, bits, gs, out))
         return fail(DFQ_ERR_UNSUPPORTED, "no work split for M=%d N=%d K=%d bits=%d gs=%d", M, N,
                     K, bits, gs);
-    ctx->plans.emplace(key, p);
-    *out = p;
     return DFQ_OK;
+}
+
+/* 9..16 rows run in one launch with two row tiles when the shape has such a split, else as
+ * two launches of up to 8 rows over the same weights. */
+static bool one_pass(dfq_ctx* ctx, int M, int N, int K, int bits, int gs) {
+    Plan p;
+    return M <= 8 || find_plan(ctx, M, N, K, bits, gs, &p);
 }
 
 static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
@@ -305,6 +321,15 @@ dfq_status dfq_init(int device, dfq_ctx** out) {
                     snprintf(name, sizeof name, "dfq_qmm_mt8_b%d_g%d_%s_%s", kBits[b], kGs[g2],
                              kDt[d], kCh[c]);
                     if ((e = hipModuleGetFunction(&ctx->mt8[b][g2][d][c], ctx->module, name)) !=
+                        hipSuccess) {
+                        (void)hipModuleUnload(ctx->module);
+                        delete ctx;
+                        return hip_fail(e, name);
+                    }
+                    if (c == 0) continue;
+                    snprintf(name, sizeof name, "dfq_qmm_mt16_b%d_g%d_%s_c8", kBits[b], kGs[g2],
+                             kDt[d]);
+                    if ((e = hipModuleGetFunction(&ctx->mt16[b][g2][d], ctx->module, name)) !=
                         hipSuccess) {
                         (void)hipModuleUnload(ctx->module);
                         delete ctx;
@@ -416,8 +441,9 @@ int dfq_qmm_supported(const dfq_ctx* ctx, int M, int N, int K, int bits, int gs,
     int ok = s == DFQ_OK;
     if (ok) {
         Plan p;
-        ok = make_plan(std::min(M, 8), N, K, bits, gs, ctx->num_cus, ctx->lds_max, &p) &&
-             (M <= 8 || make_plan(M - 8, N, K, bits, gs, ctx->num_cus, ctx->lds_max, &p));
+        ok = make_plan(M, N, K, bits, gs, ctx->num_cus, ctx->lds_max, &p) ||
+             (M > 8 && make_plan(8, N, K, bits, gs, ctx->num_cus, ctx->lds_max, &p) &&
+              make_plan(M - 8, N, K, bits, gs, ctx->num_cus, ctx->lds_max, &p));
     }
     g_last_error = saved;
     return ok;
@@ -432,13 +458,15 @@ dfq_status dfq_qmm_workspace_bytes(dfq_ctx* ctx, int M, int N, int K, int bits, 
     dfq_status s = check_fast_args(ctx, M, N, K, bits, gs, DFQ_BF16, DFQ_BF16, DFQ_BF16);
     if (s) return s;
     Plan p;
-    if ((s = get_plan(ctx, std::min(M, 8), N, K, bits, gs, &p))) return s;
-    size_t need = p.ws_bytes;
-    if (M > 8) {
-        if ((s = get_plan(ctx, M - 8, N, K, bits, gs, &p))) return s;
-        need = std::max(need, p.ws_bytes);
+    if (one_pass(ctx, M, N, K, bits, gs)) {
+        if ((s = get_plan(ctx, M, N, K, bits, gs, &p))) return s;
+        *bytes = p.ws_bytes;
+        return DFQ_OK;
     }
-    *bytes = need;
+    if ((s = get_plan(ctx, 8, N, K, bits, gs, &p))) return s;
+    size_t need = p.ws_bytes;
+    if ((s = get_plan(ctx, M - 8, N, K, bits, gs, &p))) return s;
+    *bytes = std::max(need, p.ws_bytes);
     return DFQ_OK;
 }
 
@@ -483,6 +511,7 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
     p.M = M;
     p.N = N;
     p.K = K;
+    p.mt = pl.mt;
     p.T = pl.T;
     p.chunks = pl.chunks;
     p.nkb = pl.nkb;
@@ -503,13 +532,13 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
     const int di = dt == DFQ_BF16 ? 0 : 1;
     void* args[] = {&p};
     const int ci = pl.ch > 1 ? 1 : 0;
-    hipError_t e = hipModuleLaunchKernel(ctx->mt8[bi][gi][di][ci], (unsigned)(pl.nkb * pl.Gkb), 1, 1,
-                                         kBlockThreads, 1, 1, (unsigned)pl.lds_bytes, stream, args,
-                                         nullptr);
+    hipFunction_t fn = pl.mt == 2 ? ctx->mt16[bi][gi][di] : ctx->mt8[bi][gi][di][ci];
+    hipError_t e = hipModuleLaunchKernel(fn, (unsigned)(pl.nkb * pl.Gkb), 1, 1, kBlockThreads, 1,
+                                         1, (unsigned)pl.lds_bytes, stream, args, nullptr);
     if (e != hipSuccess) return hip_fail(e, "launch dfq_qmm_mt8");
     if (pl.reduce) {
-        e = hipModuleLaunchKernel(ctx->reduce[di], (unsigned)pl.T, 1, 1, 64, 1, 1, 0, stream, args,
-                                  nullptr);
+        e = hipModuleLaunchKernel(ctx->reduce[di], (unsigned)(pl.T * pl.mt), 1, 1, 64, 1, 1, 0,
+                                  stream, args, nullptr);
         if (e != hipSuccess) return hip_fail(e, "launch dfq_qmm_reduce");
     }
     return DFQ_OK;
@@ -529,7 +558,10 @@ dfq_status dfq_qmm(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* s
                     "x and w must be 16-byte aligned, scales/biases 4-byte aligned");
     DeviceGuard g(ctx->device);
     const size_t esz = 2;
-    /* Rows beyond 8 run as a second 8-row pass over the same weights. */
+    if (one_pass(ctx, M, N, K, bits, gs))
+        return launch_mt8(ctx, x, w, scales, biases, lbias, y, M, N, K, bits, gs, xdt, ws, wsb,
+                          (hipStream_t)stream);
+    /* 9..16 rows with one-super-step chunks: two passes of up to 8 rows over the weights. */
     for (int m0 = 0; m0 < M; m0 += 8) {
         const int mc = std::min(8, M - m0);
         s = launch_mt8(ctx, (const char*)x + (size_t)m0 * K * esz, w, scales, biases, lbias,

@@ -93,8 +93,10 @@ int dfq_is_eligible(int out_features, int in_features, int bits, int group_size,
 int dfq_tiles_for(int rows);
 
 /* Whether dfq_qmm's kernels handle this problem (wider than the reference gate: any
- * M in 1..8, N >= 1, group 32/64/128, bits 4/8, bf16 or fp16 throughout, K a multiple
- * of the kernel's super-step).  Returns 1 / 0. */
+ * M in 1..16, N >= 1, group 32/64/128, bits 4/8, bf16 or fp16 throughout, K a multiple
+ * of the kernel's super-step).  9..16 rows run in one launch with two row tiles per
+ * weight tile when K is a multiple of 8 groups, else as two launches of up to 8 rows.
+ * Returns 1 / 0. */
 int dfq_qmm_supported(const dfq_ctx* ctx, int M, int N, int K, int bits, int group_size,
                       dfq_dtype x_dtype, dfq_dtype sb_dtype, dfq_dtype y_dtype);
 

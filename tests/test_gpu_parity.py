@@ -39,6 +39,22 @@ SMALL_CASES = [
     (8, 17, 8192, 8, 64, BF16),
 ]
 
+# 9..16 rows: two row tiles per weight tile in one launch (every format), and the two-launch
+# path for K that is not a multiple of 8 groups (the last case).
+SIXTEEN_ROW_CASES = [
+    (9, 16, 512, 4, 64, BF16),
+    (16, 257, 1024, 4, 64, BF16),
+    (12, 300, 512, 4, 32, BF16),
+    (16, 333, 1024, 4, 128, BF16),
+    (16, 200, 512, 8, 32, F16),
+    (13, 130, 1024, 8, 64, BF16),
+    (16, 130, 1024, 8, 128, F16),
+    (11, 96, 1024, 4, 64, F16),
+    (16, 48, 16384, 4, 64, BF16),    # several k-blocks and workgroups per tile
+    (15, 5000, 12288, 4, 64, BF16),
+    (10, 100, 384, 4, 64, BF16),     # one-super-step chunks: two launches of up to 8 rows
+]
+
 
 def run_fast(ctx, c):
     x, w, s, b, lb = upload(c)
@@ -56,6 +72,17 @@ def test_small_shapes_match_oracle(ctx, oracle, M, N, K, bits, gs, dt):
     assert rel <= TOL and ok, f"max rel err {rel:.3e}"
 
 
+@pytest.mark.parametrize("M,N,K,bits,gs,dt", SIXTEEN_ROW_CASES)
+def test_sixteen_row_shapes_match_oracle(ctx, oracle, M, N, K, bits, gs, dt):
+    c = make_case(M, N, K, bits=bits, gs=gs, xdt=dt, seed=M * 1000 + N + K + bits + gs,
+                  lbias=(N % 2 == 0))
+    announce(f"sixteen-row M={M} N={N} K={K} bits={bits} gs={gs} dt={dt}")
+    y = download(run_fast(ctx, c))
+    ref = oracle.qmm_f64(c)
+    rel, ok = tolerance_check(y, ref)
+    assert rel <= TOL and ok, f"max rel err {rel:.3e}"
+
+
 @pytest.mark.parametrize("name,M", [
     ("c1_m1_k4096_n4096_f16", 1),
     ("c2_gateup_k5120_n17408", 1), ("c2_gateup_k5120_n17408", 2),
@@ -64,6 +91,9 @@ def test_small_shapes_match_oracle(ctx, oracle, M, N, K, bits, gs, dt):
     ("c3_down_k17408_n5120", 8),
     ("c4_qkv_8bit_g64", 8), ("c4_o_8bit_g64", 8),
     ("c4_qkv_4bit_g32", 8), ("c4_o_4bit_g32", 8),
+    ("c2_gateup_k5120_n17408", 9), ("c2_gateup_k5120_n17408", 12),
+    ("c2_gateup_k5120_n17408", 16), ("c3_down_k17408_n5120", 16),
+    ("c4_qkv_8bit_g64", 16), ("c4_o_4bit_g32", 16),
 ])
 def test_benchmark_configs_match_oracle(ctx, oracle, name, M):
     c = config_case(name, M)
@@ -86,15 +116,22 @@ def test_rows_are_independent_of_m(ctx):
         assert torch.equal(y8[r:r + 1].view(torch.int16), y1.view(torch.int16)), f"row {r}"
 
 
-def test_repeat_calls_are_bit_identical(ctx):
+@pytest.mark.parametrize("M", [8, 16])
+def test_repeat_calls_are_bit_identical(ctx, M):
     """Deterministic fix-up order and a re-armed workspace: same bits on every call."""
     import torch
-    c = config_case("c3_down_k17408_n5120", 8)
+    c = config_case("c3_down_k17408_n5120", M)
     x, w, s, b, _ = upload(c)
-    announce("determinism c3 x3")
+    announce(f"determinism c3 M={M} x3")
     ys = [ctx.qmm(x, w, s, b, 4, 64).clone() for _ in range(3)]
     for y in ys[1:]:
         assert torch.equal(ys[0].view(torch.int16), y.view(torch.int16))
+
+
+def test_sixteen_rows_take_one_launch(ctx):
+    """16 rows of the gate/up shape are planned as one launch over the weights."""
+    p = ctx.plan(16, 17408, 5120, 4, 64)
+    assert p["ch"] > 1 and p["T"] == 1088
 
 
 def test_kernel_output_is_not_the_generic_path(ctx):

@@ -146,6 +146,10 @@ SHAPES = [
     (8, 257, 640, 4, 64), (8, 48, 16384, 4, 64), (4, 5000, 12288, 4, 64), (8, 17, 8192, 8, 64),
     (8, 333, 768, 4, 128), (8, 130, 1024, 8, 128), (8, 200, 512, 8, 32), (2, 3, 2560, 4, 64),
     (8, 100000, 256, 4, 64), (5, 999, 3072, 8, 64),
+    # two row tiles (9..16 rows)
+    (16, 17408, 5120, 4, 64), (9, 17408, 5120, 4, 64), (16, 5120, 17408, 4, 64),
+    (16, 7168, 5120, 8, 64), (12, 1024, 5120, 4, 32), (16, 48, 16384, 4, 128),
+    (16, 257, 1024, 8, 128), (10, 16, 512, 4, 64),
 ]
 
 
@@ -164,7 +168,8 @@ def test_split_for_other_cu_counts(cus):
 
 def test_planner_respects_lds_and_staging_limits():
     for (M, N, K, bits, gs) in [(8, 5120, 17408, 4, 64), (1, 5120, 17408, 4, 64),
-                                (8, 64, 65536, 4, 128)]:
+                                (8, 64, 65536, 4, 128), (16, 5120, 17408, 4, 64),
+                                (16, 17408, 5120, 8, 32)]:
         p = make_plan(M, N, K, bits, gs)
         assert M * p["kr"] // 8 <= 8 * 12 * 64          # x items a workgroup stages
         assert p["lds_bytes"] <= 163840
@@ -177,8 +182,20 @@ def test_long_k_uses_few_uneven_k_blocks():
     assert p["nkb"] == 3 and p["chunks"] == 34 and p["reduce"] == 1
 
 
+def test_sixteen_rows_fit_lds_with_two_row_tiles():
+    # x sums (8*mt floats per group) and partial tiles (512*mt bytes) double with mt = 2;
+    # K = 5120 at 16 rows stages 16 x 2560 per k-block
+    p = make_plan(16, 17408, 5120, 4, 64)
+    assert p["nkb"] == 2 and p["kr"] == 2560 and p["lds_bytes"] <= 163840
+    rs = 2 * p["kr"] + 16
+    xsum_off = (17 * rs + 15) & ~15
+    need = xsum_off + (p["kr"] // 64) * 64 + p["ring"] * 1028
+    assert need <= p["lds_bytes"]
+
+
 def test_planner_rejects_unsupported_shapes():
-    assert make_plan(9, 64, 512, 4, 64) is None     # more than 8 rows per launch
+    assert make_plan(17, 64, 512, 4, 64) is None    # more than 16 rows per launch
+    assert make_plan(9, 64, 384, 4, 64) is None     # 9..16 rows need 8-group chunks
     assert make_plan(8, 64, 500, 4, 64) is None     # K not a multiple of the super-step
     assert make_plan(8, 64, 192, 4, 128) is None
 
