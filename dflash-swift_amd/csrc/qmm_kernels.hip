@@ -206,6 +206,51 @@ __device__ __forceinline__ void build_operand_words(const u32x4_t (&R)[Cfg<BITS,
     }
 }
 
+/* Operand words for the 16-row form: every MFMA operand holds one quantisation group in all
+ * four lane groups, so that a full 16-row A operand (x rows 0-15) can be used.  The per-lane
+ * form above holds one group per lane half (lane groups 0-1 / 2-3); exchanging the upper half
+ * of the low lanes' words with the lower half of the high lanes' words (v_permlane32_swap:
+ * VDST's lanes 32-63 <-> VSRC's lanes 0-31) gives the 16-row form.  Where the per-lane form
+ * is itself that exchange of the loaded words (4-bit g128, 8-bit g64), the loaded words are
+ * already in the 16-row form.  Operand o then reads, for lane group q, chunk
+ * base_chunk((q & 1) + 2h) + (q >> 1) * delta_chunk(NOPS/2) + delta_chunk(o - h*NOPS/2) of the
+ * super-step (h = o >= NOPS/2), and accumulates group group_of(partial_of(o), 2h). */
+/* The 16-row form's chunk rule needs the second half of the operands to read the chunks of
+ * the first half moved by one fixed delta, with the same partial index. */
+template <class C>
+__host__ __device__ constexpr bool wide_layout_holds() {
+    for (int o = C::NOPS / 2; o < C::NOPS; ++o)
+        if (C::delta_chunk(o) != C::delta_chunk(o - C::NOPS / 2) + C::delta_chunk(C::NOPS / 2) ||
+            C::partial_of(o) != C::partial_of(o - C::NOPS / 2))
+            return false;
+    return true;
+}
+
+template <int BITS, int GS>
+__device__ __forceinline__ void build_operand_words_wide(const u32x4_t (&R)[Cfg<BITS, GS>::NS],
+                                                         uint32_t (&OW)[Cfg<BITS, GS>::NOW]) {
+    using C = Cfg<BITS, GS>;
+    if constexpr ((BITS == 4 && GS == 128) || (BITS == 8 && GS == 64)) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            OW[j] = R[0][j];
+            OW[4 + j] = R[1][j];
+        }
+    } else {
+        build_operand_words<BITS, GS>(R, OW);
+        constexpr int H = C::NOW / 2;
+        if constexpr (H == 2) {
+            __asm__ volatile(
+                "s_nop 1\n\tv_permlane32_swap_b32 %0, %2\n\tv_permlane32_swap_b32 %1, %3\n\t"
+                "s_nop 4"
+                : "+v"(OW[0]), "+v"(OW[1]), "+v"(OW[2]), "+v"(OW[3]));
+        } else {
+#pragma unroll
+            for (int h = 0; h < H; ++h) permlane32_swap(OW[h], OW[H + h]);
+        }
+    }
+}
+
 /* 8 nibbles of a word -> bf16/fp16 (MAGIC + q) pairs (q_i, q_{i+4}) in VGPR i: seven VALU
  * ops per word (three shifts, four v_and_or_b32).  gfx9 VOP3 takes no literal constant, so
  * with constant mask and magic the compiler would split each and-or into a v_and_b32 and a
@@ -361,34 +406,31 @@ __device__ __forceinline__ KBlock kblock(const QmmParams& p, int kb) {
     return KBlock{c0, SS, U / p.Gkb, U % p.Gkb};
 }
 
-/* Partial-tile slot j of k-block kb for tile t in the workspace: [T][nkb][nslot_kb][MT][128]
- * fp32 (MT row tiles of 8), lane (q, n) of lanes 0-31 owning floats n*8 + q*4 .. +3 of each
- * row tile. */
-__device__ __forceinline__ float* tile_slot(const QmmParams& p, int t, int kb, int j, int mt,
-                                            int lane) {
-    return p.slots + (((size_t)(t * p.nkb + kb) * p.nslot_kb + j) * p.mt + mt) * 128 +
-           (lane & 15) * 8 + (lane >> 4) * 4;
+/* A partial tile (8*mt rows x 16 columns, fp32) is held by lanes 0 .. 32*mt-1: lane (q, n)
+ * holds x rows 4q..4q+3 of column n.  In LDS and workspace slots it is laid out [mt][n][8]
+ * (128 floats per row tile); tile_off gives a lane's four floats. */
+__device__ __forceinline__ int tile_off(int lane) {
+    return (lane >> 5) * 128 + (lane & 15) * 8 + ((lane >> 4) & 1) * 4;
 }
 
-/* One partial tile (8 rows x 16 columns, fp32) as held by lanes 0-31: lane (q, n) holds
- * rows 4q..4q+3 of column n.  Layout in LDS / workspace slots: [n][8]. */
-struct Tile {
-    const QmmParams* p;
-    int lane;
-};
+/* Partial-tile slot j of k-block kb for tile t in the workspace: [T][nkb][nslot_kb][mt*128]
+ * fp32, at the lane's four floats. */
+__device__ __forceinline__ float* tile_slot(const QmmParams& p, int t, int kb, int j, int lane) {
+    return p.slots + ((size_t)(t * p.nkb + kb) * p.nslot_kb + j) * p.mt * 128 + tile_off(lane);
+}
 
-/* Row tile mt (rows 8*mt ..) of tile t, as held by lanes 0-31, plus the linear bias, to y. */
+/* Tile t as held by the lanes, plus the linear bias, to y. */
 template <bool F16>
-__device__ __forceinline__ void store_y(const QmmParams& p, int t, int mt, int lane, f32x4_t v) {
+__device__ __forceinline__ void store_y(const QmmParams& p, int t, int lane, f32x4_t v) {
     const int q = lane >> 4, n = lane & 15;
     const int col = t * 16 + n;
-    if (lane >= 32 || col >= p.N) return;
+    if (lane >= 32 * p.mt || col >= p.N) return;
     float lb = 0.0f;
     if (p.lbias) lb = elem_to_f32<F16>(((const uint16_t*)p.lbias)[col]);
     uint16_t* y = (uint16_t*)p.y;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        const int m = 8 * mt + 4 * q + r;
+        const int m = 4 * q + r;
         if (m < p.M) y[(size_t)m * p.N + col] = f32_to_out<F16>(v[r] + lb);
     }
 }
@@ -410,17 +452,18 @@ __device__ __forceinline__ void store_y(const QmmParams& p, int t, int mt, int l
  * in the counter scheme the slot stores are waited for before the counter increment, and
  * the last contributor only reads slots after its own increment has returned. */
 template <bool F16>
-__device__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t, int mt,
-                        int slot, int lane, f32x4_t v) {
+__device__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t, int slot,
+                        int lane, f32x4_t v) {
     const int q = lane >> 4, n = lane & 15;
+    const bool act = lane < 32 * p.mt;  // lanes holding the tile
     const int nwg = owner_wg(t * SS + SS - 1, base_u, rem_u) - owner_wg(t * SS, base_u, rem_u) + 1;
     const uint32_t total = (uint32_t)(p.nkb * nwg);
-    /* the tile's workspace area: nkb*nslot_kb slots of MT*128 floats */
+    /* the tile's workspace area: nkb*nslot_kb slots of mt*128 floats */
     uint32_t* base = (uint32_t*)p.slots + (size_t)t * p.nkb * p.nslot_kb * p.mt * 128;
     if (total == 2) {
         const int col = t * 16 + n;
-        if (lane < 32) {
-            uint64_t* sl = (uint64_t*)base + mt * 128 + n * 8 + q * 4;
+        if (act) {
+            uint64_t* sl = (uint64_t*)base + tile_off(lane);
             uint64_t old[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r)
@@ -431,7 +474,7 @@ __device__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 if (!(old[r] >> 32)) continue;
-                const int m = 8 * mt + 4 * q + r;
+                const int m = 4 * q + r;
                 const float sum = v[r] + __uint_as_float((uint32_t)old[r]);
                 if (m < p.M && col < p.N)
                     ((uint16_t*)p.y)[(size_t)m * p.N + col] = f32_to_out<F16>(sum + lb);
@@ -440,10 +483,10 @@ __device__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t
         }
         return;
     }
-    /* more than two parts: unused when the split runs in reduce mode (the planner's choice
-     * whenever a tile can have more than two parts); kept for one row tile */
-    if (lane < 32) {
-        uint32_t* sl = base + ((size_t)slot * p.mt + mt) * 128 + n * 8 + q * 4;
+    /* more than two parts (splits that do not run in reduce mode): store the part, count it,
+     * and the last of the tile's parts sums them in slot order */
+    if (act) {
+        uint32_t* sl = base + (size_t)slot * p.mt * 128 + tile_off(lane);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             __hip_atomic_store(sl + r, __float_as_uint(v[r]), __ATOMIC_RELAXED,
@@ -452,26 +495,24 @@ __device__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     uint32_t old = 0;
     if (lane == 0)
-        old = __hip_atomic_fetch_add(p.counters + t * p.mt + mt, 1u, __ATOMIC_RELAXED,
+        old = __hip_atomic_fetch_add(p.counters + t, 1u, __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_AGENT);
     old = __builtin_amdgcn_readfirstlane(old);
     if (old + 1 != total) return;
     f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (lane < 32) {
+    if (act) {
         for (int kb = 0; kb < p.nkb; ++kb)
             for (int j = 0; j < nwg; ++j) {
-                uint32_t* sl = base + (((size_t)kb * p.nslot_kb + j) * p.mt + mt) * 128 +
-                               n * 8 + q * 4;
+                uint32_t* sl = base + ((size_t)kb * p.nslot_kb + j) * p.mt * 128 + tile_off(lane);
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     sum[r] += __uint_as_float(__hip_atomic_exchange(
                         sl + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
             }
     }
-    store_y<F16>(p, t, mt, lane, sum);
+    store_y<F16>(p, t, lane, sum);
     if (lane == 0)
-        __hip_atomic_store(p.counters + t * p.mt + mt, 0u, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 /* The publisher wave of a qmm_mt8 workgroup.  The streaming waves only sum a finished tile
@@ -511,30 +552,22 @@ __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
                 const int u0 = max(a, t * SS), u1 = min(b, (t + 1) * SS);
                 const int g0 = u0 >= s1 ? u0 - s1 : nrot + (u0 - a);  // take index of u0
                 const int sl0 = g0 % p.ring;
-                f32x4_t v[MT];
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    v[mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-                    if (lane < 32)
-                        v[mt] = *(const f32x4_t*)(part + (sl0 * MT + mt) * 128 + n * 8 + q * 4);
-                }
+                f32x4_t v = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (lane < 32 * MT) v = *(const f32x4_t*)(part + sl0 * (MT * 128) + tile_off(lane));
                 /* the tile's sum is read: its slot may take the unit p.ring takes later (LDS
                  * operations of a wave complete in order, so the read precedes the release) */
                 if (lane == 0)
                     __hip_atomic_store(gen + sl0, (uint32_t)(g0 + p.ring), __ATOMIC_RELEASE,
                                        __HIP_MEMORY_SCOPE_WORKGROUP);
                 const int first = owner_wg(t * SS, base_u, rem_u);
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    if (u0 == t * SS && u1 == (t + 1) * SS && p.nkb == 1) {
-                        store_y<F16>(p, t, mt, lane, v[mt]);
-                    } else if (p.reduce) {
-                        /* summed by dfq_qmm_reduce after this kernel: no round trip here */
-                        if (lane < 32) *(f32x4_t*)tile_slot(p, t, kb, cl - first, mt, lane) = v[mt];
-                    } else {
-                        publish<F16>(p, SS, base_u, rem_u, t, mt, kb * p.nslot_kb + (cl - first),
-                                     lane, v[mt]);
-                    }
+                if (u0 == t * SS && u1 == (t + 1) * SS && p.nkb == 1) {
+                    store_y<F16>(p, t, lane, v);
+                } else if (p.reduce) {
+                    /* summed by dfq_qmm_reduce after this kernel: no round trip here */
+                    if (lane < 32 * MT) *(f32x4_t*)tile_slot(p, t, kb, cl - first, lane) = v;
+                } else {
+                    publish<F16>(p, SS, base_u, rem_u, t, kb * p.nslot_kb + (cl - first), lane,
+                                 v);
                 }
                 if (lane == 0) tcnt[base + bit] = kTileOut;
                 ++found;
@@ -713,16 +746,26 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     }
     __syncthreads();
 
-    /* ---- per-lane A / x-sum addresses */
+    /* ---- per-lane A / x-sum addresses.  Up to 8 rows: the A operand is block-diagonal,
+     * x rows 0-7 against the lane groups 0-1 (one quantisation group) in rows 0-7 and against
+     * lane groups 2-3 (the other) in rows 8-15, zeros elsewhere (LDS row 0); the two halves
+     * are folded at the end.  9..16 rows: x rows 0-15 against every lane group (operand words
+     * in the 16-row form). */
     const bool diag = (n < 8) == (q < 2);
-    uint32_t abase[MT];  // row tile mt reads x rows 8*mt + (n & 7) (row 0 of LDS is zeros)
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        const int arow = (diag && 8 * mt + (n & 7) < p.M) ? 1 + 8 * mt + (n & 7) : 0;
-        abase[mt] = (uint32_t)arow * RS + (uint32_t)C::base_chunk(q) * 16u;
-    }
-    const uint32_t xbase = (uint32_t)p.lds_xsum_off + (uint32_t)C::group_of(0, q) * (XR * 4u) +
-                           (uint32_t)(q & 1) * 16u;
+    const int arow = (MT == 1) ? ((diag && (n & 7) < p.M) ? 1 + (n & 7) : 0)
+                               : (n < p.M ? 1 + n : 0);
+    constexpr int HO = C::NOPS / 2;
+    constexpr int DH = C::delta_chunk(HO);
+    static_assert(wide_layout_holds<C>(), "16-row operand layout");
+    const uint32_t abase =
+        (uint32_t)arow * RS +
+        (uint32_t)((MT == 1) ? C::base_chunk(q) : C::base_chunk(q & 1) + (q >> 1) * DH) * 16u;
+    const uint32_t abase_hi =
+        (uint32_t)arow * RS + (uint32_t)(C::base_chunk((q & 1) + 2) + (q >> 1) * DH) * 16u;
+    const uint32_t xbase =
+        (MT == 1) ? (uint32_t)p.lds_xsum_off + (uint32_t)C::group_of(0, q) * (XR * 4u) +
+                        (uint32_t)(q & 1) * 16u
+                  : (uint32_t)p.lds_xsum_off + (uint32_t)q * 16u;
     const uint32_t sel_half = (q >> 1) ? kSelHi : kSelLo;
     constexpr float kOff = (BITS == 4) ? (F16 ? 1024.0f : 128.0f) : 0.0f;
     uint32_t magic = F16 ? 0x64006400u : 0x43004300u;
@@ -737,76 +780,104 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
         const int t = u / SS, cc = u - t * SS;
         SV rs_i, rb_i;
         split_scale_bias(rsb[i], rs_i, rb_i);
-        f32x4_t acc[MT];
+        f32x4_t v;  // lanes 0-31: rows 0-7 (MT 1); all lanes: rows 4q..4q+3 (MT 2)
+        if constexpr (MT == 1) {
+            f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int j = 0; j < CH; ++j) {
+                const int css = cc * CH + j;  // super-step within the k-block
+                uint32_t OW[C::NOW];
+                build_operand_words<BITS, GS>(rw[i][j], OW);
+                const uint32_t aoff = abase + (uint32_t)css * (C::CPS * 16);
+                f32x4_t P[C::NP];
 #pragma unroll
-        for (int j = 0; j < CH; ++j) {
-            const int css = cc * CH + j;  // super-step within the k-block
-            uint32_t OW[C::NOW];
-            build_operand_words<BITS, GS>(rw[i][j], OW);
-            f32x4_t P[MT][C::NP];
+                for (int pp = 0; pp < C::NP; ++pp) P[pp] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int pp = 0; pp < C::NP; ++pp) P[mt][pp] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int o = 0; o < C::NOPS; ++o) {
-                u32x4_t B;
-                if constexpr (BITS == 4) B = nibble_operand<F16>(OW[o], nmask, magic);
-                else B = byte_operand<F16>(OW[2 * o], OW[2 * o + 1]);
-                /* one decoded B operand serves every row tile */
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    const uint32_t aoff = abase[mt] + (uint32_t)css * (C::CPS * 16);
+                for (int o = 0; o < C::NOPS; ++o) {
                     const u32x4_t A = *(const u32x4_t*)(lds + aoff + C::delta_chunk(o) * 16);
-                    P[mt][C::partial_of(o)] = mfma<F16>(A, B, P[mt][C::partial_of(o)]);
+                    u32x4_t B;
+                    if constexpr (BITS == 4) B = nibble_operand<F16>(OW[o], nmask, magic);
+                    else B = byte_operand<F16>(OW[2 * o], OW[2 * o + 1]);
+                    P[C::partial_of(o)] = mfma<F16>(A, B, P[C::partial_of(o)]);
                 }
-            }
-            const uint32_t xo = xbase + (uint32_t)css * (C::GPS * XR * 4);
+                const uint32_t xo = xbase + (uint32_t)css * (C::GPS * XR * 4);
 #pragma unroll
-            for (int pp = 0; pp < C::NP; ++pp) {
-                uint32_t sw, bw2, sel;
-                if constexpr (CH > 1) {
-                    if constexpr (C::GPS == 4) {
-                        sw = (q >> 1) ? rs_i[2 * j + 1] : rs_i[2 * j];
-                        bw2 = (q >> 1) ? rb_i[2 * j + 1] : rb_i[2 * j];
-                        sel = pp ? kSelHi : kSelLo;
+                for (int pp = 0; pp < C::NP; ++pp) {
+                    uint32_t sw, bw2, sel;
+                    if constexpr (CH > 1) {
+                        if constexpr (C::GPS == 4) {
+                            sw = (q >> 1) ? rs_i[2 * j + 1] : rs_i[2 * j];
+                            bw2 = (q >> 1) ? rb_i[2 * j + 1] : rb_i[2 * j];
+                            sel = pp ? kSelHi : kSelLo;
+                        } else {
+                            sw = rs_i[j];
+                            bw2 = rb_i[j];
+                            sel = sel_half;
+                        }
                     } else {
-                        sw = rs_i[j];
-                        bw2 = rb_i[j];
-                        sel = sel_half;
+                        sw = rs_i;
+                        bw2 = rb_i;
+                        sel = (C::GPS == 4) ? (pp ? kSelHi : kSelLo) : sel_half;
                     }
-                } else {
-                    sw = rs_i;
-                    bw2 = rb_i;
-                    sel = (C::GPS == 4) ? (pp ? kSelHi : kSelLo) : sel_half;
-                }
-                const float s = half_sel<F16>(sw, sel);
-                const float bb = half_sel<F16>(bw2, sel);
-                const float bp = (kOff != 0.0f) ? __builtin_fmaf(-kOff, s, bb) : bb;
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    const f32x4_t X = *(const f32x4_t*)(lds + xo + pp * (XR * 4) + mt * 32);
+                    const float s = half_sel<F16>(sw, sel);
+                    const float bb = half_sel<F16>(bw2, sel);
+                    const float bp = (kOff != 0.0f) ? __builtin_fmaf(-kOff, s, bb) : bb;
+                    const f32x4_t X = *(const f32x4_t*)(lds + xo + pp * (XR * 4));
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        acc[mt][r] = __builtin_fmaf(s, P[mt][pp][r], acc[mt][r]);
-                        acc[mt][r] = __builtin_fmaf(bp, X[r], acc[mt][r]);
+                        acc[r] = __builtin_fmaf(s, P[pp][r], acc[r]);
+                        acc[r] = __builtin_fmaf(bp, X[r], acc[r]);
+                    }
+                }
+            }
+            /* fold the two group halves: lanes 0-31 hold the 8x16 partial */
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                uint32_t lo = __float_as_uint(acc[r]), hi = lo;
+                permlane32_swap(lo, hi);
+                /* lanes 0-31: own value + the value of lane + 32 */
+                v[r] = __uint_as_float(lo) + __uint_as_float(hi);
+            }
+        } else {
+            static_assert(CH > 1, "the 16-row form takes 8-group chunks");
+            v = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                const int css = cc * CH + j;
+                uint32_t OW[C::NOW];
+                build_operand_words_wide<BITS, GS>(rw[i][j], OW);
+                f32x4_t P[C::GPS];  // one partial per group of the super-step
+#pragma unroll
+                for (int gg = 0; gg < C::GPS; ++gg) P[gg] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int o = 0; o < C::NOPS; ++o) {
+                    const int h = o >= HO ? 1 : 0;
+                    const uint32_t aoff = (h ? abase_hi : abase) + (uint32_t)css * (C::CPS * 16) +
+                                          C::delta_chunk(o - h * HO) * 16;
+                    const u32x4_t A = *(const u32x4_t*)(lds + aoff);
+                    u32x4_t B;
+                    if constexpr (BITS == 4) B = nibble_operand<F16>(OW[o], nmask, magic);
+                    else B = byte_operand<F16>(OW[2 * o], OW[2 * o + 1]);
+                    const int gg = C::group_of(C::partial_of(o), 2 * h);
+                    P[gg] = mfma<F16>(A, B, P[gg]);
+                }
+                const uint32_t xo = xbase + (uint32_t)css * (C::GPS * XR * 4);
+#pragma unroll
+                for (int gg = 0; gg < C::GPS; ++gg) {
+                    const int gi = j * C::GPS + gg;  // group within the chunk
+                    const uint32_t sel = (gi & 1) ? kSelHi : kSelLo;
+                    const float s = half_sel<F16>(rs_i[gi >> 1], sel);
+                    const float bb = half_sel<F16>(rb_i[gi >> 1], sel);
+                    const float bp = (kOff != 0.0f) ? __builtin_fmaf(-kOff, s, bb) : bb;
+                    const f32x4_t X = *(const f32x4_t*)(lds + xo + gg * (XR * 4));
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        v[r] = __builtin_fmaf(s, P[gg][r], v[r]);
+                        v[r] = __builtin_fmaf(bp, X[r], v[r]);
                     }
                 }
             }
         }
-        /* fold the two group halves (lanes 0-31 hold each 8x16 partial) and park them */
-        f32x4_t v[MT];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                uint32_t lo = __float_as_uint(acc[mt][r]), hi = lo;
-                permlane32_swap(lo, hi);
-                /* lanes 0-31: own value + the value of lane + 32 */
-                v[mt][r] = __uint_as_float(lo) + __uint_as_float(hi);
-            }
         /* the slot of take g: wait until the unit that held it last (take g - R) is
          * released (never, when the range fits the ring) */
         const int sl = g % R;
@@ -815,11 +886,7 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
                                           __HIP_MEMORY_SCOPE_WORKGROUP) != g)
                 __builtin_amdgcn_s_sleep(1);
         }
-        if (lane < 32) {
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-                *(f32x4_t*)(part + (sl * MT + mt) * 128 + n * 8 + q * 4) = v[mt];
-        }
+        if (lane < 32 * MT) *(f32x4_t*)(part + sl * (MT * 128) + tile_off(lane)) = v;
         /* arrive at tile t; the wave that completes its units here sums them (in unit order)
          * into the slot of the tile's first unit, releases the other slots, and hands the
          * tile to the publisher wave */
@@ -832,14 +899,11 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
         if ((int)old + 1 == u1 - u0) {
             const int g0 = u0 >= s1 ? u0 - s1 : nrot + (u0 - a);  // the tile's takes: g0..
             const int sl0 = g0 % R;
-            if (lane < 32) {
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
-                    for (int i = 0, s2 = sl0; i < u1 - u0; ++i, s2 = (s2 + 1 == R) ? 0 : s2 + 1)
-                        sum += *(const f32x4_t*)(part + (s2 * MT + mt) * 128 + n * 8 + q * 4);
-                    *(f32x4_t*)(part + (sl0 * MT + mt) * 128 + n * 8 + q * 4) = sum;
-                }
+            if (lane < 32 * MT) {
+                f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
+                for (int i = 0, s2 = sl0; i < u1 - u0; ++i, s2 = (s2 + 1 == R) ? 0 : s2 + 1)
+                    sum += *(const f32x4_t*)(part + s2 * (MT * 128) + tile_off(lane));
+                *(f32x4_t*)(part + sl0 * (MT * 128) + tile_off(lane)) = sum;
             }
             if (lane == 0) {
                 for (int i = 1; i < u1 - u0; ++i)
@@ -1051,7 +1115,7 @@ extern "C" __global__ void __launch_bounds__(256) dfq_argmax_accept_f16(
  * the workspace zero at rest.  Tiles with one contributor were written by qmm_mt8. */
 template <bool F16>
 __device__ __forceinline__ void qmm_reduce(const QmmParams& p) {
-    const int t = blockIdx.x / p.mt, mt = blockIdx.x - t * p.mt, lane = threadIdx.x;
+    const int t = blockIdx.x, lane = threadIdx.x;
     f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
     int parts = 0;
     for (int kb = 0; kb < p.nkb; ++kb) {
@@ -1059,14 +1123,14 @@ __device__ __forceinline__ void qmm_reduce(const QmmParams& p) {
         const int first = owner_wg(t * k.SS, k.base, k.rem);
         const int nwg = owner_wg(t * k.SS + k.SS - 1, k.base, k.rem) - first + 1;
         for (int j = 0; j < nwg; ++j, ++parts) {
-            if (lane < 32) {
-                f32x4_t* sl = (f32x4_t*)tile_slot(p, t, kb, j, mt, lane);
+            if (lane < 32 * p.mt) {
+                f32x4_t* sl = (f32x4_t*)tile_slot(p, t, kb, j, lane);
                 sum += *sl;
                 *sl = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
             }
         }
     }
-    if (parts > 1) store_y<F16>(p, t, mt, lane, sum);
+    if (parts > 1) store_y<F16>(p, t, lane, sum);
 }
 
 extern "C" __global__ void __launch_bounds__(64) dfq_qmm_reduce_bf16(QmmParams p) {

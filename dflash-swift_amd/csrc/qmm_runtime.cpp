@@ -207,7 +207,7 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
         const size_t want = std::max(need, lds_max / 2 + 256);
         p.lds_bytes = (int)std::min(want, lds_max);
         p.need_ws = d > 1 || nslot > 1;
-        p.ws_counter_bytes = ((size_t)T * mt * 4 + 255) & ~(size_t)255;
+        p.ws_counter_bytes = ((size_t)T * 4 + 255) & ~(size_t)255;
         p.ws_bytes = p.need_ws ? p.ws_counter_bytes + (size_t)T * d * nslot * mt * 128 * 4 : 0;
         *pl = p;
         return true;
@@ -537,8 +537,8 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
                                          1, (unsigned)pl.lds_bytes, stream, args, nullptr);
     if (e != hipSuccess) return hip_fail(e, "launch dfq_qmm_mt8");
     if (pl.reduce) {
-        e = hipModuleLaunchKernel(ctx->reduce[di], (unsigned)(pl.T * pl.mt), 1, 1, 64, 1, 1, 0,
-                                  stream, args, nullptr);
+        e = hipModuleLaunchKernel(ctx->reduce[di], (unsigned)pl.T, 1, 1, 64, 1, 1, 0, stream,
+                                  args, nullptr);
         if (e != hipSuccess) return hip_fail(e, "launch dfq_qmm_reduce");
     }
     return DFQ_OK;
