@@ -37,6 +37,21 @@ struct Plan {
 };
 
 dfq_status fail(dfq_status s, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+/* The device a context runs on. */
+int ctx_device(const dfq_ctx* ctx);
+
+/* Makes the context's device current for a scope and restores the previous one. */
+class DeviceScope {
+public:
+    explicit DeviceScope(const dfq_ctx* ctx);
+    ~DeviceScope();
+    DeviceScope(const DeviceScope&) = delete;
+    DeviceScope& operator=(const DeviceScope&) = delete;
+
+private:
+    int prev_ = -1;
+    int dev_ = -1;
+};
 int kss_for(int bits, int gs);
 bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_max, Plan* pl);
 dfq_status check_fast_args(const dfq_ctx* ctx, int M, int N, int K, int bits, int gs,

@@ -124,6 +124,18 @@ struct DeviceGuard {
     }
 };
 
+int ctx_device(const dfq_ctx* ctx) { return ctx->device; }
+
+DeviceScope::DeviceScope(const dfq_ctx* ctx) : dev_(ctx_device(ctx)) {
+    if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
+    if (prev_ != dev_) (void)hipSetDevice(dev_);
+}
+
+DeviceScope::~DeviceScope() {
+    int cur = -1;
+    if (prev_ >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev_) (void)hipSetDevice(prev_);
+}
+
 int kss_for(int bits, int gs) {
     const int kstep = 512 / bits;
     const int ns = bits == 4 ? (gs == 128 ? 2 : 1) : gs / 32;

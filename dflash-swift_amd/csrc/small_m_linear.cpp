@@ -132,6 +132,12 @@ struct dfq_model {
 
 extern "C" {
 
+dfq_status dfq_linear_describe(const dfq_linear* lin, dfq_linear_desc* out) {
+    if (!lin || !out) return dfq::fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
+    *out = lin->impl->desc();
+    return DFQ_OK;
+}
+
 dfq_status dfq_linear_create(dfq_ctx* ctx, const dfq_linear_desc* desc, dfq_linear** out) {
     /* ctx may be NULL: such a layer can be inspected and swapped but not called. */
     if (!desc || !out) return dfq::fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");

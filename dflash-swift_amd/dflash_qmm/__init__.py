@@ -55,6 +55,29 @@ class _LinearDesc(ctypes.Structure):
     ]
 
 
+class _TensorInfo(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char_p), ("dtype", ctypes.c_int), ("ndim", ctypes.c_int),
+        ("shape", ctypes.c_int64 * 8), ("nbytes", ctypes.c_uint64), ("shard", ctypes.c_int),
+        ("offset", ctypes.c_uint64),
+    ]
+
+
+class _LayerInfo(ctypes.Structure):
+    _fields_ = [
+        ("prefix", ctypes.c_char_p), ("out_features", ctypes.c_int),
+        ("in_features", ctypes.c_int), ("bits", ctypes.c_int), ("group_size", ctypes.c_int),
+        ("has_biases", ctypes.c_int), ("has_bias", ctypes.c_int), ("dtype", ctypes.c_int),
+        ("valid", ctypes.c_int), ("problem", ctypes.c_char_p),
+    ]
+
+
+_WANT_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_char_p, ctypes.c_void_p)
+
+# safetensors dtype names in dfq_st_dtype order
+ST_DTYPES = ["BOOL", "U8", "I8", "I16", "U16", "F16", "BF16", "I32", "U32", "F32", "I64", "U64",
+             "F64", "F8_E5M2", "F8_E4M3"]
+
 _lib = None
 
 
@@ -98,6 +121,18 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         "dfq_enable_small_m_quantized_matmul": ([P], I),
         "dfq_debug_plan": ([P, I, I, I, I, I, ctypes.POINTER(I)], I),
         "dfq_debug_make_plan": ([I, I, I, I, I, I, S, ctypes.POINTER(I)], I),
+        "dfq_linear_describe": ([P, ctypes.POINTER(_LinearDesc)], I),
+        "dfq_checkpoint_open": ([ctypes.c_char_p, PP], I), "dfq_checkpoint_close": ([P], I),
+        "dfq_checkpoint_format": ([P], ctypes.c_char_p),
+        "dfq_checkpoint_tensor_count": ([P], I),
+        "dfq_checkpoint_tensor": ([P, I, ctypes.POINTER(_TensorInfo)], I),
+        "dfq_checkpoint_find": ([P, ctypes.c_char_p, ctypes.POINTER(_TensorInfo)], I),
+        "dfq_checkpoint_read": ([P, ctypes.c_char_p, P, S], I),
+        "dfq_checkpoint_upload": ([P, P, ctypes.c_char_p, P, S, P], I),
+        "dfq_checkpoint_set_quantization": ([P, ctypes.c_char_p, I, I], I),
+        "dfq_checkpoint_layer_count": ([P], I),
+        "dfq_checkpoint_layer": ([P, I, ctypes.POINTER(_LayerInfo)], I),
+        "dfq_checkpoint_load_model": ([P, P, P, _WANT_FN, P, P, ctypes.POINTER(I)], I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -400,9 +435,11 @@ class QuantizedLinear:
 
 
 def _desc(layer) -> _LinearDesc:
+    dt = getattr(layer, "dtype_code", None)
     return _LinearDesc(_ptr(layer.weight), _ptr(layer.scales), _ptr(layer.biases),
                        _ptr(layer.bias), layer.out_features, layer.in_features, layer.bits,
-                       layer.group_size, int(layer.mode == "affine"), dtype_code(layer.scales))
+                       layer.group_size, int(layer.mode == "affine"),
+                       dt if dt is not None else dtype_code(layer.scales))
 
 
 class SmallMQuantizedLinear(QuantizedLinear):
@@ -425,6 +462,9 @@ class Model:
         _check(self.lib.dfq_model_create(ctypes.byref(h)), "dfq_model_create")
         self._h = h
         self._src = {}
+        self._paths = []
+        self._ctx = None
+        self._keep = []  # what the library's leaves point into (a checkpoint)
         for name, leaf in leaves.items():
             self.set_leaf(name, leaf)
 
@@ -440,6 +480,8 @@ class Model:
                    "dfq_linear_create")
         _check(self.lib.dfq_model_set_leaf(self._h, path.encode(), h), "dfq_model_set_leaf")
         self._src[path] = leaf
+        if path not in self._paths:
+            self._paths.append(path)
 
     def __getattr__(self, path: str) -> QuantizedLinear:
         if path.startswith("_") or path in ("lib",):
@@ -452,14 +494,28 @@ class Model:
         if not h:
             raise KeyError(path)
         h = ctypes.c_void_p(h)
-        src = self._src[path]
         cls = SmallMQuantizedLinear if self.lib.dfq_linear_is_small_m(h) else QuantizedLinear
         obj = cls.__new__(cls)
-        QuantizedLinear.__init__(obj, src.ctx, src.weight, src.scales, src.biases, src.bias,
-                                 src.group_size, src.bits, src.mode, _handle=h)
+        src = self._src.get(path)
+        if src is not None:
+            QuantizedLinear.__init__(obj, src.ctx, src.weight, src.scales, src.biases, src.bias,
+                                     src.group_size, src.bits, src.mode, _handle=h)
+        else:
+            # a leaf created in the library (a checkpoint load): device addresses as ints
+            d = _LinearDesc()
+            _check(self.lib.dfq_linear_describe(h, ctypes.byref(d)), "dfq_linear_describe")
+            obj.ctx, obj.lib, obj._h = self._ctx, self.lib, h
+            obj.weight, obj.scales, obj.biases, obj.bias = d.weight, d.scales, d.biases, d.bias
+            obj.group_size, obj.bits = d.group_size, d.bits
+            obj.mode = "affine" if d.mode_affine else "other"
+            obj.out_features, obj.in_features = d.out_features, d.in_features
+            obj.dtype_code = d.dtype
         obj._owned = False  # the model owns the leaf; the view must not destroy it
         obj._model = self   # and keeps the model alive while the view exists
         return obj
+
+    def paths(self) -> list:
+        return list(self._paths)
 
     def __len__(self):
         return self.lib.dfq_model_leaf_count(self._h)
@@ -479,3 +535,109 @@ def enable_small_m_quantized_matmul(model: Model) -> int:
     if n < 0:
         _check(2, "dfq_enable_small_m_quantized_matmul")
     return n
+
+
+class Checkpoint:
+    """An MLX quantised checkpoint: one .safetensors file or a directory of shards with an
+    optional config.json (its "quantization" object gives bits / group size per layer)."""
+
+    def __init__(self, path):
+        import weakref
+        self.lib = load_library()
+        h = ctypes.c_void_p()
+        _check(self.lib.dfq_checkpoint_open(os.fsencode(path), ctypes.byref(h)),
+               "dfq_checkpoint_open")
+        self._h = h
+        self._models = weakref.WeakSet()
+
+    @property
+    def format(self) -> str:
+        return self.lib.dfq_checkpoint_format(self._h).decode()
+
+    @staticmethod
+    def _tinfo(t: _TensorInfo) -> dict:
+        return {"name": t.name.decode(), "dtype": ST_DTYPES[t.dtype],
+                "shape": tuple(t.shape[:t.ndim]), "nbytes": t.nbytes, "shard": t.shard,
+                "offset": t.offset}
+
+    def tensors(self) -> list:
+        out = []
+        for i in range(self.lib.dfq_checkpoint_tensor_count(self._h)):
+            t = _TensorInfo()
+            _check(self.lib.dfq_checkpoint_tensor(self._h, i, ctypes.byref(t)),
+                   "dfq_checkpoint_tensor")
+            out.append(self._tinfo(t))
+        return out
+
+    def tensor(self, name: str) -> dict:
+        t = _TensorInfo()
+        _check(self.lib.dfq_checkpoint_find(self._h, name.encode(), ctypes.byref(t)),
+               "dfq_checkpoint_find")
+        return self._tinfo(t)
+
+    def read(self, name: str):
+        """The tensor's bytes as stored (numpy uint8)."""
+        import numpy as np
+        buf = np.empty(self.tensor(name)["nbytes"], dtype=np.uint8)
+        _check(self.lib.dfq_checkpoint_read(self._h, name.encode(), buf.ctypes.data, buf.size),
+               "dfq_checkpoint_read")
+        return buf
+
+    def upload(self, ctx: Context, name: str, dst, stream=None):
+        _check(self.lib.dfq_checkpoint_upload(ctx.handle, self._h, name.encode(), _ptr(dst),
+                                              dst.numel() * dst.element_size(), _stream(stream)),
+               "dfq_checkpoint_upload")
+
+    def set_quantization(self, bits: int, group_size: int, prefix: str | None = None):
+        _check(self.lib.dfq_checkpoint_set_quantization(
+            self._h, prefix.encode() if prefix else None, bits, group_size),
+            "dfq_checkpoint_set_quantization")
+
+    def layers(self) -> list:
+        out = []
+        for i in range(self.lib.dfq_checkpoint_layer_count(self._h)):
+            L = _LayerInfo()
+            _check(self.lib.dfq_checkpoint_layer(self._h, i, ctypes.byref(L)),
+                   "dfq_checkpoint_layer")
+            out.append({"prefix": L.prefix.decode(), "out_features": L.out_features,
+                        "in_features": L.in_features, "bits": L.bits,
+                        "group_size": L.group_size, "has_biases": bool(L.has_biases),
+                        "has_bias": bool(L.has_bias), "dtype": L.dtype, "valid": bool(L.valid),
+                        "problem": L.problem.decode()})
+        return out
+
+    def load_model(self, ctx: Context, want=None, model: "Model | None" = None,
+                   stream=None) -> "Model":
+        """Load the quantised layers (those want(prefix) accepts) into device memory as
+        stock QuantizedLinear leaves of `model` (a new Model if None)."""
+        model = model if model is not None else Model()
+        cb = _WANT_FN(lambda p, _u: int(bool(want(p.decode())))) if want else _WANT_FN()
+        n = ctypes.c_int(0)
+        _check(self.lib.dfq_checkpoint_load_model(ctx.handle, self._h, model._h, cb, None,
+                                                  _stream(stream), ctypes.byref(n)),
+               "dfq_checkpoint_load_model")
+        model._ctx = ctx
+        model._keep.append(self)
+        for L in self.layers():
+            if L["valid"] and (want is None or want(L["prefix"])) and \
+                    L["prefix"] not in model._paths:
+                model._paths.append(L["prefix"])
+                model._src.pop(L["prefix"], None)
+        self._models.add(model)
+        self.last_loaded = n.value
+        return model
+
+    def close(self):
+        if len(self._models):
+            raise RuntimeError("models loaded from this checkpoint are still alive")
+        if self._h:
+            self.lib.dfq_checkpoint_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            if self._h:
+                self.lib.dfq_checkpoint_close(self._h)
+                self._h = None
+        except Exception:
+            pass

@@ -212,6 +212,81 @@ int dfq_model_leaf_count(const dfq_model* model);
  * Replaces enableSmallMQuantizedMatmul(in:), SmallMQuantizedMatmul.swift:303-317. */
 int dfq_enable_small_m_quantized_matmul(dfq_model* model);
 
+/* ---- MLX quantised checkpoints (safetensors) ------------------------------------------
+ * The on-disk format the fast kernel consumes, loaded as it is: for each quantised layer P,
+ * P.weight (U32 [out][in*bits/32]), P.scales and P.biases ([out][in/group_size], BF16 / F16
+ * / F32) and optionally the linear bias P.bias ([out]).  A layer is quantised when P.scales
+ * and P.weight exist; its bits and group size come from config.json's "quantization" object
+ * (top-level group_size / bits, overridden by an entry keyed by P; an entry of false turns
+ * the layer off), or from dfq_checkpoint_set_quantization.  Replaces, for the layers this path
+ * serves, the quantised-weight half of loadModel (mlx-swift-lm; reached at
+ * Sources/dflash-bench/main.swift:26) that fills the QuantizedLinear fields SmallMQuantized-
+ * Linear shares (SmallMQuantizedMatmul.swift:245-248). */
+
+typedef struct dfq_checkpoint dfq_checkpoint;
+
+typedef enum dfq_st_dtype {
+    DFQ_ST_BOOL = 0, DFQ_ST_U8, DFQ_ST_I8, DFQ_ST_I16, DFQ_ST_U16, DFQ_ST_F16, DFQ_ST_BF16,
+    DFQ_ST_I32, DFQ_ST_U32, DFQ_ST_F32, DFQ_ST_I64, DFQ_ST_U64, DFQ_ST_F64, DFQ_ST_F8_E5M2,
+    DFQ_ST_F8_E4M3
+} dfq_st_dtype;
+
+typedef struct dfq_tensor_info {
+    const char* name;     /* valid until dfq_checkpoint_close                           */
+    dfq_st_dtype dtype;
+    int ndim;
+    int64_t shape[8];
+    uint64_t nbytes;
+    int shard;            /* index of the file holding it (sorted file names)           */
+    uint64_t offset;      /* absolute byte offset of its data in that file              */
+} dfq_tensor_info;
+
+typedef struct dfq_layer_info {
+    const char* prefix;   /* P; valid until dfq_checkpoint_close                        */
+    int out_features, in_features, bits, group_size;
+    int has_biases, has_bias;
+    dfq_dtype dtype;      /* of scales / biases / bias                                  */
+    int valid;            /* 1: the tensors agree with bits / group size and can load   */
+    const char* problem;  /* why not ("" when valid); changes with set_quantization     */
+} dfq_layer_info;
+
+/* Opens a .safetensors file, or a directory of model*.safetensors shards (every
+ * *.safetensors when none is so named) with an optional config.json, and checks every
+ * header: dtype known, shape matching the byte range, ranges inside the file, no name in
+ * two shards.  Reads no tensor data. */
+dfq_status dfq_checkpoint_open(const char* path, dfq_checkpoint** out);
+/* Closes the files and frees the device memory of every dfq_checkpoint_load_model call:
+ * destroy models loaded from it first. */
+dfq_status dfq_checkpoint_close(dfq_checkpoint* ck);
+/* The header's __metadata__ "format" ("mlx" for MLX checkpoints; "" if none). */
+const char* dfq_checkpoint_format(const dfq_checkpoint* ck);
+int dfq_checkpoint_tensor_count(const dfq_checkpoint* ck);
+dfq_status dfq_checkpoint_tensor(const dfq_checkpoint* ck, int index, dfq_tensor_info* out);
+dfq_status dfq_checkpoint_find(const dfq_checkpoint* ck, const char* name, dfq_tensor_info* out);
+/* A tensor's bytes into host memory, as stored. */
+dfq_status dfq_checkpoint_read(const dfq_checkpoint* ck, const char* name, void* dst,
+                               size_t bytes);
+/* A tensor's bytes into caller-owned device memory, as stored (returns when done). */
+dfq_status dfq_checkpoint_upload(dfq_ctx* ctx, dfq_checkpoint* ck, const char* name, void* dst,
+                                 size_t bytes, void* stream);
+/* Bits and group size of layer `prefix`, or of every layer without its own (prefix NULL). */
+dfq_status dfq_checkpoint_set_quantization(dfq_checkpoint* ck, const char* prefix, int bits,
+                                           int group_size);
+/* The quantised layers, sorted by prefix. */
+int dfq_checkpoint_layer_count(const dfq_checkpoint* ck);
+dfq_status dfq_checkpoint_layer(const dfq_checkpoint* ck, int index, dfq_layer_info* out);
+/* Loads every quantised layer for which want(prefix, user) is non-zero (want NULL: all)
+ * into one device allocation, in the file layout, and adds each to `model` as a stock
+ * QuantizedLinear leaf named by its prefix (dfq_enable_small_m_quantized_matmul then swaps
+ * the eligible ones).  Fails before allocating if a chosen layer is not valid.  Files are
+ * read in order through pinned staging buffers; returns when the data is on the device.
+ * *loaded (may be NULL) gets the number of layers added. */
+dfq_status dfq_checkpoint_load_model(dfq_ctx* ctx, dfq_checkpoint* ck, dfq_model* model,
+                                     int (*want)(const char* prefix, void* user), void* user,
+                                     void* stream, int* loaded);
+/* The arrays and shape of a layer (for layers the caller did not create itself). */
+dfq_status dfq_linear_describe(const dfq_linear* lin, dfq_linear_desc* out);
+
 #ifdef __cplusplus
 }
 #endif
