@@ -621,22 +621,25 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
      * and lanes past it reload the last one. */
     const int CPR = kr / 8;  // 16-byte chunks per row of the k-block
     const int items = p.M * CPR;
-    const uint16_t* xg = (const uint16_t*)p.x;
+    /* the k-block's x as a uniform base plus 32-bit per-lane offsets (24-bit multiplies:
+     * staging is VALU-bound, so no 64-bit address arithmetic per item) */
+    const uint8_t* xb = (const uint8_t*)p.x + (size_t)k0 * 2;
+    const uint32_t xrow = (uint32_t)p.K * 2u;
     /* (row, chunk) of item tid + i * kThreads, stepped without a per-item division */
     const int dr = kThreads / CPR, dcc = kThreads - dr * CPR;  // wave-uniform
-    int xr[kMaxStageItems], xc[kMaxStageItems];
+    uint32_t xo[kMaxStageItems];  // LDS offset of the item, (1 + row) * RS + chunk * 16
+    int xs[kMaxStageItems];       // its group-sum slot, or -1 past the last item
     u32x4_t xv[kMaxStageItems];
     {
         int r = tid / CPR, cc = tid - r * CPR;
 #pragma unroll
         for (int i = 0; i < kMaxStageItems; ++i) {
-            xr[i] = r;
-            xc[i] = cc;
-            if (i * kThreads < items) {
-                const bool in = r < p.M;
-                const int rr = in ? r : p.M - 1, c2 = in ? cc : CPR - 1;
-                xv[i] = *(const u32x4_t*)(xg + (size_t)rr * p.K + k0 + c2 * 8);
-            }
+            const bool in = r < p.M;
+            const int rr = in ? r : p.M - 1, c2 = in ? cc : CPR - 1;
+            xo[i] = __umul24((uint32_t)(1 + rr), (uint32_t)p.lds_row_stride) + (uint32_t)c2 * 16u;
+            xs[i] = in ? (cc / (GS / 8)) * XR + r : -1;
+            if (i * kThreads < items)
+                xv[i] = *(const u32x4_t*)(xb + (__umul24((uint32_t)rr, xrow) + (uint32_t)c2 * 16u));
             r += dr;
             cc += dcc;
             if (cc >= CPR) {
@@ -714,22 +717,21 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p) {
     uint32_t* gcnt = tcnt + ntl;
     const int GK = kr / GS;  // groups in the k-block
     /* per item: pre-permute into the MFMA k order, and sum its 8 elements; the GS/8 items
-     * of a group sit in aligned neighbouring lanes and are summed with DPP */
+     * of a group sit in aligned neighbouring lanes (all real or all past the end, as CPR is
+     * a multiple of GS/8) and are summed with DPP.  Lanes past the last item rewrite the
+     * last item with its own value; only the group sums need a mask. */
+    const bool leader = (tid & (GS / 8 - 1)) == 0;
 #pragma unroll
     for (int i = 0; i < kMaxStageItems; ++i) {
         if (i * kThreads < items) {
-            const int r = xr[i], cc = xc[i];
-            const bool act = r < p.M;
-            float sm = act ? chunk_dot<F16>(xv[i], 0.0f) : 0.0f;
+            float sm = chunk_dot<F16>(xv[i], 0.0f);
             sm += dpp_f32<0xB1>(sm);             // lanes ^1 (quad_perm 1,0,3,2)
             sm += dpp_f32<0x4E>(sm);             // lanes ^2 (quad_perm 2,3,0,1)
             if constexpr (GS >= 64) sm += dpp_f32<0x104>(sm);   // + lane+4 (row_shl:4)
             if constexpr (GS >= 128) sm += dpp_f32<0x108>(sm);  // + lane+8 (row_shl:8)
-            if (act) {
-                const u32x4_t v = (BITS == 4) ? nibble_permute(xv[i]) : xv[i];
-                *(u32x4_t*)(lds + (size_t)(1 + r) * RS + cc * 16) = v;
-                if ((cc & (GS / 8 - 1)) == 0) xsum[(cc / (GS / 8)) * XR + r] = sm;
-            }
+            const u32x4_t v = (BITS == 4) ? nibble_permute(xv[i]) : xv[i];
+            *(u32x4_t*)(lds + xo[i]) = v;
+            if (leader && xs[i] >= 0) xsum[xs[i]] = sm;
         }
     }
     for (int c = tid; c < CPR; c += kThreads) *(u32x4_t*)(lds + c * 16) = u32x4_t{0, 0, 0, 0};
