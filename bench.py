@@ -106,11 +106,13 @@ C5_FUSED = [(7168, 5120), (5120, 5120), (34816, 5120), (5120, 17408)]
 C5_LM_HEAD = (151936, 5120)
 
 
-def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False):
+def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False):
     """The C5 verify forward at M=8: `layers` layers of seven 4-bit g64 matmuls (or, fused,
     q|k|v, o, gate|up + SiLU-mul, down), each layer captured as one HIP graph, then the
     lm_head; distinct random weights per layer (about 11.6 GiB, so every layer streams from
-    HBM).  Returns microseconds per forward."""
+    HBM).  persistent: the fused forward's 321 ops (every layer and the lm_head) as one
+    dfq_chain launch instead of per-layer graphs.  Returns microseconds per forward."""
+    fused = fused or persistent
     import dflash_qmm
     M = 8
     g = torch.Generator(device=dev)
@@ -140,11 +142,23 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False):
     lm_out = torch.empty(M, C5_LM_HEAD[0], device=dev, dtype=torch.bfloat16)
     stream = torch.cuda.Stream(device=dev)
     B = dflash_qmm.BF16
-    graphs, lw = [], []
+    graphs, lw, chain_ops = [], [], []
     for li in range(layers):
         wl = [weights(N, K) for (N, K) in layer]
         lw.append(wl)
         layer_in = x if li == 0 else outs[-1]
+        if persistent:
+            for j, (N, K) in enumerate(layer):
+                if srcs[j] == "h":
+                    chain_ops.append({"kind": "silu_mul", "x": outs[2], "y": h,
+                                      "N": C5_FUSED[3][1]})
+                    inp = h
+                else:
+                    inp = layer_in
+                w, s, b = wl[j]
+                chain_ops.append({"kind": "qmm", "x": inp, "y": outs[j], "w": w, "scales": s,
+                                  "biases": b, "N": N, "K": K})
+            continue
         ctx.graph_begin(stream)
         for j, (N, K) in enumerate(layer):
             if srcs[j] == "h":
@@ -168,7 +182,17 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False):
                     B, B, B, ws=ws, ws_bytes=ws.numel(), stream=stream)
         ctx.argmax_accept(lm_out, proposals, tokens, accepted, ws=acc_ws, stream=stream)
 
+    chain = None
+    if persistent:
+        chain_ops.append({"kind": "qmm", "x": outs[-1], "y": lm_out, "w": wlm, "scales": slm,
+                          "biases": blm, "N": C5_LM_HEAD[0], "K": C5_LM_HEAD[1]})
+        chain = ctx.chain(M, 4, 64, chain_ops)
+
     def forward():
+        if chain is not None:
+            chain.launch(stream)
+            ctx.argmax_accept(lm_out, proposals, tokens, accepted, ws=acc_ws, stream=stream)
+            return
         for gr in graphs:
             gr.launch(stream)
         lm_only()
@@ -190,6 +214,10 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False):
     lm = timed(lm_only, 20)
     for gr in graphs:
         gr.close()
+    if chain is not None:
+        if chain.failed():
+            raise RuntimeError("the persistent chain reported a timed-out wait")
+        chain.close()
     layer_bytes = sum(algorithmic_bytes(M, N, K) for (N, K) in C5_LAYER)   # the same fused
     total_bytes = layers * layer_bytes + algorithmic_bytes(M, *C5_LM_HEAD)
     ideal = total_bytes / (HBM_PEAK_GBS * 1e3)
@@ -197,7 +225,9 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False):
         "workload": (f"M=8 verify forward: {layers} layers x "
                      + ("(q|k|v, o, gate|up, silu*up, down)" if fused
                         else "(q,k,v,o,gate,up,down)")
-                     + " + lm_head + greedy accept, 4-bit g64 bf16, one HIP graph per layer"),
+                     + " + lm_head + greedy accept, 4-bit g64 bf16, "
+                     + ("the layers and lm_head as one persistent chain launch" if persistent
+                        else "one HIP graph per layer")),
         "us_per_forward": round(total, 1),
         "ideal_us_at_8TBs": round(ideal, 1),
         "frac_of_ideal": round(ideal / total, 4),
@@ -328,7 +358,8 @@ def main():
         out["c5_chain"] = chain_c5(torch, ctx, dev)
         torch.cuda.empty_cache()
         out["c5_chain_fused"] = chain_c5(torch, ctx, dev, fused=True)
-        for key in ("c5_chain", "c5_chain_fused"):
+        out["c5_chain_persistent"] = chain_c5(torch, ctx, dev, persistent=True)
+        for key in ("c5_chain", "c5_chain_fused", "c5_chain_persistent"):
             print(f"[bench] {key}: {out[key]['us_per_forward']} us/forward "
                   f"(ideal {out[key]['ideal_us_at_8TBs']})", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:

@@ -31,6 +31,7 @@ struct Plan {
     int ring = 0;       /* partial-tile slots (a ring over the take order)   */
     int umax = 0;       /* most units per workgroup                          */
     int lds_bytes = 0;  /* dynamic LDS requested per workgroup               */
+    int lds_need = 0;   /* LDS bytes the layout uses                         */
     bool need_ws = false;
     size_t ws_counter_bytes = 0;
     size_t ws_bytes = 0;

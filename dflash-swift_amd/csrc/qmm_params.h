@@ -58,6 +58,25 @@ typedef struct QmmParams {
     uint32_t s_bytes;       /* size of scales (= size of biases) in bytes             */
 } QmmParams;
 
+/* One op of a chain (dfq_chain): kind 0 is a qmm as above (its workspace fields point into
+ * the chain's workspace); kind 1 is silu_mul with x = gu [M][2N], y = h [M][N]. */
+typedef struct ChainOp {
+    QmmParams p;
+    int32_t kind;
+    int32_t pad;
+} ChainOp;
+
+/* The chain kernel's argument. */
+typedef struct ChainParams {
+    const ChainOp* ops;     /* [n_ops], device memory                                  */
+    uint32_t* sync;         /* launch epoch, error flag and the completion blocks of
+                               the ops (see the chain kernel); zero when created        */
+    int32_t n_ops;
+    int32_t G;              /* workgroups in the launch (one per CU)                   */
+    int32_t lds_flag_off;   /* byte offset of the two wait flags in LDS                */
+    uint32_t timeout;       /* s_memrealtime ticks (100 MHz) a wait may last           */
+} ChainParams;
+
 /* Parameters of the generic (stock-op stand-in) kernel. */
 typedef struct QmmGenericParams {
     const void* x;

@@ -84,8 +84,23 @@ struct dfq_ctx {
     hipFunction_t argmax_accept[2] = {}; // greedy accept of a verify pass [bf16/f16]
     hipFunction_t generic = nullptr;
     hipFunction_t fill = nullptr;
+    hipFunction_t chain[2][3][2] = {};   // the chain kernel [bits][gs][bf16/f16]
     std::mutex mu;
     std::unordered_map<PlanKey, dfq::Plan, PlanKeyHash> plans;
+};
+
+struct dfq_chain {
+    dfq_ctx* ctx = nullptr;
+    hipFunction_t fn = nullptr;
+    ChainOp* ops = nullptr;    // device
+    uint32_t* sync = nullptr;  // device, [2*n_ops + 2]
+    void* ws = nullptr;        // device workspace of the qmm ops
+    int n_ops = 0;
+    int G = 0;
+    int lds_bytes = 0;
+    int lds_flag_off = 0;
+    size_t sync_bytes = 0;
+    uint32_t timeout = 100000000u;  // 1 s of s_memrealtime ticks
 };
 
 struct dfq_graph {
@@ -218,6 +233,7 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
         /* Ask for more than half the CU's LDS so that exactly one workgroup lands per CU. */
         const size_t want = std::max(need, lds_max / 2 + 256);
         p.lds_bytes = (int)std::min(want, lds_max);
+        p.lds_need = (int)need;
         p.need_ws = d > 1 || nslot > 1;
         p.ws_counter_bytes = ((size_t)T * 4 + 255) & ~(size_t)255;
         p.ws_bytes = p.need_ws ? p.ws_counter_bytes + (size_t)T * d * nslot * mt * 128 * 4 : 0;
@@ -342,6 +358,14 @@ dfq_status dfq_init(int device, dfq_ctx** out) {
                     snprintf(name, sizeof name, "dfq_qmm_mt16_b%d_g%d_%s_c8", kBits[b], kGs[g2],
                              kDt[d]);
                     if ((e = hipModuleGetFunction(&ctx->mt16[b][g2][d], ctx->module, name)) !=
+                        hipSuccess) {
+                        (void)hipModuleUnload(ctx->module);
+                        delete ctx;
+                        return hip_fail(e, name);
+                    }
+                    snprintf(name, sizeof name, "dfq_chain_b%d_g%d_%s", kBits[b], kGs[g2],
+                             kDt[d]);
+                    if ((e = hipModuleGetFunction(&ctx->chain[b][g2][d], ctx->module, name)) !=
                         hipSuccess) {
                         (void)hipModuleUnload(ctx->module);
                         delete ctx;
@@ -498,13 +522,10 @@ dfq_status dfq_workspace_clear(dfq_ctx* ctx, void* ws, size_t bytes, void* strea
     return e == hipSuccess ? DFQ_OK : hip_fail(e, "launch dfq_fill_u32");
 }
 
-static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
-                             const void* biases, const void* lbias, void* y, int M, int N, int K,
-                             int bits, int gs, dfq_dtype dt, void* ws, size_t wsb,
-                             hipStream_t stream) {
-    Plan pl;
-    dfq_status s = get_plan(ctx, M, N, K, bits, gs, &pl);
-    if (s) return s;
+/* The kernel argument of one call of a plan (ws: the workspace, NULL when none is needed). */
+static QmmParams fill_params(const Plan& pl, const void* x, const uint32_t* w,
+                             const void* scales, const void* biases, const void* lbias, void* y,
+                             int M, int N, int K, int bits, int gs, void* ws) {
     QmmParams p{};
     p.x = x;
     p.w = w;
@@ -512,11 +533,7 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
     p.biases = biases;
     p.lbias = lbias;
     p.y = y;
-    if (pl.need_ws) {
-        if (!ws || wsb < pl.ws_bytes)
-            return fail(DFQ_ERR_WORKSPACE, "workspace of %zu bytes needed (got %zu)", pl.ws_bytes,
-                        ws ? wsb : (size_t)0);
-        if (!aligned(ws, 256)) return fail(DFQ_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+    if (pl.need_ws && ws) {
         p.counters = (uint32_t*)ws;
         p.slots = (float*)((char*)ws + pl.ws_counter_bytes);
     }
@@ -539,6 +556,23 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
     p.ring = pl.ring;
     p.w_bytes = (uint32_t)((int64_t)N * K * bits / 8);
     p.s_bytes = (uint32_t)((int64_t)N * (K / gs) * 2);
+    return p;
+}
+
+static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
+                             const void* biases, const void* lbias, void* y, int M, int N, int K,
+                             int bits, int gs, dfq_dtype dt, void* ws, size_t wsb,
+                             hipStream_t stream) {
+    Plan pl;
+    dfq_status s = get_plan(ctx, M, N, K, bits, gs, &pl);
+    if (s) return s;
+    if (pl.need_ws) {
+        if (!ws || wsb < pl.ws_bytes)
+            return fail(DFQ_ERR_WORKSPACE, "workspace of %zu bytes needed (got %zu)", pl.ws_bytes,
+                        ws ? wsb : (size_t)0);
+        if (!aligned(ws, 256)) return fail(DFQ_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+    }
+    QmmParams p = fill_params(pl, x, w, scales, biases, lbias, y, M, N, K, bits, gs, ws);
     const int bi = bits == 4 ? 0 : 1;
     const int gi = gs == 32 ? 0 : gs == 64 ? 1 : 2;
     const int di = dt == DFQ_BF16 ? 0 : 1;
@@ -555,6 +589,7 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
     }
     return DFQ_OK;
 }
+
 
 dfq_status dfq_qmm(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
                    const void* biases, const void* lbias, void* y, int M, int N, int K, int bits,
@@ -756,6 +791,160 @@ dfq_status dfq_debug_make_plan(int M, int N, int K, int bits, int gs, int num_cu
                        p.lds_bytes, p.need_ws ? 1 : 0, p.ch, p.umax, p.chunks, p.reduce ? 1 : 0,
                        p.ring};
     std::memcpy(out13, v, sizeof v);
+    return DFQ_OK;
+}
+
+/* ---- chains: a list of ops in one persistent launch ----------------------------------- */
+
+static void chain_free(dfq_chain* ch) {
+    if (!ch) return;
+    if (ch->ctx) {
+        DeviceGuard g(ch->ctx->device);
+        if (ch->ops) (void)hipFree(ch->ops);
+        if (ch->sync) (void)hipFree(ch->sync);
+        if (ch->ws) (void)hipFree(ch->ws);
+    }
+    delete ch;
+}
+
+dfq_status dfq_chain_create(dfq_ctx* ctx, int M, int bits, int gs, dfq_dtype dtype,
+                            const dfq_chain_op* ops, int n_ops, dfq_chain** out) {
+    if (!ctx || !ops || !out) return fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    if (n_ops < 1) return fail(DFQ_ERR_INVALID_ARGUMENT, "a chain needs at least one op");
+    if (M < 1 || M > 8) return fail(DFQ_ERR_UNSUPPORTED, "chains take 1..8 rows (got %d)", M);
+    if (dtype != DFQ_BF16 && dtype != DFQ_F16)
+        return fail(DFQ_ERR_UNSUPPORTED, "chains take bf16 or fp16");
+    if (ops[0].kind != DFQ_CHAIN_QMM) return fail(DFQ_ERR_INVALID_ARGUMENT, "op 0 must be a qmm");
+    const int G = ctx->num_cus;
+    std::vector<ChainOp> host(n_ops);
+    size_t ws_need = 0;
+    int need_max = 0;
+    for (int j = 0; j < n_ops; ++j) {
+        const dfq_chain_op& o = ops[j];
+        ChainOp& c = host[j];
+        std::memset(&c, 0, sizeof c);
+        if (!o.x || !o.y) return fail(DFQ_ERR_INVALID_ARGUMENT, "op %d: null x or y", j);
+        if (o.kind == DFQ_CHAIN_SILU_MUL) {
+            if (o.N < 1) return fail(DFQ_ERR_INVALID_ARGUMENT, "op %d: N must be positive", j);
+            if (!aligned(o.x, 2) || !aligned(o.y, 2))
+                return fail(DFQ_ERR_INVALID_ARGUMENT, "op %d: misaligned buffers", j);
+            c.kind = 1;
+            c.p.x = o.x;
+            c.p.y = o.y;
+            c.p.M = M;
+            c.p.N = o.N;
+            continue;
+        }
+        if (o.kind != DFQ_CHAIN_QMM) return fail(DFQ_ERR_INVALID_ARGUMENT, "op %d: unknown kind", j);
+        dfq_status st = check_fast_args(ctx, M, o.N, o.K, bits, gs, dtype, dtype, dtype);
+        if (st) return st;
+        if (!o.w || !o.scales || !o.biases)
+            return fail(DFQ_ERR_INVALID_ARGUMENT, "op %d: null w, scales or biases", j);
+        if (!aligned(o.x, 16) || !aligned(o.w, 16) || !aligned(o.scales, 4) ||
+            !aligned(o.biases, 4) || !aligned(o.y, 2) || (o.linear_bias && !aligned(o.linear_bias, 2)))
+            return fail(DFQ_ERR_INVALID_ARGUMENT, "op %d: misaligned buffers", j);
+        Plan pl;
+        if ((st = get_plan(ctx, M, o.N, o.K, bits, gs, &pl))) return st;
+        if (pl.ch == 1)
+            return fail(DFQ_ERR_UNSUPPORTED, "op %d: chains need K a multiple of 8 groups", j);
+        if (pl.nkb * pl.Gkb > G)
+            return fail(DFQ_ERR_UNSUPPORTED, "op %d: its split needs %d workgroups (%d CUs)", j,
+                        pl.nkb * pl.Gkb, G);
+        c.kind = 0;
+        c.p = fill_params(pl, o.x, o.w, o.scales, o.biases, o.linear_bias, o.y, M, o.N, o.K,
+                          bits, gs, nullptr);
+        ws_need = std::max(ws_need, pl.ws_bytes);
+        need_max = std::max(need_max, pl.lds_need);
+    }
+    auto* ch = new dfq_chain();
+    ch->ctx = ctx;
+    ch->n_ops = n_ops;
+    ch->G = G;
+    ch->lds_flag_off = (need_max + 15) & ~15;
+    /* lds_flag_off: 8 words of wait flags, gathering counters and epochs */
+    ch->lds_bytes = (int)std::max<size_t>((size_t)ch->lds_flag_off + 32, ctx->lds_max / 2 + 256);
+    if ((size_t)ch->lds_bytes > ctx->lds_max) {
+        delete ch;
+        return fail(DFQ_ERR_UNSUPPORTED, "chain needs %d bytes of LDS", ch->lds_flag_off + 32);
+    }
+    const int bi = bits == 4 ? 0 : 1, gi = gs == 32 ? 0 : gs == 64 ? 1 : 2;
+    ch->fn = ctx->chain[bi][gi][dtype == DFQ_BF16 ? 0 : 1];
+    DeviceGuard g(ctx->device);
+    hipError_t e = hipSuccess;
+    /* epoch and error lines, then (2 * n_ops + 1) blocks of 33 lines of 128 bytes */
+    const size_t sync_bytes = (size_t)(2 + (2 * n_ops + 1) * 33) * 128;
+    ch->sync_bytes = sync_bytes;
+    if ((e = hipMalloc(&ch->ops, sizeof(ChainOp) * n_ops)) != hipSuccess ||
+        (e = hipMalloc(&ch->sync, sync_bytes)) != hipSuccess ||
+        (ws_need && (e = hipMalloc(&ch->ws, ws_need)) != hipSuccess)) {
+        chain_free(ch);
+        return hip_fail(e, "chain allocation");
+    }
+    /* every qmm op shares the one workspace: ops run one after another */
+    for (int j = 0; j < n_ops; ++j) {
+        if (host[j].kind != 0 || !ch->ws) continue;
+        Plan pl;
+        (void)get_plan(ctx, M, ops[j].N, ops[j].K, bits, gs, &pl);
+        if (pl.need_ws) {
+            host[j].p.counters = (uint32_t*)ch->ws;
+            host[j].p.slots = (float*)((char*)ch->ws + pl.ws_counter_bytes);
+        }
+    }
+    if ((e = hipMemcpy(ch->ops, host.data(), sizeof(ChainOp) * n_ops, hipMemcpyHostToDevice)) !=
+            hipSuccess ||
+        (e = hipMemset(ch->sync, 0, sync_bytes)) != hipSuccess ||
+        (ch->ws && (e = hipMemset(ch->ws, 0, ws_need)) != hipSuccess) ||
+        (e = hipDeviceSynchronize()) != hipSuccess) {
+        chain_free(ch);
+        return hip_fail(e, "chain set-up");
+    }
+    *out = ch;
+    return DFQ_OK;
+}
+
+dfq_status dfq_chain_launch(dfq_chain* ch, void* stream) {
+    if (!ch) return fail(DFQ_ERR_INVALID_ARGUMENT, "null chain");
+    DeviceGuard g(ch->ctx->device);
+    ChainParams cp{};
+    cp.ops = ch->ops;
+    cp.sync = ch->sync;
+    cp.n_ops = ch->n_ops;
+    cp.G = ch->G;
+    cp.lds_flag_off = ch->lds_flag_off;
+    cp.timeout = ch->timeout;
+    void* args[] = {&cp};
+    hipError_t e = hipModuleLaunchKernel(ch->fn, (unsigned)ch->G, 1, 1, kBlockThreads, 1, 1,
+                                         (unsigned)ch->lds_bytes, (hipStream_t)stream, args,
+                                         nullptr);
+    return e == hipSuccess ? DFQ_OK : hip_fail(e, "launch dfq_chain");
+}
+
+dfq_status dfq_chain_failed(dfq_chain* ch, int* failed) {
+    if (!ch || !failed) return fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
+    DeviceGuard g(ch->ctx->device);
+    uint32_t v = 0;
+    hipError_t e = hipDeviceSynchronize();
+    if (e == hipSuccess)
+        e = hipMemcpy(&v, ch->sync + 32, 4, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(e, "chain status");
+    *failed = v != 0;
+    return DFQ_OK;
+}
+
+dfq_status dfq_chain_reset(dfq_chain* ch, void* stream) {
+    if (!ch) return fail(DFQ_ERR_INVALID_ARGUMENT, "null chain");
+    return dfq_workspace_clear(ch->ctx, ch->sync, ch->sync_bytes, stream);
+}
+
+dfq_status dfq_chain_set_timeout(dfq_chain* ch, uint32_t ticks) {
+    if (!ch) return fail(DFQ_ERR_INVALID_ARGUMENT, "null chain");
+    ch->timeout = ticks;
+    return DFQ_OK;
+}
+
+dfq_status dfq_chain_destroy(dfq_chain* ch) {
+    chain_free(ch);
     return DFQ_OK;
 }
 

@@ -74,6 +74,17 @@ class _LayerInfo(ctypes.Structure):
 
 _WANT_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_char_p, ctypes.c_void_p)
 
+
+class _ChainOp(ctypes.Structure):
+    _fields_ = [
+        ("kind", ctypes.c_int), ("x", ctypes.c_void_p), ("y", ctypes.c_void_p),
+        ("w", ctypes.c_void_p), ("scales", ctypes.c_void_p), ("biases", ctypes.c_void_p),
+        ("linear_bias", ctypes.c_void_p), ("N", ctypes.c_int), ("K", ctypes.c_int),
+    ]
+
+
+CHAIN_QMM, CHAIN_SILU_MUL = 0, 1
+
 # safetensors dtype names in dfq_st_dtype order
 ST_DTYPES = ["BOOL", "U8", "I8", "I16", "U16", "F16", "BF16", "I32", "U32", "F32", "I64", "U64",
              "F64", "F8_E5M2", "F8_E4M3"]
@@ -133,6 +144,10 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         "dfq_checkpoint_layer_count": ([P], I),
         "dfq_checkpoint_layer": ([P, I, ctypes.POINTER(_LayerInfo)], I),
         "dfq_checkpoint_load_model": ([P, P, P, _WANT_FN, P, P, ctypes.POINTER(I)], I),
+        "dfq_chain_create": ([P, I, I, I, I, ctypes.POINTER(_ChainOp), I, PP], I),
+        "dfq_chain_launch": ([P, P], I), "dfq_chain_failed": ([P, ctypes.POINTER(I)], I),
+        "dfq_chain_reset": ([P, P], I), "dfq_chain_set_timeout": ([P, ctypes.c_uint32], I),
+        "dfq_chain_destroy": ([P], I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -319,6 +334,12 @@ class Context:
         return tokens, accepted
 
     # ---- graphs ---------------------------------------------------------------------------
+    def chain(self, M: int, bits: int, gs: int, ops: list, dtype=BF16) -> "Chain":
+        """A chain of ops run in one persistent launch.  Each op is a dict:
+        {"kind": "qmm", "x", "y", "w", "scales", "biases", "N", "K", optional "lbias"} or
+        {"kind": "silu_mul", "x": gu [M][2N], "y": h [M][N], "N"} (torch device tensors)."""
+        return Chain(self, M, bits, gs, ops, dtype)
+
     def graph_begin(self, stream):
         _check(self.lib.dfq_graph_begin(self.handle, _stream(stream)), "dfq_graph_begin")
 
@@ -639,5 +660,53 @@ class Checkpoint:
             if self._h:
                 self.lib.dfq_checkpoint_close(self._h)
                 self._h = None
+        except Exception:
+            pass
+
+
+class Chain:
+    """dfq_chain: a fixed list of ops on fixed buffers, launched as one kernel."""
+
+    def __init__(self, ctx: Context, M, bits, gs, ops, dtype=BF16):
+        self.lib, self.ctx = ctx.lib, ctx
+        self._keep = ops  # the buffers must outlive the chain
+        arr = (_ChainOp * len(ops))()
+        for i, o in enumerate(ops):
+            if o["kind"] == "qmm":
+                arr[i] = _ChainOp(CHAIN_QMM, _ptr(o["x"]), _ptr(o["y"]), _ptr(o["w"]),
+                                  _ptr(o["scales"]), _ptr(o["biases"]), _ptr(o.get("lbias")),
+                                  o["N"], o["K"])
+            elif o["kind"] == "silu_mul":
+                arr[i] = _ChainOp(CHAIN_SILU_MUL, _ptr(o["x"]), _ptr(o["y"]), None, None, None,
+                                  None, o["N"], 0)
+            else:
+                raise ValueError(o["kind"])
+        h = ctypes.c_void_p()
+        _check(self.lib.dfq_chain_create(ctx.handle, M, bits, gs, dtype, arr, len(ops),
+                                         ctypes.byref(h)), "dfq_chain_create")
+        self._h = h
+
+    def launch(self, stream=None):
+        _check(self.lib.dfq_chain_launch(self._h, _stream(stream)), "dfq_chain_launch")
+
+    def failed(self) -> bool:
+        f = ctypes.c_int(0)
+        _check(self.lib.dfq_chain_failed(self._h, ctypes.byref(f)), "dfq_chain_failed")
+        return bool(f.value)
+
+    def reset(self, stream=None):
+        _check(self.lib.dfq_chain_reset(self._h, _stream(stream)), "dfq_chain_reset")
+
+    def set_timeout(self, ticks: int):
+        _check(self.lib.dfq_chain_set_timeout(self._h, ticks), "dfq_chain_set_timeout")
+
+    def close(self):
+        if self._h:
+            self.lib.dfq_chain_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
         except Exception:
             pass

@@ -163,6 +163,48 @@ dfq_status dfq_argmax_accept(dfq_ctx* ctx, const void* logits, int M, int V, dfq
                              const int32_t* proposals, int32_t* tokens, int32_t* accepted,
                              void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- chains: the ops of a verify forward in one launch ---------------------------------
+ * A chain is a fixed list of ops on fixed buffers: qmm (as dfq_qmm, with 8-group chunks, up
+ * to 8 rows) and silu_mul (as dfq_silu_mul), each reading the output of an earlier op or an
+ * input.  dfq_chain_launch runs the whole list in one persistent launch, one workgroup per
+ * CU; each workgroup fetches an op's weights while the previous op finishes, and waits on a
+ * device-wide completion count only before it reads that op's output.  The result of every
+ * op is bit-identical to the same calls made one by one.  No counterpart in the reference:
+ * there the verify forward's matmuls are separate MLX dispatches of the swapped layers
+ * (SmallMQuantizedMatmul.swift:210-224, reached per layer from the target model); this is
+ * how a layer chain (or a whole forward) of them runs here.
+ * Waits are bounded (1 s by default): a chain whose workgroups cannot all be resident ends
+ * with its error flag set rather than hanging (dfq_chain_failed; dfq_chain_reset clears it).
+ * The chain owns its workspace; launches of one chain must not overlap. */
+
+typedef struct dfq_chain dfq_chain;
+
+#define DFQ_CHAIN_QMM 0
+#define DFQ_CHAIN_SILU_MUL 1
+
+typedef struct dfq_chain_op {
+    int kind;                 /* DFQ_CHAIN_QMM or DFQ_CHAIN_SILU_MUL                        */
+    const void* x;            /* qmm: [M][K]; silu_mul: gu [M][2N] (gate | up)             */
+    void* y;                  /* qmm: [M][N]; silu_mul: h [M][N]                           */
+    const uint32_t* w;        /* qmm only: MLX layout, as dfq_qmm                          */
+    const void* scales;
+    const void* biases;
+    const void* linear_bias;  /* may be NULL                                               */
+    int N, K;                 /* silu_mul: N = hidden width, K unused                      */
+} dfq_chain_op;
+
+dfq_status dfq_chain_create(dfq_ctx* ctx, int M, int bits, int group_size, dfq_dtype dtype,
+                            const dfq_chain_op* ops, int n_ops, dfq_chain** out);
+/* One launch of the whole chain on `stream` (asynchronous; allocates nothing). */
+dfq_status dfq_chain_launch(dfq_chain* chain, void* stream);
+/* Synchronises the device and reports whether a launch's wait timed out. */
+dfq_status dfq_chain_failed(dfq_chain* chain, int* failed);
+/* Clears the counters and the error flag (a kernel on `stream`). */
+dfq_status dfq_chain_reset(dfq_chain* chain, void* stream);
+/* The wait limit in 100 MHz ticks (tests use a tiny one to drive the error path). */
+dfq_status dfq_chain_set_timeout(dfq_chain* chain, uint32_t ticks);
+dfq_status dfq_chain_destroy(dfq_chain* chain);
+
 /* ---- the drop-in layer (SmallMQuantizedMatmul.swift:227-317) -------------------------- */
 
 typedef struct dfq_linear dfq_linear;
