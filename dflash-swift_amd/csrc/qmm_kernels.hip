@@ -775,6 +775,13 @@ __device__ __forceinline__ void chain_waves_done(const ChainParams& cp, int bi, 
 template <bool F16>
 __device__ void chain_prev(const ChainParams& cp, int j, int wg) {
     if (j == 0) return;
+    if (j < cp.n_ops && chain_ops(cp)[j].independent) {
+        /* op j reads nothing op j-1 writes: it only needs op j-2 done (its workspace region
+         * is the one op j-2 used; everything before op j-2 is done with it, as every
+         * workgroup runs the ops in order) */
+        if (j >= 2) chain_wait(cp, chain_block(cp, 2 * (j - 2)), wg, 2u * j - 1u);
+        return;
+    }
     const ChainOp po = chain_ops(cp)[j - 1];
     chain_wait(cp, chain_block(cp, 2 * (j - 1)), wg, 2u * j - 1u);
     if (po.kind == 0 && po.p.reduce) {

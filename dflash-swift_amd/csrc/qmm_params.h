@@ -63,7 +63,7 @@ typedef struct QmmParams {
 typedef struct ChainOp {
     QmmParams p;
     int32_t kind;
-    int32_t pad;
+    int32_t independent;    /* 1: wait for op j-2 instead of op j-1 (see dfq_chain_op)  */
 } ChainOp;
 
 /* The chain kernel's argument. */

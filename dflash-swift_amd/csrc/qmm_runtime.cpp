@@ -830,6 +830,7 @@ dfq_status dfq_chain_create(dfq_ctx* ctx, int M, int bits, int gs, dfq_dtype dty
             if (!aligned(o.x, 2) || !aligned(o.y, 2))
                 return fail(DFQ_ERR_INVALID_ARGUMENT, "op %d: misaligned buffers", j);
             c.kind = 1;
+            c.independent = (o.independent && j > 0 && !(host[j - 1].kind == 0 && host[j - 1].p.reduce)) ? 1 : 0;
             c.p.x = o.x;
             c.p.y = o.y;
             c.p.M = M;
@@ -854,6 +855,9 @@ dfq_status dfq_chain_create(dfq_ctx* ctx, int M, int bits, int gs, dfq_dtype dty
         c.kind = 0;
         c.p = fill_params(pl, o.x, o.w, o.scales, o.biases, o.linear_bias, o.y, M, o.N, o.K,
                           bits, gs, nullptr);
+        /* independent: not op 0, and not right after a reduce split (whose second pass runs
+         * at the start of the op after it) */
+        c.independent = (o.independent && j > 0 && !(host[j - 1].kind == 0 && host[j - 1].p.reduce)) ? 1 : 0;
         ws_need = std::max(ws_need, pl.ws_bytes);
         need_max = std::max(need_max, pl.lds_need);
     }
@@ -875,9 +879,12 @@ dfq_status dfq_chain_create(dfq_ctx* ctx, int M, int bits, int gs, dfq_dtype dty
     /* epoch and error lines, then (2 * n_ops + 1) blocks of 33 lines of 128 bytes */
     const size_t sync_bytes = (size_t)(2 + (2 * n_ops + 1) * 33) * 128;
     ch->sync_bytes = sync_bytes;
+    /* two workspace regions, by op parity: an independent op may start while the op before
+     * it still uses its region */
+    ws_need = (ws_need + 255) & ~(size_t)255;
     if ((e = hipMalloc(&ch->ops, sizeof(ChainOp) * n_ops)) != hipSuccess ||
         (e = hipMalloc(&ch->sync, sync_bytes)) != hipSuccess ||
-        (ws_need && (e = hipMalloc(&ch->ws, ws_need)) != hipSuccess)) {
+        (ws_need && (e = hipMalloc(&ch->ws, 2 * ws_need)) != hipSuccess)) {
         chain_free(ch);
         return hip_fail(e, "chain allocation");
     }
@@ -887,14 +894,15 @@ dfq_status dfq_chain_create(dfq_ctx* ctx, int M, int bits, int gs, dfq_dtype dty
         Plan pl;
         (void)get_plan(ctx, M, ops[j].N, ops[j].K, bits, gs, &pl);
         if (pl.need_ws) {
-            host[j].p.counters = (uint32_t*)ch->ws;
-            host[j].p.slots = (float*)((char*)ch->ws + pl.ws_counter_bytes);
+            char* region = (char*)ch->ws + (j % 2) * ws_need;
+            host[j].p.counters = (uint32_t*)region;
+            host[j].p.slots = (float*)(region + pl.ws_counter_bytes);
         }
     }
     if ((e = hipMemcpy(ch->ops, host.data(), sizeof(ChainOp) * n_ops, hipMemcpyHostToDevice)) !=
             hipSuccess ||
         (e = hipMemset(ch->sync, 0, sync_bytes)) != hipSuccess ||
-        (ch->ws && (e = hipMemset(ch->ws, 0, ws_need)) != hipSuccess) ||
+        (ch->ws && (e = hipMemset(ch->ws, 0, 2 * ws_need)) != hipSuccess) ||
         (e = hipDeviceSynchronize()) != hipSuccess) {
         chain_free(ch);
         return hip_fail(e, "chain set-up");

@@ -80,6 +80,7 @@ class _ChainOp(ctypes.Structure):
         ("kind", ctypes.c_int), ("x", ctypes.c_void_p), ("y", ctypes.c_void_p),
         ("w", ctypes.c_void_p), ("scales", ctypes.c_void_p), ("biases", ctypes.c_void_p),
         ("linear_bias", ctypes.c_void_p), ("N", ctypes.c_int), ("K", ctypes.c_int),
+        ("independent", ctypes.c_int),
     ]
 
 
@@ -337,7 +338,8 @@ class Context:
     def chain(self, M: int, bits: int, gs: int, ops: list, dtype=BF16) -> "Chain":
         """A chain of ops run in one persistent launch.  Each op is a dict:
         {"kind": "qmm", "x", "y", "w", "scales", "biases", "N", "K", optional "lbias"} or
-        {"kind": "silu_mul", "x": gu [M][2N], "y": h [M][N], "N"} (torch device tensors)."""
+        {"kind": "silu_mul", "x": gu [M][2N], "y": h [M][N], "N"} (torch device tensors);
+        "independent": True marks an op that reads no output of the op just before it."""
         return Chain(self, M, bits, gs, ops, dtype)
 
     def graph_begin(self, stream):
@@ -675,10 +677,10 @@ class Chain:
             if o["kind"] == "qmm":
                 arr[i] = _ChainOp(CHAIN_QMM, _ptr(o["x"]), _ptr(o["y"]), _ptr(o["w"]),
                                   _ptr(o["scales"]), _ptr(o["biases"]), _ptr(o.get("lbias")),
-                                  o["N"], o["K"])
+                                  o["N"], o["K"], int(bool(o.get("independent"))))
             elif o["kind"] == "silu_mul":
                 arr[i] = _ChainOp(CHAIN_SILU_MUL, _ptr(o["x"]), _ptr(o["y"]), None, None, None,
-                                  None, o["N"], 0)
+                                  None, o["N"], 0, int(bool(o.get("independent"))))
             else:
                 raise ValueError(o["kind"])
         h = ctypes.c_void_p()

@@ -191,10 +191,16 @@ typedef struct dfq_chain_op {
     const void* biases;
     const void* linear_bias;  /* may be NULL                                               */
     int N, K;                 /* silu_mul: N = hidden width, K unused                      */
+    int independent;          /* 1: reads no output of the op just before it (e.g. k and v
+                                 after q, all reading the layer input); it then starts without
+                                 waiting for that op.  Ignored for op 0 and after a reduce
+                                 split.  0: waits for the op before it (the usual case).  */
 } dfq_chain_op;
 
 dfq_status dfq_chain_create(dfq_ctx* ctx, int M, int bits, int group_size, dfq_dtype dtype,
                             const dfq_chain_op* ops, int n_ops, dfq_chain** out);
+/* An independent op waits instead for the op two places back, so consecutive independent
+ * ops stream back to back; their workspaces alternate between two regions. */
 /* One launch of the whole chain on `stream` (asynchronous; allocates nothing). */
 dfq_status dfq_chain_launch(dfq_chain* chain, void* stream);
 /* Synchronises the device and reports whether a launch's wait timed out. */

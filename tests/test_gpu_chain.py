@@ -147,6 +147,46 @@ def test_chain_wait_timeout_sets_the_error_flag_and_ends(ctx):
     chain.close()
 
 
+def test_independent_ops_match_calls_one_by_one(ctx):
+    """q, k, v and o-like ops that all read the layer input, marked independent, plus a
+    dependent op and a reduce split followed by an op marked independent (which must then
+    wait anyway): every output bit-identical to the ops run one by one, over repeated
+    launches."""
+    import torch
+    bf = torch.bfloat16
+    xc = make_case(M, D, D, seed=77)
+    x = to_dev16(xc.x, BF16)
+    outs = [torch.empty(M, n, dtype=bf, device="cuda") for n in (QKV, D, D, D, D, D)]
+    shapes = [(QKV, D, x, 0, False), (D, D, x, 1, True), (D, D, x, 2, True),
+              (D, QKV, outs[0], 3, False), (D, D, x, 4, True)]
+    ops = []
+    for k, (N, K, src, oi, ind) in enumerate(shapes):
+        c, w, s, b = weights(torch, N, K, 50 + k)
+        ops.append({"kind": "qmm", "x": src, "y": outs[oi], "w": w, "scales": s, "biases": b,
+                    "N": N, "K": K, "independent": ind})
+    # a reduce split, then an op marked independent that reads its output
+    hb = torch.randn(M, H, device="cuda").to(bf)
+    c, w, s, b = weights(torch, D, H, 60)
+    ops.append({"kind": "qmm", "x": hb, "y": outs[5], "w": w, "scales": s, "biases": b,
+                "N": D, "K": H, "independent": True})
+    tail = torch.empty(M, D, dtype=bf, device="cuda")
+    c, w, s, b = weights(torch, D, D, 61)
+    ops.append({"kind": "qmm", "x": outs[5], "y": tail, "w": w, "scales": s, "biases": b,
+                "N": D, "K": D, "independent": True})
+    ref = run_one_by_one(torch, ctx, ops)
+    chain = ctx.chain(M, 4, 64, ops)
+    for rep in range(3):
+        for o in ops:
+            o["y"].fill_(0)
+        announce(f"independent chain launch {rep}")
+        chain.launch()
+        torch.cuda.synchronize()
+        assert not chain.failed()
+        for j, o in enumerate(ops):
+            assert torch.equal(o["y"].view(torch.int16), ref[j].view(torch.int16)), (rep, j)
+    chain.close()
+
+
 def test_chain_rejects_what_it_cannot_run(ctx):
     import torch
     ops, x, xc, _ = build(torch, layers=1)
