@@ -97,6 +97,31 @@ def time_m(torch, ctx, stream, sets, M, steps, warmup, N, K, bits, gs, ws, wsb):
     return e0.elapsed_time(e1) * 1000.0 / steps
 
 
+def time_chained(torch, ctx, stream, sets, M, reps, N, K, bits, gs):
+    """The same M-row calls over the rotated weight sets as one dfq_chain launch of independent
+    ops (each reads x, none reads another's output): microseconds per call."""
+    dev = sets[0][0].device
+    x = torch.randn(M, K, device=dev).to(torch.bfloat16)
+    ys = [torch.empty(M, N, device=dev, dtype=torch.bfloat16) for _ in sets]
+    chain = ctx.chain(M, bits, gs, [
+        {"kind": "qmm", "x": x, "y": ys[i], "w": w, "scales": s, "biases": b, "N": N, "K": K,
+         "independent": i > 0} for i, (w, s, b) in enumerate(sets)])
+    with torch.cuda.stream(stream):
+        chain.launch(stream)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            chain.launch(stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+    if chain.failed():
+        raise RuntimeError("the chain reported a timed-out wait")
+    chain.close()
+    return e0.elapsed_time(e1) * 1000.0 / (reps * len(sets))
+
+
 # One verify-pass layer of the C5 chain (N, K): q, k, v, o, gate, up, down; then the lm_head.
 C5_LAYER = [(5120, 5120), (1024, 5120), (1024, 5120), (5120, 5120), (17408, 5120),
             (17408, 5120), (5120, 17408)]
@@ -353,6 +378,15 @@ def main():
         },
     }
     if not args.no_chain:
+        uc = time_chained(torch, ctx, stream, sets, 8, 25, N_OUT, K_IN, BITS, GS)
+        out["chained_independent_m8"] = {
+            "workload": (f"the same M=8 calls over the {args.sets} weight sets as one dfq_chain "
+                         "launch of independent ops (not the headline: the verify forward's "
+                         "matmuls depend on each other)"),
+            "us_per_call": round(uc, 3),
+            "gbs": round(algorithmic_bytes(8) / (uc * 1e-6) / 1e9, 1),
+        }
+        print(f"[bench] chained independent M=8: {uc:.2f} us/call", file=sys.stderr, flush=True)
         del sets
         torch.cuda.empty_cache()
         out["c5_chain"] = chain_c5(torch, ctx, dev)
