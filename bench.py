@@ -133,10 +133,10 @@ C5_LM_HEAD = (151936, 5120)
 
 def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False):
     """The C5 verify forward at M=8: `layers` layers of seven 4-bit g64 matmuls (or, fused,
-    q|k|v, o, gate|up + SiLU-mul, down), each layer captured as one HIP graph, then the
-    lm_head; distinct random weights per layer (about 11.6 GiB, so every layer streams from
-    HBM).  persistent: the fused forward's 321 ops (every layer and the lm_head) as one
-    dfq_chain launch instead of per-layer graphs.  Returns microseconds per forward."""
+    q|k|v, o, gate|up with the SiLU-mul epilogue, down), each layer captured as one HIP
+    graph, then the lm_head; distinct random weights per layer (about 11.6 GiB, so every layer
+    streams from HBM).  persistent: the fused forward's 257 ops (every layer and the lm_head)
+    as one dfq_chain launch instead of per-layer graphs.  Returns microseconds per forward."""
     fused = fused or persistent
     import dflash_qmm
     M = 8
@@ -155,15 +155,18 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False):
     wsb = max(ctx.workspace_bytes(M, N, K, 4, 64) for (N, K) in shapes)
     ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
     x = torch.randn(M, 5120, device=dev, generator=g).to(torch.bfloat16)
-    outs = [torch.empty(M, N, device=dev, dtype=torch.bfloat16) for (N, K) in layer]
     if fused:
         # q|k|v, o and gate|up read the layer input (o stands in for attention's output);
-        # down reads the SiLU-mul of gate|up
-        srcs = [None, None, None, "h"]
-        h = torch.empty(M, C5_FUSED[3][1], device=dev, dtype=torch.bfloat16)
+        # gate|up (weights interleaved by 8 rows) writes silu(gate) * up; down reads it
+        outs = [torch.empty(M, N // 2 if j == 2 else N, device=dev, dtype=torch.bfloat16)
+                for j, (N, K) in enumerate(layer)]
+        srcs = [None, None, None, 2]
+        kinds = ["qmm", "qmm", "qmm_silu_gate_up", "qmm"]
     else:
         # q, k, v, gate, up read x (the layer input); o reads q; down reads gate
+        outs = [torch.empty(M, N, device=dev, dtype=torch.bfloat16) for (N, K) in layer]
         srcs = [None, None, None, 0, None, None, 4]
+        kinds = ["qmm"] * len(layer)
     lm_out = torch.empty(M, C5_LM_HEAD[0], device=dev, dtype=torch.bfloat16)
     stream = torch.cuda.Stream(device=dev)
     B = dflash_qmm.BF16
@@ -174,26 +177,20 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False):
         layer_in = x if li == 0 else outs[-1]
         if persistent:
             for j, (N, K) in enumerate(layer):
-                if srcs[j] == "h":
-                    chain_ops.append({"kind": "silu_mul", "x": outs[2], "y": h,
-                                      "N": C5_FUSED[3][1]})
-                    inp = h
-                else:
-                    inp = layer_in
+                inp = layer_in if srcs[j] is None else outs[srcs[j]]
                 w, s, b = wl[j]
-                chain_ops.append({"kind": "qmm", "x": inp, "y": outs[j], "w": w, "scales": s,
-                                  "biases": b, "N": N, "K": K})
+                chain_ops.append({"kind": kinds[j], "x": inp, "y": outs[j], "w": w,
+                                  "scales": s, "biases": b, "N": N, "K": K})
             continue
         ctx.graph_begin(stream)
         for j, (N, K) in enumerate(layer):
-            if srcs[j] == "h":
-                ctx.silu_mul(outs[2], h, stream=stream)
-                inp = h
-            else:
-                inp = layer_in if srcs[j] is None else outs[srcs[j]]
+            inp = layer_in if srcs[j] is None else outs[srcs[j]]
             w, s, b = wl[j]
-            ctx.qmm_raw(inp, w, s, b, outs[j], M, N, K, 4, 64, B, B, B, ws=ws,
-                        ws_bytes=ws.numel(), stream=stream)
+            if kinds[j] == "qmm_silu_gate_up":
+                ctx.qmm_silu_gate_up(inp, w, s, b, 4, 64, out=outs[j], ws=ws, stream=stream)
+            else:
+                ctx.qmm_raw(inp, w, s, b, outs[j], M, N, K, 4, 64, B, B, B, ws=ws,
+                            ws_bytes=ws.numel(), stream=stream)
         graphs.append(ctx.graph_end(stream))
     wlm, slm, blm = weights(*C5_LM_HEAD)
     proposals = torch.zeros(M - 1, dtype=torch.int32, device=dev)
@@ -248,7 +245,7 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False):
     ideal = total_bytes / (HBM_PEAK_GBS * 1e3)
     return {
         "workload": (f"M=8 verify forward: {layers} layers x "
-                     + ("(q|k|v, o, gate|up, silu*up, down)" if fused
+                     + ("(q|k|v, o, gate|up with silu*up epilogue, down)" if fused
                         else "(q,k,v,o,gate,up,down)")
                      + " + lm_head + greedy accept, 4-bit g64 bf16, "
                      + ("the layers and lm_head as one persistent chain launch" if persistent

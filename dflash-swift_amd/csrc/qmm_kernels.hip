@@ -440,9 +440,47 @@ __device__ __forceinline__ void put_tile4(float* ptr, f32x4_t v) {
     }
 }
 
+/* silu(g) * u as the MLP activation computes it from a stored gate|up output: g and u
+ * rounded to the output dtype first, then silu in fp32 and one rounding (the same
+ * arithmetic as silu_mul below, so the fused epilogue is bit-identical to it). */
+template <bool F16>
+__device__ __forceinline__ uint16_t silu_mul_round(float g, float u) {
+    const float gr = elem_to_f32<F16>(f32_to_out<F16>(g));
+    const float ur = elem_to_f32<F16>(f32_to_out<F16>(u));
+    return f32_to_out<F16>(gr / (1.0f + __expf(-gr)) * ur);
+}
+
+/* The gate|up epilogue (p.epi): the weight's rows are interleaved by 8, so tile t holds gate
+ * columns 8t..8t+7 in its columns 0-7 and the matching up columns in 8-15; lane n < 8 takes
+ * its up partner from lane n + 8 (DPP row_ror:8, every lane active) and writes h[m][8t+n]. */
+template <bool F16, bool COH>
+__device__ __forceinline__ void store_h(const QmmParams& p, int t, int lane, f32x4_t v) {
+    const int q = lane >> 4, n = lane & 15;
+    float lb = 0.0f;
+    if (p.lbias) lb = elem_to_f32<F16>(((const uint16_t*)p.lbias)[t * 16 + n]);
+    f32x4_t u;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        v[r] += lb;
+        u[r] = dpp_f32<0x128>(v[r]);
+    }
+    if (lane >= 32 * p.mt || n >= 8) return;
+    const int H = p.N / 2;
+    uint16_t* h = (uint16_t*)p.y;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int m = 4 * q + r;
+        if (m < p.M) put16<COH>(h + (size_t)m * H + t * 8 + n, silu_mul_round<F16>(v[r], u[r]));
+    }
+}
+
 /* Tile t as held by the lanes, plus the linear bias, to y. */
 template <bool F16, bool COH = false>
 __device__ __forceinline__ void store_y(const QmmParams& p, int t, int lane, f32x4_t v) {
+    if (p.epi) {
+        store_h<F16, COH>(p, t, lane, v);
+        return;
+    }
     const int q = lane >> 4, n = lane & 15;
     const int col = t * 16 + n;
     if (lane >= 32 * p.mt || col >= p.N) return;
@@ -481,6 +519,56 @@ __device__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t
     const uint32_t total = (uint32_t)(p.nkb * nwg);
     /* the tile's workspace area: nkb*nslot_kb slots of mt*128 floats */
     uint32_t* base = (uint32_t*)p.slots + (size_t)t * p.nkb * p.nslot_kb * p.mt * 128;
+    if (total == 2 && p.epi) {
+        /* the gate|up epilogue needs g and u of one element summed by the same contributor:
+         * lanes n < 8 hold g and take u from lane n + 8; each element has a u word (the
+         * slot lane n + 8 would use) and a g word.  u goes in first; once that has
+         * completed, g is exchanged, and the contributor that gets back a tagged g finishes:
+         * the other's u is in its u word by then (deposited before the other's g), or came
+         * back from our own u exchange (then our u sits in the word and is cleared).  Every
+         * word is zero again afterwards. */
+        f32x4_t u;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) u[r] = dpp_f32<0x128>(v[r]);
+        if (!act || n >= 8) return;
+        uint64_t* sg = (uint64_t*)base + tile_off(lane);
+        uint64_t* su = sg + 64;
+        uint64_t ou[4], og[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            ou[r] = __hip_atomic_exchange(su + r, (1ull << 32) | __float_as_uint(u[r]),
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            og[r] = __hip_atomic_exchange(sg + r, (1ull << 32) | __float_as_uint(v[r]),
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int H = p.N / 2;
+        float lbg = 0.0f, lbu = 0.0f;
+        if (p.lbias) {
+            lbg = elem_to_f32<F16>(((const uint16_t*)p.lbias)[t * 16 + n]);
+            lbu = elem_to_f32<F16>(((const uint16_t*)p.lbias)[t * 16 + n + 8]);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if (!(og[r] >> 32)) continue;
+            float up;
+            if (ou[r] >> 32) {
+                up = __uint_as_float((uint32_t)ou[r]);
+                __hip_atomic_store(su + r, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                up = __uint_as_float((uint32_t)__hip_atomic_exchange(
+                    su + r, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+            }
+            const float g = v[r] + __uint_as_float((uint32_t)og[r]);
+            const int m = 4 * q + r;
+            if (m < p.M)
+                put16<COH>((uint16_t*)p.y + (size_t)m * H + t * 8 + n,
+                           silu_mul_round<F16>(g + lbg, u[r] + up + lbu));
+            __hip_atomic_store(sg + r, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    }
     if (total == 2) {
         const int col = t * 16 + n;
         if (act) {
@@ -1288,7 +1376,7 @@ __device__ __forceinline__ void silu_mul(const uint16_t* gu, uint16_t* h, int M,
         const int64_t m = i / N, n = i - m * N;
         const float g = elem_to_f32<F16>(gu[m * 2 * N + n]);
         const float u = elem_to_f32<F16>(gu[m * 2 * N + N + n]);
-        put16<COH>(h + i, f32_to_out<F16>(g / (1.0f + __expf(-g)) * u));
+        put16<COH>(h + i, silu_mul_round<F16>(g, u));
     }
 }
 extern "C" __global__ void __launch_bounds__(256) dfq_silu_mul_bf16(const uint16_t* gu,

@@ -47,6 +47,8 @@ typedef struct QmmParams {
     int32_t Gkb;            /* workgroups per k-block                                 */
     int32_t nslot_kb;       /* partial slots per tile per k-block                     */
     int32_t reduce;         /* 1: shared tiles go to slots summed by dfq_qmm_reduce   */
+    int32_t epi;            /* 1: y = silu(gate) * up of a gate|up weight interleaved
+                               by 8 rows (y is [M][N/2])                              */
     int32_t lds_row_stride; /* bytes per staged x row in LDS                          */
     int32_t lds_xsum_off;   /* byte offset of the per-group x sums in LDS             */
     int32_t lds_part_off;   /* byte offset of the per-unit partial tiles in LDS       */

@@ -562,7 +562,7 @@ static QmmParams fill_params(const Plan& pl, const void* x, const uint32_t* w,
 static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
                              const void* biases, const void* lbias, void* y, int M, int N, int K,
                              int bits, int gs, dfq_dtype dt, void* ws, size_t wsb,
-                             hipStream_t stream) {
+                             hipStream_t stream, int epi = 0) {
     Plan pl;
     dfq_status s = get_plan(ctx, M, N, K, bits, gs, &pl);
     if (s) return s;
@@ -573,6 +573,7 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
         if (!aligned(ws, 256)) return fail(DFQ_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
     }
     QmmParams p = fill_params(pl, x, w, scales, biases, lbias, y, M, N, K, bits, gs, ws);
+    p.epi = epi;
     const int bi = bits == 4 ? 0 : 1;
     const int gi = gs == 32 ? 0 : gs == 64 ? 1 : 2;
     const int di = dt == DFQ_BF16 ? 0 : 1;
@@ -591,10 +592,50 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
 }
 
 
+static dfq_status qmm_any(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
+                          const void* biases, const void* lbias, void* y, int M, int N, int K,
+                          int bits, int gs, dfq_dtype xdt, dfq_dtype sdt, dfq_dtype ydt, void* ws,
+                          size_t wsb, void* stream, int epi);
+
 dfq_status dfq_qmm(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
                    const void* biases, const void* lbias, void* y, int M, int N, int K, int bits,
                    int gs, dfq_dtype xdt, dfq_dtype sdt, dfq_dtype ydt, void* ws, size_t wsb,
                    void* stream) {
+    return qmm_any(ctx, x, w, scales, biases, lbias, y, M, N, K, bits, gs, xdt, sdt, ydt, ws, wsb,
+                   stream, 0);
+}
+
+dfq_status dfq_qmm_silu_gate_up(dfq_ctx* ctx, const void* x, const uint32_t* w_gu,
+                                const void* scales_gu, const void* biases_gu,
+                                const void* linear_bias_gu, void* h, int M, int H, int K,
+                                int bits, int gs, dfq_dtype dtype, void* ws, size_t wsb,
+                                void* stream) {
+    if (H < 8 || H % 8)
+        return fail(DFQ_ERR_UNSUPPORTED, "the gate|up epilogue needs H a multiple of 8 (got %d)", H);
+    return qmm_any(ctx, x, w_gu, scales_gu, biases_gu, linear_bias_gu, h, M, 2 * H, K, bits, gs,
+                   dtype, dtype, dtype, ws, wsb, stream, 1);
+}
+
+dfq_status dfq_interleave_gate_up(dfq_ctx* ctx, const void* gate, const void* up, void* out,
+                                  int H, size_t row_bytes, void* stream) {
+    if (!ctx || !gate || !up || !out) return fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
+    if (H < 8 || H % 8 || !row_bytes)
+        return fail(DFQ_ERR_INVALID_ARGUMENT, "H must be a positive multiple of 8");
+    DeviceGuard g(ctx->device);
+    /* blocks of 8 rows: gate rows 8b.. to out rows 16b.., up rows 8b.. to out rows 16b+8.. */
+    const size_t blk = 8 * row_bytes;
+    hipError_t e = hipMemcpy2DAsync(out, 2 * blk, gate, blk, blk, (size_t)(H / 8),
+                                     hipMemcpyDeviceToDevice, (hipStream_t)stream);
+    if (e == hipSuccess)
+        e = hipMemcpy2DAsync((char*)out + blk, 2 * blk, up, blk, blk, (size_t)(H / 8),
+                             hipMemcpyDeviceToDevice, (hipStream_t)stream);
+    return e == hipSuccess ? DFQ_OK : hip_fail(e, "interleave gate|up");
+}
+
+static dfq_status qmm_any(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
+                          const void* biases, const void* lbias, void* y, int M, int N, int K,
+                          int bits, int gs, dfq_dtype xdt, dfq_dtype sdt, dfq_dtype ydt, void* ws,
+                          size_t wsb, void* stream, int epi) {
     dfq_status s = check_fast_args(ctx, M, N, K, bits, gs, xdt, sdt, ydt);
     if (s) return s;
     if (!x || !w || !scales || !biases || !y)
@@ -607,13 +648,14 @@ dfq_status dfq_qmm(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* s
     const size_t esz = 2;
     if (one_pass(ctx, M, N, K, bits, gs))
         return launch_mt8(ctx, x, w, scales, biases, lbias, y, M, N, K, bits, gs, xdt, ws, wsb,
-                          (hipStream_t)stream);
+                          (hipStream_t)stream, epi);
     /* 9..16 rows with one-super-step chunks: two passes of up to 8 rows over the weights. */
+    const size_t ypitch = (size_t)(epi ? N / 2 : N) * esz;
     for (int m0 = 0; m0 < M; m0 += 8) {
         const int mc = std::min(8, M - m0);
         s = launch_mt8(ctx, (const char*)x + (size_t)m0 * K * esz, w, scales, biases, lbias,
-                       (char*)y + (size_t)m0 * N * esz, mc, N, K, bits, gs, xdt, ws, wsb,
-                       (hipStream_t)stream);
+                       (char*)y + (size_t)m0 * ypitch, mc, N, K, bits, gs, xdt, ws, wsb,
+                       (hipStream_t)stream, epi);
         if (s) return s;
     }
     return DFQ_OK;
@@ -837,7 +879,10 @@ dfq_status dfq_chain_create(dfq_ctx* ctx, int M, int bits, int gs, dfq_dtype dty
             c.p.N = o.N;
             continue;
         }
-        if (o.kind != DFQ_CHAIN_QMM) return fail(DFQ_ERR_INVALID_ARGUMENT, "op %d: unknown kind", j);
+        if (o.kind != DFQ_CHAIN_QMM && o.kind != DFQ_CHAIN_QMM_SILU_GATE_UP)
+            return fail(DFQ_ERR_INVALID_ARGUMENT, "op %d: unknown kind", j);
+        if (o.kind == DFQ_CHAIN_QMM_SILU_GATE_UP && (o.N < 16 || o.N % 16))
+            return fail(DFQ_ERR_UNSUPPORTED, "op %d: gate|up epilogue needs N = 2H, H %% 8 == 0", j);
         dfq_status st = check_fast_args(ctx, M, o.N, o.K, bits, gs, dtype, dtype, dtype);
         if (st) return st;
         if (!o.w || !o.scales || !o.biases)
@@ -855,6 +900,7 @@ dfq_status dfq_chain_create(dfq_ctx* ctx, int M, int bits, int gs, dfq_dtype dty
         c.kind = 0;
         c.p = fill_params(pl, o.x, o.w, o.scales, o.biases, o.linear_bias, o.y, M, o.N, o.K,
                           bits, gs, nullptr);
+        c.p.epi = o.kind == DFQ_CHAIN_QMM_SILU_GATE_UP ? 1 : 0;
         /* independent: not op 0, and not right after a reduce split (whose second pass runs
          * at the start of the op after it) */
         c.independent = (o.independent && j > 0 && !(host[j - 1].kind == 0 && host[j - 1].p.reduce)) ? 1 : 0;

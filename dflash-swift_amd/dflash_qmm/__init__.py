@@ -84,7 +84,7 @@ class _ChainOp(ctypes.Structure):
     ]
 
 
-CHAIN_QMM, CHAIN_SILU_MUL = 0, 1
+CHAIN_QMM, CHAIN_SILU_MUL, CHAIN_QMM_SILU_GATE_UP = 0, 1, 2
 
 # safetensors dtype names in dfq_st_dtype order
 ST_DTYPES = ["BOOL", "U8", "I8", "I16", "U16", "F16", "BF16", "I32", "U32", "F32", "I64", "U64",
@@ -149,6 +149,8 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         "dfq_chain_launch": ([P, P], I), "dfq_chain_failed": ([P, ctypes.POINTER(I)], I),
         "dfq_chain_reset": ([P, P], I), "dfq_chain_set_timeout": ([P, ctypes.c_uint32], I),
         "dfq_chain_destroy": ([P], I),
+        "dfq_qmm_silu_gate_up": ([P, P, P, P, P, P, P, I, I, I, I, I, I, P, S, P], I),
+        "dfq_interleave_gate_up": ([P, P, P, P, I, S, P], I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -283,6 +285,36 @@ class Context:
         self.qmm_raw(x, w, scales, biases, out, M, N, K, bits, gs, dt, dtype_code(scales), dt,
                      lbias=lbias, ws=ws, ws_bytes=(ws.numel() if ws is not None else 0),
                      stream=stream)
+        return out
+
+    def qmm_silu_gate_up(self, x, w_gu, scales_gu, biases_gu, bits, gs, lbias=None, out=None,
+                         ws=None, stream=None):
+        """h = silu(x @ Wg.T) * (x @ Wu.T) over a gate|up weight interleaved by 8 rows
+        (interleave_gate_up): h is [M, H] with 2H = rows of w_gu."""
+        import torch
+        M, K = x.shape
+        H = w_gu.shape[0] // 2
+        if out is None:
+            out = torch.empty((M, H), dtype=x.dtype, device=x.device)
+        need = self.workspace_bytes(M, 2 * H, K, bits, gs)
+        if ws is None:
+            ws = self.workspace(need)
+        _check(self.lib.dfq_qmm_silu_gate_up(
+            self.handle, _ptr(x), _ptr(w_gu), _ptr(scales_gu), _ptr(biases_gu), _ptr(lbias),
+            _ptr(out), M, H, K, bits, gs, dtype_code(x), _ptr(ws),
+            ws.numel() if ws is not None else 0, _stream(stream)), "dfq_qmm_silu_gate_up")
+        return out
+
+    def interleave_gate_up(self, gate, up, stream=None):
+        """The gate and up arrays (same shape, rows = H) interleaved in blocks of 8 rows."""
+        import torch
+        if not (gate.is_contiguous() and up.is_contiguous()) or gate.shape != up.shape:
+            raise ValueError("gate and up must be contiguous arrays of one shape")
+        H = gate.shape[0]
+        out = torch.empty((2 * H,) + tuple(gate.shape[1:]), dtype=gate.dtype, device=gate.device)
+        row = gate[0].numel() * gate.element_size()
+        _check(self.lib.dfq_interleave_gate_up(self.handle, _ptr(gate), _ptr(up), _ptr(out), H,
+                                               row, _stream(stream)), "dfq_interleave_gate_up")
         return out
 
     def fallback(self, x, w, scales, biases, bits, gs, lbias=None, out=None, out_dtype=None,
@@ -674,8 +706,9 @@ class Chain:
         self._keep = ops  # the buffers must outlive the chain
         arr = (_ChainOp * len(ops))()
         for i, o in enumerate(ops):
-            if o["kind"] == "qmm":
-                arr[i] = _ChainOp(CHAIN_QMM, _ptr(o["x"]), _ptr(o["y"]), _ptr(o["w"]),
+            if o["kind"] in ("qmm", "qmm_silu_gate_up"):
+                kind = CHAIN_QMM if o["kind"] == "qmm" else CHAIN_QMM_SILU_GATE_UP
+                arr[i] = _ChainOp(kind, _ptr(o["x"]), _ptr(o["y"]), _ptr(o["w"]),
                                   _ptr(o["scales"]), _ptr(o["biases"]), _ptr(o.get("lbias")),
                                   o["N"], o["K"], int(bool(o.get("independent"))))
             elif o["kind"] == "silu_mul":

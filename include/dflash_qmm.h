@@ -120,6 +120,26 @@ dfq_status dfq_qmm(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* s
                    int bits, int group_size, dfq_dtype x_dtype, dfq_dtype sb_dtype,
                    dfq_dtype y_dtype, void* workspace, size_t workspace_bytes, void* stream);
 
+/* The MLP's fused gate|up projection with its SiLU-mul epilogue: h[M][H] = silu(x . Wg^T) *
+ * (x . Wu^T), over one weight whose gate and up rows are interleaved in blocks of 8 (rows
+ * 16b..16b+7 = gate rows 8b.., rows 16b+8.. = up rows 8b..; dfq_interleave_gate_up builds it,
+ * and the scales, biases and linear bias alike).  g and u are rounded to the dtype before
+ * silu, exactly as dfq_silu_mul applied to the stored gate|up output, so h is bit-identical
+ * to that pair of calls on the interleaved weight.  H % 8 == 0; the workspace is
+ * dfq_qmm_workspace_bytes(M, 2*H, K, ...).  The fused form of the MLP activation of the
+ * target layers (the SiLU-gated MLP of DFlashDecoderLayer.swift:26) around the swapped
+ * gate and up projections. */
+dfq_status dfq_qmm_silu_gate_up(dfq_ctx* ctx, const void* x, const uint32_t* w_gu,
+                                const void* scales_gu, const void* biases_gu,
+                                const void* linear_bias_gu, void* h, int M, int H, int K,
+                                int bits, int group_size, dfq_dtype dtype, void* workspace,
+                                size_t workspace_bytes, void* stream);
+/* out[2H rows] = gate and up rows (row_bytes each) interleaved in blocks of 8, on `stream`;
+ * for the weight (row_bytes = K*bits/8), scales and biases (K/group_size*2) and linear bias
+ * (2). */
+dfq_status dfq_interleave_gate_up(dfq_ctx* ctx, const void* gate, const void* up, void* out,
+                                  int H, size_t row_bytes, void* stream);
+
 /* The generic path: any M >= 1, bits 2/4/8, any group size dividing K; x and scales may
  * differ in dtype (y dtype follows MLX promotion: equal -> same, else fp32).  Re-reads W
  * for every row.  Stands in for the stock op MLX falls back to,
@@ -181,6 +201,7 @@ typedef struct dfq_chain dfq_chain;
 
 #define DFQ_CHAIN_QMM 0
 #define DFQ_CHAIN_SILU_MUL 1
+#define DFQ_CHAIN_QMM_SILU_GATE_UP 2  /* dfq_qmm_silu_gate_up: N = 2H, y = h [M][H] */
 
 typedef struct dfq_chain_op {
     int kind;                 /* DFQ_CHAIN_QMM or DFQ_CHAIN_SILU_MUL                        */

@@ -62,6 +62,8 @@ def run_one_by_one(torch, ctx, ops):
     for o in ops:
         if o["kind"] == "qmm":
             ctx.qmm(o["x"], o["w"], o["scales"], o["biases"], 4, 64, out=o["y"])
+        elif o["kind"] == "qmm_silu_gate_up":
+            ctx.qmm_silu_gate_up(o["x"], o["w"], o["scales"], o["biases"], 4, 64, out=o["y"])
         else:
             ctx.silu_mul(o["x"], o["y"])
         torch.cuda.synchronize()
@@ -179,6 +181,36 @@ def test_independent_ops_match_calls_one_by_one(ctx):
         for o in ops:
             o["y"].fill_(0)
         announce(f"independent chain launch {rep}")
+        chain.launch()
+        torch.cuda.synchronize()
+        assert not chain.failed()
+        for j, o in enumerate(ops):
+            assert torch.equal(o["y"].view(torch.int16), ref[j].view(torch.int16)), (rep, j)
+    chain.close()
+
+
+def test_chain_with_the_gate_up_epilogue(ctx):
+    """A layer whose MLP is the fused gate|up epilogue then down: bit-identical to the calls."""
+    import torch
+    bf = torch.bfloat16
+    x = to_dev16(make_case(M, D, D, seed=91).x, BF16)
+    A = torch.empty(M, QKV, dtype=bf, device="cuda")
+    Hb = torch.empty(M, H, dtype=bf, device="cuda")
+    out = torch.empty(M, D, dtype=bf, device="cuda")
+    ops = []
+    c, w, s, b = weights(torch, QKV, D, 92)
+    ops.append({"kind": "qmm", "x": x, "y": A, "w": w, "scales": s, "biases": b, "N": QKV, "K": D})
+    c, w, s, b = weights(torch, 2 * H, QKV, 93)      # read as an interleaved gate|up weight
+    ops.append({"kind": "qmm_silu_gate_up", "x": A, "y": Hb, "w": w, "scales": s, "biases": b,
+                "N": 2 * H, "K": QKV})
+    c, w, s, b = weights(torch, D, H, 94)
+    ops.append({"kind": "qmm", "x": Hb, "y": out, "w": w, "scales": s, "biases": b, "N": D, "K": H})
+    ref = run_one_by_one(torch, ctx, ops)
+    chain = ctx.chain(M, 4, 64, ops)
+    for rep in range(2):
+        for o in ops:
+            o["y"].fill_(0)
+        announce(f"gate|up chain launch {rep}")
         chain.launch()
         torch.cuda.synchronize()
         assert not chain.failed()
