@@ -133,10 +133,11 @@ C5_LM_HEAD = (151936, 5120)
 
 def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False):
     """The C5 verify forward at M=8: `layers` layers of seven 4-bit g64 matmuls (or, fused,
-    q|k|v, o, gate|up with the SiLU-mul epilogue, down), each layer captured as one HIP
-    graph, then the lm_head; distinct random weights per layer (about 11.6 GiB, so every layer
-    streams from HBM).  persistent: the fused forward's 257 ops (every layer and the lm_head)
-    as one dfq_chain launch instead of per-layer graphs.  Returns microseconds per forward."""
+    q|k|v, o, gate|up with the SiLU-mul epilogue, down), then the lm_head and the greedy
+    accept, the whole forward captured as one HIP graph; distinct random weights per layer
+    (about 11.6 GiB, so every layer streams from HBM).  persistent: the fused forward's 257
+    ops (every layer and the lm_head) as one dfq_chain launch instead of the graph.  Returns
+    microseconds per forward."""
     fused = fused or persistent
     import dflash_qmm
     M = 8
@@ -170,10 +171,18 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False):
     lm_out = torch.empty(M, C5_LM_HEAD[0], device=dev, dtype=torch.bfloat16)
     stream = torch.cuda.Stream(device=dev)
     B = dflash_qmm.BF16
-    graphs, lw, chain_ops = [], [], []
+    graphs, chain_ops = [], []
+    lw = [[weights(N, K) for (N, K) in layer] for _ in range(layers)]
+    wlm, slm, blm = weights(*C5_LM_HEAD)
+    proposals = torch.zeros(M - 1, dtype=torch.int32, device=dev)
+    tokens = torch.empty(M, dtype=torch.int32, device=dev)
+    accepted = torch.empty(1, dtype=torch.int32, device=dev)
+    acc_ws = torch.zeros(256, dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+    if not persistent:
+        ctx.graph_begin(stream)
     for li in range(layers):
-        wl = [weights(N, K) for (N, K) in layer]
-        lw.append(wl)
+        wl = lw[li]
         layer_in = x if li == 0 else outs[-1]
         if persistent:
             for j, (N, K) in enumerate(layer):
@@ -182,7 +191,6 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False):
                 chain_ops.append({"kind": kinds[j], "x": inp, "y": outs[j], "w": w,
                                   "scales": s, "biases": b, "N": N, "K": K})
             continue
-        ctx.graph_begin(stream)
         for j, (N, K) in enumerate(layer):
             inp = layer_in if srcs[j] is None else outs[srcs[j]]
             w, s, b = wl[j]
@@ -191,12 +199,6 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False):
             else:
                 ctx.qmm_raw(inp, w, s, b, outs[j], M, N, K, 4, 64, B, B, B, ws=ws,
                             ws_bytes=ws.numel(), stream=stream)
-        graphs.append(ctx.graph_end(stream))
-    wlm, slm, blm = weights(*C5_LM_HEAD)
-    proposals = torch.zeros(M - 1, dtype=torch.int32, device=dev)
-    tokens = torch.empty(M, dtype=torch.int32, device=dev)
-    accepted = torch.empty(1, dtype=torch.int32, device=dev)
-    acc_ws = torch.zeros(256, dtype=torch.uint8, device=dev)
 
     def lm_only():
         """the lm_head and the greedy accept: only M + 1 ints leave the device"""
@@ -205,6 +207,9 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False):
         ctx.argmax_accept(lm_out, proposals, tokens, accepted, ws=acc_ws, stream=stream)
 
     chain = None
+    if not persistent:
+        lm_only()
+        graphs.append(ctx.graph_end(stream))
     if persistent:
         chain_ops.append({"kind": "qmm", "x": outs[-1], "y": lm_out, "w": wlm, "scales": slm,
                           "biases": blm, "N": C5_LM_HEAD[0], "K": C5_LM_HEAD[1]})
@@ -215,9 +220,7 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False):
             chain.launch(stream)
             ctx.argmax_accept(lm_out, proposals, tokens, accepted, ws=acc_ws, stream=stream)
             return
-        for gr in graphs:
-            gr.launch(stream)
-        lm_only()
+        graphs[0].launch(stream)
 
     def timed(fn, n):
         with torch.cuda.stream(stream):
@@ -249,7 +252,7 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False):
                         else "(q,k,v,o,gate,up,down)")
                      + " + lm_head + greedy accept, 4-bit g64 bf16, "
                      + ("the layers and lm_head as one persistent chain launch" if persistent
-                        else "one HIP graph per layer")),
+                        else "one HIP graph per forward")),
         "us_per_forward": round(total, 1),
         "ideal_us_at_8TBs": round(ideal, 1),
         "frac_of_ideal": round(ideal / total, 4),

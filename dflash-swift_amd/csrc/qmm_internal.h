@@ -33,7 +33,6 @@ struct Plan {
     int lds_bytes = 0;  /* dynamic LDS requested per workgroup               */
     int lds_need = 0;   /* LDS bytes the layout uses                         */
     bool need_ws = false;
-    size_t ws_counter_bytes = 0;
     size_t ws_bytes = 0;
 };
 

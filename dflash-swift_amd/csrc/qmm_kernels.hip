@@ -502,14 +502,14 @@ __device__ __forceinline__ void store_y(const QmmParams& p, int t, int lane, f32
  * arrived second, adds the two values (fp32 addition of two terms does not depend on their
  * order), writes that y element and zeroes the word.  One round trip, no counter.
  *
- * More contributors: the last contributor (found with a per-tile arrival counter) sums all
- * slots of the tile in a fixed order, writes y, zeroes the slots and re-arms the counter.
+ * Tiles with more contributors belong to reduce splits, which store their parts with no
+ * round trip and leave the sum to the second pass (a per-tile arrival counter here costs
+ * the publisher two memory round trips per tile under full HBM load, which made such
+ * splits 1.7-2.2x slower than the second pass).
  *
- * Either way the workspace is zero again when the kernel ends.  Workgroups on different
- * XCDs exchange these partials: every access to a slot or a counter is an agent-scope
- * atomic (coherent across the XCDs' L2s without a whole-cache write-back or invalidate);
- * in the counter scheme the slot stores are waited for before the counter increment, and
- * the last contributor only reads slots after its own increment has returned. */
+ * The workspace is zero again when the kernel ends.  Workgroups on different XCDs exchange
+ * these partials: every access to a slot is an agent-scope atomic (coherent across the
+ * XCDs' L2s without a whole-cache write-back or invalidate). */
 template <bool F16, bool COH = false>
 __device__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t, int slot,
                         int lane, f32x4_t v) {
@@ -569,60 +569,25 @@ __device__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t
         }
         return;
     }
-    if (total == 2) {
-        const int col = t * 16 + n;
-        if (act) {
-            uint64_t* sl = (uint64_t*)base + tile_off(lane);
-            uint64_t old[4];
+    if (total != 2 || !act) return;  // one part: stored by the caller; more: reduce splits
+    const int col = t * 16 + n;
+    uint64_t* sl = (uint64_t*)base + tile_off(lane);
+    uint64_t old[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                old[r] = __hip_atomic_exchange(sl + r, (1ull << 32) | __float_as_uint(v[r]),
-                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            float lb = 0.0f;
-            if (p.lbias && col < p.N) lb = elem_to_f32<F16>(((const uint16_t*)p.lbias)[col]);
+    for (int r = 0; r < 4; ++r)
+        old[r] = __hip_atomic_exchange(sl + r, (1ull << 32) | __float_as_uint(v[r]),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float lb = 0.0f;
+    if (p.lbias && col < p.N) lb = elem_to_f32<F16>(((const uint16_t*)p.lbias)[col]);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if (!(old[r] >> 32)) continue;
-                const int m = 4 * q + r;
-                const float sum = v[r] + __uint_as_float((uint32_t)old[r]);
-                if (m < p.M && col < p.N)
-                    put16<COH>((uint16_t*)p.y + (size_t)m * p.N + col,
-                               f32_to_out<F16>(sum + lb));
-                __hip_atomic_store(sl + r, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
-        return;
+    for (int r = 0; r < 4; ++r) {
+        if (!(old[r] >> 32)) continue;
+        const int m = 4 * q + r;
+        const float sum = v[r] + __uint_as_float((uint32_t)old[r]);
+        if (m < p.M && col < p.N)
+            put16<COH>((uint16_t*)p.y + (size_t)m * p.N + col, f32_to_out<F16>(sum + lb));
+        __hip_atomic_store(sl + r, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    /* more than two parts (splits that do not run in reduce mode): store the part, count it,
-     * and the last of the tile's parts sums them in slot order */
-    if (act) {
-        uint32_t* sl = base + (size_t)slot * p.mt * 128 + tile_off(lane);
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-            __hip_atomic_store(sl + r, __float_as_uint(v[r]), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    uint32_t old = 0;
-    if (lane == 0)
-        old = __hip_atomic_fetch_add(p.counters + t, 1u, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-    old = __builtin_amdgcn_readfirstlane(old);
-    if (old + 1 != total) return;
-    f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (act) {
-        for (int kb = 0; kb < p.nkb; ++kb)
-            for (int j = 0; j < nwg; ++j) {
-                uint32_t* sl = base + ((size_t)kb * p.nslot_kb + j) * p.mt * 128 + tile_off(lane);
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    sum[r] += __uint_as_float(__hip_atomic_exchange(
-                        sl + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-            }
-    }
-    store_y<F16, COH>(p, t, lane, sum);
-    if (lane == 0)
-        __hip_atomic_store(p.counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 /* The publisher wave of a qmm_mt8 workgroup.  The streaming waves only sum a finished tile

@@ -38,7 +38,6 @@ typedef struct QmmParams {
     const void* lbias;      /* [N] optional linear bias (NULL if none)               */
     void* y;                /* [M][N] output, same dtype as x                         */
     float* slots;           /* workspace: per-tile partial sums                       */
-    uint32_t* counters;     /* workspace: per-tile arrival counters (zero at rest)    */
     int32_t M, N, K;
     int32_t mt;             /* row tiles of 8 the launch computes (1: M<=8, 2: M<=16) */
     int32_t T;              /* column tiles of 16                                     */

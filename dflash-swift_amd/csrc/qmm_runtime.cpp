@@ -235,8 +235,7 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
         p.lds_bytes = (int)std::min(want, lds_max);
         p.lds_need = (int)need;
         p.need_ws = d > 1 || nslot > 1;
-        p.ws_counter_bytes = ((size_t)T * 4 + 255) & ~(size_t)255;
-        p.ws_bytes = p.need_ws ? p.ws_counter_bytes + (size_t)T * d * nslot * mt * 128 * 4 : 0;
+        p.ws_bytes = p.need_ws ? (size_t)T * d * nslot * mt * 128 * 4 : 0;
         *pl = p;
         return true;
     }
@@ -533,10 +532,7 @@ static QmmParams fill_params(const Plan& pl, const void* x, const uint32_t* w,
     p.biases = biases;
     p.lbias = lbias;
     p.y = y;
-    if (pl.need_ws && ws) {
-        p.counters = (uint32_t*)ws;
-        p.slots = (float*)((char*)ws + pl.ws_counter_bytes);
-    }
+    if (pl.need_ws && ws) p.slots = (float*)ws;
     p.M = M;
     p.N = N;
     p.K = K;
@@ -941,8 +937,7 @@ dfq_status dfq_chain_create(dfq_ctx* ctx, int M, int bits, int gs, dfq_dtype dty
         (void)get_plan(ctx, M, ops[j].N, ops[j].K, bits, gs, &pl);
         if (pl.need_ws) {
             char* region = (char*)ch->ws + (j % 2) * ws_need;
-            host[j].p.counters = (uint32_t*)region;
-            host[j].p.slots = (float*)(region + pl.ws_counter_bytes);
+            host[j].p.slots = (float*)region;
         }
     }
     if ((e = hipMemcpy(ch->ops, host.data(), sizeof(ChainOp) * n_ops, hipMemcpyHostToDevice)) !=
