@@ -1356,79 +1356,115 @@ extern "C" __global__ void __launch_bounds__(256) dfq_silu_mul_f16(const uint16_
 }
 
 /* Greedy accept of a verify pass (the reference's acceptedPrefix).  Blocks of one row cover
- * chunks of its V logits; each folds its chunk's maximum into the row's 64-bit key with an
- * agent-scope atomic max: the high word is the logit's bits made order-preserving (sign flip
- * or full flip for negatives), the low word is ~index, so the largest key is the largest
- * logit and, among equal logits, the first index (MLX's argMax).  NaN logits are skipped.
- * The last block to arrive (counter) turns the keys into tokens, counts the leading run of
- * tokens[i] == proposals[i] (i < M-1), writes both, and re-arms keys and counter to zero. */
+ * DFQ_ACCEPT_CHUNK of its V logits; each folds its chunk's maximum into the row's 64-bit key
+ * with an agent-scope atomic max: the high word is the logit's bits made order-preserving
+ * (sign flip or full flip for negatives), the low word is ~index, so the largest key is the
+ * largest logit and, among equal logits, the first index (MLX's argMax).  NaN logits are
+ * skipped.  The last block to arrive (counter) turns the keys into tokens, finds the leading
+ * run of tokens[i] == proposals[i] (i < M-1), writes both, and re-arms keys and counter.
+ *
+ * A thread issues both of its 16-byte loads before using either (rows 16-byte aligned: V a
+ * multiple of 8); other rows take 2-byte loads, four in flight.  Keys are only touched by
+ * agent-scope atomics, so a block's max is visible to the last block once it has completed
+ * (vmcnt) before the block's relaxed counter increment: no cache write-back or invalidate. */
 __device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
     const uint32_t b = __float_as_uint(v);
     const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
     return ((uint64_t)o << 32) | (uint32_t)~(uint32_t)idx;
 }
 
+__device__ __forceinline__ uint64_t max_key_wave(uint64_t k) {
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)k, s, 64);
+        const uint32_t hi = __shfl_xor((uint32_t)(k >> 32), s, 64);
+        const uint64_t o = ((uint64_t)hi << 32) | lo;
+        k = o > k ? o : k;
+    }
+    return k;
+}
+
 template <bool F16>
-__device__ __forceinline__ void argmax_accept(const uint16_t* logits, int M, int V, int chunk,
+__device__ __forceinline__ void argmax_accept(const uint16_t* logits, int M, int V,
                                               const int32_t* proposals, int32_t* tokens,
                                               int32_t* accepted, uint64_t* keys,
                                               uint32_t* counter) {
-    const int per_row = (V + chunk - 1) / chunk;
+    constexpr int C = DFQ_ACCEPT_CHUNK;
+    const int tid = threadIdx.x;
+    const int per_row = (V + C - 1) / C;
     const int row = blockIdx.x / per_row, c = blockIdx.x - row * per_row;
-    const int lo = c * chunk, hi = min(V, lo + chunk);
+    const int lo = c * C, hi = min(V, lo + C);
     const uint16_t* lr = logits + (size_t)row * V;
     uint64_t best = 0;
-    for (int i = lo + (int)threadIdx.x; i < hi; i += 256) {
-        const float v = elem_to_f32<F16>(lr[i]);
-        if (v != v) continue;
-        const uint64_t k = argmax_key(v, i);
-        best = k > best ? k : best;
-    }
-    /* tree reduction of the block's keys through LDS */
-    __shared__ uint64_t red[256];
-    red[threadIdx.x] = best;
-    __syncthreads();
-    for (int s2 = 128; s2 > 0; s2 >>= 1) {
-        if ((int)threadIdx.x < s2) {
-            const uint64_t o = red[threadIdx.x + s2];
-            if (o > red[threadIdx.x]) red[threadIdx.x] = o;
+    if ((V & 7) == 0 && ((uintptr_t)logits & 15) == 0) {
+        u32x4_t v[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int i = lo + (u * 256 + tid) * 8;
+            if (i < hi) v[u] = *(const u32x4_t*)(lr + i);
         }
-        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int i = lo + (u * 256 + tid) * 8;
+            if (i >= hi) continue;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float f = elem_to_f32<F16>((uint16_t)(v[u][e >> 1] >> (16 * (e & 1))));
+                if (f != f) continue;
+                const uint64_t k = argmax_key(f, i + e);
+                best = k > best ? k : best;
+            }
+        }
+    } else {
+#pragma unroll 4
+        for (int i = lo + tid; i < hi; i += 256) {
+            const float f = elem_to_f32<F16>(lr[i]);
+            if (f != f) continue;
+            const uint64_t k = argmax_key(f, i);
+            best = k > best ? k : best;
+        }
     }
+    best = max_key_wave(best);
+    __shared__ uint64_t wbest[4];
     __shared__ uint32_t last;
-    if (threadIdx.x == 0) {
-        if (red[0]) __hip_atomic_fetch_max(keys + row, red[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint32_t n = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL,
+    __shared__ int first_bad;
+    if ((tid & 63) == 0) wbest[tid >> 6] = best;
+    __syncthreads();
+    if (tid == 0) {
+        uint64_t b = wbest[0];
+        for (int w = 1; w < 4; ++w) b = wbest[w] > b ? wbest[w] : b;
+        if (b) __hip_atomic_fetch_max(keys + row, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const uint32_t n = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED,
                                                   __HIP_MEMORY_SCOPE_AGENT);
         last = (n + 1 == gridDim.x) ? 1u : 0u;
+        first_bad = M - 1;
     }
     __syncthreads();
-    if (!last || threadIdx.x != 0) return;
-    int run = 0;
-    bool agree = true;
-    for (int m = 0; m < M; ++m) {
+    if (!last) return;
+    for (int m = tid; m < M; m += 256) {
         const uint64_t k = __hip_atomic_exchange(keys + m, 0ull, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
         const int32_t tok = k ? (int32_t)~(uint32_t)k : -1;
         if (tokens) tokens[m] = tok;
-        if (m < M - 1) {
-            agree = agree && proposals && proposals[m] == tok;
-            run += agree ? 1 : 0;
-        }
+        if (m < M - 1 && !(proposals && proposals[m] == tok)) atomicMin(&first_bad, m);
     }
-    if (accepted) *accepted = run;
-    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (tid == 0) {
+        if (accepted) *accepted = first_bad;
+        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 extern "C" __global__ void __launch_bounds__(256) dfq_argmax_accept_bf16(
-    const uint16_t* logits, int M, int V, int chunk, const int32_t* proposals, int32_t* tokens,
+    const uint16_t* logits, int M, int V, const int32_t* proposals, int32_t* tokens,
     int32_t* accepted, uint64_t* keys, uint32_t* counter) {
-    argmax_accept<false>(logits, M, V, chunk, proposals, tokens, accepted, keys, counter);
+    argmax_accept<false>(logits, M, V, proposals, tokens, accepted, keys, counter);
 }
 extern "C" __global__ void __launch_bounds__(256) dfq_argmax_accept_f16(
-    const uint16_t* logits, int M, int V, int chunk, const int32_t* proposals, int32_t* tokens,
+    const uint16_t* logits, int M, int V, const int32_t* proposals, int32_t* tokens,
     int32_t* accepted, uint64_t* keys, uint32_t* counter) {
-    argmax_accept<true>(logits, M, V, chunk, proposals, tokens, accepted, keys, counter);
+    argmax_accept<true>(logits, M, V, proposals, tokens, accepted, keys, counter);
 }
 
 /* The second pass of a split whose tiles can have more than two contributors (several

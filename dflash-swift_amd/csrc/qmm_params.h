@@ -90,4 +90,7 @@ typedef struct QmmGenericParams {
     int32_t xdt, sdt, ydt;  /* 0 bf16, 1 fp16, 2 fp32 */
 } QmmGenericParams;
 
+/* Logits per block of dfq_argmax_accept: 256 threads x two 16-byte loads of 8 logits. */
+#define DFQ_ACCEPT_CHUNK 4096
+
 #endif

@@ -700,13 +700,12 @@ dfq_status dfq_argmax_accept(dfq_ctx* ctx, const void* logits, int M, int V, dfq
     if (!aligned(ws, 8) || !aligned(logits, 2))
         return fail(DFQ_ERR_INVALID_ARGUMENT, "workspace must be 8-byte aligned");
     DeviceGuard g(ctx->device);
-    int chunk = 4096;
-    const int64_t per_row = ((int64_t)V + chunk - 1) / chunk;
+    const int64_t per_row = ((int64_t)V + DFQ_ACCEPT_CHUNK - 1) / DFQ_ACCEPT_CHUNK;
     if ((int64_t)M * per_row > 0x7fffffff) return fail(DFQ_ERR_UNSUPPORTED, "grid too large");
     uint64_t* keys = (uint64_t*)ws;
     uint32_t* counter = (uint32_t*)((char*)ws + (size_t)M * 8);
-    void* args[] = {(void*)&logits, &M, &V, &chunk, (void*)&proposals, &tokens, &accepted,
-                    &keys, &counter};
+    void* args[] = {(void*)&logits, &M, &V, (void*)&proposals, &tokens, &accepted, &keys,
+                    &counter};
     hipError_t e = hipModuleLaunchKernel(ctx->argmax_accept[dtype == DFQ_BF16 ? 0 : 1],
                                          (unsigned)(M * per_row), 1, 1, 256, 1, 1, 0,
                                          (hipStream_t)stream, args, nullptr);

@@ -137,7 +137,8 @@ def test_fused_mlp_chain_matches_oracle(ctx):
     gr.close()
 
 
-@pytest.mark.parametrize("dt,M,V", [("bf16", 8, 151936), ("f16", 3, 1000), ("bf16", 1, 4097)])
+@pytest.mark.parametrize("dt,M,V", [("bf16", 8, 151936), ("f16", 3, 1000), ("bf16", 1, 4097),
+                                    ("bf16", 5, 3001), ("f16", 16, 20000)])
 def test_argmax_accept_matches_oracle(ctx, dt, M, V):
     import numpy as np
     from gpu_util import to_dev16
@@ -149,6 +150,10 @@ def test_argmax_accept_matches_oracle(ctx, dt, M, V):
     if M > 2:
         a[2, :] = np.nan
         a[2, V - 1] = -7.0                               # one number among NaNs
+    if M > 4:
+        a[3, :] = -np.inf
+        a[3, V // 2] = -1e30 if dt == "bf16" else -60000.0   # the one finite value wins
+        a[4, 5] = np.inf                                 # +inf beats every finite logit
     bits = to_bits(a, code)
     logits = to_dev16(bits, code)
     want_tokens, _ = argmax_accept(bits, code)
