@@ -304,6 +304,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-chain", action="store_true",
                     help="skip the 64-layer verify-forward measurement (c5_chain)")
+    ap.add_argument("--c5-only", choices=["separate", "fused", "persistent"], default=None,
+                    help="only time this form of the 64-layer verify forward (for profiling) "
+                         "and print its figures")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run 20 plain device copies of this many MiB (the reference "
                          "point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -329,6 +332,12 @@ def main():
         print(json.dumps({"copy_bytes_per_launch": n, "launches": 20}), flush=True)
         return
     ctx = dflash_qmm.Context(0)
+    if args.c5_only:
+        r = chain_c5(torch, ctx, dev, fused=args.c5_only == "fused",
+                     persistent=args.c5_only == "persistent")
+        print(json.dumps({"c5_" + args.c5_only: r}), flush=True)
+        ctx.close()
+        return
     stream = torch.cuda.Stream(device=dev)
     sets = make_sets(torch, args.sets, N_OUT, K_IN, BITS, GS, dev)
     ms = [int(v) for v in args.ms.split(",")]

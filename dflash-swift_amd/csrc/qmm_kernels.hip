@@ -677,24 +677,38 @@ __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
 /* One tile of a reduce split's second pass: the tile's partial slots summed in (k-block,
  * workgroup) order -- a fixed order, so the result does not depend on timing -- plus the
  * linear bias, to y; the slots are zeroed, which leaves the workspace zero at rest.  Tiles
- * with one contributor were written by the main kernel. */
+ * with one contributor were written by the main kernel.
+ *
+ * All nkb * nslot_kb slots of the tile are read, eight loads in flight before any use: the
+ * slots a k-block leaves unused are zero, and adding +0.0f to a sum that is never -0.0f
+ * (it starts at +0.0f) leaves it unchanged, so the result equals the sum of the used slots
+ * alone.  One memory latency per eight slots instead of one per slot. */
 template <bool F16, bool COH = false>
 __device__ __forceinline__ void reduce_tile(const QmmParams& p, int t, int lane) {
-    f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
     int parts = 0;
     for (int kb = 0; kb < p.nkb; ++kb) {
         const KBlock k = kblock(p, kb);
-        const int first = owner_wg(t * k.SS, k.base, k.rem);
-        const int nwg = owner_wg(t * k.SS + k.SS - 1, k.base, k.rem) - first + 1;
-        for (int j = 0; j < nwg; ++j, ++parts) {
-            if (lane < 32 * p.mt) {
-                float* sl = tile_slot(p, t, kb, j, lane);
-                sum += *(const f32x4_t*)sl;
-                put_tile4<COH>(sl, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f});
-            }
+        parts += owner_wg(t * k.SS + k.SS - 1, k.base, k.rem) - owner_wg(t * k.SS, k.base, k.rem) + 1;
+    }
+    if (parts <= 1) return;
+    f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (lane < 32 * p.mt) {
+        const int S = p.nkb * p.nslot_kb, stride = p.mt * 128;
+        float* s0 = tile_slot(p, t, 0, 0, lane);  // slot i = kb * nslot_kb + j at s0 + i * stride
+        for (int b = 0; b < S; b += 8) {
+            f32x4_t v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (b + i < S) v[i] = *(const f32x4_t*)(s0 + (size_t)(b + i) * stride);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (b + i < S) {
+                    sum += v[i];
+                    put_tile4<COH>(s0 + (size_t)(b + i) * stride, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f});
+                }
         }
     }
-    if (parts > 1) store_y<F16, COH>(p, t, lane, sum);
+    store_y<F16, COH>(p, t, lane, sum);
 }
 
 /* ---- the chain kernel's synchronisation ------------------------------------------------
