@@ -204,10 +204,11 @@ typedef struct dfq_chain dfq_chain;
 #define DFQ_CHAIN_QMM_SILU_GATE_UP 2  /* dfq_qmm_silu_gate_up: N = 2H, y = h [M][H] */
 
 typedef struct dfq_chain_op {
-    int kind;                 /* DFQ_CHAIN_QMM or DFQ_CHAIN_SILU_MUL                        */
+    int kind;                 /* DFQ_CHAIN_QMM, DFQ_CHAIN_SILU_MUL, DFQ_CHAIN_QMM_SILU_GATE_UP */
     const void* x;            /* qmm: [M][K]; silu_mul: gu [M][2N] (gate | up)             */
-    void* y;                  /* qmm: [M][N]; silu_mul: h [M][N]                           */
-    const uint32_t* w;        /* qmm only: MLX layout, as dfq_qmm                          */
+    void* y;                  /* qmm: [M][N]; silu_mul: h [M][N]; gate_up: h [M][N/2]      */
+    const uint32_t* w;        /* qmm kinds only: MLX layout, as dfq_qmm (interleaved for
+                                 the gate_up kind)                                         */
     const void* scales;
     const void* biases;
     const void* linear_bias;  /* may be NULL                                               */
