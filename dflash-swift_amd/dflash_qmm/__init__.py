@@ -293,6 +293,8 @@ class Context:
         (interleave_gate_up): h is [M, H] with 2H = rows of w_gu."""
         import torch
         M, K = x.shape
+        if w_gu.shape[0] % 2:
+            raise ValueError("an interleaved gate|up weight has an even number of rows")
         H = w_gu.shape[0] // 2
         if out is None:
             out = torch.empty((M, H), dtype=x.dtype, device=x.device)
