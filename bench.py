@@ -131,13 +131,15 @@ C5_FUSED = [(7168, 5120), (5120, 5120), (34816, 5120), (5120, 17408)]
 C5_LM_HEAD = (151936, 5120)
 
 
-def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False):
+def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False,
+             one_graph=False):
     """The C5 verify forward at M=8: `layers` layers of seven 4-bit g64 matmuls (or, fused,
     q|k|v, o, gate|up with the SiLU-mul epilogue, down), then the lm_head and the greedy
-    accept, the whole forward captured as one HIP graph; distinct random weights per layer
-    (about 11.6 GiB, so every layer streams from HBM).  persistent: the fused forward's 257
-    ops (every layer and the lm_head) as one dfq_chain launch instead of the graph.  Returns
-    microseconds per forward."""
+    accept; distinct random weights per layer (about 11.6 GiB, so every layer streams from
+    HBM).  Each layer is captured as one HIP graph (the configuration's form), or with
+    one_graph the whole forward, lm_head and accept included, as a single graph.
+    persistent: the fused forward's 257 ops (every layer and the lm_head) as one dfq_chain
+    launch instead.  Returns the figures of one form."""
     fused = fused or persistent
     import dflash_qmm
     M = 8
@@ -179,7 +181,7 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False):
     accepted = torch.empty(1, dtype=torch.int32, device=dev)
     acc_ws = torch.zeros(256, dtype=torch.uint8, device=dev)
     torch.cuda.synchronize()
-    if not persistent:
+    if one_graph and not persistent:
         ctx.graph_begin(stream)
     for li in range(layers):
         wl = lw[li]
@@ -191,6 +193,8 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False):
                 chain_ops.append({"kind": kinds[j], "x": inp, "y": outs[j], "w": w,
                                   "scales": s, "biases": b, "N": N, "K": K})
             continue
+        if not one_graph:
+            ctx.graph_begin(stream)
         for j, (N, K) in enumerate(layer):
             inp = layer_in if srcs[j] is None else outs[srcs[j]]
             w, s, b = wl[j]
@@ -199,6 +203,8 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False):
             else:
                 ctx.qmm_raw(inp, w, s, b, outs[j], M, N, K, 4, 64, B, B, B, ws=ws,
                             ws_bytes=ws.numel(), stream=stream)
+        if not one_graph:
+            graphs.append(ctx.graph_end(stream))
 
     def lm_only():
         """the lm_head and the greedy accept: only M + 1 ints leave the device"""
@@ -207,7 +213,7 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False):
         ctx.argmax_accept(lm_out, proposals, tokens, accepted, ws=acc_ws, stream=stream)
 
     chain = None
-    if not persistent:
+    if one_graph and not persistent:
         lm_only()
         graphs.append(ctx.graph_end(stream))
     if persistent:
@@ -220,7 +226,10 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False):
             chain.launch(stream)
             ctx.argmax_accept(lm_out, proposals, tokens, accepted, ws=acc_ws, stream=stream)
             return
-        graphs[0].launch(stream)
+        for gr in graphs:
+            gr.launch(stream)
+        if not one_graph:
+            lm_only()
 
     def timed(fn, n):
         with torch.cuda.stream(stream):
@@ -252,7 +261,8 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False):
                         else "(q,k,v,o,gate,up,down)")
                      + " + lm_head + greedy accept, 4-bit g64 bf16, "
                      + ("the layers and lm_head as one persistent chain launch" if persistent
-                        else "one HIP graph per forward")),
+                        else "one HIP graph per forward" if one_graph
+                        else "one HIP graph per layer")),
         "us_per_forward": round(total, 1),
         "ideal_us_at_8TBs": round(ideal, 1),
         "frac_of_ideal": round(ideal / total, 4),
@@ -304,7 +314,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-chain", action="store_true",
                     help="skip the 64-layer verify-forward measurement (c5_chain)")
-    ap.add_argument("--c5-only", choices=["separate", "fused", "persistent"], default=None,
+    ap.add_argument("--c5-only", choices=["separate", "fused", "fused_one_graph", "persistent"],
+                    default=None,
                     help="only time this form of the 64-layer verify forward (for profiling) "
                          "and print its figures")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -333,8 +344,9 @@ def main():
         return
     ctx = dflash_qmm.Context(0)
     if args.c5_only:
-        r = chain_c5(torch, ctx, dev, fused=args.c5_only == "fused",
-                     persistent=args.c5_only == "persistent")
+        r = chain_c5(torch, ctx, dev, fused=args.c5_only.startswith("fused"),
+                     persistent=args.c5_only == "persistent",
+                     one_graph=args.c5_only == "fused_one_graph")
         print(json.dumps({"c5_" + args.c5_only: r}), flush=True)
         ctx.close()
         return
@@ -401,8 +413,10 @@ def main():
         out["c5_chain"] = chain_c5(torch, ctx, dev)
         torch.cuda.empty_cache()
         out["c5_chain_fused"] = chain_c5(torch, ctx, dev, fused=True)
+        out["c5_chain_fused_one_graph"] = chain_c5(torch, ctx, dev, fused=True, one_graph=True)
         out["c5_chain_persistent"] = chain_c5(torch, ctx, dev, persistent=True)
-        for key in ("c5_chain", "c5_chain_fused", "c5_chain_persistent"):
+        for key in ("c5_chain", "c5_chain_fused", "c5_chain_fused_one_graph",
+                    "c5_chain_persistent"):
             print(f"[bench] {key}: {out[key]['us_per_forward']} us/forward "
                   f"(ideal {out[key]['ideal_us_at_8TBs']})", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
