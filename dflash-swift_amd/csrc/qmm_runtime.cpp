@@ -95,6 +95,7 @@ struct dfq_chain {
     ChainOp* ops = nullptr;    // device
     uint32_t* sync = nullptr;  // device, [2*n_ops + 2]
     void* ws = nullptr;        // device workspace of the qmm ops
+    size_t ws_bytes = 0;
     int n_ops = 0;
     int G = 0;
     int lds_bytes = 0;
@@ -170,6 +171,10 @@ static int tile_owners(int64_t t, int64_t SS, int64_t G, int64_t T) {
     return (int)(owner_wg(t * SS + SS - 1, base, rem) - owner_wg(t * SS, base, rem) + 1);
 }
 
+/* Largest workgroup share (units) for which a narrow N is split into two k-blocks of one tile
+ * per workgroup. */
+static constexpr int kShortSplitUnits = 24;
+
 bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_max, Plan* pl) {
     const int kss = kss_for(bits, gs);
     if (M < 1 || M > 16 || N < 1 || K < kss || K % kss) return false;
@@ -185,10 +190,12 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
     /* Fewest k-blocks (at least DFQ_MIN_KBLOCKS) whose largest x slice, plus the per-unit
      * partial slots of the split, fits in LDS.  The chunks spread over the k-blocks with
      * sizes differing by at most one. */
-    for (int d = std::min(DFQ_MIN_KBLOCKS, chunks); d <= chunks; ++d) {
+    /* The split into d k-blocks, starting from G0 workgroups per k-block (more when the LDS
+     * ring would not fit); false when it does not fit at all. */
+    auto split = [&](int d, int64_t G0, Plan* out) -> bool {
         const int ss_max = (chunks + d - 1) / d, ss_min = chunks / d;
         const int kr = ss_max * kch;
-        if ((int64_t)M * (kr / 8) > (int64_t)kMaxStageItems * kThreads) continue;
+        if ((int64_t)M * (kr / 8) > (int64_t)kMaxStageItems * kThreads) return false;
         Plan p{};
         p.kss = kss;
         p.mt = mt;
@@ -208,7 +215,7 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
          * per tile.  More workgroups than one per CU shorten the ranges when even that would
          * not fit. */
         const int64_t U = (int64_t)T * ss_max;
-        int64_t G = std::min<int64_t>(std::max(1, num_cus / d), U);
+        int64_t G = std::min<int64_t>(std::max<int64_t>(1, G0), U);
         size_t need = 0;
         for (;; G = std::min<int64_t>(U, G + std::max<int64_t>(1, G / 8))) {
             const int64_t umax = U / G + ((U % G) ? 1 : 0);
@@ -221,7 +228,7 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
             need = (size_t)p.cnt_off + (size_t)(ntl_max + 1) * 4;
             if (need <= lds_max || G == U) break;
         }
-        if (need > lds_max) continue;
+        if (need > lds_max) return false;
         p.Gkb = (int)G;
         int nslot = 1;
         for (int ss : {ss_min, ss_max})
@@ -236,7 +243,19 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
         p.lds_need = (int)need;
         p.need_ws = d > 1 || nslot > 1;
         p.ws_bytes = p.need_ws ? (size_t)T * d * nslot * mt * 128 * 4 : 0;
-        *pl = p;
+        *out = p;
+        return true;
+    };
+    for (int d = std::min(DFQ_MIN_KBLOCKS, chunks); d <= chunks; ++d) {
+        if (!split(d, num_cus / d, pl)) continue;
+        /* Few tiles (a narrow N): one k-block over every CU spreads each tile over more than
+         * two workgroups, which needs the second pass.  Two k-blocks of one tile per
+         * workgroup finish every tile with the pair exchange instead, and stage half of x,
+         * at the price of fewer CUs; taken while a workgroup's share stays short. */
+        Plan alt;
+        if (pl->reduce && d == 1 && chunks >= 2 && 2 * T <= num_cus &&
+            (chunks + 1) / 2 <= kShortSplitUnits && split(2, T, &alt) && !alt.reduce)
+            *pl = alt;
         return true;
     }
     return false;
@@ -923,6 +942,7 @@ dfq_status dfq_chain_create(dfq_ctx* ctx, int M, int bits, int gs, dfq_dtype dty
     /* two workspace regions, by op parity: an independent op may start while the op before
      * it still uses its region */
     ws_need = (ws_need + 255) & ~(size_t)255;
+    ch->ws_bytes = 2 * ws_need;
     if ((e = hipMalloc(&ch->ops, sizeof(ChainOp) * n_ops)) != hipSuccess ||
         (e = hipMalloc(&ch->sync, sync_bytes)) != hipSuccess ||
         (ws_need && (e = hipMalloc(&ch->ws, 2 * ws_need)) != hipSuccess)) {
@@ -982,7 +1002,11 @@ dfq_status dfq_chain_failed(dfq_chain* ch, int* failed) {
 
 dfq_status dfq_chain_reset(dfq_chain* ch, void* stream) {
     if (!ch) return fail(DFQ_ERR_INVALID_ARGUMENT, "null chain");
-    return dfq_workspace_clear(ch->ctx, ch->sync, ch->sync_bytes, stream);
+    /* a launch whose waits timed out may have left partial tiles (tagged pair words, slots)
+     * in the workspace: clear it too */
+    dfq_status st = dfq_workspace_clear(ch->ctx, ch->sync, ch->sync_bytes, stream);
+    if (st == DFQ_OK && ch->ws) st = dfq_workspace_clear(ch->ctx, ch->ws, ch->ws_bytes, stream);
+    return st;
 }
 
 dfq_status dfq_chain_set_timeout(dfq_chain* ch, uint32_t ticks) {

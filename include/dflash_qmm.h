@@ -227,7 +227,8 @@ dfq_status dfq_chain_create(dfq_ctx* ctx, int M, int bits, int group_size, dfq_d
 dfq_status dfq_chain_launch(dfq_chain* chain, void* stream);
 /* Synchronises the device and reports whether a launch's wait timed out. */
 dfq_status dfq_chain_failed(dfq_chain* chain, int* failed);
-/* Clears the counters and the error flag (a kernel on `stream`). */
+/* Clears the counters, the error flag and the workspace (kernels on `stream`): after a
+ * timed-out launch the workspace may hold partial tiles. */
 dfq_status dfq_chain_reset(dfq_chain* chain, void* stream);
 /* The wait limit in 100 MHz ticks (tests use a tiny one to drive the error path). */
 dfq_status dfq_chain_set_timeout(dfq_chain* chain, uint32_t ticks);

@@ -146,6 +146,7 @@ SHAPES = [
     (8, 257, 640, 4, 64), (8, 48, 16384, 4, 64), (4, 5000, 12288, 4, 64), (8, 17, 8192, 8, 64),
     (8, 333, 768, 4, 128), (8, 130, 1024, 8, 128), (8, 200, 512, 8, 32), (2, 3, 2560, 4, 64),
     (8, 100000, 256, 4, 64), (5, 999, 3072, 8, 64),
+    (8, 512, 5120, 4, 64), (8, 2048, 5120, 4, 64), (8, 1024, 16384, 4, 64), (8, 64, 1536, 4, 64),
     # two row tiles (9..16 rows)
     (16, 17408, 5120, 4, 64), (9, 17408, 5120, 4, 64), (16, 5120, 17408, 4, 64),
     (16, 7168, 5120, 8, 64), (12, 1024, 5120, 4, 32), (16, 48, 16384, 4, 128),
@@ -180,6 +181,17 @@ def test_long_k_uses_few_uneven_k_blocks():
     # K = 17408 at M = 8: 34 chunks of 512 k; three k-blocks of 11-12 chunks fit LDS
     p = make_plan(8, 5120, 17408, 4, 64)
     assert p["nkb"] == 3 and p["chunks"] == 34 and p["reduce"] == 1
+
+
+def test_narrow_n_splits_k_in_two_with_one_tile_per_workgroup():
+    # N = 1024 at K = 5120: 64 tiles over 256 workgroups would spread each tile over four
+    # (a reduce split); two k-blocks of one tile per workgroup pair every tile instead
+    p = make_plan(8, 1024, 5120, 4, 64)
+    assert (p["nkb"], p["Gkb"], p["nslot_kb"], p["reduce"]) == (2, 64, 1, 0)
+    # wide enough N keeps one k-block over every CU
+    assert make_plan(8, 2048, 5120, 4, 64)["nkb"] == 1
+    # long K: a workgroup's share would be too long; the reduce split stays
+    assert make_plan(8, 1024, 32768, 4, 64)["reduce"] == 1
 
 
 def test_sixteen_rows_fit_lds_with_two_row_tiles():
