@@ -24,6 +24,10 @@ CASES = [
     (8, 2048, 16384, 4, 64, BF16, False),   # a reduce split
     (5, 1536, 1024, 8, 64, F16, True),      # 8-bit, fp16
     (12, 1024, 384, 4, 64, BF16, False),    # one-super-step chunks: two launches of <= 8 rows
+    (8, 256, 5120, 4, 64, BF16, True),      # narrow: two k-blocks, one tile per workgroup
+    (6, 2048, 2048, 8, 128, F16, True),     # 8-bit g128
+    (16, 1024, 1024, 4, 32, BF16, True),    # 4-bit g32, two row tiles
+    (1, 4096, 4096, 4, 64, F16, False),     # one row
 ]
 
 

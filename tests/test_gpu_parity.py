@@ -56,6 +56,23 @@ SIXTEEN_ROW_CASES = [
 ]
 
 
+# Narrow N: two k-blocks of one tile per workgroup, every tile finished by the pair exchange
+# (the planner's split for few tiles); every format, 1..16 rows, ragged N.
+NARROW_CASES = [
+    (8, 1024, 5120, 4, 64, BF16),
+    (1, 1024, 5120, 4, 64, BF16),
+    (8, 512, 5120, 4, 64, F16),
+    (6, 64, 1536, 4, 64, BF16),
+    (8, 1024, 5120, 8, 64, BF16),
+    (8, 1024, 5120, 4, 32, BF16),
+    (8, 1024, 5120, 4, 128, F16),
+    (9, 1024, 5120, 4, 64, BF16),
+    (16, 512, 2048, 8, 64, BF16),
+    (3, 200, 3072, 4, 64, BF16),
+    (8, 1000, 6144, 8, 128, BF16),
+]
+
+
 def run_fast(ctx, c):
     x, w, s, b, lb = upload(c)
     return ctx.qmm(x, w, s, b, c.bits, c.gs, lbias=lb)
@@ -70,6 +87,25 @@ def test_small_shapes_match_oracle(ctx, oracle, M, N, K, bits, gs, dt):
     ref = oracle.qmm_f64(c)
     rel, ok = tolerance_check(y, ref)
     assert rel <= TOL and ok, f"max rel err {rel:.3e}"
+
+
+@pytest.mark.parametrize("M,N,K,bits,gs,dt", NARROW_CASES)
+def test_narrow_n_split_matches_oracle_and_repeats(ctx, oracle, M, N, K, bits, gs, dt):
+    import torch
+    p = ctx.plan(M, N, K, bits, gs)
+    assert p["nkb"] == 2 and p["reduce"] == 0 and p["nslot_kb"] == 1, p
+    c = make_case(M, N, K, bits=bits, gs=gs, xdt=dt, seed=7 * M + N + K + bits + gs,
+                  lbias=(N % 2 == 0))
+    announce(f"narrow M={M} N={N} K={K} bits={bits} gs={gs} dt={dt}")
+    x, w, s, b, lb = upload(c)
+    y = ctx.qmm(x, w, s, b, c.bits, c.gs, lbias=lb)
+    torch.cuda.synchronize()
+    rel, ok = tolerance_check(download(y), oracle.qmm_f64(c))
+    assert rel <= TOL and ok, f"max rel err {rel:.3e}"
+    for _ in range(3):                       # the pair exchange leaves the workspace re-armed
+        y2 = ctx.qmm(x, w, s, b, c.bits, c.gs, lbias=lb)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
 
 
 @pytest.mark.parametrize("M,N,K,bits,gs,dt", SIXTEEN_ROW_CASES)
