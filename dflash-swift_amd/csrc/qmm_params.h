@@ -18,11 +18,13 @@
  *    (kb+1)*chunks/nkb); its x slice must fit in LDS);
  *  - the U = T*SS units (tile, chunk) of a k-block of SS chunks are split into Gkb
  *    contiguous ranges whose sizes differ by at most one (the first U % Gkb get one more);
+ *    a narrow N (few tiles) takes two k-blocks with Gkb = T, one tile per workgroup;
  *  - inside a workgroup the waves take units of its range one at a time from a counter in
  *    LDS (the first ones by wave index), in a rotated order that starts with the tile shared
  *    with the next workgroup and continues with the one shared with the previous, so that
  *    cross-workgroup fix-ups happen early;
- *  - every unit's partial tile goes to its own LDS slot; the wave that completes a tile's
+ *  - every unit's partial tile goes to a slot of an LDS ring over the take order (a slot is
+ *    reused once its generation allows); the wave that completes a tile's
  *    units in this workgroup (an LDS arrival counter) sums the slots in unit order and marks
  *    the tile done; the workgroup's publisher wave then writes y, or, for a tile shared with
  *    other workgroups (or k-blocks), its part: with at most two parts per tile anywhere in
