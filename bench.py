@@ -97,6 +97,29 @@ def time_m(torch, ctx, stream, sets, M, steps, warmup, N, K, bits, gs, ws, wsb):
     return e0.elapsed_time(e1) * 1000.0 / steps
 
 
+def time_copy(torch, stream, nbytes, nsets, steps):
+    """A plain device copy moving `nbytes` per launch (nbytes/2 read, nbytes/2 written),
+    rotated over buffers larger than the Infinity Cache and timed back to back like the
+    matmul: the launch-for-launch bandwidth a memory-bound kernel of this size reaches on
+    the box.  Microseconds per copy."""
+    dev = torch.device("cuda:0")
+    half = nbytes // 2
+    src = [torch.ones(half, dtype=torch.uint8, device=dev) for _ in range(nsets)]
+    dst = [torch.empty(half, dtype=torch.uint8, device=dev) for _ in range(nsets)]
+    with torch.cuda.stream(stream):
+        for i in range(20):
+            dst[i % nsets].copy_(src[(i + 1) % nsets])
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(steps):
+            dst[i % nsets].copy_(src[(i + 1) % nsets])
+        e1.record(stream)
+        torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1000.0 / steps
+
+
 def time_chained(torch, ctx, stream, sets, M, reps, N, K, bits, gs):
     """The same M-row calls over the rotated weight sets as one dfq_chain launch of independent
     ops (each reads x, none reads another's output): microseconds per call."""
@@ -367,6 +390,10 @@ def main():
               f"{algorithmic_bytes(m) / us[m] / 1e3:.0f} GB/s", file=sys.stderr, flush=True)
 
     gbs = {m: algorithmic_bytes(m) / (us[m] * 1e-6) / 1e9 for m in ms}
+    copy_bytes = algorithmic_bytes(8)
+    uc_copy = time_copy(torch, stream, copy_bytes, args.sets, args.steps)
+    print(f"[bench] device copy moving {copy_bytes / 1e6:.1f} MB: {uc_copy:.2f} us/copy, "
+          f"{copy_bytes / uc_copy / 1e3:.0f} GB/s", file=sys.stderr, flush=True)
     achieved = gbs[8]
     out = {
         "metric": "us/call + HBM GB/s, 4-bit qmatmul K5120xN17408, M=1..8; M8/M1 time ratio",
@@ -389,6 +416,14 @@ def main():
         "us_per_call": {str(m): round(us[m], 3) for m in ms},
         "gbs_by_M": {str(m): round(gbs[m], 1) for m in ms},
         "m8_m1_ratio": round(us[8] / us[1], 4) if 1 in us else None,
+        "device_copy": {
+            "workload": ("torch copy_ of half the M=8 call's algorithmic bytes into another "
+                         "buffer (the same bytes moved per launch), rotated, back to back: the "
+                         "per-launch bandwidth a memory-bound kernel of this size reaches here"),
+            "bytes_per_launch": copy_bytes,
+            "us_per_copy": round(uc_copy, 3),
+            "gbs": round(copy_bytes / (uc_copy * 1e-6) / 1e9, 1),
+        },
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),
