@@ -348,7 +348,7 @@ def main():
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
-              "(the path is single-GPU, see the sharding notes in DESIGN.md)", file=sys.stderr)
+              "(the matmul path runs on a single GPU)", file=sys.stderr)
         sys.exit(2)
 
     import torch
