@@ -679,10 +679,11 @@ __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
  * linear bias, to y; the slots are zeroed, which leaves the workspace zero at rest.  Tiles
  * with one contributor were written by the main kernel.
  *
- * All nkb * nslot_kb slots of the tile are read, eight loads in flight before any use: the
- * slots a k-block leaves unused are zero, and adding +0.0f to a sum that is never -0.0f
- * (it starts at +0.0f) leaves it unchanged, so the result equals the sum of the used slots
- * alone.  One memory latency per eight slots instead of one per slot. */
+ * All nkb * nslot_kb slots of the tile are read, eight loads (two in a chain) in flight
+ * before any use: the slots a k-block leaves unused are zero, and adding +0.0f to a sum
+ * that is never -0.0f (it starts at +0.0f) leaves it unchanged, so the result equals the
+ * sum of the used slots alone.  One memory latency per eight slots instead of one per
+ * slot. */
 template <bool F16, bool COH = false>
 __device__ __forceinline__ void reduce_tile(const QmmParams& p, int t, int lane) {
     int parts = 0;
@@ -695,13 +696,16 @@ __device__ __forceinline__ void reduce_tile(const QmmParams& p, int t, int lane)
     if (lane < 32 * p.mt) {
         const int S = p.nkb * p.nslot_kb, stride = p.mt * 128;
         float* s0 = tile_slot(p, t, 0, 0, lane);  // slot i = kb * nslot_kb + j at s0 + i * stride
-        for (int b = 0; b < S; b += 8) {
-            f32x4_t v[8];
+        /* in a chain this runs inside the persistent kernel, beside the streaming loop's
+         * registers: two loads in flight there keep it from spilling */
+        constexpr int NB = COH ? 2 : 8;
+        for (int b = 0; b < S; b += NB) {
+            f32x4_t v[NB];
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
+            for (int i = 0; i < NB; ++i)
                 if (b + i < S) v[i] = *(const f32x4_t*)(s0 + (size_t)(b + i) * stride);
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
+            for (int i = 0; i < NB; ++i)
                 if (b + i < S) {
                     sum += v[i];
                     put_tile4<COH>(s0 + (size_t)(b + i) * stride, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f});
