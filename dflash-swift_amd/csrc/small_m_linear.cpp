@@ -21,6 +21,7 @@
 #include <map>
 #include <memory>
 #include <string>
+#include <vector>
 
 #include "dflash_qmm.h"
 #include "qmm_internal.h"
@@ -87,14 +88,23 @@ class SmallMQuantizedLinear final : public QuantizedLinear {
 public:
     explicit SmallMQuantizedLinear(const QuantizedLinear& other)
         : QuantizedLinear(other.ctx(), other.desc()),
-          kernelEligible_(SmallMQuantizedMatmul::isEligible(other.desc())) {}
+          kernelEligible_(SmallMQuantizedMatmul::isEligible(other.desc())) {
+        /* The reference gate says nothing of the kernel's own limits (weights under 2 GiB,
+         * a work split for the shape).  Rows the fast kernel cannot take fall through to the
+         * stock op like any other ineligible call (:254-266), decided once here. */
+        if (kernelEligible_ && ctx_)
+            for (int r = SmallMQuantizedMatmul::minimumRows; r <= SmallMQuantizedMatmul::maximumRows; ++r)
+                if (dfq_qmm_supported(ctx_, r, d_.out_features, d_.in_features, d_.bits,
+                                      d_.group_size, DFQ_BF16, DFQ_BF16, DFQ_BF16))
+                    rowsFit_ |= 1u << r;
+    }
 
     bool isSmallM() const override { return true; }
 
     bool takesKernel(dfq_dtype xdt, int rows) const {
         return kernelEligible_ && rows >= SmallMQuantizedMatmul::minimumRows &&
-               rows <= SmallMQuantizedMatmul::maximumRows && xdt == DFQ_BF16 &&
-               d_.biases != nullptr && d_.dtype == DFQ_BF16;
+               rows <= SmallMQuantizedMatmul::maximumRows && ((rowsFit_ >> rows) & 1u) &&
+               xdt == DFQ_BF16 && d_.biases != nullptr && d_.dtype == DFQ_BF16;
     }
 
     dfq_status callAsFunction(const void* x, dfq_dtype xdt, int rows, void* y, void* ws,
@@ -116,6 +126,7 @@ public:
 
 private:
     bool kernelEligible_;
+    uint32_t rowsFit_ = 0;  /* bit r: the fast kernel has a split for r rows of this layer */
 };
 
 }  // namespace dflash
@@ -126,8 +137,12 @@ struct dfq_linear {
     std::shared_ptr<dflash::QuantizedLinear> impl;
 };
 
+/* The model owns one handle per leaf it has ever held: dfq_model_leaf hands out borrowed
+ * handles, which stay valid (describing the layer they named) until the model is destroyed,
+ * also after a swap or set_leaf replaced that leaf. */
 struct dfq_model {
-    std::map<std::string, std::shared_ptr<dflash::QuantizedLinear>> leaves;
+    std::map<std::string, dfq_linear*> leaves;
+    std::vector<std::unique_ptr<dfq_linear>> owned;
 };
 
 extern "C" {
@@ -202,16 +217,15 @@ dfq_status dfq_model_destroy(dfq_model* model) {
 
 dfq_status dfq_model_set_leaf(dfq_model* model, const char* path, dfq_linear* lin) {
     if (!model || !path || !lin) return dfq::fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
-    model->leaves[path] = lin->impl;
-    delete lin;
+    model->owned.emplace_back(lin);
+    model->leaves[path] = lin;
     return DFQ_OK;
 }
 
 dfq_linear* dfq_model_leaf(dfq_model* model, const char* path) {
     if (!model || !path) return nullptr;
     auto it = model->leaves.find(path);
-    if (it == model->leaves.end()) return nullptr;
-    return new dfq_linear{it->second};
+    return it == model->leaves.end() ? nullptr : it->second;
 }
 
 int dfq_model_leaf_count(const dfq_model* model) {
@@ -225,10 +239,13 @@ int dfq_enable_small_m_quantized_matmul(dfq_model* model) {
     }
     int swapped = 0;
     for (auto& kv : model->leaves) {
-        auto& leaf = kv.second;
+        const auto& leaf = kv.second->impl;
         if (leaf->isSmallM()) continue;                                       // :309
         if (!dflash::SmallMQuantizedMatmul::isEligible(leaf->desc())) continue; // :310-311
-        leaf = std::make_shared<dflash::SmallMQuantizedLinear>(*leaf);        // :313
+        auto* swapped_leaf =                                                   // :313
+            new dfq_linear{std::make_shared<dflash::SmallMQuantizedLinear>(*leaf)};
+        model->owned.emplace_back(swapped_leaf);
+        kv.second = swapped_leaf;
         ++swapped;
     }
     return swapped;                                                           // :315-316

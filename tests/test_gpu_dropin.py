@@ -115,3 +115,30 @@ def test_linear_bias_is_added(ctx):
     announce("dropin linear bias")
     d = (fast(x).float() - (nob(x).float() + lb.float()[None, :])).abs().max().item()
     assert d <= TOL * max(nob(x).float().abs().max().item(), 1.0)
+
+
+def test_layer_past_the_kernels_size_limit_falls_through(ctx):
+    """An eligible layer whose weights reach 2 GiB (262144 x 16384 at 4 bits) is past the
+    fast kernel's own limit: the swapped layer must fall through to the stock path like any
+    ineligible call (SmallMQuantizedMatmul.swift:254-266), not fail.  No device memory is
+    needed: the descriptor's pointers are never dereferenced, the workspace query answers 0
+    and a forward with a null input is refused by the stock path's argument check
+    (status 1, took_kernel 0) before any launch."""
+    import ctypes
+    import dflash_qmm
+    lib = dflash_qmm.load_library()
+    fake = 1 << 40
+    d = dflash_qmm._LinearDesc(fake, fake, fake, None, 262144, 16384, 4, 64, 1, BF16)
+    h = ctypes.c_void_p()
+    assert lib.dfq_linear_create(ctx.handle, ctypes.byref(d), ctypes.byref(h)) == 0
+    fast = ctypes.c_void_p()
+    assert lib.dfq_small_m_linear_create(h, ctypes.byref(fast)) == 0
+    assert lib.dfq_is_eligible(262144, 16384, 4, 64, 1, 1) == 1
+    assert not ctx.supported(8, 262144, 16384, 4, 64)
+    nb = ctypes.c_size_t(123)
+    assert lib.dfq_linear_workspace_bytes(fast, 8, ctypes.byref(nb)) == 0 and nb.value == 0
+    took = ctypes.c_int(-1)
+    rc = lib.dfq_linear_forward(fast, None, BF16, 8, None, None, 0, None, ctypes.byref(took))
+    assert rc == 1 and took.value == 0, (rc, took.value, lib.dfq_last_error())
+    lib.dfq_linear_destroy(fast)
+    lib.dfq_linear_destroy(h)
