@@ -189,18 +189,24 @@ class QmmCase:
 
 
 def make_case(M, N, K, bits=4, gs=64, xdt=BF16, sdt=None, seed=0, x_sigma=1.0,
-              s_sigma=None, b_sigma=0.01, lbias=False) -> QmmCase:
+              s_sigma=None, b_sigma=0.01, lbias=False, words=False) -> QmmCase:
     """Generate codes -> scales -> biases -> x (in that order) from one PCG64 stream.
 
     codes ~ U{0..2^bits-1}; scales ~ |N(0, s_sigma)|; biases ~ N(0, b_sigma);
-    x ~ N(0, x_sigma).  s_sigma defaults to 0.02 (4-bit) / 0.004 (8-bit).
+    x ~ N(0, x_sigma).  s_sigma defaults to 0.02 (4-bit) / 0.004 (8-bit).  words=True draws
+    the packed uint32 words directly (uniform words are uniform codes in every slot), which
+    is what full-size cases such as a 151936-row LM head use: packing codes one by one there
+    takes gigabytes of temporaries.
     """
     sdt = xdt if sdt is None else sdt
     if s_sigma is None:
         s_sigma = 0.02 if bits <= 4 else 0.004
     rng = np.random.Generator(np.random.PCG64(seed))
-    codes = rng.integers(0, 1 << bits, size=(N, K), dtype=np.uint8)
-    w = pack(codes, bits)
+    if words:
+        w = rng.integers(0, 1 << 32, size=(N, K * bits // 32), dtype=np.uint32)
+    else:
+        codes = rng.integers(0, 1 << bits, size=(N, K), dtype=np.uint8)
+        w = pack(codes, bits)
     scales = to_bits(np.abs(rng.normal(0.0, s_sigma, size=(N, K // gs))), sdt)
     biases = to_bits(rng.normal(0.0, b_sigma, size=(N, K // gs)), sdt)
     x = to_bits(rng.normal(0.0, x_sigma, size=(M, K)), xdt)

@@ -1,0 +1,113 @@
+"""Bit-exact GPU pin of the kernel's integer unpack and dequantisation.
+
+With one-hot activation rows (x[m] = e_k) the product is a column of the dequantised
+matrix: y[m, n] = s[n, k/gs] * q[n, k] + b[n, k/gs].  Scales are powers of two and biases
+small integers, chosen per group so that every such value is exact in fp32 and in the output
+dtype; the kernel's factored form (s * sum x (MAGIC + q) + (b - MAGIC s) * sum x) is then
+exact too, and y must equal the oracle's bit-exact dequant (Sources/DFlashKit/
+SmallMQuantizedMatmul.swift:55-71: code t of a word is (p >> bits*t) & mask, element 0 in the
+low bits; dequant s*q + b) bit for bit.  The one-hot rows walk every k position of a chunk
+(8 quantisation groups, several super-steps), so a mistake confined to a few codes, lanes,
+words or groups cannot hide under a tolerance.
+
+Covered: every bits x group size x dtype in the 1..8-row form with 8-group chunks (c8), the
+9..16-row form (mt16) and one-super-step chunks (c1), plus the narrow split (two k-blocks,
+one tile per workgroup, pair exchange) and a reduce split (several k-blocks, second pass).
+"""
+import numpy as np
+import pytest
+
+from gpu_util import announce, to_dev16
+from onehot import exact_case
+from oracle.qmm_oracle import BF16, F16, from_bits, to_bits
+
+pytestmark = pytest.mark.gpu
+
+FORMATS = [(bits, gs, dt) for bits in (4, 8) for gs in (32, 64, 128) for dt in (BF16, F16)]
+
+
+def kss(bits, gs):
+    return (512 // bits) * ((2 if gs == 128 else 1) if bits == 4 else gs // 32)
+
+
+def chunk_k(bits, gs):
+    return 8 * gs  # 8 groups: the chunk of the c8 kernels
+
+
+def run_one_hot(ctx, N, K, bits, gs, dt, M, positions, seed, expect_plan=None):
+    """y for one-hot rows at `positions` (M per call) against the exact dequant columns."""
+    import torch
+    if expect_plan is not None:
+        p = ctx.plan(M, N, K, bits, gs)
+        for key, val in expect_plan.items():
+            assert p[key] == val, (key, p)
+    w, sb, bb, deq = exact_case(N, K, bits, gs, dt, seed)
+    pos = np.asarray(positions, dtype=np.int64)
+    pad = (-len(pos)) % M
+    pos = np.concatenate([pos, pos[:pad]])
+    calls = len(pos) // M
+    tdt = torch.bfloat16 if dt == BF16 else torch.float16
+    wd = torch.from_numpy(w.view(np.int32)).cuda()
+    sd, bd = to_dev16(sb, dt), to_dev16(bb, dt)
+    x = torch.zeros(len(pos), K, dtype=tdt, device="cuda")
+    x[torch.arange(len(pos), device="cuda"), torch.from_numpy(pos).cuda()] = 1.0
+    y = torch.empty(len(pos), N, dtype=tdt, device="cuda")
+    announce(f"one-hot bits={bits} gs={gs} dt={dt} M={M} N={N} K={K} calls={calls}")
+    for c in range(calls):
+        ctx.qmm(x[c * M:(c + 1) * M], wd, sd, bd, bits, gs, out=y[c * M:(c + 1) * M])
+    torch.cuda.synchronize()
+    got = y.view(torch.int16).cpu().numpy().view(np.uint16)
+    want = to_bits(deq[:, pos].T, dt)
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, (
+        f"{len(bad)} of {got.size} outputs differ; first (row k={pos[bad[0][0]]}, n={bad[0][1]}):"
+        f" got {from_bits(got[tuple(bad[0])], dt)} want {deq[bad[0][1], pos[bad[0][0]]]}")
+
+
+@pytest.mark.parametrize("bits,gs,dt", FORMATS)
+def test_unpack_is_exact_up_to_8_rows(ctx, bits, gs, dt):
+    """1..8 rows, 8-group chunks: every k of two chunks, ragged N (a partial last tile)."""
+    K = 2 * chunk_k(bits, gs)
+    run_one_hot(ctx, 40, K, bits, gs, dt, 8, range(K), seed=bits * 1000 + gs + dt,
+                expect_plan={"ch": 8 * gs // kss(bits, gs), "nkb": 1})
+
+
+@pytest.mark.parametrize("bits,gs,dt", FORMATS)
+def test_unpack_is_exact_for_16_rows(ctx, bits, gs, dt):
+    """9..16 rows in one launch (two row tiles per weight tile): every k of one chunk."""
+    K = chunk_k(bits, gs)
+    run_one_hot(ctx, 48, K, bits, gs, dt, 16, range(K), seed=bits * 2000 + gs + dt,
+                expect_plan={"ch": 8 * gs // kss(bits, gs)})
+
+
+@pytest.mark.parametrize("bits,gs,dt", FORMATS)
+def test_unpack_is_exact_with_one_super_step_chunks(ctx, bits, gs, dt):
+    """K not a multiple of 8 groups: one-super-step chunks (c1), every k."""
+    K = 3 * kss(bits, gs)
+    if K % chunk_k(bits, gs) == 0:
+        K += kss(bits, gs)
+    run_one_hot(ctx, 24, K, bits, gs, dt, 7, range(K), seed=bits * 3000 + gs + dt,
+                expect_plan={"ch": 1})
+
+
+@pytest.mark.parametrize("bits,gs,dt,M", [(4, 64, BF16, 8), (8, 32, F16, 8), (4, 64, BF16, 12),
+                                           (8, 128, F16, 5)])
+def test_unpack_is_exact_in_the_narrow_split(ctx, bits, gs, dt, M):
+    """Few tiles, long K: two k-blocks of one tile per workgroup (pair exchange).  Every k of
+    the first and the last chunk, and of one chunk in the second k-block's start."""
+    ck = chunk_k(bits, gs)
+    K = 8 * ck
+    pos = list(range(ck)) + list(range(4 * ck, 5 * ck)) + list(range(7 * ck, 8 * ck))
+    run_one_hot(ctx, 64, K, bits, gs, dt, M, pos, seed=bits * 4000 + gs + dt,
+                expect_plan={"nkb": 2, "reduce": 0, "nslot_kb": 1})
+
+
+@pytest.mark.parametrize("bits,gs,dt,M", [(4, 64, BF16, 8), (8, 64, F16, 16)])
+def test_unpack_is_exact_in_a_reduce_split(ctx, bits, gs, dt, M):
+    """Several k-blocks and workgroups per tile, summed by the second pass: every k of the
+    first, a middle and the last chunk."""
+    ck = chunk_k(bits, gs)
+    K = 32 * ck
+    pos = list(range(ck)) + list(range(15 * ck, 16 * ck)) + list(range(31 * ck, 32 * ck))
+    run_one_hot(ctx, 48, K, bits, gs, dt, M, pos, seed=bits * 5000 + gs + dt,
+                expect_plan={"reduce": 1})

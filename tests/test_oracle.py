@@ -287,3 +287,37 @@ def test_argmax_accept_closed_forms():
             run += 1
         assert acc == run
     assert argmax_accept(bits[:1], BF16, proposals=[])[1] == 0
+
+
+def test_one_hot_columns_catch_a_slip_a_tolerance_misses():
+    """The one-hot unpack test compares exact dequant columns bit for bit.  A slip confined to
+    one code value in one slot of the first 64 words of a row (code 15 in the top nibble
+    read as 14) moves a random-x product of the headline's distributions by well under the
+    1e-2 parity bar, yet changes the exact columns it touches."""
+    import os
+    import sys
+    sys.path.insert(0, os.path.dirname(__file__))
+    from onehot import exact_case
+
+    def slipped(w, K):
+        q = Q.unpack(w, 4, K).astype(np.float32)
+        top = q[:, 7:512:8]
+        top[top == 15] = 14
+        q[:, 7:512:8] = top
+        return q
+
+    def deq_from(q, sb, bb, gs=64):
+        s = np.repeat(Q.from_bits(sb, Q.BF16), gs, axis=1)
+        b = np.repeat(Q.from_bits(bb, Q.BF16), gs, axis=1)
+        return (q * s + b).astype(np.float64)
+
+    N, K = 64, 5120
+    c = Q.make_case(8, N, K, bits=4, gs=64, seed=21)
+    x = Q.from_bits(c.x, c.xdt).astype(np.float64)
+    good = Q.dequant(c.w, c.scales, c.biases, c.sdt, 4, 64, K).astype(np.float64)
+    rel, ok = Q.tolerance_check(x @ deq_from(slipped(c.w, K), c.scales, c.biases).T, x @ good.T)
+    assert 0 < rel < 1e-2 and ok                             # hides under the tolerance
+    w, sb, bb, deq = exact_case(16, 512, 4, 64, Q.BF16, 21)
+    cols = list(range(7, 512, 8))
+    assert not np.array_equal(Q.to_bits(deq_from(slipped(w, 512), sb, bb)[:, cols], Q.BF16),
+                              Q.to_bits(deq[:, cols], Q.BF16))  # the exact columns differ

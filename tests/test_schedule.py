@@ -154,7 +154,31 @@ SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("shape", SHAPES)
+def _unpack_test_shapes():
+    """The one-hot unpack test's shapes (every format, c8 / mt16 / c1, narrow and reduce)."""
+    out = []
+    for bits in (4, 8):
+        for gs in (32, 64, 128):
+            kss = (512 // bits) * ((2 if gs == 128 else 1) if bits == 4 else gs // 32)
+            ck = 8 * gs
+            k1 = 3 * kss + (kss if (3 * kss) % ck == 0 else 0)
+            out += [(8, 40, 2 * ck, bits, gs), (16, 48, ck, bits, gs), (7, 24, k1, bits, gs)]
+    out += [(M, 64, 64 * gs, bits, gs) for (bits, gs, M) in
+            ((4, 64, 8), (8, 32, 8), (4, 64, 12), (8, 128, 5))]
+    out += [(8, 48, 256 * 64, 4, 64), (16, 48, 256 * 64, 8, 64)]
+    return out
+
+
+# the C5 projections and LM head at 8 and 16 rows, the one-hot unpack shapes, and the
+# no-allocation entry point's sequence
+EXTRA_SHAPES = ([(m, n, k, 4, 64) for m in (8, 16) for (n, k) in
+                 ((5120, 5120), (7168, 5120), (1024, 5120), (5120, 17408), (151936, 5120),
+                  (34816, 5120))]
+                + _unpack_test_shapes()
+                + [(16, 4096, 5120, 8, 64), (6, 1024, 5120, 4, 128), (3, 40, 256, 4, 32)])
+
+
+@pytest.mark.parametrize("shape", SHAPES + EXTRA_SHAPES)
 def test_split_covers_every_unit_once(shape):
     p = make_plan(*shape)
     assert p is not None, shape
@@ -248,7 +272,7 @@ def fetched_units(a, b, SS, U, wave, pf):
     return out + [unit_of(g) for g in range(L)]
 
 
-@pytest.mark.parametrize("shape", SHAPES + [(8, 1024, 5120, 4, 64), (8, 151936, 5120, 4, 64)])
+@pytest.mark.parametrize("shape", SHAPES + EXTRA_SHAPES)
 def test_prefetch_addresses_stay_in_bounds(shape):
     M, N, K, bits, gs = shape
     p = make_plan(*shape)
