@@ -3,17 +3,24 @@
 
 Workload (the headline configuration): y[M,17408] = x[M,5120] . dequant(W)^T, W 4-bit
 group 64 in MLX's affine layout, bf16 activations / scales / biases / output, M swept over
-1, 2, 4, 6, 8.  A "step" is one call at M = 8 (a verify pass's width).
+1, 2, 4, 6, 8 (and 16).  A "step" is one call at M = 8 (a verify pass's width).
 
 Method:
   * 8 distinct weight sets (~400 MB, more than the 256 MB Infinity Cache) are rotated so
     every call streams its weights from HBM;
   * the `steps` calls of one M are captured into one HIP graph on a non-default stream and
-    replayed; HIP events on that stream bracket the replay (plus a device synchronize on
-    both sides), so `us_per_call` is back-to-back time per call including launch gaps;
+    replayed R >= 10 times (at least 200 calls); HIP events on that stream bracket each
+    replay, so a replay's time / steps is the back-to-back time per call including launch
+    gaps; us_per_call is the median over the replays, with p10 / p90 beside it;
   * algorithmic bytes per call = N*K*bits/8 + 2*N*(K/gs)*2 + M*K*2 + M*N*2;
+  * read_ceiling: the library's plain streaming-read kernel moving the M=8 call's
+    algorithmic bytes per launch over the same rotation, timed the same way: the
+    single-launch read rate this memory system reaches with no compute;
   * the CPU baseline is the oracle's fp32 restatement of MLX's CPU algorithm (dequantise a
     group, multiply-accumulate), OpenMP over the host cores, timed on a bounded sample.
+
+--profile-timed brackets only the timed replays with roctxProfilerResume / Pause, for
+`rocprofv3 --selected-regions`: the trace then holds exactly the calls the figures time.
 
 Prints ONE JSON line.  --gpus > 1 is refused: this build measures one GPU.
 """
@@ -46,6 +53,42 @@ def measured_traffic():
     return None
 
 
+class TimedRegion:
+    """roctxProfilerResume / Pause around the timed replays (for rocprofv3
+    --selected-regions), or nothing when not asked for."""
+
+    def __init__(self, enabled):
+        self.lib = None
+        if enabled:
+            import ctypes
+            self.lib = ctypes.CDLL("librocprofiler-sdk-roctx.so")
+            self.lib.roctxProfilerPause(0)   # nothing is traced until a timed region
+
+    def __enter__(self):
+        if self.lib:
+            self.lib.roctxProfilerResume(0)
+
+    def __exit__(self, *exc):
+        if self.lib:
+            self.lib.roctxProfilerPause(0)
+
+
+TIMED = TimedRegion(False)
+
+
+def stats(per_call):
+    """median / p10 / p90 (us) of per-call times, one per replay."""
+    import numpy as np
+    a = np.asarray(per_call, dtype=np.float64)
+    return {"median": float(np.median(a)), "p10": float(np.percentile(a, 10)),
+            "p90": float(np.percentile(a, 90)), "replays": int(a.size)}
+
+
+def replays_for(steps):
+    """Replays of a `steps`-call graph: at least 10, and at least 200 calls in all."""
+    return max(10, -(-200 // max(1, steps)))
+
+
 def algorithmic_bytes(M, N=N_OUT, K=K_IN, bits=BITS, gs=GS):
     return N * K * bits // 8 + 2 * N * (K // gs) * 2 + M * K * 2 + M * N * 2
 
@@ -63,8 +106,24 @@ def make_sets(torch, nsets, N, K, bits, gs, dev, seed=1):
     return sets
 
 
+def time_replays(torch, stream, graph, steps, reps):
+    """Per-call microseconds of `reps` back-to-back replays of a `steps`-call graph, each
+    bracketed by HIP events on the graph's stream."""
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(reps)]
+    torch.cuda.synchronize()
+    with TIMED:
+        for e0, e1 in events:
+            e0.record(stream)
+            graph.launch(stream)
+            e1.record(stream)
+        torch.cuda.synchronize()
+    return [e0.elapsed_time(e1) * 1000.0 / steps for e0, e1 in events]
+
+
 def time_m(torch, ctx, stream, sets, M, steps, warmup, N, K, bits, gs, ws, wsb):
-    """Average microseconds per call over `steps` graph-replayed calls at row count M."""
+    """Per-call microseconds (one figure per replay) of `steps` graph-replayed calls at row
+    count M, over replays_for(steps) replays."""
     import dflash_qmm
     dev = sets[0][0].device
     g = torch.Generator(device=dev)
@@ -86,15 +145,26 @@ def time_m(torch, ctx, stream, sets, M, steps, warmup, N, K, bits, gs, ws, wsb):
     with torch.cuda.stream(stream):
         issue(warmup, 1)               # eager warm-up (also checks the eager path)
         graph.launch(stream)           # graph warm-up
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        graph.launch(stream)
-        e1.record(stream)
-        torch.cuda.synchronize()
+        times = time_replays(torch, stream, graph, steps, replays_for(steps))
     graph.close()
-    return e0.elapsed_time(e1) * 1000.0 / steps
+    return times
+
+
+def time_read(torch, ctx, stream, nbytes, nsets, steps, dev):
+    """The read ceiling: the plain streaming-read kernel over `nsets` rotated buffers of
+    `nbytes`, `steps` launches per graph, replayed like the matmul; per-launch us."""
+    bufs = [torch.ones(nbytes // 4, dtype=torch.int32, device=dev) for _ in range(nsets)]
+    sink = torch.zeros(8 * ctx.num_cus, dtype=torch.int32, device=dev)
+    torch.cuda.synchronize()
+    ctx.graph_begin(stream)
+    for i in range(steps):
+        ctx.read_stream(bufs[i % nsets], nbytes, sink, stream=stream)
+    graph = ctx.graph_end(stream)
+    with torch.cuda.stream(stream):
+        graph.launch(stream)
+        times = time_replays(torch, stream, graph, steps, replays_for(steps))
+    graph.close()
+    return times
 
 
 def time_copy(torch, stream, nbytes, nsets, steps):
@@ -120,31 +190,6 @@ def time_copy(torch, stream, nbytes, nsets, steps):
     return e0.elapsed_time(e1) * 1000.0 / steps
 
 
-def time_chained(torch, ctx, stream, sets, M, reps, N, K, bits, gs):
-    """The same M-row calls over the rotated weight sets as one dfq_chain launch of independent
-    ops (each reads x, none reads another's output): microseconds per call."""
-    dev = sets[0][0].device
-    x = torch.randn(M, K, device=dev).to(torch.bfloat16)
-    ys = [torch.empty(M, N, device=dev, dtype=torch.bfloat16) for _ in sets]
-    chain = ctx.chain(M, bits, gs, [
-        {"kind": "qmm", "x": x, "y": ys[i], "w": w, "scales": s, "biases": b, "N": N, "K": K,
-         "independent": i > 0} for i, (w, s, b) in enumerate(sets)])
-    with torch.cuda.stream(stream):
-        chain.launch(stream)
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(reps):
-            chain.launch(stream)
-        e1.record(stream)
-        torch.cuda.synchronize()
-    if chain.failed():
-        raise RuntimeError("the chain reported a timed-out wait")
-    chain.close()
-    return e0.elapsed_time(e1) * 1000.0 / (reps * len(sets))
-
-
 # One verify-pass layer of the C5 chain (N, K): q, k, v, o, gate, up, down; then the lm_head.
 C5_LAYER = [(5120, 5120), (1024, 5120), (1024, 5120), (5120, 5120), (17408, 5120),
             (17408, 5120), (5120, 17408)]
@@ -154,16 +199,13 @@ C5_FUSED = [(7168, 5120), (5120, 5120), (34816, 5120), (5120, 17408)]
 C5_LM_HEAD = (151936, 5120)
 
 
-def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False,
-             one_graph=False):
+def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, one_graph=False):
     """The C5 verify forward at M=8: `layers` layers of seven 4-bit g64 matmuls (or, fused,
     q|k|v, o, gate|up with the SiLU-mul epilogue, down), then the lm_head and the greedy
     accept; distinct random weights per layer (about 11.6 GiB, so every layer streams from
     HBM).  Each layer is captured as one HIP graph (the configuration's form), or with
-    one_graph the whole forward, lm_head and accept included, as a single graph.
-    persistent: the fused forward's 257 ops (every layer and the lm_head) as one dfq_chain
-    launch instead.  Returns the figures of one form."""
-    fused = fused or persistent
+    one_graph the whole forward, lm_head and accept included, as a single graph.  Returns
+    the figures of one form."""
     import dflash_qmm
     M = 8
     g = torch.Generator(device=dev)
@@ -193,29 +235,22 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False,
         outs = [torch.empty(M, N, device=dev, dtype=torch.bfloat16) for (N, K) in layer]
         srcs = [None, None, None, 0, None, None, 4]
         kinds = ["qmm"] * len(layer)
-    lm_out = torch.empty(M, C5_LM_HEAD[0], device=dev, dtype=torch.bfloat16)
     stream = torch.cuda.Stream(device=dev)
     B = dflash_qmm.BF16
-    graphs, chain_ops = [], []
+    graphs = []
     lw = [[weights(N, K) for (N, K) in layer] for _ in range(layers)]
     wlm, slm, blm = weights(*C5_LM_HEAD)
     proposals = torch.zeros(M - 1, dtype=torch.int32, device=dev)
     tokens = torch.empty(M, dtype=torch.int32, device=dev)
     accepted = torch.empty(1, dtype=torch.int32, device=dev)
-    acc_ws = torch.zeros(256, dtype=torch.uint8, device=dev)
+    acc_ws = torch.zeros(ctx.qmm_argmax_accept_workspace_bytes(M, *C5_LM_HEAD, 4, 64),
+                         dtype=torch.uint8, device=dev)
     torch.cuda.synchronize()
-    if one_graph and not persistent:
+    if one_graph:
         ctx.graph_begin(stream)
     for li in range(layers):
         wl = lw[li]
         layer_in = x if li == 0 else outs[-1]
-        if persistent:
-            for j, (N, K) in enumerate(layer):
-                inp = layer_in if srcs[j] is None else outs[srcs[j]]
-                w, s, b = wl[j]
-                chain_ops.append({"kind": kinds[j], "x": inp, "y": outs[j], "w": w,
-                                  "scales": s, "biases": b, "N": N, "K": K})
-            continue
         if not one_graph:
             ctx.graph_begin(stream)
         for j, (N, K) in enumerate(layer):
@@ -230,25 +265,15 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False,
             graphs.append(ctx.graph_end(stream))
 
     def lm_only():
-        """the lm_head and the greedy accept: only M + 1 ints leave the device"""
-        ctx.qmm_raw(outs[-1], wlm, slm, blm, lm_out, M, C5_LM_HEAD[0], C5_LM_HEAD[1], 4, 64,
-                    B, B, B, ws=ws, ws_bytes=ws.numel(), stream=stream)
-        ctx.argmax_accept(lm_out, proposals, tokens, accepted, ws=acc_ws, stream=stream)
+        """the lm_head fused with the greedy accept: only M + 1 ints leave the device"""
+        ctx.qmm_argmax_accept(outs[-1], wlm, slm, blm, 4, 64, proposals=proposals,
+                              tokens=tokens, accepted=accepted, ws=acc_ws, stream=stream)
 
-    chain = None
-    if one_graph and not persistent:
+    if one_graph:
         lm_only()
         graphs.append(ctx.graph_end(stream))
-    if persistent:
-        chain_ops.append({"kind": "qmm", "x": outs[-1], "y": lm_out, "w": wlm, "scales": slm,
-                          "biases": blm, "N": C5_LM_HEAD[0], "K": C5_LM_HEAD[1]})
-        chain = ctx.chain(M, 4, 64, chain_ops)
 
     def forward():
-        if chain is not None:
-            chain.launch(stream)
-            ctx.argmax_accept(lm_out, proposals, tokens, accepted, ws=acc_ws, stream=stream)
-            return
         for gr in graphs:
             gr.launch(stream)
         if not one_graph:
@@ -260,21 +285,18 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False,
             torch.cuda.synchronize()
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            for _ in range(n):
-                fn()
-            e1.record(stream)
-            torch.cuda.synchronize()
+            with TIMED:
+                e0.record(stream)
+                for _ in range(n):
+                    fn()
+                e1.record(stream)
+                torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1000.0 / n
 
     total = timed(forward, reps)
     lm = timed(lm_only, 20)
     for gr in graphs:
         gr.close()
-    if chain is not None:
-        if chain.failed():
-            raise RuntimeError("the persistent chain reported a timed-out wait")
-        chain.close()
     layer_bytes = sum(algorithmic_bytes(M, N, K) for (N, K) in C5_LAYER)   # the same fused
     total_bytes = layers * layer_bytes + algorithmic_bytes(M, *C5_LM_HEAD)
     ideal = total_bytes / (HBM_PEAK_GBS * 1e3)
@@ -283,9 +305,7 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False,
                      + ("(q|k|v, o, gate|up with silu*up epilogue, down)" if fused
                         else "(q,k,v,o,gate,up,down)")
                      + " + lm_head + greedy accept, 4-bit g64 bf16, "
-                     + ("the layers and lm_head as one persistent chain launch" if persistent
-                        else "one HIP graph per forward" if one_graph
-                        else "one HIP graph per layer")),
+                     + ("one HIP graph per forward" if one_graph else "one HIP graph per layer")),
         "us_per_forward": round(total, 1),
         "ideal_us_at_8TBs": round(ideal, 1),
         "frac_of_ideal": round(ideal / total, 4),
@@ -294,6 +314,51 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, persistent=False,
         "layer_ideal_us": round(layer_bytes / (HBM_PEAK_GBS * 1e3), 2),
         "lm_head_accept_us": round(lm, 2),
         "lm_head_ideal_us": round(algorithmic_bytes(M, *C5_LM_HEAD) / (HBM_PEAK_GBS * 1e3), 2),
+    }
+
+
+def time_lm_head(torch, ctx, stream, dev, steps=20, nsets=2):
+    """The C5 LM head (M=8, 151936 x 5120, 4-bit g64) with the greedy accept, graph-replayed
+    over rotated weights: fused (dfq_qmm_argmax_accept, no logits written) and as two calls
+    (dfq_qmm to logits, then dfq_argmax_accept).  Per-call us."""
+    import dflash_qmm
+    M, (V, K) = 8, C5_LM_HEAD
+    sets = make_sets(torch, nsets, V, K, 4, 64, dev, seed=9)
+    x = torch.randn(M, K, device=dev).to(torch.bfloat16)
+    logits = torch.empty(M, V, device=dev, dtype=torch.bfloat16)
+    props = torch.zeros(M - 1, dtype=torch.int32, device=dev)
+    tokens = torch.empty(M, dtype=torch.int32, device=dev)
+    acc = torch.empty(1, dtype=torch.int32, device=dev)
+    ws = torch.zeros(max(ctx.qmm_argmax_accept_workspace_bytes(M, V, K, 4, 64),
+                         ctx.workspace_bytes(M, V, K, 4, 64)), dtype=torch.uint8, device=dev)
+    acc_ws = torch.zeros(256, dtype=torch.uint8, device=dev)
+    B = dflash_qmm.BF16
+    out = {}
+    for form in ("fused", "two_calls"):
+        torch.cuda.synchronize()
+        ctx.graph_begin(stream)
+        for i in range(steps):
+            w, s, b = sets[i % nsets]
+            if form == "fused":
+                ctx.qmm_argmax_accept(x, w, s, b, 4, 64, proposals=props, tokens=tokens,
+                                      accepted=acc, ws=ws, stream=stream)
+            else:
+                ctx.qmm_raw(x, w, s, b, logits, M, V, K, 4, 64, B, B, B, ws=ws,
+                            ws_bytes=ws.numel(), stream=stream)
+                ctx.argmax_accept(logits, props, tokens, acc, ws=acc_ws, stream=stream)
+        graph = ctx.graph_end(stream)
+        with torch.cuda.stream(stream):
+            graph.launch(stream)
+            out[form] = stats(time_replays(torch, stream, graph, steps, 10))["median"]
+        graph.close()
+    nb = algorithmic_bytes(M, V, K)
+    return {
+        "workload": ("LM head M=8, 151936 x 5120 4-bit g64 bf16, with the greedy accept; "
+                     f"{nsets} rotated weight sets (880 MB)"),
+        "fused_us": round(out["fused"], 2),
+        "two_calls_us": round(out["two_calls"], 2),
+        "ideal_us_at_8TBs": round(nb / (HBM_PEAK_GBS * 1e3), 2),
+        "fused_gbs": round(nb / (out["fused"] * 1e-6) / 1e9, 1),
     }
 
 
@@ -327,6 +392,7 @@ def cpu_baseline(seconds):
 
 
 def main():
+    global TIMED
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
@@ -337,13 +403,17 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-chain", action="store_true",
                     help="skip the 64-layer verify-forward measurement (c5_chain)")
-    ap.add_argument("--c5-only", choices=["separate", "fused", "fused_one_graph", "persistent"],
+    ap.add_argument("--no-reference", action="store_true",
+                    help="skip the read-ceiling and device-copy reference legs")
+    ap.add_argument("--c5-only", choices=["separate", "fused", "fused_one_graph"],
                     default=None,
                     help="only time this form of the 64-layer verify forward (for profiling) "
                          "and print its figures")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run 20 plain device copies of this many MiB (the reference "
                          "point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
+    ap.add_argument("--profile-timed", action="store_true",
+                    help="trace only the timed replays (rocprofv3 --selected-regions)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -355,6 +425,7 @@ def main():
     import dflash_qmm
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    TIMED = TimedRegion(args.profile_timed)
     dev = torch.device("cuda:0")
     if args.copy_mib:
         n = args.copy_mib << 20
@@ -368,7 +439,6 @@ def main():
     ctx = dflash_qmm.Context(0)
     if args.c5_only:
         r = chain_c5(torch, ctx, dev, fused=args.c5_only.startswith("fused"),
-                     persistent=args.c5_only == "persistent",
                      one_graph=args.c5_only == "fused_one_graph")
         print(json.dumps({"c5_" + args.c5_only: r}), flush=True)
         ctx.close()
@@ -383,21 +453,23 @@ def main():
 
     torch.cuda.synchronize()
     # one untimed pass first: the first M timed on a cold GPU otherwise reads up to ~1 us slow
+    saved, TIMED = TIMED, TimedRegion(False)
     time_m(torch, ctx, stream, sets, ms[0], args.steps, args.warmup, N_OUT, K_IN, BITS, GS, ws,
            ws.numel())
-    us = {}
+    TIMED = saved
+    dist = {}
     for m in ms:
-        us[m] = time_m(torch, ctx, stream, sets, m, args.steps, args.warmup, N_OUT, K_IN, BITS,
-                       GS, ws, ws.numel())
-        print(f"[bench] M={m}: {us[m]:.2f} us/call, "
-              f"{algorithmic_bytes(m) / us[m] / 1e3:.0f} GB/s", file=sys.stderr, flush=True)
-
+        dist[m] = stats(time_m(torch, ctx, stream, sets, m, args.steps, args.warmup, N_OUT,
+                               K_IN, BITS, GS, ws, ws.numel()))
+        d = dist[m]
+        print(f"[bench] M={m}: {d['median']:.2f} us/call (p10 {d['p10']:.2f}, p90 "
+              f"{d['p90']:.2f}, {d['replays']} replays of {args.steps}), "
+              f"{algorithmic_bytes(m) / d['median'] / 1e3:.0f} GB/s", file=sys.stderr,
+              flush=True)
+    us = {m: dist[m]["median"] for m in ms}
     gbs = {m: algorithmic_bytes(m) / (us[m] * 1e-6) / 1e9 for m in ms}
-    copy_bytes = algorithmic_bytes(8)
-    uc_copy = time_copy(torch, stream, copy_bytes, args.sets, args.steps)
-    print(f"[bench] device copy moving {copy_bytes / 1e6:.1f} MB: {uc_copy:.2f} us/copy, "
-          f"{copy_bytes / uc_copy / 1e3:.0f} GB/s", file=sys.stderr, flush=True)
     achieved = gbs[8]
+    nb8 = algorithmic_bytes(8)
     out = {
         "metric": "us/call + HBM GB/s, 4-bit qmatmul K5120xN17408, M=1..8; M8/M1 time ratio",
         "value": round(achieved, 2),
@@ -415,18 +487,13 @@ def main():
             "workload": "affine qmm 4-bit g64, K=5120, N=17408, bf16, M=8 per step",
             "M_sweep": ms,
             "rotated_weight_sets": args.sets,
+            "replays_per_M": replays_for(args.steps),
         },
         "us_per_call": {str(m): round(us[m], 3) for m in ms},
+        "us_per_call_p10": {str(m): round(dist[m]["p10"], 3) for m in ms},
+        "us_per_call_p90": {str(m): round(dist[m]["p90"], 3) for m in ms},
         "gbs_by_M": {str(m): round(gbs[m], 1) for m in ms},
         "m8_m1_ratio": round(us[8] / us[1], 4) if 1 in us else None,
-        "device_copy": {
-            "workload": ("torch copy_ of half the M=8 call's algorithmic bytes into another "
-                         "buffer (the same bytes moved per launch), rotated, back to back: the "
-                         "per-launch bandwidth a memory-bound kernel of this size reaches here"),
-            "bytes_per_launch": copy_bytes,
-            "us_per_copy": round(uc_copy, 3),
-            "gbs": round(copy_bytes / (uc_copy * 1e-6) / 1e9, 1),
-        },
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),
@@ -436,25 +503,42 @@ def main():
             "traffic": measured_traffic(),
         },
     }
-    if not args.no_chain:
-        uc = time_chained(torch, ctx, stream, sets, 8, 25, N_OUT, K_IN, BITS, GS)
-        out["chained_independent_m8"] = {
-            "workload": (f"the same M=8 calls over the {args.sets} weight sets as one dfq_chain "
-                         "launch of independent ops (not the headline: the verify forward's "
-                         "matmuls depend on each other)"),
-            "us_per_call": round(uc, 3),
-            "gbs": round(algorithmic_bytes(8) / (uc * 1e-6) / 1e9, 1),
+    if not args.no_reference:
+        rd = stats(time_read(torch, ctx, stream, nb8, args.sets, args.steps, dev))
+        out["read_ceiling"] = {
+            "workload": ("the library's plain streaming-read kernel (one workgroup of 8 waves "
+                         "per CU, contiguous 4 KB blocks) reading the M=8 call's algorithmic "
+                         "bytes per launch, rotated over buffers, replayed like the matmul"),
+            "bytes_per_launch": nb8,
+            "us_per_launch": round(rd["median"], 3),
+            "p10": round(rd["p10"], 3),
+            "p90": round(rd["p90"], 3),
+            "gbs": round(nb8 / (rd["median"] * 1e-6) / 1e9, 1),
+            "matmul_frac_of_ceiling": round(rd["median"] / us[8], 4),
         }
-        print(f"[bench] chained independent M=8: {uc:.2f} us/call", file=sys.stderr, flush=True)
+        print(f"[bench] read ceiling {nb8 / 1e6:.1f} MB: {rd['median']:.2f} us/launch, "
+              f"{nb8 / rd['median'] / 1e3:.0f} GB/s", file=sys.stderr, flush=True)
+        uc_copy = time_copy(torch, stream, nb8, args.sets, args.steps)
+        out["device_copy"] = {
+            "workload": ("torch copy_ of half the M=8 call's algorithmic bytes into another "
+                         "buffer (the same bytes moved per launch), rotated, back to back"),
+            "bytes_per_launch": nb8,
+            "us_per_copy": round(uc_copy, 3),
+            "gbs": round(nb8 / (uc_copy * 1e-6) / 1e9, 1),
+        }
+        print(f"[bench] device copy moving {nb8 / 1e6:.1f} MB: {uc_copy:.2f} us/copy",
+              file=sys.stderr, flush=True)
+    if not args.no_chain:
         del sets
         torch.cuda.empty_cache()
+        out["lm_head_accept"] = time_lm_head(torch, ctx, stream, dev)
+        print(f"[bench] lm_head + accept: fused {out['lm_head_accept']['fused_us']} us, two "
+              f"calls {out['lm_head_accept']['two_calls_us']} us", file=sys.stderr, flush=True)
         out["c5_chain"] = chain_c5(torch, ctx, dev)
         torch.cuda.empty_cache()
         out["c5_chain_fused"] = chain_c5(torch, ctx, dev, fused=True)
         out["c5_chain_fused_one_graph"] = chain_c5(torch, ctx, dev, fused=True, one_graph=True)
-        out["c5_chain_persistent"] = chain_c5(torch, ctx, dev, persistent=True)
-        for key in ("c5_chain", "c5_chain_fused", "c5_chain_fused_one_graph",
-                    "c5_chain_persistent"):
+        for key in ("c5_chain", "c5_chain_fused", "c5_chain_fused_one_graph"):
             print(f"[bench] {key}: {out[key]['us_per_forward']} us/forward "
                   f"(ideal {out[key]['ideal_us_at_8TBs']})", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:

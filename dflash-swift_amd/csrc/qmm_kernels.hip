@@ -419,25 +419,37 @@ __device__ __forceinline__ float* tile_slot(const QmmParams& p, int t, int kb, i
     return p.slots + ((size_t)(t * p.nkb + kb) * p.nslot_kb + j) * p.mt * 128 + tile_off(lane);
 }
 
-/* Stores of data another workgroup reads within the same launch (a chain's outputs and its
- * workspace): COH makes them agent-scope atomic stores, written through the XCD's L2, so the
- * reader needs no whole-L2 write-back from the writer, and no dirty line of an older value
- * can later be written back over a newer one from another XCD. */
-template <bool COH>
-__device__ __forceinline__ void put16(uint16_t* ptr, uint16_t v) {
-    if constexpr (COH) __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else *ptr = v;
+__device__ __forceinline__ void put16(uint16_t* ptr, uint16_t v) { *ptr = v; }
+__device__ __forceinline__ void put_tile4(float* ptr, f32x4_t v) { *(f32x4_t*)ptr = v; }
+
+/* Keys of the greedy accept: the logit's bits made order-preserving (sign flip, or full
+ * flip for negatives) in the high word and ~index in the low word, so the largest key is
+ * the largest logit and, among equal logits, the first index (MLX's argMax); 0 = none. */
+__device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
+    const uint32_t b = __float_as_uint(v);
+    const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((uint64_t)o << 32) | (uint32_t)~(uint32_t)idx;
 }
-template <bool COH>
-__device__ __forceinline__ void put_tile4(float* ptr, f32x4_t v) {
-    if constexpr (COH) {
+
+__device__ __forceinline__ uint64_t max_key_wave(uint64_t k) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            __hip_atomic_store((uint32_t*)ptr + r, __float_as_uint(v[r]), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-        *(f32x4_t*)ptr = v;
+    for (int s = 32; s > 0; s >>= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)k, s, 64);
+        const uint32_t hi = __shfl_xor((uint32_t)(k >> 32), s, 64);
+        const uint64_t o = ((uint64_t)hi << 32) | lo;
+        k = o > k ? o : k;
     }
+    return k;
+}
+
+/* Folds output element (its rounded bits o, column col) into a row's running key; NaN is
+ * skipped. */
+template <bool F16>
+__device__ __forceinline__ void fold_key(uint64_t& best, uint16_t o, int col) {
+    const float f = elem_to_f32<F16>(o);
+    if (f != f) return;
+    const uint64_t k = argmax_key(f, col);
+    best = k > best ? k : best;
 }
 
 /* silu(g) * u as the MLP activation computes it from a stored gate|up output: g and u
@@ -453,7 +465,7 @@ __device__ __forceinline__ uint16_t silu_mul_round(float g, float u) {
 /* The gate|up epilogue (p.epi): the weight's rows are interleaved by 8, so tile t holds gate
  * columns 8t..8t+7 in its columns 0-7 and the matching up columns in 8-15; lane n < 8 takes
  * its up partner from lane n + 8 (DPP row_ror:8, every lane active) and writes h[m][8t+n]. */
-template <bool F16, bool COH>
+template <bool F16>
 __device__ __forceinline__ void store_h(const QmmParams& p, int t, int lane, f32x4_t v) {
     const int q = lane >> 4, n = lane & 15;
     float lb = 0.0f;
@@ -470,15 +482,17 @@ __device__ __forceinline__ void store_h(const QmmParams& p, int t, int lane, f32
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int m = 4 * q + r;
-        if (m < p.M) put16<COH>(h + (size_t)m * H + t * 8 + n, silu_mul_round<F16>(v[r], u[r]));
+        if (m < p.M) put16(h + (size_t)m * H + t * 8 + n, silu_mul_round<F16>(v[r], u[r]));
     }
 }
 
-/* Tile t as held by the lanes, plus the linear bias, to y. */
-template <bool F16, bool COH = false>
-__device__ __forceinline__ void store_y(const QmmParams& p, int t, int lane, f32x4_t v) {
+/* Tile t as held by the lanes, plus the linear bias, to y; in greedy-accept mode (p.am_keys)
+ * also folded into the lane's keys of rows 4q..4q+3 (best), and y may be NULL. */
+template <bool F16>
+__device__ __forceinline__ void store_y(const QmmParams& p, int t, int lane, f32x4_t v,
+                                        uint64_t (&best)[4]) {
     if (p.epi) {
-        store_h<F16, COH>(p, t, lane, v);
+        store_h<F16>(p, t, lane, v);
         return;
     }
     const int q = lane >> 4, n = lane & 15;
@@ -490,7 +504,10 @@ __device__ __forceinline__ void store_y(const QmmParams& p, int t, int lane, f32
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int m = 4 * q + r;
-        if (m < p.M) put16<COH>(y + (size_t)m * p.N + col, f32_to_out<F16>(v[r] + lb));
+        if (m >= p.M) continue;
+        const uint16_t o = f32_to_out<F16>(v[r] + lb);
+        if (y) put16(y + (size_t)m * p.N + col, o);
+        if (p.am_keys) fold_key<F16>(best[r], o, col);
     }
 }
 
@@ -510,9 +527,9 @@ __device__ __forceinline__ void store_y(const QmmParams& p, int t, int lane, f32
  * The workspace is zero again when the kernel ends.  Workgroups on different XCDs exchange
  * these partials: every access to a slot is an agent-scope atomic (coherent across the
  * XCDs' L2s without a whole-cache write-back or invalidate). */
-template <bool F16, bool COH = false>
-__device__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t, int slot,
-                        int lane, f32x4_t v) {
+template <bool F16>
+__device__ __forceinline__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t,
+                                        int slot, int lane, f32x4_t v, uint64_t (&best)[4]) {
     const int q = lane >> 4, n = lane & 15;
     const bool act = lane < 32 * p.mt;  // lanes holding the tile
     const int nwg = owner_wg(t * SS + SS - 1, base_u, rem_u) - owner_wg(t * SS, base_u, rem_u) + 1;
@@ -563,7 +580,7 @@ __device__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t
             const float g = v[r] + __uint_as_float((uint32_t)og[r]);
             const int m = 4 * q + r;
             if (m < p.M)
-                put16<COH>((uint16_t*)p.y + (size_t)m * H + t * 8 + n,
+                put16((uint16_t*)p.y + (size_t)m * H + t * 8 + n,
                            silu_mul_round<F16>(g + lbg, u[r] + up + lbu));
             __hip_atomic_store(sg + r, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -584,8 +601,11 @@ __device__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t
         if (!(old[r] >> 32)) continue;
         const int m = 4 * q + r;
         const float sum = v[r] + __uint_as_float((uint32_t)old[r]);
-        if (m < p.M && col < p.N)
-            put16<COH>((uint16_t*)p.y + (size_t)m * p.N + col, f32_to_out<F16>(sum + lb));
+        if (m < p.M && col < p.N) {
+            const uint16_t o = f32_to_out<F16>(sum + lb);
+            if (p.y) put16((uint16_t*)p.y + (size_t)m * p.N + col, o);
+            if (p.am_keys) fold_key<F16>(best[r], o, col);
+        }
         __hip_atomic_store(sl + r, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
@@ -599,10 +619,72 @@ __device__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t
  * It polls the tile counters of its workgroup (one lane per tile, sleeping between empty
  * polls) until each of the ntl tiles has been written.  Every unit of [a, b) is taken by
  * exactly one streaming wave, so every tile reaches kTileDone and the loop ends. */
-template <bool F16, int MT, bool COH = false>
+/* Greedy-accept mode, after the publisher's last tile: its keys of each row (lane (q, n)
+ * holds rows 4q..4q+3 of the columns it finished) are reduced over the 16 columns of the lane
+ * group and folded into the workgroup group's keys with an agent-scope atomic max (16 groups
+ * of workgroups, so that no key takes more than a sixteenth of the atomics).  Arrivals are
+ * counted the same way: a counter per group, then one over the groups.  The last workgroup
+ * takes every group's keys (exchanging them with zero), writes each row's token (the column
+ * of its key, -1 for a row of NaN) and the accepted run -- the first verify row i < M-1 whose
+ * token differs from proposals[i], or M-1 -- and re-arms the counters.  The keys are only
+ * touched by agent-scope atomics, which complete (vmcnt) before the arrival is counted: no
+ * cache write-back or invalidate. */
+template <int MT>
+__device__ void accept_finish(const QmmParams& p, uint64_t (&best)[4], int lane, int wg) {
+    const int q = lane >> 4, n = lane & 15;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int s = 8; s > 0; s >>= 1) {
+            const uint32_t lo = __shfl_xor((uint32_t)best[r], s, 16);
+            const uint32_t hi = __shfl_xor((uint32_t)(best[r] >> 32), s, 16);
+            const uint64_t o = ((uint64_t)hi << 32) | lo;
+            best[r] = o > best[r] ? o : best[r];
+        }
+    const int G = (int)gridDim.x, ng = min(16, G), grp = wg % ng;
+    if (n == 0 && lane < 32 * MT) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = 4 * q + r;
+            if (m < p.M && best[r])
+                __hip_atomic_fetch_max(p.am_keys + (size_t)grp * p.M + m, best[r],
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the maxima have completed
+    uint32_t last = 0;
+    if (lane == 0) {
+        const uint32_t size_g = (uint32_t)(G / ng + (grp < G % ng ? 1 : 0));
+        if (__hip_atomic_fetch_add(p.am_count + grp * 32, 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT) + 1u == size_g)
+            last = __hip_atomic_fetch_add(p.am_count + 16 * 32, 1u, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT) + 1u == (uint32_t)ng;
+    }
+    if (!__builtin_amdgcn_readfirstlane(last)) return;
+    bool bad = false;
+    if (lane < p.M) {
+        uint64_t k = 0;
+        for (int g = 0; g < ng; ++g) {
+            const uint64_t kk = __hip_atomic_exchange(p.am_keys + (size_t)g * p.M + lane, 0ull,
+                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            k = kk > k ? kk : k;
+        }
+        const int32_t tok = k ? (int32_t)~(uint32_t)k : -1;
+        if (p.am_tokens) p.am_tokens[lane] = tok;
+        bad = lane < p.M - 1 && !(p.am_proposals && p.am_proposals[lane] == tok);
+    }
+    const uint64_t badm = __builtin_amdgcn_ballot_w64(bad);
+    if (lane == 0) {
+        if (p.am_accepted) *p.am_accepted = badm ? (int32_t)__builtin_ctzll(badm) : p.M - 1;
+        for (int g = 0; g < ng; ++g)
+            __hip_atomic_store(p.am_count + g * 32, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.am_count + 16 * 32, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+template <bool F16, int MT>
 __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b, int SS,
-                               int base_u, int rem_u, int lane, uint32_t* err = nullptr,
-                               uint32_t timeout = 0) {
+                               int base_u, int rem_u, int lane, int wg) {
     const int q = lane >> 4, n = lane & 15;
     const int ta = a / SS;
     const int ntl = (b > a) ? (b - 1) / SS - ta + 1 : 0;
@@ -611,8 +693,8 @@ __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
     const float* part = (const float*)(lds_base() + p.lds_part_off);
     const int s1 = max(a, ((b - 1) / SS) * SS), nrot = b - s1;  // the take order (unit_of)
     __syncthreads();  // the staging barrier of the streaming waves (tile counters zeroed)
+    uint64_t best[4] = {0, 0, 0, 0};  // greedy-accept keys of rows 4q..4q+3
     int remaining = ntl;
-    uint64_t deadline = 0;
     while (remaining > 0) {
         int found = 0;
         for (int base = 0; base < ntl; base += 64) {
@@ -638,33 +720,22 @@ __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
                                        __HIP_MEMORY_SCOPE_WORKGROUP);
                 const int first = owner_wg(t * SS, base_u, rem_u);
                 if (u0 == t * SS && u1 == (t + 1) * SS && p.nkb == 1) {
-                    store_y<F16, COH>(p, t, lane, v);
+                    store_y<F16>(p, t, lane, v, best);
                 } else if (p.reduce) {
                     /* summed by the second pass: no round trip here */
-                    if (lane < 32 * MT) put_tile4<COH>(tile_slot(p, t, kb, cl - first, lane), v);
+                    if (lane < 32 * MT) put_tile4(tile_slot(p, t, kb, cl - first, lane), v);
                 } else {
-                    publish<F16, COH>(p, SS, base_u, rem_u, t, kb * p.nslot_kb + (cl - first),
-                                      lane, v);
+                    publish<F16>(p, SS, base_u, rem_u, t, kb * p.nslot_kb + (cl - first),
+                                 lane, v, best);
                 }
                 if (lane == 0) tcnt[base + bit] = kTileOut;
                 ++found;
             }
         }
         remaining -= found;
-        if (found) deadline = 0;
-        if (!found) {
-            /* in a chain the wait is bounded like every other (err: the chain's flag) */
-            if (err) {
-                if (!deadline) deadline = __builtin_amdgcn_s_memrealtime() + timeout;
-                if (__builtin_amdgcn_s_memrealtime() > deadline) {
-                    if (lane == 0)
-                        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    break;
-                }
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
+        if (!found) __builtin_amdgcn_s_sleep(1);
     }
+    if (p.am_keys) accept_finish<MT>(p, best, lane, wg);
 }
 
 /* ---------------------------------------------------------------------------------- */
@@ -679,12 +750,12 @@ __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
  * linear bias, to y; the slots are zeroed, which leaves the workspace zero at rest.  Tiles
  * with one contributor were written by the main kernel.
  *
- * All nkb * nslot_kb slots of the tile are read, eight loads (two in a chain) in flight
+ * All nkb * nslot_kb slots of the tile are read, eight loads in flight
  * before any use: the slots a k-block leaves unused are zero, and adding +0.0f to a sum
  * that is never -0.0f (it starts at +0.0f) leaves it unchanged, so the result equals the
  * sum of the used slots alone.  One memory latency per eight slots instead of one per
  * slot. */
-template <bool F16, bool COH = false>
+template <bool F16>
 __device__ __forceinline__ void reduce_tile(const QmmParams& p, int t, int lane) {
     int parts = 0;
     for (int kb = 0; kb < p.nkb; ++kb) {
@@ -696,9 +767,7 @@ __device__ __forceinline__ void reduce_tile(const QmmParams& p, int t, int lane)
     if (lane < 32 * p.mt) {
         const int S = p.nkb * p.nslot_kb, stride = p.mt * 128;
         float* s0 = tile_slot(p, t, 0, 0, lane);  // slot i = kb * nslot_kb + j at s0 + i * stride
-        /* in a chain this runs inside the persistent kernel, beside the streaming loop's
-         * registers: two loads in flight there keep it from spilling */
-        constexpr int NB = COH ? 2 : 8;
+        constexpr int NB = 8;
         for (int b = 0; b < S; b += NB) {
             f32x4_t v[NB];
 #pragma unroll
@@ -708,183 +777,16 @@ __device__ __forceinline__ void reduce_tile(const QmmParams& p, int t, int lane)
             for (int i = 0; i < NB; ++i)
                 if (b + i < S) {
                     sum += v[i];
-                    put_tile4<COH>(s0 + (size_t)(b + i) * stride, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f});
+                    put_tile4(s0 + (size_t)(b + i) * stride, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f});
                 }
         }
     }
-    store_y<F16, COH>(p, t, lane, sum);
+    uint64_t unused[4] = {0, 0, 0, 0};  // a reduce split never runs in greedy-accept mode
+    store_y<F16>(p, t, lane, sum, unused);
 }
 
-/* ---- the chain kernel's synchronisation ------------------------------------------------
- * Ops of a chain run one after another on every workgroup of one launch (one workgroup per
- * CU, all resident).  A workgroup issues op j's first weight loads, then waits for op j-1
- * to complete before it reads op j-1's output; a reduce split's second pass and an
- * elementwise op are shared by all workgroups and complete the same way.
- *
- * Completion counts are hierarchical: device-scope atomics on one address serialise at the
- * memory side, so each workgroup counts in one of 16 group counters (separate 128-byte
- * lines), the last of a group counts in the block's total, and the last group raises every
- * group's "go" flag, which the waiting workgroups of that group poll.  Counters never reset:
- * they grow by one epoch per launch (read at the start from the epoch word, raised by the
- * last arrival of the end block), so no reset can race a late reader.
- *
- * Waits are bounded: one elected wave per workgroup polls (the others watch an LDS flag);
- * past the deadline, or once any wave has failed, a wait sets the error flag and returns,
- * so every wave runs to the end.  A workgroup's streaming waves re-arm their LDS for op j
- * only after their own publisher has posted that it is done with op j-1 (an LDS epoch), so
- * a failed wait cannot pull LDS from under the publisher. */
-/* The op table is written once, before any launch: read through the constant address space,
- * its fields come by scalar loads into SGPRs.  Through a plain global pointer the compiler
- * must assume the kernel's own stores may change it and re-reads fields with vector loads
- * inside the streaming loop, whose waits then cover the whole prefetch. */
-typedef const __attribute__((address_space(4))) ChainOp* ConstOps;
-
-__device__ __forceinline__ ConstOps chain_ops(const ChainParams& cp) { return (ConstOps)cp.ops; }
-
-constexpr int kSyncGroups = 16;
-constexpr int kSyncLine = 32;  // words per 128-byte line
-constexpr int kSyncBlock = (2 * kSyncGroups + 1) * kSyncLine;
-/* sync words: [0] launch epoch, [32] error flag, then blocks of kSyncBlock words: op j's
- * completion (2j), op j's second pass (2j + 1), the end of the chain (2 n_ops) */
-__device__ __forceinline__ uint32_t* chain_err(const ChainParams& cp) { return cp.sync + kSyncLine; }
-__device__ __forceinline__ uint32_t* chain_block(const ChainParams& cp, int i) {
-    return cp.sync + 2 * kSyncLine + (size_t)i * kSyncBlock;
-}
-
-/* LDS words at lds_flag_off: [0] elected wait id, [1] passed wait id, [2] reduce / end
- * gathering, [3] elementwise gathering, [4] publisher's op epoch, [5] launch epoch */
-__device__ __forceinline__ uint32_t* chain_lds(const ChainParams& cp) {
-    return (uint32_t*)(lds_base() + cp.lds_flag_off);
-}
-
-/* One workgroup's arrival at block blk (one lane, after the workgroup's stores for it are
- * complete).  final: the end block, whose completion raises the launch epoch. */
-__device__ void chain_arrive(const ChainParams& cp, uint32_t* blk, int wg, bool final) {
-    const uint32_t e1 = chain_lds(cp)[5] + 1u;
-    const int ng = min(kSyncGroups, cp.G);
-    const int g = wg % ng;
-    const uint32_t size_g = (uint32_t)(cp.G / ng + (g < cp.G % ng ? 1 : 0));
-    /* relaxed: everything a waiter reads was written with coherent stores that completed
-     * (s_waitcnt vmcnt(0)) before this arrival was issued */
-    const uint32_t old =
-        __hip_atomic_fetch_add(blk + g * kSyncLine, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (old + 1u != e1 * size_g) return;
-    const uint32_t o2 = __hip_atomic_fetch_add(blk + kSyncGroups * kSyncLine, 1u, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-    if (o2 + 1u != e1 * (uint32_t)ng) return;
-    if (final) {
-        __hip_atomic_fetch_add(cp.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return;
-    }
-    for (int g2 = 0; g2 < ng; ++g2)
-        __hip_atomic_store(blk + (kSyncGroups + 1 + g2) * kSyncLine, e1, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-}
-
-/* Waits until block blk is complete for this launch.  wid: this wait's number, increasing
- * through the chain (it elects one poller per workgroup per wait). */
-__device__ void chain_wait(const ChainParams& cp, uint32_t* blk, int wg, uint32_t wid) {
-    uint32_t* lf = chain_lds(cp);
-    if ((threadIdx.x & 63) == 0) {
-        const uint32_t prev =
-            __hip_atomic_fetch_max(lf, wid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        if (prev < wid) {
-            const uint32_t e1 = lf[5] + 1u;
-            const int ng = min(kSyncGroups, cp.G);
-            uint32_t* go = blk + (kSyncGroups + 1 + wg % ng) * kSyncLine;
-            const uint64_t deadline = __builtin_amdgcn_s_memrealtime() + cp.timeout;
-            uint32_t* err = chain_err(cp);
-            while ((int32_t)(__hip_atomic_load(go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) -
-                             e1) < 0) {
-                if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)
-                    break;
-                if (__builtin_amdgcn_s_memrealtime() > deadline) {
-                    __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(4);
-            }
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            __hip_atomic_store(lf + 1, wid, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-        } else {
-            while (__hip_atomic_load(lf + 1, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < wid)
-                __builtin_amdgcn_s_sleep(2);
-        }
-    }
-}
-
-/* The publisher's arrival for op j: its stores are complete, and it is done with the
- * workgroup's LDS. */
-__device__ __forceinline__ void chain_publisher_done(const ChainParams& cp, int j, int wg) {
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if ((threadIdx.x & 63) == 0) {
-        __hip_atomic_store(chain_lds(cp) + 4, (uint32_t)(j + 1), __ATOMIC_RELEASE,
-                           __HIP_MEMORY_SCOPE_WORKGROUP);
-        chain_arrive(cp, chain_block(cp, 2 * j), wg, false);
-    }
-}
-
-/* The streaming waves' arrival at block bi: they gather in LDS word lw (zero before the
- * first arrives) and the last of the kWaves arrives for the workgroup. */
-__device__ __forceinline__ void chain_waves_done(const ChainParams& cp, int bi, int lw, int wg,
-                                                 bool final) {
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if ((threadIdx.x & 63) == 0) {
-        uint32_t* lc = chain_lds(cp) + lw;
-        const uint32_t old =
-            __hip_atomic_fetch_add(lc, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
-        if (old + 1 == (uint32_t)kWaves) {
-            __hip_atomic_store(lc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            chain_arrive(cp, chain_block(cp, bi), wg, final);
-        }
-    }
-}
-
-/* Before op j (or, with j = n_ops, before the chain ends), a streaming wave waits for op
- * j-1, and runs its share of op j-1's second pass if op j-1 is a reduce split.  wg: this
- * workgroup; the G workgroups' streaming waves split the tiles. */
-template <bool F16>
-__device__ void chain_prev(const ChainParams& cp, int j, int wg) {
-    if (j == 0) return;
-    if (j < cp.n_ops && chain_ops(cp)[j].independent) {
-        /* op j reads nothing op j-1 writes: it only needs op j-2 done (its workspace region
-         * is the one op j-2 used; everything before op j-2 is done with it, as every
-         * workgroup runs the ops in order) */
-        if (j >= 2) chain_wait(cp, chain_block(cp, 2 * (j - 2)), wg, 2u * j - 1u);
-        return;
-    }
-    const ChainOp po = chain_ops(cp)[j - 1];
-    chain_wait(cp, chain_block(cp, 2 * (j - 1)), wg, 2u * j - 1u);
-    if (po.kind == 0 && po.p.reduce) {
-        const int lane = threadIdx.x & 63;
-        const int nw = cp.G * kWaves;
-        for (int t = wg * kWaves + (int)(threadIdx.x >> 6); t < po.p.T; t += nw)
-            reduce_tile<F16, true>(po.p, t, lane);
-        chain_waves_done(cp, 2 * (j - 1) + 1, 2, wg, false);
-        chain_wait(cp, chain_block(cp, 2 * (j - 1) + 1), wg, 2u * j);
-    }
-}
-
-/* A streaming wave about to re-arm the workgroup's LDS for op j waits until the publisher
- * has left op j-1 (bounded: the publisher's remaining tiles are already summed). */
-__device__ __forceinline__ void chain_lds_free(const ChainParams& cp, int j) {
-    if (j == 0) return;
-    if ((threadIdx.x & 63) == 0) {
-        const uint64_t deadline = __builtin_amdgcn_s_memrealtime() + cp.timeout;
-        while (__hip_atomic_load(chain_lds(cp) + 4, __ATOMIC_ACQUIRE,
-                                 __HIP_MEMORY_SCOPE_WORKGROUP) < (uint32_t)j) {
-            if (__builtin_amdgcn_s_memrealtime() > deadline) {
-                __hip_atomic_store(chain_err(cp), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-    }
-}
-
-template <int BITS, int GS, bool F16, int CH, int PF, int MT, bool CHAIN = false>
-__device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg,
-                                        const ChainParams* cp = nullptr, int jop = 0) {
+template <int BITS, int GS, bool F16, int CH, int PF, int MT>
+__device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
     using C = Cfg<BITS, GS>;
     constexpr int XR = 8 * MT;  // rows of x sums per group in LDS
     static_assert(CH == 1 || CH * C::GPS == 8, "chunk = one super-step or 8 groups");
@@ -896,23 +798,15 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg,
     const int q = lane >> 4;  // lane group: k slot for A/B, row block for the result
     const int n = lane & 15;  // B column / A row / result column
 
-    /* a chain op may use fewer workgroups than the launch has: the rest hold empty ranges */
-    const bool idle = wg >= p.nkb * p.Gkb;
-    const int kb = idle ? 0 : wg / p.Gkb;
-    const int cl = idle ? 0 : wg - kb * p.Gkb;
+    const int kb = wg / p.Gkb;          // the launch has nkb * Gkb workgroups
+    const int cl = wg - kb * p.Gkb;
     const KBlock kbk = kblock(p, kb);
     const int SS = kbk.SS;    // chunks per tile in this k-block
-    const int a = idle ? 0 : wg_start(cl, kbk.base, kbk.rem);
-    const int b = idle ? 0 : wg_start(cl + 1, kbk.base, kbk.rem);
+    const int a = wg_start(cl, kbk.base, kbk.rem);
+    const int b = wg_start(cl + 1, kbk.base, kbk.rem);
 
     if (wave == kWaves) {
-        if constexpr (CHAIN) {
-            publisher_wave<F16, MT, true>(p, kb, cl, a, b, SS, kbk.base, kbk.rem, lane, chain_err(*cp),
-                                    cp->timeout);
-            chain_publisher_done(*cp, jop, wg);
-        } else {
-            publisher_wave<F16, MT>(p, kb, cl, a, b, SS, kbk.base, kbk.rem, lane);
-        }
+        publisher_wave<F16, MT>(p, kb, cl, a, b, SS, kbk.base, kbk.rem, lane, wg);
         return;
     }
 
@@ -955,8 +849,8 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg,
         }
         __builtin_amdgcn_sched_barrier(0);
     };
-    /* alone, x goes out before the split's scalar arithmetic, which overlaps its latency */
-    if constexpr (!CHAIN) stage_loads();
+    /* x goes out before the split's scalar arithmetic, which overlaps its latency */
+    stage_loads();
 
     /* ---- units of this workgroup, in the order its waves take them: the tile it shares
      * with the next workgroup first ([s1, b)), then the rest from a (which starts with the
@@ -1029,10 +923,10 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg,
      * a multiple of GS/8) and are summed with DPP.  Lanes past the last item rewrite the
      * last item with its own value; only the group sums need a mask. */
     const bool leader = (tid & (GS / 8 - 1)) == 0;
-    auto stage_finish = [&](bool with_items) {
+    auto stage_finish = [&]() {
 #pragma unroll
     for (int i = 0; i < kMaxStageItems; ++i) {
-        if (with_items && i * kThreads < items) {
+        if (i * kThreads < items) {
             float sm = chunk_dot<F16>(xv[i], 0.0f);
             sm += dpp_f32<0xB1>(sm);             // lanes ^1 (quad_perm 1,0,3,2)
             sm += dpp_f32<0x4E>(sm);             // lanes ^2 (quad_perm 2,3,0,1)
@@ -1058,19 +952,9 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg,
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    if constexpr (CHAIN) {
-        /* the weights do not depend on the previous op: fetch them, then wait for its
-         * output (this workgroup's LDS is free once every publisher has counted) */
-        issue_first();
-        chain_prev<F16>(*cp, jop, wg);
-        if (L > 0) stage_loads();
-        chain_lds_free(*cp, jop);
-        stage_finish(L > 0);
-    } else {
-        /* x first (issued above): issued after the weights, its wait would cover them */
-        stage_finish(true);
-        issue_first();
-    }
+    /* x first (issued above): issued after the weights, its wait would cover them */
+    stage_finish();
+    issue_first();
     __syncthreads();
 
     /* ---- per-lane A / x-sum addresses.  Up to 8 rows: the A operand is block-diagonal,
@@ -1209,21 +1093,9 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg,
          * released (never, when the range fits the ring) */
         const int sl = g % R;
         if (L > R) {
-            uint64_t deadline = 0;
             while ((int)__hip_atomic_load(gen + sl, __ATOMIC_ACQUIRE,
-                                          __HIP_MEMORY_SCOPE_WORKGROUP) != g) {
-                if constexpr (CHAIN) {
-                    /* bounded in a chain, where a failed wait elsewhere can re-arm LDS */
-                    if (!deadline) deadline = __builtin_amdgcn_s_memrealtime() + cp->timeout;
-                    if (__builtin_amdgcn_s_memrealtime() > deadline) {
-                        if (lane == 0)
-                            __hip_atomic_store(chain_err(*cp), 1u, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-                        break;
-                    }
-                }
+                                          __HIP_MEMORY_SCOPE_WORKGROUP) != g)
                 __builtin_amdgcn_s_sleep(1);
-            }
         }
         if (lane < 32 * MT) *(f32x4_t*)(part + sl * (MT * 128) + tile_off(lane)) = v;
         /* arrive at tile t; the wave that completes its units here sums them (in unit order)
@@ -1372,9 +1244,41 @@ extern "C" __global__ void __launch_bounds__(256) dfq_fill_u32(uint32_t* ptr, ui
         ptr[i] = v;
 }
 
+/* The read ceiling: a plain streaming read of `units` 4 KB blocks, the best single-launch
+ * read this memory system does with nothing else in the kernel.  Every wave streams a
+ * contiguous range of blocks, one block (four 16-byte loads a lane, 1 KB per instruction) in
+ * flight, and XORs what it read into one word per wave (sink[8 * blockIdx.x + wave]) so that
+ * no load is dead.  Past its last block a wave re-reads that block (an L2 hit), so every
+ * pass of the loop has the same loads in flight. */
+extern "C" __global__ void __launch_bounds__(512) dfq_read_stream(const u32x4_t* src,
+                                                                  uint64_t units,
+                                                                  uint32_t* sink) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t nw = (uint64_t)gridDim.x * 8, gw = (uint64_t)blockIdx.x * 8 + wave;
+    const uint64_t base = units / nw, rem = units % nw;
+    const uint64_t a = gw * base + (gw < rem ? gw : rem), b = a + base + (gw < rem ? 1 : 0);
+    u32x4_t acc = {0u, 0u, 0u, 0u};
+    if (a < b) {
+        u32x4_t buf[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) buf[j] = src[a * 256 + j * 64 + lane];
+        for (uint64_t u = a; u < b; ++u) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc ^= buf[j];
+            const uint64_t nu = (u + 1 < b) ? u + 1 : u;
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) buf[j] = src[nu * 256 + j * 64 + lane];
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    const uint32_t v = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+    if (lane == 0) sink[gw] = v;
+}
+
 /* h[m][n] = silu(g) * u with g = gu[m][n], u = gu[m][N + n] (gu row pitch 2N), in fp32,
  * rounded once to the output dtype. */
-template <bool F16, bool COH = false>
+template <bool F16>
 __device__ __forceinline__ void silu_mul(const uint16_t* gu, uint16_t* h, int M, int N,
                                          int64_t first, int64_t stride) {
     const int64_t total = (int64_t)M * N;
@@ -1382,7 +1286,7 @@ __device__ __forceinline__ void silu_mul(const uint16_t* gu, uint16_t* h, int M,
         const int64_t m = i / N, n = i - m * N;
         const float g = elem_to_f32<F16>(gu[m * 2 * N + n]);
         const float u = elem_to_f32<F16>(gu[m * 2 * N + N + n]);
-        put16<COH>(h + i, silu_mul_round<F16>(g, u));
+        put16(h + i, silu_mul_round<F16>(g, u));
     }
 }
 extern "C" __global__ void __launch_bounds__(256) dfq_silu_mul_bf16(const uint16_t* gu,
@@ -1408,23 +1312,6 @@ extern "C" __global__ void __launch_bounds__(256) dfq_silu_mul_f16(const uint16_
  * multiple of 8); other rows take 2-byte loads, four in flight.  Keys are only touched by
  * agent-scope atomics, so a block's max is visible to the last block once it has completed
  * (vmcnt) before the block's relaxed counter increment: no cache write-back or invalidate. */
-__device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
-    const uint32_t b = __float_as_uint(v);
-    const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    return ((uint64_t)o << 32) | (uint32_t)~(uint32_t)idx;
-}
-
-__device__ __forceinline__ uint64_t max_key_wave(uint64_t k) {
-#pragma unroll
-    for (int s = 32; s > 0; s >>= 1) {
-        const uint32_t lo = __shfl_xor((uint32_t)k, s, 64);
-        const uint32_t hi = __shfl_xor((uint32_t)(k >> 32), s, 64);
-        const uint64_t o = ((uint64_t)hi << 32) | lo;
-        k = o > k ? o : k;
-    }
-    return k;
-}
-
 template <bool F16>
 __device__ __forceinline__ void argmax_accept(const uint16_t* logits, int M, int V,
                                               const int32_t* proposals, int32_t* tokens,
@@ -1556,61 +1443,3 @@ DFQ_MT8_FORMAT(4, 128, true, f16)
 DFQ_MT8_FORMAT(8, 32, true, f16)
 DFQ_MT8_FORMAT(8, 64, true, f16)
 DFQ_MT8_FORMAT(8, 128, true, f16)
-
-/* ---- the chain kernel: a list of ops in one launch (see the synchronisation notes above).
- * One workgroup per CU, G = gridDim.x.  Op kinds: 0 a qmm (8-group chunks, up to 8 rows),
- * 1 silu_mul with x = gu [M][2N] and y = h [M][N]. */
-template <int BITS, int GS, bool F16>
-__device__ __forceinline__ void qmm_chain(const ChainParams& cp) {
-    constexpr int CH = 8 / Cfg<BITS, GS>::GPS;
-    constexpr int PF = prefetch_depth<BITS, GS, CH>();
-    const int wg = blockIdx.x, tid = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    if (tid == 0) {
-        uint32_t* lf = chain_lds(cp);
-        for (int i = 0; i < 5; ++i) lf[i] = 0u;
-        /* this launch's epoch (ordered before any use by op 0's staging barrier; an op-0
-         * elementwise op is refused by the runtime) */
-        lf[5] = __hip_atomic_load(cp.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    for (int j = 0; j < cp.n_ops; ++j) {
-        const ChainOp op = chain_ops(cp)[j];
-        if (op.kind == 0) {
-            qmm_mt8<BITS, GS, F16, CH, PF, 1, true>(op.p, wg, &cp, j);
-        } else if (wave < kWaves) {
-            chain_prev<F16>(cp, j, wg);
-            silu_mul<F16, true>((const uint16_t*)op.p.x, (uint16_t*)op.p.y, op.p.M, op.p.N,
-                          (int64_t)wg * kThreads + tid, (int64_t)cp.G * kThreads);
-            chain_waves_done(cp, 2 * j, 3, wg, false);
-        } else if ((tid & 63) == 0) {
-            /* the publisher has nothing to do in an elementwise op: it is done with op j */
-            __hip_atomic_store(chain_lds(cp) + 4, (uint32_t)(j + 1), __ATOMIC_RELEASE,
-                               __HIP_MEMORY_SCOPE_WORKGROUP);
-        }
-    }
-    if (wave == kWaves) return;
-    /* the end: wait for the last op (and run its second pass); the last streaming wave of
-     * the launch to get here re-arms every counter to zero (all others have passed every
-     * wait by then) */
-    chain_prev<F16>(cp, cp.n_ops, wg);
-    /* the end: the last arrival raises the launch epoch */
-    chain_waves_done(cp, 2 * cp.n_ops, 2, wg, true);
-}
-
-#define DFQ_CHAIN_KERNEL(BITS, GS, F16, NAME)                                                  \
-    extern "C" __global__ void __launch_bounds__(kBlock)                                     \
-        dfq_chain_b##BITS##_g##GS##_##NAME(ChainParams cp) {                                  \
-        qmm_chain<BITS, GS, F16>(cp);                                                        \
-    }
-DFQ_CHAIN_KERNEL(4, 32, false, bf16)
-DFQ_CHAIN_KERNEL(4, 64, false, bf16)
-DFQ_CHAIN_KERNEL(4, 128, false, bf16)
-DFQ_CHAIN_KERNEL(8, 32, false, bf16)
-DFQ_CHAIN_KERNEL(8, 64, false, bf16)
-DFQ_CHAIN_KERNEL(8, 128, false, bf16)
-DFQ_CHAIN_KERNEL(4, 32, true, f16)
-DFQ_CHAIN_KERNEL(4, 64, true, f16)
-DFQ_CHAIN_KERNEL(4, 128, true, f16)
-DFQ_CHAIN_KERNEL(8, 32, true, f16)
-DFQ_CHAIN_KERNEL(8, 64, true, f16)
-DFQ_CHAIN_KERNEL(8, 128, true, f16)

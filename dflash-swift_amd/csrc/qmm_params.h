@@ -59,26 +59,15 @@ typedef struct QmmParams {
     int32_t ring;           /* partial-tile slots in LDS (a ring over the take order) */
     uint32_t w_bytes;       /* size of w in bytes (< 2^31)                            */
     uint32_t s_bytes;       /* size of scales (= size of biases) in bytes             */
+    /* greedy-accept mode (am_keys != NULL; splits without a second pass only): every
+     * finished output also folds (its rounded value, its column) into its row's 64-bit key,
+     * the last workgroup turns the keys into tokens and the accepted run; y may be NULL */
+    uint64_t* am_keys;      /* [16][M] keys, one row of M per workgroup group; zero at rest */
+    uint32_t* am_count;     /* 17 arrival counters, 32 words apart; zero at rest            */
+    const int32_t* am_proposals;  /* [M-1] or NULL                                         */
+    int32_t* am_tokens;     /* [M] or NULL                                                  */
+    int32_t* am_accepted;   /* [1] or NULL                                                  */
 } QmmParams;
-
-/* One op of a chain (dfq_chain): kind 0 is a qmm as above (its workspace fields point into
- * the chain's workspace); kind 1 is silu_mul with x = gu [M][2N], y = h [M][N]. */
-typedef struct ChainOp {
-    QmmParams p;
-    int32_t kind;
-    int32_t independent;    /* 1: wait for op j-2 instead of op j-1 (see dfq_chain_op)  */
-} ChainOp;
-
-/* The chain kernel's argument. */
-typedef struct ChainParams {
-    const ChainOp* ops;     /* [n_ops], device memory                                  */
-    uint32_t* sync;         /* launch epoch, error flag and the completion blocks of
-                               the ops (see the chain kernel); zero when created        */
-    int32_t n_ops;
-    int32_t G;              /* workgroups in the launch (one per CU)                   */
-    int32_t lds_flag_off;   /* byte offset of the two wait flags in LDS                */
-    uint32_t timeout;       /* s_memrealtime ticks (100 MHz) a wait may last           */
-} ChainParams;
 
 /* Parameters of the generic (stock-op stand-in) kernel. */
 typedef struct QmmGenericParams {

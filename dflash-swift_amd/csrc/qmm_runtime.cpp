@@ -84,24 +84,9 @@ struct dfq_ctx {
     hipFunction_t argmax_accept[2] = {}; // greedy accept of a verify pass [bf16/f16]
     hipFunction_t generic = nullptr;
     hipFunction_t fill = nullptr;
-    hipFunction_t chain[2][3][2] = {};   // the chain kernel [bits][gs][bf16/f16]
+    hipFunction_t read_stream = nullptr; // the plain streaming read (bandwidth reference)
     std::mutex mu;
     std::unordered_map<PlanKey, dfq::Plan, PlanKeyHash> plans;
-};
-
-struct dfq_chain {
-    dfq_ctx* ctx = nullptr;
-    hipFunction_t fn = nullptr;
-    ChainOp* ops = nullptr;    // device
-    uint32_t* sync = nullptr;  // device, [2*n_ops + 2]
-    void* ws = nullptr;        // device workspace of the qmm ops
-    size_t ws_bytes = 0;
-    int n_ops = 0;
-    int G = 0;
-    int lds_bytes = 0;
-    int lds_flag_off = 0;
-    size_t sync_bytes = 0;
-    uint32_t timeout = 100000000u;  // 1 s of s_memrealtime ticks
 };
 
 struct dfq_graph {
@@ -261,22 +246,27 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
     return false;
 }
 
-/* The cached split for a shape; a shape with none is cached too (T == 0). */
-static bool find_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, Plan* out) {
+/* The split for a shape, from the context's cache; a shape with none is cached too (T == 0).
+ * cache = false (the no-allocation path) computes a missing split without storing it. */
+static bool find_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, Plan* out,
+                      bool cache = true) {
     PlanKey key{M, N, K, bits, gs};
     std::lock_guard<std::mutex> lk(ctx->mu);
     auto it = ctx->plans.find(key);
-    if (it == ctx->plans.end()) {
+    if (it != ctx->plans.end()) {
+        *out = it->second;
+    } else {
         Plan p;
         if (!make_plan(M, N, K, bits, gs, ctx->num_cus, ctx->lds_max, &p)) p = Plan{};
-        it = ctx->plans.emplace(key, p).first;
+        if (cache) ctx->plans.emplace(key, p);
+        *out = p;
     }
-    *out = it->second;
     return out->T > 0;
 }
 
-static dfq_status get_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, Plan* out) {
-    if (!find_plan(ctx, M, N, K, bits, gs, out))
+static dfq_status get_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, Plan* out,
+                           bool cache = true) {
+    if (!find_plan(ctx, M, N, K, bits, gs, out, cache))
         return fail(DFQ_ERR_UNSUPPORTED, "no work split for M=%d N=%d K=%d bits=%d gs=%d", M, N,
                     K, bits, gs);
     return DFQ_OK;
@@ -284,9 +274,9 @@ static dfq_status get_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, 
 
 /* 9..16 rows run in one launch with two row tiles when the shape has such a split, else as
  * two launches of up to 8 rows over the same weights. */
-static bool one_pass(dfq_ctx* ctx, int M, int N, int K, int bits, int gs) {
+static bool one_pass(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, bool cache = true) {
     Plan p;
-    return M <= 8 || find_plan(ctx, M, N, K, bits, gs, &p);
+    return M <= 8 || find_plan(ctx, M, N, K, bits, gs, &p, cache);
 }
 
 static bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
@@ -381,14 +371,6 @@ dfq_status dfq_init(int device, dfq_ctx** out) {
                         delete ctx;
                         return hip_fail(e, name);
                     }
-                    snprintf(name, sizeof name, "dfq_chain_b%d_g%d_%s", kBits[b], kGs[g2],
-                             kDt[d]);
-                    if ((e = hipModuleGetFunction(&ctx->chain[b][g2][d], ctx->module, name)) !=
-                        hipSuccess) {
-                        (void)hipModuleUnload(ctx->module);
-                        delete ctx;
-                        return hip_fail(e, name);
-                    }
                 }
     if ((e = hipModuleGetFunction(&ctx->generic, ctx->module, "dfq_qmm_generic")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->reduce[0], ctx->module, "dfq_qmm_reduce_bf16")) != hipSuccess ||
@@ -397,7 +379,8 @@ dfq_status dfq_init(int device, dfq_ctx** out) {
         (e = hipModuleGetFunction(&ctx->silu_mul[1], ctx->module, "dfq_silu_mul_f16")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->argmax_accept[0], ctx->module, "dfq_argmax_accept_bf16")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->argmax_accept[1], ctx->module, "dfq_argmax_accept_f16")) != hipSuccess ||
-        (e = hipModuleGetFunction(&ctx->fill, ctx->module, "dfq_fill_u32")) != hipSuccess) {
+        (e = hipModuleGetFunction(&ctx->fill, ctx->module, "dfq_fill_u32")) != hipSuccess ||
+        (e = hipModuleGetFunction(&ctx->read_stream, ctx->module, "dfq_read_stream")) != hipSuccess) {
         (void)hipModuleUnload(ctx->module);
         delete ctx;
         return hip_fail(e, "hipModuleGetFunction");
@@ -505,23 +488,30 @@ int dfq_qmm_supported(const dfq_ctx* ctx, int M, int N, int K, int bits, int gs,
 
 /* ---- the matmul ----------------------------------------------------------------------- */
 
+/* Workspace of a checked shape: one launch's, or the larger of the two row passes'. */
+static dfq_status workspace_need(dfq_ctx* ctx, int M, int N, int K, int bits, int gs,
+                                 bool cache, size_t* bytes) {
+    dfq_status s;
+    Plan p;
+    if (one_pass(ctx, M, N, K, bits, gs, cache)) {
+        if ((s = get_plan(ctx, M, N, K, bits, gs, &p, cache))) return s;
+        *bytes = p.ws_bytes;
+        return DFQ_OK;
+    }
+    if ((s = get_plan(ctx, 8, N, K, bits, gs, &p, cache))) return s;
+    size_t need = p.ws_bytes;
+    if ((s = get_plan(ctx, M - 8, N, K, bits, gs, &p, cache))) return s;
+    *bytes = std::max(need, p.ws_bytes);
+    return DFQ_OK;
+}
+
 dfq_status dfq_qmm_workspace_bytes(dfq_ctx* ctx, int M, int N, int K, int bits, int gs,
                                    size_t* bytes) {
     if (!bytes) return fail(DFQ_ERR_INVALID_ARGUMENT, "null bytes");
     *bytes = 0;
     dfq_status s = check_fast_args(ctx, M, N, K, bits, gs, DFQ_BF16, DFQ_BF16, DFQ_BF16);
     if (s) return s;
-    Plan p;
-    if (one_pass(ctx, M, N, K, bits, gs)) {
-        if ((s = get_plan(ctx, M, N, K, bits, gs, &p))) return s;
-        *bytes = p.ws_bytes;
-        return DFQ_OK;
-    }
-    if ((s = get_plan(ctx, 8, N, K, bits, gs, &p))) return s;
-    size_t need = p.ws_bytes;
-    if ((s = get_plan(ctx, M - 8, N, K, bits, gs, &p))) return s;
-    *bytes = std::max(need, p.ws_bytes);
-    return DFQ_OK;
+    return workspace_need(ctx, M, N, K, bits, gs, true, bytes);
 }
 
 dfq_status dfq_workspace_clear(dfq_ctx* ctx, void* ws, size_t bytes, void* stream) {
@@ -574,13 +564,25 @@ static QmmParams fill_params(const Plan& pl, const void* x, const uint32_t* w,
     return p;
 }
 
+/* The greedy-accept block of a fused LM-head launch (see dfq_qmm_argmax_accept). */
+struct AcceptArgs {
+    uint64_t* keys = nullptr;
+    uint32_t* count = nullptr;
+    const int32_t* proposals = nullptr;
+    int32_t* tokens = nullptr;
+    int32_t* accepted = nullptr;
+};
+
 static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
                              const void* biases, const void* lbias, void* y, int M, int N, int K,
                              int bits, int gs, dfq_dtype dt, void* ws, size_t wsb,
-                             hipStream_t stream, int epi = 0) {
+                             hipStream_t stream, int epi = 0, bool cache = true,
+                             const AcceptArgs* acc = nullptr) {
     Plan pl;
-    dfq_status s = get_plan(ctx, M, N, K, bits, gs, &pl);
+    dfq_status s = get_plan(ctx, M, N, K, bits, gs, &pl, cache);
     if (s) return s;
+    if (acc && (pl.reduce || epi))
+        return fail(DFQ_ERR_STATE, "greedy-accept mode needs a split without a second pass");
     if (pl.need_ws) {
         if (!ws || wsb < pl.ws_bytes)
             return fail(DFQ_ERR_WORKSPACE, "workspace of %zu bytes needed (got %zu)", pl.ws_bytes,
@@ -589,6 +591,13 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
     }
     QmmParams p = fill_params(pl, x, w, scales, biases, lbias, y, M, N, K, bits, gs, ws);
     p.epi = epi;
+    if (acc) {
+        p.am_keys = acc->keys;
+        p.am_count = acc->count;
+        p.am_proposals = acc->proposals;
+        p.am_tokens = acc->tokens;
+        p.am_accepted = acc->accepted;
+    }
     const int bi = bits == 4 ? 0 : 1;
     const int gi = gs == 32 ? 0 : gs == 64 ? 1 : 2;
     const int di = dt == DFQ_BF16 ? 0 : 1;
@@ -610,7 +619,7 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
 static dfq_status qmm_any(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
                           const void* biases, const void* lbias, void* y, int M, int N, int K,
                           int bits, int gs, dfq_dtype xdt, dfq_dtype sdt, dfq_dtype ydt, void* ws,
-                          size_t wsb, void* stream, int epi);
+                          size_t wsb, void* stream, int epi, bool cache = true);
 
 dfq_status dfq_qmm(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
                    const void* biases, const void* lbias, void* y, int M, int N, int K, int bits,
@@ -650,7 +659,7 @@ dfq_status dfq_interleave_gate_up(dfq_ctx* ctx, const void* gate, const void* up
 static dfq_status qmm_any(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
                           const void* biases, const void* lbias, void* y, int M, int N, int K,
                           int bits, int gs, dfq_dtype xdt, dfq_dtype sdt, dfq_dtype ydt, void* ws,
-                          size_t wsb, void* stream, int epi) {
+                          size_t wsb, void* stream, int epi, bool cache) {
     dfq_status s = check_fast_args(ctx, M, N, K, bits, gs, xdt, sdt, ydt);
     if (s) return s;
     if (!x || !w || !scales || !biases || !y)
@@ -661,16 +670,16 @@ static dfq_status qmm_any(dfq_ctx* ctx, const void* x, const uint32_t* w, const 
                     "x and w must be 16-byte aligned, scales/biases 4-byte aligned");
     DeviceGuard g(ctx->device);
     const size_t esz = 2;
-    if (one_pass(ctx, M, N, K, bits, gs))
+    if (one_pass(ctx, M, N, K, bits, gs, cache))
         return launch_mt8(ctx, x, w, scales, biases, lbias, y, M, N, K, bits, gs, xdt, ws, wsb,
-                          (hipStream_t)stream, epi);
+                          (hipStream_t)stream, epi, cache);
     /* 9..16 rows with one-super-step chunks: two passes of up to 8 rows over the weights. */
     const size_t ypitch = (size_t)(epi ? N / 2 : N) * esz;
     for (int m0 = 0; m0 < M; m0 += 8) {
         const int mc = std::min(8, M - m0);
         s = launch_mt8(ctx, (const char*)x + (size_t)m0 * K * esz, w, scales, biases, lbias,
                        (char*)y + (size_t)m0 * ypitch, mc, N, K, bits, gs, xdt, ws, wsb,
-                       (hipStream_t)stream, epi);
+                       (hipStream_t)stream, epi, cache);
         if (s) return s;
     }
     return DFQ_OK;
@@ -729,6 +738,82 @@ dfq_status dfq_argmax_accept(dfq_ctx* ctx, const void* logits, int M, int V, dfq
                                          (unsigned)(M * per_row), 1, 1, 256, 1, 1, 0,
                                          (hipStream_t)stream, args, nullptr);
     return e == hipSuccess ? DFQ_OK : hip_fail(e, "launch dfq_argmax_accept");
+}
+
+/* Workspace of dfq_qmm_argmax_accept: the qmm's, then the keys ([16][M] x 8 bytes) and 17
+ * arrival counters on 128-byte lines, then, for a split with a second pass, room for the
+ * logits. */
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+static constexpr size_t kAcceptCountBytes = 17 * 128;
+
+static dfq_status qmm_accept_layout(dfq_ctx* ctx, int M, int V, int K, int bits, int gs,
+                                    bool* fused, size_t* qmm_ws, size_t* total) {
+    dfq_status s = check_fast_args(ctx, M, V, K, bits, gs, DFQ_BF16, DFQ_BF16, DFQ_BF16);
+    if (s) return s;
+    size_t need = 0;
+    if ((s = workspace_need(ctx, M, V, K, bits, gs, true, &need))) return s;
+    Plan pl;
+    *fused = one_pass(ctx, M, V, K, bits, gs) && get_plan(ctx, M, V, K, bits, gs, &pl) == DFQ_OK &&
+             !pl.reduce;
+    *qmm_ws = align256(need);
+    *total = *qmm_ws + align256((size_t)16 * M * 8) + align256(kAcceptCountBytes);
+    if (!*fused) *total += align256((size_t)M * V * 2);
+    return DFQ_OK;
+}
+
+dfq_status dfq_qmm_argmax_accept_workspace_bytes(dfq_ctx* ctx, int M, int V, int K, int bits,
+                                                 int gs, size_t* bytes) {
+    if (!bytes) return fail(DFQ_ERR_INVALID_ARGUMENT, "null bytes");
+    *bytes = 0;
+    bool fused;
+    size_t qws;
+    return qmm_accept_layout(ctx, M, V, K, bits, gs, &fused, &qws, bytes);
+}
+
+dfq_status dfq_qmm_argmax_accept(dfq_ctx* ctx, const void* x, const uint32_t* w,
+                                 const void* scales, const void* biases, const void* lbias,
+                                 void* logits, int M, int V, int K, int bits, int gs,
+                                 dfq_dtype dt, const int32_t* proposals, int32_t* tokens,
+                                 int32_t* accepted, void* ws, size_t wsb, void* stream) {
+    dfq_status s = check_fast_args(ctx, M, V, K, bits, gs, dt, dt, dt);
+    if (s) return s;
+    if (!x || !w || !scales || !biases)
+        return fail(DFQ_ERR_INVALID_ARGUMENT, "null x, w, scales or biases");
+    if (!aligned(x, 16) || !aligned(w, 16) || !aligned(scales, 4) || !aligned(biases, 4) ||
+        (logits && !aligned(logits, 2)) || (lbias && !aligned(lbias, 2)))
+        return fail(DFQ_ERR_INVALID_ARGUMENT,
+                    "x and w must be 16-byte aligned, scales/biases 4-byte aligned");
+    bool fused;
+    size_t qws, total;
+    if ((s = qmm_accept_layout(ctx, M, V, K, bits, gs, &fused, &qws, &total))) return s;
+    if (!ws || wsb < total)
+        return fail(DFQ_ERR_WORKSPACE, "workspace of %zu bytes needed (got %zu)", total,
+                    ws ? wsb : (size_t)0);
+    if (!aligned(ws, 256)) return fail(DFQ_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+    DeviceGuard g(ctx->device);
+    char* base = (char*)ws;
+    uint64_t* keys = (uint64_t*)(base + qws);
+    uint32_t* count = (uint32_t*)(base + qws + align256((size_t)16 * M * 8));
+    if (fused) {
+        AcceptArgs acc;
+        acc.keys = keys;
+        acc.count = count;
+        acc.proposals = proposals;
+        acc.tokens = tokens;
+        acc.accepted = accepted;
+        return launch_mt8(ctx, x, w, scales, biases, lbias, logits, M, V, K, bits, gs, dt, ws,
+                          qws, (hipStream_t)stream, 0, true, &acc);
+    }
+    /* a split with a second pass: the logits first (to `logits` or the workspace), then the
+     * accept kernel over them, its keys and counter in the accept region */
+    void* lg = logits ? logits
+                      : (void*)(base + qws + align256((size_t)16 * M * 8) +
+                                align256(kAcceptCountBytes));
+    if ((s = qmm_any(ctx, x, w, scales, biases, lbias, lg, M, V, K, bits, gs, dt, dt, dt, ws,
+                     qws, stream, 0)))
+        return s;
+    return dfq_argmax_accept(ctx, lg, M, V, dt, proposals, tokens, accepted, keys,
+                             align256((size_t)16 * M * 8) + align256(kAcceptCountBytes), stream);
 }
 
 dfq_status dfq_qmm_fallback(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
@@ -836,6 +921,22 @@ dfq_status dfq_debug_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, i
     return DFQ_OK;
 }
 
+/* The bandwidth reference: one launch reading `bytes` (a multiple of 4096) from src as a plain
+ * streaming read, one workgroup of 8 waves per CU; sink receives 8 * dfq_num_cus words. */
+dfq_status dfq_debug_read_stream(dfq_ctx* ctx, const void* src, size_t bytes, uint32_t* sink,
+                                 void* stream) {
+    if (!ctx || !src || !sink) return fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
+    if (!bytes || bytes % 4096 || !aligned(src, 16))
+        return fail(DFQ_ERR_INVALID_ARGUMENT, "bytes must be a positive multiple of 4096, src 16-byte aligned");
+    DeviceGuard g(ctx->device);
+    const void* p = src;
+    uint64_t units = bytes / 4096;
+    void* args[] = {(void*)&p, &units, &sink};
+    hipError_t e = hipModuleLaunchKernel(ctx->read_stream, (unsigned)ctx->num_cus, 1, 1, 512, 1,
+                                         1, 0, (hipStream_t)stream, args, nullptr);
+    return e == hipSuccess ? DFQ_OK : hip_fail(e, "launch dfq_read_stream");
+}
+
 /* The same split computed without a device, for a given CU count and LDS limit. */
 dfq_status dfq_debug_make_plan(int M, int N, int K, int bits, int gs, int num_cus,
                                size_t lds_max, int* out13) {
@@ -847,176 +948,6 @@ dfq_status dfq_debug_make_plan(int M, int N, int K, int bits, int gs, int num_cu
                        p.lds_bytes, p.need_ws ? 1 : 0, p.ch, p.umax, p.chunks, p.reduce ? 1 : 0,
                        p.ring};
     std::memcpy(out13, v, sizeof v);
-    return DFQ_OK;
-}
-
-/* ---- chains: a list of ops in one persistent launch ----------------------------------- */
-
-static void chain_free(dfq_chain* ch) {
-    if (!ch) return;
-    if (ch->ctx) {
-        DeviceGuard g(ch->ctx->device);
-        if (ch->ops) (void)hipFree(ch->ops);
-        if (ch->sync) (void)hipFree(ch->sync);
-        if (ch->ws) (void)hipFree(ch->ws);
-    }
-    delete ch;
-}
-
-dfq_status dfq_chain_create(dfq_ctx* ctx, int M, int bits, int gs, dfq_dtype dtype,
-                            const dfq_chain_op* ops, int n_ops, dfq_chain** out) {
-    if (!ctx || !ops || !out) return fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
-    *out = nullptr;
-    if (n_ops < 1) return fail(DFQ_ERR_INVALID_ARGUMENT, "a chain needs at least one op");
-    if (M < 1 || M > 8) return fail(DFQ_ERR_UNSUPPORTED, "chains take 1..8 rows (got %d)", M);
-    if (dtype != DFQ_BF16 && dtype != DFQ_F16)
-        return fail(DFQ_ERR_UNSUPPORTED, "chains take bf16 or fp16");
-    if (ops[0].kind != DFQ_CHAIN_QMM) return fail(DFQ_ERR_INVALID_ARGUMENT, "op 0 must be a qmm");
-    const int G = ctx->num_cus;
-    std::vector<ChainOp> host(n_ops);
-    size_t ws_need = 0;
-    int need_max = 0;
-    for (int j = 0; j < n_ops; ++j) {
-        const dfq_chain_op& o = ops[j];
-        ChainOp& c = host[j];
-        std::memset(&c, 0, sizeof c);
-        if (!o.x || !o.y) return fail(DFQ_ERR_INVALID_ARGUMENT, "op %d: null x or y", j);
-        if (o.kind == DFQ_CHAIN_SILU_MUL) {
-            if (o.N < 1) return fail(DFQ_ERR_INVALID_ARGUMENT, "op %d: N must be positive", j);
-            if (!aligned(o.x, 2) || !aligned(o.y, 2))
-                return fail(DFQ_ERR_INVALID_ARGUMENT, "op %d: misaligned buffers", j);
-            c.kind = 1;
-            c.independent = (o.independent && j > 0 && !(host[j - 1].kind == 0 && host[j - 1].p.reduce)) ? 1 : 0;
-            c.p.x = o.x;
-            c.p.y = o.y;
-            c.p.M = M;
-            c.p.N = o.N;
-            continue;
-        }
-        if (o.kind != DFQ_CHAIN_QMM && o.kind != DFQ_CHAIN_QMM_SILU_GATE_UP)
-            return fail(DFQ_ERR_INVALID_ARGUMENT, "op %d: unknown kind", j);
-        if (o.kind == DFQ_CHAIN_QMM_SILU_GATE_UP && (o.N < 16 || o.N % 16))
-            return fail(DFQ_ERR_UNSUPPORTED, "op %d: gate|up epilogue needs N = 2H, H %% 8 == 0", j);
-        dfq_status st = check_fast_args(ctx, M, o.N, o.K, bits, gs, dtype, dtype, dtype);
-        if (st) return st;
-        if (!o.w || !o.scales || !o.biases)
-            return fail(DFQ_ERR_INVALID_ARGUMENT, "op %d: null w, scales or biases", j);
-        if (!aligned(o.x, 16) || !aligned(o.w, 16) || !aligned(o.scales, 4) ||
-            !aligned(o.biases, 4) || !aligned(o.y, 2) || (o.linear_bias && !aligned(o.linear_bias, 2)))
-            return fail(DFQ_ERR_INVALID_ARGUMENT, "op %d: misaligned buffers", j);
-        Plan pl;
-        if ((st = get_plan(ctx, M, o.N, o.K, bits, gs, &pl))) return st;
-        if (pl.ch == 1)
-            return fail(DFQ_ERR_UNSUPPORTED, "op %d: chains need K a multiple of 8 groups", j);
-        if (pl.nkb * pl.Gkb > G)
-            return fail(DFQ_ERR_UNSUPPORTED, "op %d: its split needs %d workgroups (%d CUs)", j,
-                        pl.nkb * pl.Gkb, G);
-        c.kind = 0;
-        c.p = fill_params(pl, o.x, o.w, o.scales, o.biases, o.linear_bias, o.y, M, o.N, o.K,
-                          bits, gs, nullptr);
-        c.p.epi = o.kind == DFQ_CHAIN_QMM_SILU_GATE_UP ? 1 : 0;
-        /* independent: not op 0, and not right after a reduce split (whose second pass runs
-         * at the start of the op after it) */
-        c.independent = (o.independent && j > 0 && !(host[j - 1].kind == 0 && host[j - 1].p.reduce)) ? 1 : 0;
-        ws_need = std::max(ws_need, pl.ws_bytes);
-        need_max = std::max(need_max, pl.lds_need);
-    }
-    auto* ch = new dfq_chain();
-    ch->ctx = ctx;
-    ch->n_ops = n_ops;
-    ch->G = G;
-    ch->lds_flag_off = (need_max + 15) & ~15;
-    /* lds_flag_off: 8 words of wait flags, gathering counters and epochs */
-    ch->lds_bytes = (int)std::max<size_t>((size_t)ch->lds_flag_off + 32, ctx->lds_max / 2 + 256);
-    if ((size_t)ch->lds_bytes > ctx->lds_max) {
-        delete ch;
-        return fail(DFQ_ERR_UNSUPPORTED, "chain needs %d bytes of LDS", ch->lds_flag_off + 32);
-    }
-    const int bi = bits == 4 ? 0 : 1, gi = gs == 32 ? 0 : gs == 64 ? 1 : 2;
-    ch->fn = ctx->chain[bi][gi][dtype == DFQ_BF16 ? 0 : 1];
-    DeviceGuard g(ctx->device);
-    hipError_t e = hipSuccess;
-    /* epoch and error lines, then (2 * n_ops + 1) blocks of 33 lines of 128 bytes */
-    const size_t sync_bytes = (size_t)(2 + (2 * n_ops + 1) * 33) * 128;
-    ch->sync_bytes = sync_bytes;
-    /* two workspace regions, by op parity: an independent op may start while the op before
-     * it still uses its region */
-    ws_need = (ws_need + 255) & ~(size_t)255;
-    ch->ws_bytes = 2 * ws_need;
-    if ((e = hipMalloc(&ch->ops, sizeof(ChainOp) * n_ops)) != hipSuccess ||
-        (e = hipMalloc(&ch->sync, sync_bytes)) != hipSuccess ||
-        (ws_need && (e = hipMalloc(&ch->ws, 2 * ws_need)) != hipSuccess)) {
-        chain_free(ch);
-        return hip_fail(e, "chain allocation");
-    }
-    /* every qmm op shares the one workspace: ops run one after another */
-    for (int j = 0; j < n_ops; ++j) {
-        if (host[j].kind != 0 || !ch->ws) continue;
-        Plan pl;
-        (void)get_plan(ctx, M, ops[j].N, ops[j].K, bits, gs, &pl);
-        if (pl.need_ws) {
-            char* region = (char*)ch->ws + (j % 2) * ws_need;
-            host[j].p.slots = (float*)region;
-        }
-    }
-    if ((e = hipMemcpy(ch->ops, host.data(), sizeof(ChainOp) * n_ops, hipMemcpyHostToDevice)) !=
-            hipSuccess ||
-        (e = hipMemset(ch->sync, 0, sync_bytes)) != hipSuccess ||
-        (ch->ws && (e = hipMemset(ch->ws, 0, 2 * ws_need)) != hipSuccess) ||
-        (e = hipDeviceSynchronize()) != hipSuccess) {
-        chain_free(ch);
-        return hip_fail(e, "chain set-up");
-    }
-    *out = ch;
-    return DFQ_OK;
-}
-
-dfq_status dfq_chain_launch(dfq_chain* ch, void* stream) {
-    if (!ch) return fail(DFQ_ERR_INVALID_ARGUMENT, "null chain");
-    DeviceGuard g(ch->ctx->device);
-    ChainParams cp{};
-    cp.ops = ch->ops;
-    cp.sync = ch->sync;
-    cp.n_ops = ch->n_ops;
-    cp.G = ch->G;
-    cp.lds_flag_off = ch->lds_flag_off;
-    cp.timeout = ch->timeout;
-    void* args[] = {&cp};
-    hipError_t e = hipModuleLaunchKernel(ch->fn, (unsigned)ch->G, 1, 1, kBlockThreads, 1, 1,
-                                         (unsigned)ch->lds_bytes, (hipStream_t)stream, args,
-                                         nullptr);
-    return e == hipSuccess ? DFQ_OK : hip_fail(e, "launch dfq_chain");
-}
-
-dfq_status dfq_chain_failed(dfq_chain* ch, int* failed) {
-    if (!ch || !failed) return fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
-    DeviceGuard g(ch->ctx->device);
-    uint32_t v = 0;
-    hipError_t e = hipDeviceSynchronize();
-    if (e == hipSuccess)
-        e = hipMemcpy(&v, ch->sync + 32, 4, hipMemcpyDeviceToHost);
-    if (e != hipSuccess) return hip_fail(e, "chain status");
-    *failed = v != 0;
-    return DFQ_OK;
-}
-
-dfq_status dfq_chain_reset(dfq_chain* ch, void* stream) {
-    if (!ch) return fail(DFQ_ERR_INVALID_ARGUMENT, "null chain");
-    /* a launch whose waits timed out may have left partial tiles (tagged pair words, slots)
-     * in the workspace: clear it too */
-    dfq_status st = dfq_workspace_clear(ch->ctx, ch->sync, ch->sync_bytes, stream);
-    if (st == DFQ_OK && ch->ws) st = dfq_workspace_clear(ch->ctx, ch->ws, ch->ws_bytes, stream);
-    return st;
-}
-
-dfq_status dfq_chain_set_timeout(dfq_chain* ch, uint32_t ticks) {
-    if (!ch) return fail(DFQ_ERR_INVALID_ARGUMENT, "null chain");
-    ch->timeout = ticks;
-    return DFQ_OK;
-}
-
-dfq_status dfq_chain_destroy(dfq_chain* ch) {
-    chain_free(ch);
     return DFQ_OK;
 }
 

@@ -75,17 +75,6 @@ class _LayerInfo(ctypes.Structure):
 _WANT_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_char_p, ctypes.c_void_p)
 
 
-class _ChainOp(ctypes.Structure):
-    _fields_ = [
-        ("kind", ctypes.c_int), ("x", ctypes.c_void_p), ("y", ctypes.c_void_p),
-        ("w", ctypes.c_void_p), ("scales", ctypes.c_void_p), ("biases", ctypes.c_void_p),
-        ("linear_bias", ctypes.c_void_p), ("N", ctypes.c_int), ("K", ctypes.c_int),
-        ("independent", ctypes.c_int),
-    ]
-
-
-CHAIN_QMM, CHAIN_SILU_MUL, CHAIN_QMM_SILU_GATE_UP = 0, 1, 2
-
 # safetensors dtype names in dfq_st_dtype order
 ST_DTYPES = ["BOOL", "U8", "I8", "I16", "U16", "F16", "BF16", "I32", "U32", "F32", "I64", "U64",
              "F64", "F8_E5M2", "F8_E4M3"]
@@ -121,6 +110,9 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         "dfq_silu_mul": ([P, P, P, I, I, I, P], I),
         "dfq_argmax_accept_workspace_bytes": ([I, ctypes.POINTER(S)], I),
         "dfq_argmax_accept": ([P, P, I, I, I, P, P, P, P, S, P], I),
+        "dfq_qmm_argmax_accept_workspace_bytes": ([P, I, I, I, I, I, Z], I),
+        "dfq_qmm_argmax_accept": ([P, P, P, P, P, P, P, I, I, I, I, I, I, P, P, P, P, S, P],
+                                  I),
         "dfq_graph_launch": ([P, P], I), "dfq_graph_destroy": ([P], I),
         "dfq_linear_create": ([P, ctypes.POINTER(_LinearDesc), PP], I),
         "dfq_small_m_linear_create": ([P, PP], I), "dfq_linear_destroy": ([P], I),
@@ -133,6 +125,7 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         "dfq_enable_small_m_quantized_matmul": ([P], I),
         "dfq_debug_plan": ([P, I, I, I, I, I, ctypes.POINTER(I)], I),
         "dfq_debug_make_plan": ([I, I, I, I, I, I, S, ctypes.POINTER(I)], I),
+        "dfq_debug_read_stream": ([P, P, S, P, P], I),
         "dfq_linear_describe": ([P, ctypes.POINTER(_LinearDesc)], I),
         "dfq_checkpoint_open": ([ctypes.c_char_p, PP], I), "dfq_checkpoint_close": ([P], I),
         "dfq_checkpoint_format": ([P], ctypes.c_char_p),
@@ -145,10 +138,6 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         "dfq_checkpoint_layer_count": ([P], I),
         "dfq_checkpoint_layer": ([P, I, ctypes.POINTER(_LayerInfo)], I),
         "dfq_checkpoint_load_model": ([P, P, P, _WANT_FN, P, P, ctypes.POINTER(I)], I),
-        "dfq_chain_create": ([P, I, I, I, I, ctypes.POINTER(_ChainOp), I, PP], I),
-        "dfq_chain_launch": ([P, P], I), "dfq_chain_failed": ([P, ctypes.POINTER(I)], I),
-        "dfq_chain_reset": ([P, P], I), "dfq_chain_set_timeout": ([P, ctypes.c_uint32], I),
-        "dfq_chain_destroy": ([P], I),
         "dfq_qmm_silu_gate_up": ([P, P, P, P, P, P, P, I, I, I, I, I, I, P, S, P], I),
         "dfq_interleave_gate_up": ([P, P, P, P, I, S, P], I),
     }
@@ -208,12 +197,16 @@ class Context:
         _check(self.lib.dfq_init(device, ctypes.byref(h)), "dfq_init")
         self.handle = h
         self.device = device
-        self._ws = None  # lazily grown torch workspace for the convenience calls
+        # lazily grown workspaces of the convenience calls, one per stream; a grown one
+        # replaces the old, which is kept (a graph or another stream may still hold it)
+        self._ws = {}
+        self._retired = []
 
     def close(self):
         if self.handle:
             self.lib.dfq_destroy(self.handle)
             self.handle = None
+        self._ws, self._retired = {}, []
 
     def __del__(self):
         try:
@@ -248,6 +241,12 @@ class Context:
                 "chunks", "reduce", "ring"]
         return dict(zip(keys, list(out)))
 
+    def read_stream(self, src, nbytes, sink, stream=None):
+        """One launch of the plain streaming read of nbytes of src (the bandwidth reference);
+        sink holds 8 * num_cus uint32."""
+        _check(self.lib.dfq_debug_read_stream(self.handle, _ptr(src), nbytes, _ptr(sink),
+                                              _stream(stream)), "dfq_debug_read_stream")
+
     def qmm_raw(self, x, w, scales, biases, y, M, N, K, bits, gs, xdt, sdt, ydt, lbias=None,
                 ws=None, ws_bytes=0, stream=None):
         _check(self.lib.dfq_qmm(self.handle, _ptr(x), _ptr(w), _ptr(scales), _ptr(biases),
@@ -261,15 +260,29 @@ class Context:
                                          xdt, sdt, ydt, _stream(stream)), "dfq_qmm_fallback")
 
     # ---- torch conveniences -------------------------------------------------------------
-    def workspace(self, nbytes: int):
-        """A zeroed device workspace of at least nbytes, owned by this context."""
+    def workspace(self, nbytes: int, stream=None):
+        """A device workspace of at least nbytes for calls on `stream`, owned by this context.
+
+        Each stream gets its own (calls on different streams would race on a shared one).
+        A new workspace is zero-filled on `stream` itself, so it is zero before any call
+        enqueued after it on that stream; every call leaves it zero again.  A workspace that
+        grows is replaced, and the old one is kept until the context closes, since earlier
+        work or a captured graph may still use its address.  The convenience calls are
+        therefore not capture-safe when they grow a workspace: pass `ws` explicitly to the
+        calls a graph captures."""
         import torch
         if nbytes == 0:
             return None
-        if self._ws is None or self._ws.numel() < nbytes:
-            self._ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8,
-                                   device=f"cuda:{self.device}")
-        return self._ws
+        key = _stream(stream)
+        ws = self._ws.get(key)
+        if ws is None or ws.numel() < nbytes:
+            if ws is not None:
+                self._retired.append(ws)
+            ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8,
+                             device=f"cuda:{self.device}")
+            self.workspace_clear(ws, ws.numel(), stream=key)
+            self._ws[key] = ws
+        return ws
 
     def qmm(self, x, w, scales, biases, bits, gs, lbias=None, out=None, ws=None, stream=None):
         """y = x @ dequant(w).T on the fast kernel; x [M,K], w [N,K*bits/32] int32/uint32."""
@@ -281,7 +294,7 @@ class Context:
             out = torch.empty((M, N), dtype=x.dtype, device=x.device)
         need = self.workspace_bytes(M, N, K, bits, gs)
         if ws is None:
-            ws = self.workspace(need)
+            ws = self.workspace(need, stream)
         self.qmm_raw(x, w, scales, biases, out, M, N, K, bits, gs, dt, dtype_code(scales), dt,
                      lbias=lbias, ws=ws, ws_bytes=(ws.numel() if ws is not None else 0),
                      stream=stream)
@@ -300,7 +313,7 @@ class Context:
             out = torch.empty((M, H), dtype=x.dtype, device=x.device)
         need = self.workspace_bytes(M, 2 * H, K, bits, gs)
         if ws is None:
-            ws = self.workspace(need)
+            ws = self.workspace(need, stream)
         _check(self.lib.dfq_qmm_silu_gate_up(
             self.handle, _ptr(x), _ptr(w_gu), _ptr(scales_gu), _ptr(biases_gu), _ptr(lbias),
             _ptr(out), M, H, K, bits, gs, dtype_code(x), _ptr(ws),
@@ -368,14 +381,36 @@ class Context:
                "dfq_argmax_accept")
         return tokens, accepted
 
-    # ---- graphs ---------------------------------------------------------------------------
-    def chain(self, M: int, bits: int, gs: int, ops: list, dtype=BF16) -> "Chain":
-        """A chain of ops run in one persistent launch.  Each op is a dict:
-        {"kind": "qmm", "x", "y", "w", "scales", "biases", "N", "K", optional "lbias"} or
-        {"kind": "silu_mul", "x": gu [M][2N], "y": h [M][N], "N"} (torch device tensors);
-        "independent": True marks an op that reads no output of the op just before it."""
-        return Chain(self, M, bits, gs, ops, dtype)
+    def qmm_argmax_accept_workspace_bytes(self, M, V, K, bits, gs) -> int:
+        b = ctypes.c_size_t()
+        _check(self.lib.dfq_qmm_argmax_accept_workspace_bytes(self.handle, M, V, K, bits, gs,
+                                                              ctypes.byref(b)),
+               "dfq_qmm_argmax_accept_workspace_bytes")
+        return b.value
 
+    def qmm_argmax_accept(self, x, w, scales, biases, bits, gs, proposals=None, lbias=None,
+                          logits=None, tokens=None, accepted=None, ws=None, stream=None):
+        """The LM head fused with the greedy accept: (tokens [M] int32, accepted [1] int32)
+        for x [M, K] against w [V, K*bits/32]; logits [M, V] are written only when given."""
+        import torch
+        M, K = x.shape
+        V = w.shape[0]
+        dev = x.device
+        if tokens is None:
+            tokens = torch.empty(M, dtype=torch.int32, device=dev)
+        if accepted is None:
+            accepted = torch.empty(1, dtype=torch.int32, device=dev)
+        if ws is None:
+            need = self.qmm_argmax_accept_workspace_bytes(M, V, K, bits, gs)
+            ws = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+            self.workspace_clear(ws, ws.numel(), stream=stream)
+        _check(self.lib.dfq_qmm_argmax_accept(
+            self.handle, _ptr(x), _ptr(w), _ptr(scales), _ptr(biases), _ptr(lbias),
+            _ptr(logits), M, V, K, bits, gs, dtype_code(x), _ptr(proposals), _ptr(tokens),
+            _ptr(accepted), _ptr(ws), ws.numel(), _stream(stream)), "dfq_qmm_argmax_accept")
+        return tokens, accepted
+
+    # ---- graphs ---------------------------------------------------------------------------
     def graph_begin(self, stream):
         _check(self.lib.dfq_graph_begin(self.handle, _stream(stream)), "dfq_graph_begin")
 
@@ -481,7 +516,7 @@ class QuantizedLinear:
         nb = ctypes.c_size_t()
         _check(self.lib.dfq_linear_workspace_bytes(self._h, rows, ctypes.byref(nb)),
                "dfq_linear_workspace_bytes")
-        ws = self.ctx.workspace(nb.value)
+        ws = self.ctx.workspace(nb.value, stream)
         took = ctypes.c_int(0)
         _check(self.lib.dfq_linear_forward(
             self._h, _ptr(flat), dtype_code(x), rows, _ptr(y), _ptr(ws),
@@ -696,54 +731,5 @@ class Checkpoint:
             if self._h:
                 self.lib.dfq_checkpoint_close(self._h)
                 self._h = None
-        except Exception:
-            pass
-
-
-class Chain:
-    """dfq_chain: a fixed list of ops on fixed buffers, launched as one kernel."""
-
-    def __init__(self, ctx: Context, M, bits, gs, ops, dtype=BF16):
-        self.lib, self.ctx = ctx.lib, ctx
-        self._keep = ops  # the buffers must outlive the chain
-        arr = (_ChainOp * len(ops))()
-        for i, o in enumerate(ops):
-            if o["kind"] in ("qmm", "qmm_silu_gate_up"):
-                kind = CHAIN_QMM if o["kind"] == "qmm" else CHAIN_QMM_SILU_GATE_UP
-                arr[i] = _ChainOp(kind, _ptr(o["x"]), _ptr(o["y"]), _ptr(o["w"]),
-                                  _ptr(o["scales"]), _ptr(o["biases"]), _ptr(o.get("lbias")),
-                                  o["N"], o["K"], int(bool(o.get("independent"))))
-            elif o["kind"] == "silu_mul":
-                arr[i] = _ChainOp(CHAIN_SILU_MUL, _ptr(o["x"]), _ptr(o["y"]), None, None, None,
-                                  None, o["N"], 0, int(bool(o.get("independent"))))
-            else:
-                raise ValueError(o["kind"])
-        h = ctypes.c_void_p()
-        _check(self.lib.dfq_chain_create(ctx.handle, M, bits, gs, dtype, arr, len(ops),
-                                         ctypes.byref(h)), "dfq_chain_create")
-        self._h = h
-
-    def launch(self, stream=None):
-        _check(self.lib.dfq_chain_launch(self._h, _stream(stream)), "dfq_chain_launch")
-
-    def failed(self) -> bool:
-        f = ctypes.c_int(0)
-        _check(self.lib.dfq_chain_failed(self._h, ctypes.byref(f)), "dfq_chain_failed")
-        return bool(f.value)
-
-    def reset(self, stream=None):
-        _check(self.lib.dfq_chain_reset(self._h, _stream(stream)), "dfq_chain_reset")
-
-    def set_timeout(self, ticks: int):
-        _check(self.lib.dfq_chain_set_timeout(self._h, ticks), "dfq_chain_set_timeout")
-
-    def close(self):
-        if self._h:
-            self.lib.dfq_chain_destroy(self._h)
-            self._h = None
-
-    def __del__(self):
-        try:
-            self.close()
         except Exception:
             pass

@@ -183,56 +183,30 @@ dfq_status dfq_argmax_accept(dfq_ctx* ctx, const void* logits, int M, int V, dfq
                              const int32_t* proposals, int32_t* tokens, int32_t* accepted,
                              void* workspace, size_t workspace_bytes, void* stream);
 
-/* ---- chains: the ops of a verify forward in one launch ---------------------------------
- * A chain is a fixed list of ops on fixed buffers: qmm (as dfq_qmm, with 8-group chunks, up
- * to 8 rows) and silu_mul (as dfq_silu_mul), each reading the output of an earlier op or an
- * input.  dfq_chain_launch runs the whole list in one persistent launch, one workgroup per
- * CU; each workgroup fetches an op's weights while the previous op finishes, and waits on a
- * device-wide completion count only before it reads that op's output.  The result of every
- * op is bit-identical to the same calls made one by one.  No counterpart in the reference:
- * there the verify forward's matmuls are separate MLX dispatches of the swapped layers
- * (SmallMQuantizedMatmul.swift:210-224, reached per layer from the target model); this is
- * how a layer chain (or a whole forward) of them runs here.
- * Waits are bounded (1 s by default): a chain whose workgroups cannot all be resident ends
- * with its error flag set rather than hanging (dfq_chain_failed; dfq_chain_reset clears it).
- * The chain owns its workspace; launches of one chain must not overlap. */
-
-typedef struct dfq_chain dfq_chain;
-
-#define DFQ_CHAIN_QMM 0
-#define DFQ_CHAIN_SILU_MUL 1
-#define DFQ_CHAIN_QMM_SILU_GATE_UP 2  /* dfq_qmm_silu_gate_up: N = 2H, y = h [M][H] */
-
-typedef struct dfq_chain_op {
-    int kind;                 /* DFQ_CHAIN_QMM, DFQ_CHAIN_SILU_MUL, DFQ_CHAIN_QMM_SILU_GATE_UP */
-    const void* x;            /* qmm: [M][K]; silu_mul: gu [M][2N] (gate | up)             */
-    void* y;                  /* qmm: [M][N]; silu_mul: h [M][N]; gate_up: h [M][N/2]      */
-    const uint32_t* w;        /* qmm kinds only: MLX layout, as dfq_qmm (interleaved for
-                                 the gate_up kind)                                         */
-    const void* scales;
-    const void* biases;
-    const void* linear_bias;  /* may be NULL                                               */
-    int N, K;                 /* silu_mul: N = hidden width, K unused                      */
-    int independent;          /* 1: reads no output of the op just before it (e.g. k and v
-                                 after q, all reading the layer input); it then starts without
-                                 waiting for that op.  Ignored for op 0 and after a reduce
-                                 split.  0: waits for the op before it (the usual case).  */
-} dfq_chain_op;
-
-dfq_status dfq_chain_create(dfq_ctx* ctx, int M, int bits, int group_size, dfq_dtype dtype,
-                            const dfq_chain_op* ops, int n_ops, dfq_chain** out);
-/* An independent op waits instead for the op two places back, so consecutive independent
- * ops stream back to back; their workspaces alternate between two regions. */
-/* One launch of the whole chain on `stream` (asynchronous; allocates nothing). */
-dfq_status dfq_chain_launch(dfq_chain* chain, void* stream);
-/* Synchronises the device and reports whether a launch's wait timed out. */
-dfq_status dfq_chain_failed(dfq_chain* chain, int* failed);
-/* Clears the counters, the error flag and the workspace (kernels on `stream`): after a
- * timed-out launch the workspace may hold partial tiles. */
-dfq_status dfq_chain_reset(dfq_chain* chain, void* stream);
-/* The wait limit in 100 MHz ticks (tests use a tiny one to drive the error path). */
-dfq_status dfq_chain_set_timeout(dfq_chain* chain, uint32_t ticks);
-dfq_status dfq_chain_destroy(dfq_chain* chain);
+/* The LM head fused with the greedy accept: logits[M][V] = x . dequant(w)^T (+ linear bias)
+ * on the fast kernel, and from them, as dfq_argmax_accept computes them, tokens[m] (the first
+ * index of each row's largest logit, NaN skipped, -1 for a row with no number) and *accepted
+ * (the leading run of proposals[i] == tokens[i], i < M-1).  Every logit is folded into its
+ * row's key where the kernel finishes it, and the last workgroup decodes the keys: the
+ * logits need not go to memory and no second kernel reads them back.  logits may be NULL
+ * (then nothing of them is written).  Results are identical to dfq_qmm followed by
+ * dfq_argmax_accept on its output.  Shapes whose split needs the second pass (dfq_qmm's
+ * reduce splits) run as exactly that pair of calls, with the logits in `logits` or, when it
+ * is NULL, in the workspace's tail.  dtype is that of x, scales, biases and the logits.  The
+ * workspace (dfq_qmm_argmax_accept_workspace_bytes, 256-byte aligned) must be zero before
+ * the first call (dfq_workspace_clear); every call leaves it zero again, except the logits
+ * tail of that two-call form, which only ever holds logits and needs no clearing.
+ * Replaces the lm_head projection and acceptedPrefix(targetLogits:proposals:) of a verify
+ * round (DFlashSpeculativeGenerator.swift:389-398, 555-571; argMax / == / cumprod / sum at
+ * :562-564): only M tokens and one count leave the device. */
+dfq_status dfq_qmm_argmax_accept_workspace_bytes(dfq_ctx* ctx, int M, int V, int K, int bits,
+                                                 int group_size, size_t* bytes);
+dfq_status dfq_qmm_argmax_accept(dfq_ctx* ctx, const void* x, const uint32_t* w,
+                                 const void* scales, const void* biases,
+                                 const void* linear_bias, void* logits, int M, int V, int K,
+                                 int bits, int group_size, dfq_dtype dtype,
+                                 const int32_t* proposals, int32_t* tokens, int32_t* accepted,
+                                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- the drop-in layer (SmallMQuantizedMatmul.swift:227-317) -------------------------- */
 
@@ -276,6 +250,9 @@ dfq_status dfq_model_create(dfq_model** out);
 dfq_status dfq_model_destroy(dfq_model* model);
 /* Adds (or replaces) the leaf at `path`; the model takes ownership of `lin`. */
 dfq_status dfq_model_set_leaf(dfq_model* model, const char* path, dfq_linear* lin);
+/* The leaf at `path` (NULL if none) as a borrowed handle: never pass it to
+ * dfq_linear_destroy.  It stays valid until dfq_model_destroy, also after the leaf is
+ * swapped or replaced (it then still describes the layer it named). */
 dfq_linear* dfq_model_leaf(dfq_model* model, const char* path);
 int dfq_model_leaf_count(const dfq_model* model);
 /* Swaps every eligible stock leaf for a SmallMQuantizedLinear; returns how many were
