@@ -54,6 +54,9 @@ private:
 };
 int kss_for(int bits, int gs);
 bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_max, Plan* pl);
+/* The device address of the fixed scratch array (qmm_scratch.hip) on `device`, which must be
+ * current; taken and cleared once per device. */
+dfq_status scratch_setup(int device, void** out);
 dfq_status check_fast_args(const dfq_ctx* ctx, int M, int N, int K, int bits, int gs,
                            dfq_dtype xdt, dfq_dtype sdt, dfq_dtype ydt);
 

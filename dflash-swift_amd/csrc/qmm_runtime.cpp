@@ -85,6 +85,7 @@ struct dfq_ctx {
     hipFunction_t generic = nullptr;
     hipFunction_t fill = nullptr;
     hipFunction_t read_stream = nullptr; // the plain streaming read (bandwidth reference)
+    void* scratch = nullptr;             // the fixed scratch of dfq_qmm_noalloc (this device)
     std::mutex mu;
     std::unordered_map<PlanKey, dfq::Plan, PlanKeyHash> plans;
 };
@@ -385,6 +386,12 @@ dfq_status dfq_init(int device, dfq_ctx** out) {
         delete ctx;
         return hip_fail(e, "hipModuleGetFunction");
     }
+    dfq_status st = scratch_setup(device, &ctx->scratch);
+    if (st != DFQ_OK) {
+        (void)hipModuleUnload(ctx->module);
+        delete ctx;
+        return st;
+    }
     *out = ctx;
     return DFQ_OK;
 }
@@ -627,6 +634,25 @@ dfq_status dfq_qmm(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* s
                    void* stream) {
     return qmm_any(ctx, x, w, scales, biases, lbias, y, M, N, K, bits, gs, xdt, sdt, ydt, ws, wsb,
                    stream, 0);
+}
+
+dfq_status dfq_qmm_noalloc(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
+                           const void* biases, const void* lbias, void* y, int M, int N, int K,
+                           int bits, int gs, dfq_dtype xdt, dfq_dtype sdt, dfq_dtype ydt,
+                           void* stream) {
+    dfq_status s = check_fast_args(ctx, M, N, K, bits, gs, xdt, sdt, ydt);
+    if (s) return s;
+    if (!ctx->scratch) return fail(DFQ_ERR_STATE, "the context has no scratch");
+    /* the shape's split is looked up, or computed, without storing it: no allocation */
+    size_t need = 0;
+    if ((s = workspace_need(ctx, M, N, K, bits, gs, false, &need))) return s;
+    if (need > DFQ_SCRATCH_MAX_BYTES)
+        return fail(DFQ_ERR_WORKSPACE,
+                    "M=%d N=%d K=%d needs %zu bytes of workspace; the fixed scratch of "
+                    "dfq_qmm_noalloc holds %zu (use dfq_qmm with a workspace)",
+                    M, N, K, need, (size_t)DFQ_SCRATCH_MAX_BYTES);
+    return qmm_any(ctx, x, w, scales, biases, lbias, y, M, N, K, bits, gs, xdt, sdt, ydt,
+                   ctx->scratch, DFQ_SCRATCH_MAX_BYTES, stream, 0, false);
 }
 
 dfq_status dfq_qmm_silu_gate_up(dfq_ctx* ctx, const void* x, const uint32_t* w_gu,

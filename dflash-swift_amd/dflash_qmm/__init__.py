@@ -106,6 +106,7 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         "dfq_workspace_clear": ([P, P, S, P], I),
         "dfq_qmm": ([P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, P, S, P], I),
         "dfq_qmm_fallback": ([P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, P], I),
+        "dfq_qmm_noalloc": ([P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, P], I),
         "dfq_graph_begin": ([P, P], I), "dfq_graph_end": ([P, P, PP], I),
         "dfq_silu_mul": ([P, P, P, I, I, I, P], I),
         "dfq_argmax_accept_workspace_bytes": ([I, ctypes.POINTER(S)], I),

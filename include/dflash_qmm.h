@@ -120,6 +120,22 @@ dfq_status dfq_qmm(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* s
                    int bits, int group_size, dfq_dtype x_dtype, dfq_dtype sb_dtype,
                    dfq_dtype y_dtype, void* workspace, size_t workspace_bytes, void* stream);
 
+/* dfq_qmm with no workspace argument, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference, where MLX allocates every output and scratch itself.
+ * The workspace is a fixed array of DFQ_SCRATCH_MAX_BYTES per GPU inside the library, taken
+ * at dfq_init and held until the process ends; this call allocates nothing (no hipMalloc,
+ * hipFree or host allocation) and returns DFQ_ERR_WORKSPACE for a shape whose workspace
+ * (dfq_qmm_workspace_bytes) is larger.  Every call on one GPU shares that array: calls that
+ * overlap on one GPU (other streams, other threads, other contexts) race, so serialise
+ * them.  Each call leaves the array zero, as dfq_qmm leaves its workspace.  Same arguments,
+ * results and errors as dfq_qmm otherwise (bit-identical outputs). */
+#define DFQ_SCRATCH_MAX_BYTES ((size_t)64 << 20)
+dfq_status dfq_qmm_noalloc(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
+                           const void* biases, const void* linear_bias, void* y, int M, int N,
+                           int K, int bits, int group_size, dfq_dtype x_dtype,
+                           dfq_dtype sb_dtype, dfq_dtype y_dtype, void* stream);
+
 /* The MLP's fused gate|up projection with its SiLU-mul epilogue: h[M][H] = silu(x . Wg^T) *
  * (x . Wu^T), over one weight whose gate and up rows are interleaved in blocks of 8 (rows
  * 16b..16b+7 = gate rows 8b.., rows 16b+8.. = up rows 8b..; dfq_interleave_gate_up builds it,
