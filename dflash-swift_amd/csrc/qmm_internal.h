@@ -23,6 +23,7 @@ struct Plan {
     int nslot_kb = 0;   /* partial slots per tile per k-block                */
     int kr = 0;         /* k elements in the largest k-block                 */
     bool reduce = false; /* shared tiles summed by the second kernel         */
+    bool aligned = false; /* workgroup ranges of whole tiles (two k-blocks)   */
     int rs = 0;         /* LDS bytes per staged x row                        */
     int xsum_off = 0;   /* LDS offset of the per-group x sums                */
     int part_off = 0;   /* LDS offset of the per-unit partial tiles          */

@@ -72,9 +72,17 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 #endif
 constexpr int kWaves = DFQ_WAVES;
 constexpr uint32_t kTileDone = 0x80000000u;  // tile counter value once its units are summed
-constexpr uint32_t kTileOut = 0x80000001u;   // ... and once the publisher wave wrote it
+constexpr uint32_t kTileOut = 0x80000001u;   // ... and once its publisher wave wrote it
 constexpr int kThreads = kWaves * 64;        // streaming threads
-constexpr int kBlock = kThreads + 64;        // + the publisher wave
+#ifndef DFQ_PUBLISHERS
+/* publisher waves per workgroup; the host is built with the same value.  A second one takes
+ * half the tiles, so that two tiles' fix-ups (device-scope round trips) overlap: measured on
+ * MI355X, M = 8, K = 5120: N = 17408 16.6 -> 15.7 us, N = 5120 10.6 -> 9.6 us; more than two
+ * gained nothing further. */
+#define DFQ_PUBLISHERS 2
+#endif
+constexpr int kPublishers = DFQ_PUBLISHERS;
+constexpr int kBlock = kThreads + 64 * kPublishers;  // + the publisher waves
 constexpr int kMaxStageItems = 96 / DFQ_WAVES;  // 16-byte x chunks staged per thread
 
 /* The dynamic LDS block of a qmm_mt8 workgroup (its layout is fixed by the host plan). */
@@ -396,14 +404,33 @@ __device__ __forceinline__ int owner_wg(int u, int base, int rem) {
 }
 
 /* k-block kb holds chunks [c0, c0 + SS) of K (the chunks spread over the k-blocks with
- * sizes differing by at most one); its T*SS units go to the Gkb workgroups as above. */
+ * sizes differing by at most one); its T*SS units go to the Gkb workgroups as above, or, in
+ * an aligned split, its T tiles do (base and rem then count tiles, and a range is whole
+ * tiles). */
 struct KBlock {
     int c0, SS, base, rem;
+    bool aligned;
 };
 __device__ __forceinline__ KBlock kblock(const QmmParams& p, int kb) {
     const int c0 = kb * p.chunks / p.nkb, c1 = (kb + 1) * p.chunks / p.nkb;
-    const int SS = c1 - c0, U = p.T * SS;
-    return KBlock{c0, SS, U / p.Gkb, U % p.Gkb};
+    const int SS = c1 - c0, U = p.aligned ? p.T : p.T * SS;
+    return KBlock{c0, SS, U / p.Gkb, U % p.Gkb, p.aligned != 0};
+}
+
+/* First unit of workgroup c's range in k-block k. */
+__device__ __forceinline__ int range_start(const KBlock& k, int c) {
+    const int s = wg_start(c, k.base, k.rem);
+    return k.aligned ? s * k.SS : s;
+}
+
+/* The first workgroup (within the k-block) whose range holds units of tile t, and how many
+ * workgroups of the k-block hold its units (one in an aligned split). */
+__device__ __forceinline__ int tile_first_owner(const KBlock& k, int t) {
+    return k.aligned ? owner_wg(t, k.base, k.rem) : owner_wg(t * k.SS, k.base, k.rem);
+}
+__device__ __forceinline__ int tile_owners(const KBlock& k, int t) {
+    return k.aligned ? 1 : owner_wg(t * k.SS + k.SS - 1, k.base, k.rem) -
+                               owner_wg(t * k.SS, k.base, k.rem) + 1;
 }
 
 /* A partial tile (8*mt rows x 16 columns, fp32) is held by lanes 0 .. 32*mt-1: lane (q, n)
@@ -486,9 +513,10 @@ __device__ __forceinline__ void store_h(const QmmParams& p, int t, int lane, f32
     }
 }
 
-/* Tile t as held by the lanes, plus the linear bias, to y; in greedy-accept mode (p.am_keys)
- * also folded into the lane's keys of rows 4q..4q+3 (best), and y may be NULL. */
-template <bool F16>
+/* Tile t as held by the lanes, plus the linear bias, to y; in greedy-accept mode (AM, the
+ * kernels built for dfq_qmm_argmax_accept) also folded into the lane's keys of rows
+ * 4q..4q+3 (best), and y may be NULL. */
+template <bool F16, bool AM = false>
 __device__ __forceinline__ void store_y(const QmmParams& p, int t, int lane, f32x4_t v,
                                         uint64_t (&best)[4]) {
     if (p.epi) {
@@ -506,8 +534,8 @@ __device__ __forceinline__ void store_y(const QmmParams& p, int t, int lane, f32
         const int m = 4 * q + r;
         if (m >= p.M) continue;
         const uint16_t o = f32_to_out<F16>(v[r] + lb);
-        if (y) put16(y + (size_t)m * p.N + col, o);
-        if (p.am_keys) fold_key<F16>(best[r], o, col);
+        if (!AM || y) put16(y + (size_t)m * p.N + col, o);
+        if constexpr (AM) fold_key<F16>(best[r], o, col);
     }
 }
 
@@ -527,12 +555,12 @@ __device__ __forceinline__ void store_y(const QmmParams& p, int t, int lane, f32
  * The workspace is zero again when the kernel ends.  Workgroups on different XCDs exchange
  * these partials: every access to a slot is an agent-scope atomic (coherent across the
  * XCDs' L2s without a whole-cache write-back or invalidate). */
-template <bool F16>
-__device__ __forceinline__ void publish(const QmmParams& p, int SS, int base_u, int rem_u, int t,
+template <bool F16, bool AM>
+__device__ __forceinline__ void publish(const QmmParams& p, const KBlock& kbk, int t,
                                         int slot, int lane, f32x4_t v, uint64_t (&best)[4]) {
     const int q = lane >> 4, n = lane & 15;
     const bool act = lane < 32 * p.mt;  // lanes holding the tile
-    const int nwg = owner_wg(t * SS + SS - 1, base_u, rem_u) - owner_wg(t * SS, base_u, rem_u) + 1;
+    const int nwg = tile_owners(kbk, t);
     const uint32_t total = (uint32_t)(p.nkb * nwg);
     /* the tile's workspace area: nkb*nslot_kb slots of mt*128 floats */
     uint32_t* base = (uint32_t*)p.slots + (size_t)t * p.nkb * p.nslot_kb * p.mt * 128;
@@ -603,8 +631,8 @@ __device__ __forceinline__ void publish(const QmmParams& p, int SS, int base_u, 
         const float sum = v[r] + __uint_as_float((uint32_t)old[r]);
         if (m < p.M && col < p.N) {
             const uint16_t o = f32_to_out<F16>(sum + lb);
-            if (p.y) put16((uint16_t*)p.y + (size_t)m * p.N + col, o);
-            if (p.am_keys) fold_key<F16>(best[r], o, col);
+            if (!AM || p.y) put16((uint16_t*)p.y + (size_t)m * p.N + col, o);
+            if constexpr (AM) fold_key<F16>(best[r], o, col);
         }
         __hip_atomic_store(sl + r, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -654,7 +682,8 @@ __device__ void accept_finish(const QmmParams& p, uint64_t (&best)[4], int lane,
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the maxima have completed
     uint32_t last = 0;
     if (lane == 0) {
-        const uint32_t size_g = (uint32_t)(G / ng + (grp < G % ng ? 1 : 0));
+        /* every publisher wave of the group's workgroups arrives */
+        const uint32_t size_g = (uint32_t)((G / ng + (grp < G % ng ? 1 : 0)) * kPublishers);
         if (__hip_atomic_fetch_add(p.am_count + grp * 32, 1u, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT) + 1u == size_g)
             last = __hip_atomic_fetch_add(p.am_count + 16 * 32, 1u, __ATOMIC_RELAXED,
@@ -682,9 +711,10 @@ __device__ void accept_finish(const QmmParams& p, uint64_t (&best)[4], int lane,
     }
 }
 
-template <bool F16, int MT>
-__device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b, int SS,
-                               int base_u, int rem_u, int lane, int wg) {
+template <bool F16, int MT, bool AM>
+__device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
+                               const KBlock& kbk, int lane, int wg, int pi) {
+    const int SS = kbk.SS;
     const int q = lane >> 4, n = lane & 15;
     const int ta = a / SS;
     const int ntl = (b > a) ? (b - 1) / SS - ta + 1 : 0;
@@ -694,20 +724,23 @@ __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
     const int s1 = max(a, ((b - 1) / SS) * SS), nrot = b - s1;  // the take order (unit_of)
     __syncthreads();  // the staging barrier of the streaming waves (tile counters zeroed)
     uint64_t best[4] = {0, 0, 0, 0};  // greedy-accept keys of rows 4q..4q+3
-    int remaining = ntl;
+    /* publisher pi takes the tiles pi, pi + kPublishers, ... of the workgroup */
+    const int nown = ntl > pi ? (ntl - pi + kPublishers - 1) / kPublishers : 0;
+    int remaining = nown;
     while (remaining > 0) {
         int found = 0;
-        for (int base = 0; base < ntl; base += 64) {
-            const int tl = base + lane;
+        for (int base = 0; base < nown; base += 64) {
+            const int tl = pi + (base + lane) * kPublishers;
             bool ready = false;
-            if (tl < ntl)
+            if (base + lane < nown)
                 ready = __hip_atomic_load(tcnt + tl, __ATOMIC_ACQUIRE,
                                           __HIP_MEMORY_SCOPE_WORKGROUP) == kTileDone;
             uint64_t m = __builtin_amdgcn_ballot_w64(ready);
             while (m) {
                 const int bit = __builtin_ctzll(m);
                 m &= m - 1;
-                const int t = ta + base + bit;
+                const int tlb = pi + (base + bit) * kPublishers;
+                const int t = ta + tlb;
                 const int u0 = max(a, t * SS), u1 = min(b, (t + 1) * SS);
                 const int g0 = u0 >= s1 ? u0 - s1 : nrot + (u0 - a);  // take index of u0
                 const int sl0 = g0 % p.ring;
@@ -718,24 +751,24 @@ __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
                 if (lane == 0)
                     __hip_atomic_store(gen + sl0, (uint32_t)(g0 + p.ring), __ATOMIC_RELEASE,
                                        __HIP_MEMORY_SCOPE_WORKGROUP);
-                const int first = owner_wg(t * SS, base_u, rem_u);
+                const int first = tile_first_owner(kbk, t);
                 if (u0 == t * SS && u1 == (t + 1) * SS && p.nkb == 1) {
-                    store_y<F16>(p, t, lane, v, best);
+                    store_y<F16, AM>(p, t, lane, v, best);
                 } else if (p.reduce) {
                     /* summed by the second pass: no round trip here */
                     if (lane < 32 * MT) put_tile4(tile_slot(p, t, kb, cl - first, lane), v);
                 } else {
-                    publish<F16>(p, SS, base_u, rem_u, t, kb * p.nslot_kb + (cl - first),
-                                 lane, v, best);
+                    publish<F16, AM>(p, kbk, t, kb * p.nslot_kb + (cl - first),
+                                     lane, v, best);
                 }
-                if (lane == 0) tcnt[base + bit] = kTileOut;
+                if (lane == 0) tcnt[tlb] = kTileOut;
                 ++found;
             }
         }
         remaining -= found;
         if (!found) __builtin_amdgcn_s_sleep(1);
     }
-    if (p.am_keys) accept_finish<MT>(p, best, lane, wg);
+    if constexpr (AM) accept_finish<MT>(p, best, lane, wg);
 }
 
 /* ---------------------------------------------------------------------------------- */
@@ -759,8 +792,7 @@ template <bool F16>
 __device__ __forceinline__ void reduce_tile(const QmmParams& p, int t, int lane) {
     int parts = 0;
     for (int kb = 0; kb < p.nkb; ++kb) {
-        const KBlock k = kblock(p, kb);
-        parts += owner_wg(t * k.SS + k.SS - 1, k.base, k.rem) - owner_wg(t * k.SS, k.base, k.rem) + 1;
+        parts += tile_owners(kblock(p, kb), t);
     }
     if (parts <= 1) return;
     f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -785,7 +817,7 @@ __device__ __forceinline__ void reduce_tile(const QmmParams& p, int t, int lane)
     store_y<F16>(p, t, lane, sum, unused);
 }
 
-template <int BITS, int GS, bool F16, int CH, int PF, int MT>
+template <int BITS, int GS, bool F16, int CH, int PF, int MT, bool AM = false>
 __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
     using C = Cfg<BITS, GS>;
     constexpr int XR = 8 * MT;  // rows of x sums per group in LDS
@@ -802,11 +834,11 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
     const int cl = wg - kb * p.Gkb;
     const KBlock kbk = kblock(p, kb);
     const int SS = kbk.SS;    // chunks per tile in this k-block
-    const int a = wg_start(cl, kbk.base, kbk.rem);
-    const int b = wg_start(cl + 1, kbk.base, kbk.rem);
+    const int a = range_start(kbk, cl);
+    const int b = range_start(kbk, cl + 1);
 
-    if (wave == kWaves) {
-        publisher_wave<F16, MT>(p, kb, cl, a, b, SS, kbk.base, kbk.rem, lane, wg);
+    if (wave >= kWaves) {
+        publisher_wave<F16, MT, AM>(p, kb, cl, a, b, kbk, lane, wg, wave - kWaves);
         return;
     }
 
@@ -1420,16 +1452,19 @@ constexpr int prefetch_depth() {
     return d < 1 ? 1 : (d > 8 ? 8 : d);
 }
 
-#define DFQ_MT8_KERNEL(BITS, GS, F16, NAME, CHN, CH, MTN, MT)                               \
+#define DFQ_MT8_KERNEL(BITS, GS, F16, NAME, CHN, CH, MTN, MT, AM, SFX)                     \
     extern "C" __global__ void __launch_bounds__(kBlock)                                     \
-        dfq_qmm_##MTN##_b##BITS##_g##GS##_##NAME##_##CHN(QmmParams p) {                       \
-        qmm_mt8<BITS, GS, F16, CH, prefetch_depth<BITS, GS, CH>(), MT>(p, blockIdx.x);        \
+        dfq_qmm_##MTN##_b##BITS##_g##GS##_##NAME##_##CHN##SFX(QmmParams p) {                  \
+        qmm_mt8<BITS, GS, F16, CH, prefetch_depth<BITS, GS, CH>(), MT, AM>(p, blockIdx.x);    \
     }
-/* per format: one super-step or 8-group chunks at up to 8 rows; 8-group chunks at up to 16 */
+/* per format: one super-step or 8-group chunks at up to 8 rows; 8-group chunks at up to 16;
+ * and the greedy-accept forms (_am) of the 8-group-chunk kernels */
 #define DFQ_MT8_FORMAT(BITS, GS, F16, NAME)                                                    \
-    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c1, 1, mt8, 1)                                        \
-    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt8, 1)                 \
-    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt16, 2)
+    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c1, 1, mt8, 1, false, )                               \
+    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt8, 1, false, )        \
+    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt16, 2, false, )       \
+    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt8, 1, true, _am)      \
+    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt16, 2, true, _am)
 
 DFQ_MT8_FORMAT(4, 32, false, bf16)
 DFQ_MT8_FORMAT(4, 64, false, bf16)

@@ -18,7 +18,9 @@
  *    (kb+1)*chunks/nkb); its x slice must fit in LDS);
  *  - the U = T*SS units (tile, chunk) of a k-block of SS chunks are split into Gkb
  *    contiguous ranges whose sizes differ by at most one (the first U % Gkb get one more);
- *    a narrow N (few tiles) takes two k-blocks with Gkb = T, one tile per workgroup;
+ *    or, in an "aligned" split of two k-blocks, the T tiles are split that way and each
+ *    workgroup takes whole tiles, so that every tile has exactly one part per k-block (a
+ *    narrow N is the case Gkb = T, one tile per workgroup);
  *  - inside a workgroup the waves take units of its range one at a time from a counter in
  *    LDS (the first ones by wave index), in a rotated order that starts with the tile shared
  *    with the next workgroup and continues with the one shared with the previous, so that
@@ -48,6 +50,7 @@ typedef struct QmmParams {
     int32_t Gkb;            /* workgroups per k-block                                 */
     int32_t nslot_kb;       /* partial slots per tile per k-block                     */
     int32_t reduce;         /* 1: shared tiles go to slots summed by dfq_qmm_reduce   */
+    int32_t aligned;        /* 1: each workgroup's range is whole tiles (of its k-block) */
     int32_t epi;            /* 1: y = silu(gate) * up of a gate|up weight interleaved
                                by 8 rows (y is [M][N/2])                              */
     int32_t lds_row_stride; /* bytes per staged x row in LDS                          */

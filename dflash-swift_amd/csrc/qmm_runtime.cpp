@@ -50,7 +50,10 @@ thread_local std::string g_last_error;
 #endif
 constexpr int kWaves = DFQ_WAVES;
 constexpr int kThreads = kWaves * 64;             // qmm_mt8 streaming threads
-constexpr int kBlockThreads = kThreads + 64;      // + the publisher wave: the workgroup size
+#ifndef DFQ_PUBLISHERS
+#define DFQ_PUBLISHERS 2               // must match the kernels' build
+#endif
+constexpr int kBlockThreads = kThreads + 64 * DFQ_PUBLISHERS;  // + the publisher waves
 constexpr int kMaxStageItems = 96 / DFQ_WAVES;    // must match qmm_kernels.hip
 
 struct PlanKey {
@@ -79,6 +82,7 @@ struct dfq_ctx {
     hipModule_t module = nullptr;
     hipFunction_t mt8[2][3][2][2] = {};  // [bits 4/8][gs 32/64/128][bf16/f16][chunk 1/8 groups]
     hipFunction_t mt16[2][3][2] = {};    // up to 16 rows, 8-group chunks [bits][gs][bf16/f16]
+    hipFunction_t am[2][3][2][2] = {};   // greedy-accept forms, 8-group chunks [..][rows 8/16]
     hipFunction_t reduce[2] = {};        // second pass of reduce splits [bf16/f16]
     hipFunction_t silu_mul[2] = {};      // SiLU-mul of a fused gate||up output [bf16/f16]
     hipFunction_t argmax_accept[2] = {}; // greedy accept of a verify pass [bf16/f16]
@@ -160,6 +164,13 @@ static int tile_owners(int64_t t, int64_t SS, int64_t G, int64_t T) {
 /* Largest workgroup share (units) for which a narrow N is split into two k-blocks of one tile
  * per workgroup. */
 static constexpr int kShortSplitUnits = 24;
+/* Most tiles per workgroup for which two k-blocks take an aligned split rather than
+ * stream-K ranges with the second pass.  Every tile of an aligned split is finished by a
+ * pair exchange of per-element device-scope atomics.  Measured on MI355X with 16 rows at
+ * K = 5120 (us, aligned against the second pass): N = 1024 (one tile per workgroup) 8.2
+ * against 9.6; N = 5120 (three) 12.2 against 12.1; N = 7168 (four) 13.8 against 13.7;
+ * N = 17408 (nine) 24.4 against 20.7. */
+static constexpr int kAlignedMaxTiles = 2;
 
 bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_max, Plan* pl) {
     const int kss = kss_for(bits, gs);
@@ -232,8 +243,58 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
         *out = p;
         return true;
     };
+    /* Two k-blocks whose workgroups take whole tiles (an "aligned" split of G0 workgroups per
+     * k-block, at most one per tile): every tile then has one part per k-block, finished by
+     * the pair exchange, so no second pass is needed, at the price of up to one tile of
+     * imbalance between workgroups. */
+    auto split_aligned = [&](int64_t G0, Plan* out) -> bool {
+        if (chunks < 2) return false;
+        const int ss_max = (chunks + 1) / 2;
+        const int kr = ss_max * kch;
+        if ((int64_t)M * (kr / 8) > (int64_t)kMaxStageItems * kThreads) return false;
+        const int64_t G = std::min<int64_t>(std::max<int64_t>(1, G0), T);
+        const int64_t tmax = (T + G - 1) / G;
+        Plan p{};
+        p.kss = kss;
+        p.mt = mt;
+        p.ch = ch;
+        p.T = T;
+        p.chunks = chunks;
+        p.nkb = 2;
+        p.kr = kr;
+        p.SS = ss_max;
+        p.rs = 2 * kr + 16;
+        p.xsum_off = ((M + 1) * p.rs + 15) & ~15;
+        p.part_off = p.xsum_off + (kr / gs) * 32 * mt;
+        p.umax = (int)(tmax * ss_max);
+        p.ring = (int)std::min<int64_t>(p.umax, 4 * ss_max + 24);
+        p.gen_off = p.part_off + p.ring * 512 * mt;
+        p.cnt_off = p.gen_off + p.ring * 4;
+        const size_t need = (size_t)p.cnt_off + (size_t)(tmax + 1) * 4;
+        if (need > lds_max) return false;
+        p.Gkb = (int)G;
+        p.nslot_kb = 1;
+        p.reduce = false;
+        p.aligned = true;
+        p.lds_bytes = (int)std::min(std::max(need, lds_max / 2 + 256), lds_max);
+        p.lds_need = (int)need;
+        p.need_ws = true;
+        p.ws_bytes = (size_t)T * 2 * mt * 128 * 4;
+        *out = p;
+        return true;
+    };
     for (int d = std::min(DFQ_MIN_KBLOCKS, chunks); d <= chunks; ++d) {
         if (!split(d, num_cus / d, pl)) continue;
+        /* Two k-blocks of stream-K ranges give tiles three or four parts (second pass); whole
+         * tiles per workgroup give two, finished in the kernel, which pays where each
+         * workgroup holds few tiles. */
+        Plan al;
+        if (pl->reduce && d == 2 && split_aligned(num_cus / 2, &al) &&
+            (T + al.Gkb - 1) / al.Gkb <= kAlignedMaxTiles) {
+            *pl = al;
+            return true;
+        }
+
         /* Few tiles (a narrow N): one k-block over every CU spreads each tile over more than
          * two workgroups, which needs the second pass.  Two k-blocks of one tile per
          * workgroup finish every tile with the pair exchange instead, and stage half of x,
@@ -371,6 +432,16 @@ dfq_status dfq_init(int device, dfq_ctx** out) {
                         (void)hipModuleUnload(ctx->module);
                         delete ctx;
                         return hip_fail(e, name);
+                    }
+                    for (int t = 0; t < 2; ++t) {
+                        snprintf(name, sizeof name, "dfq_qmm_mt%d_b%d_g%d_%s_c8_am", 8 * (t + 1),
+                                 kBits[b], kGs[g2], kDt[d]);
+                        if ((e = hipModuleGetFunction(&ctx->am[b][g2][d][t], ctx->module,
+                                                      name)) != hipSuccess) {
+                            (void)hipModuleUnload(ctx->module);
+                            delete ctx;
+                            return hip_fail(e, name);
+                        }
                     }
                 }
     if ((e = hipModuleGetFunction(&ctx->generic, ctx->module, "dfq_qmm_generic")) != hipSuccess ||
@@ -559,6 +630,7 @@ static QmmParams fill_params(const Plan& pl, const void* x, const uint32_t* w,
     p.Gkb = pl.Gkb;
     p.nslot_kb = pl.nslot_kb;
     p.reduce = pl.reduce ? 1 : 0;
+    p.aligned = pl.aligned ? 1 : 0;
     p.lds_row_stride = pl.rs;
     p.lds_xsum_off = pl.xsum_off;
     p.lds_part_off = pl.part_off;
@@ -588,8 +660,9 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
     Plan pl;
     dfq_status s = get_plan(ctx, M, N, K, bits, gs, &pl, cache);
     if (s) return s;
-    if (acc && (pl.reduce || epi))
-        return fail(DFQ_ERR_STATE, "greedy-accept mode needs a split without a second pass");
+    if (acc && (pl.reduce || epi || pl.ch == 1))
+        return fail(DFQ_ERR_STATE,
+                    "greedy-accept mode needs 8-group chunks and a split without a second pass");
     if (pl.need_ws) {
         if (!ws || wsb < pl.ws_bytes)
             return fail(DFQ_ERR_WORKSPACE, "workspace of %zu bytes needed (got %zu)", pl.ws_bytes,
@@ -610,7 +683,9 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
     const int di = dt == DFQ_BF16 ? 0 : 1;
     void* args[] = {&p};
     const int ci = pl.ch > 1 ? 1 : 0;
-    hipFunction_t fn = pl.mt == 2 ? ctx->mt16[bi][gi][di] : ctx->mt8[bi][gi][di][ci];
+    hipFunction_t fn = acc           ? ctx->am[bi][gi][di][pl.mt - 1]
+                       : pl.mt == 2 ? ctx->mt16[bi][gi][di]
+                                    : ctx->mt8[bi][gi][di][ci];
     hipError_t e = hipModuleLaunchKernel(fn, (unsigned)(pl.nkb * pl.Gkb), 1, 1, kBlockThreads, 1,
                                          1, (unsigned)pl.lds_bytes, stream, args, nullptr);
     if (e != hipSuccess) return hip_fail(e, "launch dfq_qmm_mt8");
@@ -780,7 +855,7 @@ static dfq_status qmm_accept_layout(dfq_ctx* ctx, int M, int V, int K, int bits,
     if ((s = workspace_need(ctx, M, V, K, bits, gs, true, &need))) return s;
     Plan pl;
     *fused = one_pass(ctx, M, V, K, bits, gs) && get_plan(ctx, M, V, K, bits, gs, &pl) == DFQ_OK &&
-             !pl.reduce;
+             !pl.reduce && pl.ch > 1;
     *qmm_ws = align256(need);
     *total = *qmm_ws + align256((size_t)16 * M * 8) + align256(kAcceptCountBytes);
     if (!*fused) *total += align256((size_t)M * V * 2);
@@ -933,17 +1008,23 @@ dfq_status dfq_graph_destroy(dfq_graph* gr) {
 
 /* ---- introspection used by tests and the benchmark (not part of the drop-in surface) -- */
 
+/* The fields of a split as the debug calls report them. */
+static void plan_fields(const Plan& p, int* out) {
+    const int v[14] = {p.T,   p.SS,          p.nkb,           p.Gkb, p.nslot_kb, p.kr,
+                       p.lds_bytes, p.need_ws ? 1 : 0, p.ch, p.umax, p.chunks,
+                       p.reduce ? 1 : 0, p.ring, p.aligned ? 1 : 0};
+    std::memcpy(out, v, sizeof v);
+}
+
 /* Fills the work split the fast kernel uses for a shape: {T, SS, nkb, Gkb, nslot_kb, kr,
- * lds_bytes, need_ws, ch, umax, chunks, reduce, ring} (SS and kr of the largest k-block). */
-dfq_status dfq_debug_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, int* out13) {
-    if (!out13) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
+ * lds_bytes, need_ws, ch, umax, chunks, reduce, ring, aligned} (SS and kr of the largest
+ * k-block). */
+dfq_status dfq_debug_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, int* out14) {
+    if (!out14) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
     Plan p;
     dfq_status s = get_plan(ctx, M, N, K, bits, gs, &p);
     if (s) return s;
-    const int v[13] = {p.T,  p.SS,        p.nkb,            p.Gkb, p.nslot_kb, p.kr,
-                       p.lds_bytes, p.need_ws ? 1 : 0, p.ch, p.umax, p.chunks, p.reduce ? 1 : 0,
-                       p.ring};
-    std::memcpy(out13, v, sizeof v);
+    plan_fields(p, out14);
     return DFQ_OK;
 }
 
@@ -965,15 +1046,12 @@ dfq_status dfq_debug_read_stream(dfq_ctx* ctx, const void* src, size_t bytes, ui
 
 /* The same split computed without a device, for a given CU count and LDS limit. */
 dfq_status dfq_debug_make_plan(int M, int N, int K, int bits, int gs, int num_cus,
-                               size_t lds_max, int* out13) {
-    if (!out13) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
+                               size_t lds_max, int* out14) {
+    if (!out14) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
     Plan p;
     if (!make_plan(M, N, K, bits, gs, num_cus, lds_max, &p))
         return fail(DFQ_ERR_UNSUPPORTED, "no work split");
-    const int v[13] = {p.T,  p.SS,        p.nkb,            p.Gkb, p.nslot_kb, p.kr,
-                       p.lds_bytes, p.need_ws ? 1 : 0, p.ch, p.umax, p.chunks, p.reduce ? 1 : 0,
-                       p.ring};
-    std::memcpy(out13, v, sizeof v);
+    plan_fields(p, out14);
     return DFQ_OK;
 }
 

@@ -207,8 +207,9 @@ dfq_status dfq_argmax_accept(dfq_ctx* ctx, const void* logits, int M, int V, dfq
  * logits need not go to memory and no second kernel reads them back.  logits may be NULL
  * (then nothing of them is written).  Results are identical to dfq_qmm followed by
  * dfq_argmax_accept on its output.  Shapes whose split needs the second pass (dfq_qmm's
- * reduce splits) run as exactly that pair of calls, with the logits in `logits` or, when it
- * is NULL, in the workspace's tail.  dtype is that of x, scales, biases and the logits.  The
+ * reduce splits), or whose K is not a multiple of 8 groups, run as exactly that pair of
+ * calls, with the logits in `logits` or, when it is NULL, in the workspace's tail.  dtype is
+ * that of x, scales, biases and the logits.  The
  * workspace (dfq_qmm_argmax_accept_workspace_bytes, 256-byte aligned) must be zero before
  * the first call (dfq_workspace_clear); every call leaves it zero again, except the logits
  * tail of that two-call form, which only ever holds logits and needs no clearing.

@@ -4,9 +4,10 @@ Its tokens and accepted count must be identical to dfq_qmm followed by dfq_argma
 that output (itself pinned against the oracle's argmax_accept, and here once more directly),
 its logits (when asked for) identical to dfq_qmm's, and its workspace zero again after every
 call.  Cases: the C5 LM head (151936 x 5120, tiles shared by two workgroups) at 8 rows and at
-16 rows (a split with a second pass, which runs as the pair of calls); whole tiles; the narrow
-split; fp16 with a linear bias; a tie across workgroups (two identical weight rows dominating
-every row: the first index wins) and a row of NaN (token -1).
+16 rows (a split with a second pass, which runs as the pair of calls); whole tiles; the
+narrow split; fp16 with a linear bias; one-super-step chunks (also the pair of calls); a tie
+across workgroups (two identical weight rows dominating every row: the first index wins) and
+a row of NaN (token -1).
 Reference: acceptedPrefix, DFlashSpeculativeGenerator.swift:555-571 (argMax, ==, cumprod and
 sum at :562-564).
 """
@@ -27,6 +28,7 @@ CASES = [
     (5, 3000, 2048, 8, 64, F16, True, False),       # fp16, 8-bit, linear bias
     (1, 32000, 4096, 4, 64, BF16, False, False),    # one row: nothing to accept
     (12, 20000, 1024, 4, 32, BF16, False, False),   # 12 rows, group 32
+    (8, 3000, 640, 4, 64, BF16, True, False),       # K not 8 groups' worth: two calls
 ]
 
 
@@ -52,8 +54,10 @@ def test_fused_accept_matches_the_two_calls(ctx, M, V, K, bits, gs, dt, lb, word
     assert want_tok.tolist() == oracle_tok.tolist()
     need = ctx.qmm_argmax_accept_workspace_bytes(M, V, K, bits, gs)
     ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
-    # a split with a second pass keeps its logits in the workspace's tail (not re-zeroed)
-    tail = (M * V * 2 + 255) // 256 * 256 if ctx.plan(M, V, K, bits, gs)["reduce"] else 0
+    # the two-call form (a second pass, or one-super-step chunks) keeps its logits in the
+    # workspace's tail, which is not re-zeroed
+    pl = ctx.plan(M, V, K, bits, gs)
+    tail = (M * V * 2 + 255) // 256 * 256 if pl["reduce"] or pl["ch"] == 1 else 0
     for agree in sorted({0, M // 2, M - 1}):          # proposals matching the first `agree`
         props = want_tok[: M - 1].astype(np.int32).copy()
         if agree < M - 1:

@@ -73,6 +73,21 @@ NARROW_CASES = [
 ]
 
 
+# Two k-blocks whose workgroups take whole tiles (the aligned split: every tile has exactly one
+# part per k-block, finished by the pair exchange, no second pass), which the planner takes for
+# 9..16 rows at long K where each workgroup holds at most two tiles: ragged N, one and two
+# tiles per workgroup, a k-block pair of unequal length (K = 9 chunks), fewer tiles than
+# workgroups.
+ALIGNED_CASES = [
+    (16, 1024, 5120, 4, 32, F16),
+    (10, 3000, 5120, 4, 128, BF16),
+    (14, 3333, 4608, 4, 64, BF16),
+    (16, 4000, 5120, 8, 32, BF16),
+    (16, 2000, 4096, 4, 64, BF16),
+    (16, 40, 5120, 4, 64, F16),
+]
+
+
 def run_fast(ctx, c):
     x, w, s, b, lb = upload(c)
     return ctx.qmm(x, w, s, b, c.bits, c.gs, lbias=lb)
@@ -103,6 +118,25 @@ def test_narrow_n_split_matches_oracle_and_repeats(ctx, oracle, M, N, K, bits, g
     rel, ok = tolerance_check(download(y), oracle.qmm_f64(c))
     assert rel <= TOL and ok, f"max rel err {rel:.3e}"
     for _ in range(3):                       # the pair exchange leaves the workspace re-armed
+        y2 = ctx.qmm(x, w, s, b, c.bits, c.gs, lbias=lb)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
+
+
+@pytest.mark.parametrize("M,N,K,bits,gs,dt", ALIGNED_CASES)
+def test_aligned_split_matches_oracle_and_repeats(ctx, oracle, M, N, K, bits, gs, dt):
+    import torch
+    p = ctx.plan(M, N, K, bits, gs)
+    assert p["aligned"] == 1 and p["nkb"] == 2 and p["reduce"] == 0, p
+    c = make_case(M, N, K, bits=bits, gs=gs, xdt=dt, seed=11 * M + N + K + bits + gs,
+                  lbias=(N % 2 == 1))
+    announce(f"aligned M={M} N={N} K={K} bits={bits} gs={gs} dt={dt}")
+    x, w, s, b, lb = upload(c)
+    y = ctx.qmm(x, w, s, b, c.bits, c.gs, lbias=lb)
+    torch.cuda.synchronize()
+    rel, ok = tolerance_check(download(y), oracle.qmm_f64(c))
+    assert rel <= TOL and ok, f"max rel err {rel:.3e}"
+    for _ in range(3):                       # pair exchange: deterministic, workspace re-armed
         y2 = ctx.qmm(x, w, s, b, c.bits, c.gs, lbias=lb)
         torch.cuda.synchronize()
         assert torch.equal(y.view(torch.int16), y2.view(torch.int16))

@@ -12,7 +12,8 @@ words or groups cannot hide under a tolerance.
 
 Covered: every bits x group size x dtype in the 1..8-row form with 8-group chunks (c8), the
 9..16-row form (mt16) and one-super-step chunks (c1), plus the narrow split (two k-blocks,
-one tile per workgroup, pair exchange) and a reduce split (several k-blocks, second pass).
+one tile per workgroup, pair exchange), the aligned split (two k-blocks of whole tiles per
+workgroup) and a reduce split (several k-blocks, second pass).
 """
 import numpy as np
 import pytest
@@ -100,6 +101,17 @@ def test_unpack_is_exact_in_the_narrow_split(ctx, bits, gs, dt, M):
     pos = list(range(ck)) + list(range(4 * ck, 5 * ck)) + list(range(7 * ck, 8 * ck))
     run_one_hot(ctx, 64, K, bits, gs, dt, M, pos, seed=bits * 4000 + gs + dt,
                 expect_plan={"nkb": 2, "reduce": 0, "nslot_kb": 1})
+
+
+@pytest.mark.parametrize("bits,gs,dt,M", [(4, 64, BF16, 16), (8, 64, F16, 12)])
+def test_unpack_is_exact_in_the_aligned_split(ctx, bits, gs, dt, M):
+    """Two k-blocks of whole tiles per workgroup (16 tiles, K = 10 chunks): every k of the
+    first chunk of each k-block and of the last chunk."""
+    ck = chunk_k(bits, gs)
+    K = 10 * ck
+    pos = list(range(ck)) + list(range(5 * ck, 6 * ck)) + list(range(9 * ck, 10 * ck))
+    run_one_hot(ctx, 256, K, bits, gs, dt, M, pos, seed=bits * 6000 + gs + dt,
+                expect_plan={"nkb": 2, "aligned": 1, "reduce": 0})
 
 
 @pytest.mark.parametrize("bits,gs,dt,M", [(4, 64, BF16, 8), (8, 64, F16, 16)])

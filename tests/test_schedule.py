@@ -20,12 +20,12 @@ import dflash_qmm
 
 def make_plan(M, N, K, bits, gs, cus=256, lds=163840):
     lib = dflash_qmm.load_library()
-    out = (ctypes.c_int * 13)()
+    out = (ctypes.c_int * 14)()
     rc = lib.dfq_debug_make_plan(M, N, K, bits, gs, cus, lds, out)
     if rc:
         return None
     keys = ["T", "SS", "nkb", "Gkb", "nslot_kb", "kr", "lds_bytes", "need_ws", "ch", "umax",
-            "chunks", "reduce", "ring"]
+            "chunks", "reduce", "ring", "aligned"]
     return dict(zip(keys, list(out)))
 
 
@@ -39,11 +39,31 @@ def owner_wg(u, base, rem):
 
 
 def kblock(p, kb):
-    """Chunks [c0, c0 + SS) of k-block kb and its workgroup split (the kernel's kblock)."""
+    """Chunks [c0, c0 + SS) of k-block kb and its workgroup split (the kernel's kblock): base
+    and rem count units, or tiles in an aligned split."""
     c0 = kb * p["chunks"] // p["nkb"]
     SS = (kb + 1) * p["chunks"] // p["nkb"] - c0
-    base, rem = divmod(p["T"] * SS, p["Gkb"])
+    base, rem = divmod(p["T"] * (1 if p["aligned"] else SS), p["Gkb"])
     return c0, SS, base, rem
+
+
+def wg_range(p, kb, cl):
+    """Units [a, b) of workgroup cl of k-block kb (the kernel's range_start)."""
+    _, SS, base, rem = kblock(p, kb)
+    scale = SS if p["aligned"] else 1
+    return wg_start(cl, base, rem) * scale, wg_start(cl + 1, base, rem) * scale
+
+
+def tile_first_owner(p, kb, t):
+    _, SS, base, rem = kblock(p, kb)
+    return owner_wg(t, base, rem) if p["aligned"] else owner_wg(t * SS, base, rem)
+
+
+def tile_owners(p, kb, t):
+    _, SS, base, rem = kblock(p, kb)
+    if p["aligned"]:
+        return 1
+    return owner_wg(t * SS + SS - 1, base, rem) - owner_wg(t * SS, base, rem) + 1
 
 
 def take_order(a, b, SS):
@@ -68,10 +88,9 @@ def replay(p):
         c0, SS, base, rem = kblock(p, kb)
         assert SS in (chunks // nkb, -(-chunks // nkb)) and SS <= p["SS"]
         assert p["kr"] == p["SS"] * (p["kr"] // p["SS"])
-        assert base + (1 if rem else 0) <= umax
+        assert (base + (1 if rem else 0)) * (SS if p["aligned"] else 1) <= umax
         for t in range(T):
-            parts_of[t] = parts_of.get(t, 0) + (owner_wg(t * SS + SS - 1, base, rem)
-                                                - owner_wg(t * SS, base, rem) + 1)
+            parts_of[t] = parts_of.get(t, 0) + tile_owners(p, kb, t)
     max_parts = max(parts_of.values())
     assert p["reduce"] == int(max_parts > 2), (max_parts, p["reduce"])
 
@@ -96,7 +115,7 @@ def replay(p):
     for kb in range(nkb):
         c0, SS, base, rem = kblock(p, kb)
         for cl in range(G):
-            a, b = wg_start(cl, base, rem), wg_start(cl + 1, base, rem)
+            a, b = wg_range(p, kb, cl)
             order = take_order(a, b, SS) if b > a else []
             assert sorted(order) == list(range(a, b))
             if b <= a:
@@ -128,7 +147,7 @@ def replay(p):
                     if u0 == t * SS and u1 == (t + 1) * SS and nkb == 1:
                         finalize(t, units)
                     else:
-                        publish(t, kb, cl - owner_wg(t * SS, base, rem), units)
+                        publish(t, kb, cl - tile_first_owner(p, kb, t), units)
             assert all(c == min(b, (t + 1) * SS) - max(a, t * SS)
                        for c, t in zip(tcnt, range(ta, tlast + 1)))
     assert len(seen) == sum(T * kblock(p, kb)[1] for kb in range(nkb))
@@ -166,7 +185,14 @@ def _unpack_test_shapes():
     out += [(M, 64, 64 * gs, bits, gs) for (bits, gs, M) in
             ((4, 64, 8), (8, 32, 8), (4, 64, 12), (8, 128, 5))]
     out += [(8, 48, 256 * 64, 4, 64), (16, 48, 256 * 64, 8, 64)]
+    out += [(16, 256, 5120, 4, 64), (12, 256, 5120, 8, 64)]
     return out
+
+
+# two k-blocks of whole tiles per workgroup (the aligned split)
+ALIGNED_SHAPES = [(16, 1024, 5120, 4, 32), (10, 3000, 5120, 4, 128), (14, 3333, 4608, 4, 64),
+                  (16, 4000, 5120, 8, 32), (16, 2000, 4096, 4, 64), (16, 40, 5120, 4, 64),
+                  (16, 1024, 5120, 4, 64)]
 
 
 # the C5 projections and LM head at 8 and 16 rows, the one-hot unpack shapes, and the
@@ -175,7 +201,22 @@ EXTRA_SHAPES = ([(m, n, k, 4, 64) for m in (8, 16) for (n, k) in
                  ((5120, 5120), (7168, 5120), (1024, 5120), (5120, 17408), (151936, 5120),
                   (34816, 5120))]
                 + _unpack_test_shapes()
-                + [(16, 4096, 5120, 8, 64), (6, 1024, 5120, 4, 128), (3, 40, 256, 4, 32)])
+                + [(16, 4096, 5120, 8, 64), (6, 1024, 5120, 4, 128), (3, 40, 256, 4, 32)]
+                + ALIGNED_SHAPES)
+
+
+@pytest.mark.parametrize("shape", ALIGNED_SHAPES)
+def test_aligned_shapes_take_the_aligned_split(shape):
+    p = make_plan(*shape)
+    assert p["aligned"] == 1 and p["nkb"] == 2 and p["reduce"] == 0 and p["nslot_kb"] == 1, p
+    assert -(-p["T"] // p["Gkb"]) <= 2, p
+
+
+def test_many_tiles_per_workgroup_keep_the_second_pass():
+    """With nine tiles per workgroup the aligned split measured slower than the second pass:
+    the 16-row gate/up shape keeps stream-K ranges and the reduce kernel."""
+    p = make_plan(16, 17408, 5120, 4, 64)
+    assert p["aligned"] == 0 and p["reduce"] == 1 and p["nkb"] == 2, p
 
 
 @pytest.mark.parametrize("shape", SHAPES + EXTRA_SHAPES)
@@ -290,7 +331,7 @@ def test_prefetch_addresses_stay_in_bounds(shape):
         k0 = c0 * kch
         assert k0 + kr <= K and M * (kr // 8) <= WAVES * 64 * (96 // WAVES)
         for cl in range(G):
-            a, b = wg_start(cl, base, rem), wg_start(cl + 1, base, rem)
+            a, b = wg_range(p, kb, cl)
             units = set()
             for wave in range(WAVES):
                 units.update(fetched_units(a, b, SS, U, wave, pf))
