@@ -75,3 +75,55 @@ def test_fast_path_shape_checks_need_no_device():
     """dfq_qmm_supported's argument checks run on the host; without a context it says no."""
     lib = dflash_qmm.load_library()
     assert lib.dfq_qmm_supported(None, 8, 17408, 5120, 4, 64, 0, 0, 0) == 0
+
+
+SWIFT = os.path.join(ROOT, "dflash-swift_amd", "swift", "Sources", "DFlashKitHIP",
+                     "SmallMQuantizedMatmulHIP.swift")
+
+
+def _split_top(text):
+    """Comma-separated items of `text` at bracket depth 0."""
+    items, depth, cur = [], 0, ""
+    for ch in text:
+        if ch in "([{":
+            depth += 1
+        elif ch in ")]}":
+            depth -= 1
+        if ch == "," and depth == 0:
+            items.append(cur)
+            cur = ""
+        else:
+            cur += ch
+    if cur.strip():
+        items.append(cur)
+    return items
+
+
+def _calls(src, name_re):
+    """(name, argument count) of every call matching name_re, parentheses balanced."""
+    out = []
+    for m in re.finditer(name_re + r"\s*\(", src):
+        i, depth = m.end(), 1
+        while depth:
+            depth += {"(": 1, ")": -1}.get(src[i], 0)
+            i += 1
+        args = src[m.end():i - 1]
+        n = 0 if args.strip() in ("", "void") else len(_split_top(args))
+        out.append((m.group(1), n))
+    return out
+
+
+def test_swift_shim_calls_match_the_header():
+    """The Swift surface (no Swift toolchain here to build it) calls only functions the header
+    declares, each with the header's number of arguments, and reads only its constants."""
+    hdr = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    arity = dict(_calls(hdr, r"\b(dfq_[a-z0-9_]+)"))
+    src = re.sub(r"//[^\n]*", "", open(SWIFT).read())
+    calls = _calls(src, r"\b(dfq_[a-z0-9_]+)")
+    assert len(calls) >= 15
+    for name, n in calls:
+        assert name in arity, name
+        assert n == arity[name], (name, n, arity[name])
+    consts = set(re.findall(r"\b(DFQ_[A-Z_]+)\b", src))
+    for c in consts:
+        assert re.search(r"\b%s\b" % c, hdr), c
