@@ -19,8 +19,8 @@ Method:
   * the CPU baseline is the oracle's fp32 restatement of MLX's CPU algorithm (dequantise a
     group, multiply-accumulate), OpenMP over the host cores, timed on a bounded sample.
 
---profile-timed brackets only the timed replays with roctxProfilerResume / Pause, for
-`rocprofv3 --selected-regions`: the trace then holds exactly the calls the figures time.
+--profile-timed dispatches the matmul only as graph replays (one warm-up replay, then the
+timed ones), so that `rocprofv3 --kernel-trace --stats` averages the calls the figures time.
 
 Prints ONE JSON line.  --gpus > 1 is refused: this build measures one GPU.
 """
@@ -53,34 +53,18 @@ def measured_traffic():
     return None
 
 
-class TimedRegion:
-    """roctxProfilerResume / Pause around the timed replays (for rocprofv3
-    --selected-regions), or nothing when not asked for."""
-
-    def __init__(self, enabled):
-        self.lib = None
-        if enabled:
-            import ctypes
-            self.lib = ctypes.CDLL("librocprofiler-sdk-roctx.so")
-            self.lib.roctxProfilerPause(0)   # nothing is traced until a timed region
-
-    def __enter__(self):
-        if self.lib:
-            self.lib.roctxProfilerResume(0)
-
-    def __exit__(self, *exc):
-        if self.lib:
-            self.lib.roctxProfilerPause(0)
-
-
-TIMED = TimedRegion(False)
+# Set by --profile-timed: the matmul is then dispatched only as graph replays (no eager
+# warm-up calls, no untimed pre-pass), so a kernel trace's per-kernel statistics cover the
+# same dispatches the HIP events time.
+GRAPH_ONLY = False
 
 
 def stats(per_call):
-    """median / p10 / p90 (us) of per-call times, one per replay."""
+    """median / mean / p10 / p90 (us) of per-call times, one per replay."""
     import numpy as np
     a = np.asarray(per_call, dtype=np.float64)
-    return {"median": float(np.median(a)), "p10": float(np.percentile(a, 10)),
+    return {"median": float(np.median(a)), "mean": float(a.mean()),
+            "p10": float(np.percentile(a, 10)),
             "p90": float(np.percentile(a, 90)), "replays": int(a.size)}
 
 
@@ -112,12 +96,11 @@ def time_replays(torch, stream, graph, steps, reps):
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for _ in range(reps)]
     torch.cuda.synchronize()
-    with TIMED:
-        for e0, e1 in events:
-            e0.record(stream)
-            graph.launch(stream)
-            e1.record(stream)
-        torch.cuda.synchronize()
+    for e0, e1 in events:
+        e0.record(stream)
+        graph.launch(stream)
+        e1.record(stream)
+    torch.cuda.synchronize()
     return [e0.elapsed_time(e1) * 1000.0 / steps for e0, e1 in events]
 
 
@@ -143,7 +126,8 @@ def time_m(torch, ctx, stream, sets, M, steps, warmup, N, K, bits, gs, ws, wsb):
     issue(steps, 0)
     graph = ctx.graph_end(stream)
     with torch.cuda.stream(stream):
-        issue(warmup, 1)               # eager warm-up (also checks the eager path)
+        if not GRAPH_ONLY:
+            issue(warmup, 1)           # eager warm-up (also checks the eager path)
         graph.launch(stream)           # graph warm-up
         times = time_replays(torch, stream, graph, steps, replays_for(steps))
     graph.close()
@@ -285,12 +269,11 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, one_graph=False):
             torch.cuda.synchronize()
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
-            with TIMED:
-                e0.record(stream)
-                for _ in range(n):
-                    fn()
-                e1.record(stream)
-                torch.cuda.synchronize()
+            e0.record(stream)
+            for _ in range(n):
+                fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1000.0 / n
 
     total = timed(forward, reps)
@@ -391,8 +374,36 @@ def cpu_baseline(seconds):
     }
 
 
+def trace_summary(path, steps):
+    """Per-dispatch kernel durations (ns) from a rocprofv3 kernel-trace CSV of a
+    --profile-timed run, per dfq_qmm kernel in dispatch order: its first `steps` dispatches
+    are the warm-up replay, the rest the timed replays."""
+    import csv
+    import numpy as np
+    runs = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if r["Kernel_Name"].startswith("dfq_qmm"):
+                runs.setdefault(r["Kernel_Name"], []).append(
+                    (int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+    out = {}
+    for name, ev in runs.items():
+        ev.sort()
+        d = np.array([e - s for s, e in ev], dtype=np.float64)
+
+        def st(a):
+            if not a.size:
+                return None
+            return {"dispatches": int(a.size), "mean": round(float(a.mean()), 1),
+                    "median": round(float(np.median(a)), 1),
+                    "p10": round(float(np.percentile(a, 10)), 1),
+                    "p90": round(float(np.percentile(a, 90)), 1)}
+        out[name] = {"all": st(d), "warmup_replay": st(d[:steps]), "timed": st(d[steps:])}
+    return out
+
+
 def main():
-    global TIMED
+    global GRAPH_ONLY
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
@@ -413,8 +424,17 @@ def main():
                     help="only run 20 plain device copies of this many MiB (the reference "
                          "point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     ap.add_argument("--profile-timed", action="store_true",
-                    help="trace only the timed replays (rocprofv3 --selected-regions)")
+                    help="dispatch the matmul only as graph replays, so that a kernel "
+                         "trace covers the timed calls (plus one warm-up replay)")
+    ap.add_argument("--trace-summary", metavar="CSV", default=None,
+                    help="summarise the run_kernel_trace.csv of a --profile-timed rocprofv3 "
+                         "run (per-dispatch durations of each dfq_qmm kernel, the warm-up "
+                         "replay apart from the timed replays) and exit; needs no GPU")
     args = ap.parse_args()
+
+    if args.trace_summary:
+        print(json.dumps(trace_summary(args.trace_summary, args.steps)), flush=True)
+        return
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -425,7 +445,7 @@ def main():
     import dflash_qmm
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
-    TIMED = TimedRegion(args.profile_timed)
+    GRAPH_ONLY = args.profile_timed
     dev = torch.device("cuda:0")
     if args.copy_mib:
         n = args.copy_mib << 20
@@ -453,16 +473,16 @@ def main():
 
     torch.cuda.synchronize()
     # one untimed pass first: the first M timed on a cold GPU otherwise reads up to ~1 us slow
-    saved, TIMED = TIMED, TimedRegion(False)
-    time_m(torch, ctx, stream, sets, ms[0], args.steps, args.warmup, N_OUT, K_IN, BITS, GS, ws,
-           ws.numel())
-    TIMED = saved
+    if not GRAPH_ONLY:
+        time_m(torch, ctx, stream, sets, ms[0], args.steps, args.warmup, N_OUT, K_IN, BITS, GS,
+               ws, ws.numel())
     dist = {}
     for m in ms:
         dist[m] = stats(time_m(torch, ctx, stream, sets, m, args.steps, args.warmup, N_OUT,
                                K_IN, BITS, GS, ws, ws.numel()))
         d = dist[m]
-        print(f"[bench] M={m}: {d['median']:.2f} us/call (p10 {d['p10']:.2f}, p90 "
+        print(f"[bench] M={m}: {d['median']:.2f} us/call (mean {d['mean']:.2f}, p10 "
+              f"{d['p10']:.2f}, p90 "
               f"{d['p90']:.2f}, {d['replays']} replays of {args.steps}), "
               f"{algorithmic_bytes(m) / d['median'] / 1e3:.0f} GB/s", file=sys.stderr,
               flush=True)
