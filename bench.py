@@ -402,6 +402,47 @@ def trace_summary(path, steps):
     return out
 
 
+def c5_trace_summary(path, layers=64):
+    """Per-op kernel durations of the timed verify forwards in a rocprofv3 kernel-trace CSV
+    of `bench.py --c5-only ...`.  A forward ends with the LM head's greedy-accept dispatch;
+    the first forward (the warm-up) and the LM-head-only calls after the forwards are left
+    out.  Per position within a layer: the kernel, its mean duration and the mean gap before
+    it (us)."""
+    import csv
+    rows = []
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if r["Kernel_Name"].startswith("dfq_"):
+                rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]),
+                             r["Kernel_Name"]))
+    rows.sort()
+    ends = [i for i, r in enumerate(rows) if r[2].endswith("_am") or "argmax_accept" in r[2]]
+    fwds = []
+    for i0, i1 in zip(ends, ends[1:]):
+        seg = rows[i0 + 1:i1 + 1]
+        if len(seg) < layers + 1 or (len(seg) - 1) % layers:
+            continue
+        fwds.append(seg)
+    if not fwds:
+        return {"forwards": 0}
+    per = (len(fwds[0]) - 1) // layers
+    ops = []
+    for j in range(per + 1):
+        dur, gap = [], []
+        for seg in fwds:
+            idx = [j + per * li for li in range(layers)] if j < per else [len(seg) - 1]
+            for i in idx:
+                dur.append(seg[i][1] - seg[i][0])
+                if i:
+                    gap.append(seg[i][0] - seg[i - 1][1])
+        name = fwds[0][j][2] if j < per else fwds[0][-1][2]
+        ops.append({"kernel": name, "mean_us": round(sum(dur) / len(dur) / 1e3, 2),
+                    "gap_before_us": round(sum(gap) / max(1, len(gap)) / 1e3, 2)})
+    spans = [(seg[-1][1] - seg[0][0]) / 1e3 for seg in fwds]
+    return {"forwards": len(fwds), "dispatches_per_forward": len(fwds[0]),
+            "span_us_per_forward": [round(v, 1) for v in spans], "ops": ops}
+
+
 def main():
     global GRAPH_ONLY
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
@@ -426,12 +467,18 @@ def main():
     ap.add_argument("--profile-timed", action="store_true",
                     help="dispatch the matmul only as graph replays, so that a kernel "
                          "trace covers the timed calls (plus one warm-up replay)")
+    ap.add_argument("--c5-trace-summary", metavar="CSV", default=None,
+                    help="summarise the run_kernel_trace.csv of a --c5-only rocprofv3 run "
+                         "(per-op durations of the timed forwards) and exit; needs no GPU")
     ap.add_argument("--trace-summary", metavar="CSV", default=None,
                     help="summarise the run_kernel_trace.csv of a --profile-timed rocprofv3 "
                          "run (per-dispatch durations of each dfq_qmm kernel, the warm-up "
                          "replay apart from the timed replays) and exit; needs no GPU")
     args = ap.parse_args()
 
+    if args.c5_trace_summary:
+        print(json.dumps(c5_trace_summary(args.c5_trace_summary)), flush=True)
+        return
     if args.trace_summary:
         print(json.dumps(trace_summary(args.trace_summary, args.steps)), flush=True)
         return
