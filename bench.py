@@ -77,15 +77,18 @@ def algorithmic_bytes(M, N=N_OUT, K=K_IN, bits=BITS, gs=GS):
     return N * K * bits // 8 + 2 * N * (K // gs) * 2 + M * K * 2 + M * N * 2
 
 
-def make_sets(torch, nsets, N, K, bits, gs, dev, seed=1):
+def make_sets(torch, nsets, N, K, bits, gs, dev, seed=1, dtype=None, scale_sd=0.02):
+    """`nsets` weight sets of uniform random codes, scales |N(0, scale_sd)| and biases
+    N(0, 0.01) in `dtype` (bf16 by default)."""
+    dtype = dtype or torch.bfloat16
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     sets = []
     for _ in range(nsets):
         w = torch.randint(-(2 ** 31), 2 ** 31 - 1, (N, K * bits // 32), dtype=torch.int32,
                           device=dev, generator=g)
-        s = (torch.randn(N, K // gs, device=dev, generator=g) * 0.02).abs().to(torch.bfloat16)
-        b = (torch.randn(N, K // gs, device=dev, generator=g) * 0.01).to(torch.bfloat16)
+        s = (torch.randn(N, K // gs, device=dev, generator=g) * scale_sd).abs().to(dtype)
+        b = (torch.randn(N, K // gs, device=dev, generator=g) * 0.01).to(dtype)
         sets.append((w, s, b))
     return sets
 
@@ -104,16 +107,18 @@ def time_replays(torch, stream, graph, steps, reps):
     return [e0.elapsed_time(e1) * 1000.0 / steps for e0, e1 in events]
 
 
-def time_m(torch, ctx, stream, sets, M, steps, warmup, N, K, bits, gs, ws, wsb):
+def time_m(torch, ctx, stream, sets, M, steps, warmup, N, K, bits, gs, ws, wsb, f16=False,
+           x_sd=1.0):
     """Per-call microseconds (one figure per replay) of `steps` graph-replayed calls at row
-    count M, over replays_for(steps) replays."""
+    count M, over replays_for(steps) replays (fp16 throughout with f16, else bf16)."""
     import dflash_qmm
     dev = sets[0][0].device
     g = torch.Generator(device=dev)
     g.manual_seed(100 + M)
-    x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
-    y = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
-    B = dflash_qmm.BF16
+    tdt = torch.float16 if f16 else torch.bfloat16
+    x = (torch.randn(M, K, device=dev, generator=g) * x_sd).to(tdt)
+    y = torch.empty(M, N, device=dev, dtype=tdt)
+    B = dflash_qmm.F16 if f16 else dflash_qmm.BF16
 
     def issue(count, start):
         for i in range(count):
@@ -132,6 +137,42 @@ def time_m(torch, ctx, stream, sets, M, steps, warmup, N, K, bits, gs, ws, wsb):
         times = time_replays(torch, stream, graph, steps, replays_for(steps))
     graph.close()
     return times
+
+
+# The other benchmark configurations, timed like the headline (one graph of `steps` calls,
+# replays_for(steps) replays, weights rotated over enough sets to exceed the 256 MB
+# Infinity Cache): (name, M, N, K, bits, group, fp16, x standard deviation, scale sd).
+CONFIGS = [
+    ("c1_m1_k4096_n4096_b4g64_f16", 1, 4096, 4096, 4, 64, True, 1.0, 0.02),
+    ("c3_down_m8_k17408_n5120_b4g64", 8, 5120, 17408, 4, 64, False, 0.5, 0.02),
+    ("c4_qkv_m8_k5120_n7168_b8g64", 8, 7168, 5120, 8, 64, False, 1.0, 0.004),
+    ("c4_o_m8_k5120_n5120_b8g64", 8, 5120, 5120, 8, 64, False, 1.0, 0.004),
+    ("c4_qkv_m8_k5120_n7168_b4g32", 8, 7168, 5120, 4, 32, False, 1.0, 0.02),
+    ("c4_o_m8_k5120_n5120_b4g32", 8, 5120, 5120, 4, 32, False, 1.0, 0.02),
+]
+
+
+def time_configs(torch, ctx, stream, dev, steps, warmup):
+    """Median per-call us, GB/s and fraction of 8 TB/s for each of CONFIGS."""
+    out = {}
+    for (name, M, N, K, bits, gs, f16, x_sd, s_sd) in CONFIGS:
+        nb = algorithmic_bytes(M, N, K, bits, gs)
+        nsets = max(2, -(-400_000_000 // (N * K * bits // 8)))
+        sets = make_sets(torch, nsets, N, K, bits, gs, dev, seed=3,
+                         dtype=torch.float16 if f16 else torch.bfloat16, scale_sd=s_sd)
+        wsb = ctx.workspace_bytes(M, N, K, bits, gs)
+        ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
+        d = stats(time_m(torch, ctx, stream, sets, M, steps, warmup, N, K, bits, gs, ws,
+                         ws.numel(), f16=f16, x_sd=x_sd))
+        out[name] = {"us_per_call": round(d["median"], 3), "p10": round(d["p10"], 3),
+                     "p90": round(d["p90"], 3), "bytes": nb,
+                     "gbs": round(nb / (d["median"] * 1e-6) / 1e9, 1),
+                     "frac": round(nb / (d["median"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "rotated_sets": nsets}
+        print(f"[bench] {name}: {d['median']:.2f} us/call, {out[name]['gbs']:.0f} GB/s",
+              file=sys.stderr, flush=True)
+        del sets
+    return out
 
 
 def time_read(torch, ctx, stream, nbytes, nsets, steps, dev):
@@ -455,6 +496,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-chain", action="store_true",
                     help="skip the 64-layer verify-forward measurement (c5_chain)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other benchmark configurations (C1, C3, C4)")
     ap.add_argument("--no-reference", action="store_true",
                     help="skip the read-ceiling and device-copy reference legs")
     ap.add_argument("--c5-only", choices=["separate", "fused", "fused_one_graph"],
@@ -595,9 +638,12 @@ def main():
         }
         print(f"[bench] device copy moving {nb8 / 1e6:.1f} MB: {uc_copy:.2f} us/copy",
               file=sys.stderr, flush=True)
-    if not args.no_chain:
-        del sets
+    del sets
+    torch.cuda.empty_cache()
+    if not args.no_configs:
+        out["configs"] = time_configs(torch, ctx, stream, dev, args.steps, args.warmup)
         torch.cuda.empty_cache()
+    if not args.no_chain:
         out["lm_head_accept"] = time_lm_head(torch, ctx, stream, dev)
         print(f"[bench] lm_head + accept: fused {out['lm_head_accept']['fused_us']} us, two "
               f"calls {out['lm_head_accept']['two_calls_us']} us", file=sys.stderr, flush=True)
