@@ -658,7 +658,8 @@ __device__ __forceinline__ void publish(const QmmParams& p, const KBlock& kbk, i
  * touched by agent-scope atomics, which complete (vmcnt) before the arrival is counted: no
  * cache write-back or invalidate. */
 template <int MT>
-__device__ void accept_finish(const QmmParams& p, uint64_t (&best)[4], int lane, int wg) {
+__device__ void accept_finish(const QmmParams& p, uint64_t (&best)[4], int lane,
+                              uint32_t* wg_arrivals) {
     const int q = lane >> 4, n = lane & 15;
 #pragma unroll
     for (int r = 0; r < 4; ++r)
@@ -669,7 +670,7 @@ __device__ void accept_finish(const QmmParams& p, uint64_t (&best)[4], int lane,
             const uint64_t o = ((uint64_t)hi << 32) | lo;
             best[r] = o > best[r] ? o : best[r];
         }
-    const int G = (int)gridDim.x, ng = min(16, G), grp = wg % ng;
+    const int G = (int)gridDim.x, ng = min(16, G), grp = (int)blockIdx.x % ng;
     if (n == 0 && lane < 32 * MT) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -682,31 +683,33 @@ __device__ void accept_finish(const QmmParams& p, uint64_t (&best)[4], int lane,
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the maxima have completed
     uint32_t last = 0;
     if (lane == 0) {
-        /* every publisher wave of the group's workgroups arrives */
-        const uint32_t size_g = (uint32_t)((G / ng + (grp < G % ng ? 1 : 0)) * kPublishers);
-        if (__hip_atomic_fetch_add(p.am_count + grp * 32, 1u, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT) + 1u == size_g)
+        /* the workgroup's publishers meet in LDS; the second counts the workgroup */
+        if (__hip_atomic_fetch_add(wg_arrivals, 1u, __ATOMIC_ACQ_REL,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP) + 1u == (uint32_t)kPublishers)
             last = __hip_atomic_fetch_add(p.am_count + 16 * 32, 1u, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT) + 1u == (uint32_t)ng;
+                                          __HIP_MEMORY_SCOPE_AGENT) + 1u == (uint32_t)G;
     }
     if (!__builtin_amdgcn_readfirstlane(last)) return;
     bool bad = false;
     if (lane < p.M) {
+        /* every group's key and the proposal in flight together: one round trip, not one
+         * per group */
+        const int32_t prop = (p.am_proposals && lane < p.M - 1) ? p.am_proposals[lane] : 0;
+        uint64_t kk[16];  // groups past ng hold zero keys (never raised): read them too
+#pragma unroll
+        for (int g = 0; g < 16; ++g)
+            kk[g] = __hip_atomic_exchange(p.am_keys + (size_t)g * p.M + lane, 0ull,
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         uint64_t k = 0;
-        for (int g = 0; g < ng; ++g) {
-            const uint64_t kk = __hip_atomic_exchange(p.am_keys + (size_t)g * p.M + lane, 0ull,
-                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            k = kk > k ? kk : k;
-        }
+#pragma unroll
+        for (int g = 0; g < 16; ++g) k = kk[g] > k ? kk[g] : k;
         const int32_t tok = k ? (int32_t)~(uint32_t)k : -1;
         if (p.am_tokens) p.am_tokens[lane] = tok;
-        bad = lane < p.M - 1 && !(p.am_proposals && p.am_proposals[lane] == tok);
+        bad = lane < p.M - 1 && !(p.am_proposals && prop == tok);
     }
     const uint64_t badm = __builtin_amdgcn_ballot_w64(bad);
     if (lane == 0) {
         if (p.am_accepted) *p.am_accepted = badm ? (int32_t)__builtin_ctzll(badm) : p.M - 1;
-        for (int g = 0; g < ng; ++g)
-            __hip_atomic_store(p.am_count + g * 32, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(p.am_count + 16 * 32, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
@@ -768,7 +771,8 @@ __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
         remaining -= found;
         if (!found) __builtin_amdgcn_s_sleep(1);
     }
-    if constexpr (AM) accept_finish<MT>(p, best, lane, wg);
+    /* the word after the take counter (the streaming waves' tcnt + ntl, by their formula) */
+    if constexpr (AM) accept_finish<MT>(p, best, lane, tcnt + ((b - 1) / SS - ta + 1) + 1);
 }
 
 /* ---------------------------------------------------------------------------------- */
@@ -974,7 +978,10 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
         if ((i & (XR - 1)) >= p.M) xsum[i] = 0.0f;
     for (int i = tid; i < ntl; i += kThreads) tcnt[i] = 0u;
     for (int i = tid; i < R; i += kThreads) gen[i] = (uint32_t)i;
-    if (tid == 0) *gcnt = (uint32_t)(kWaves * PF);
+    if (tid == 0) {
+        *gcnt = (uint32_t)(kWaves * PF);
+        gcnt[1] = 0u;  // the publishers' arrival count (greedy-accept mode)
+    }
     __builtin_amdgcn_sched_barrier(0);
     };
     auto issue_first = [&]() {

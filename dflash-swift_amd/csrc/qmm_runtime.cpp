@@ -222,7 +222,7 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
             p.ring = (int)ring;
             p.gen_off = p.part_off + (int)ring * 512 * mt;
             p.cnt_off = p.gen_off + (int)ring * 4;
-            need = (size_t)p.cnt_off + (size_t)(ntl_max + 1) * 4;
+            need = (size_t)p.cnt_off + (size_t)(ntl_max + 2) * 4;
             if (need <= lds_max || G == U) break;
         }
         if (need > lds_max) return false;
@@ -270,7 +270,7 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
         p.ring = (int)std::min<int64_t>(p.umax, 4 * ss_max + 24);
         p.gen_off = p.part_off + p.ring * 512 * mt;
         p.cnt_off = p.gen_off + p.ring * 4;
-        const size_t need = (size_t)p.cnt_off + (size_t)(tmax + 1) * 4;
+        const size_t need = (size_t)p.cnt_off + (size_t)(tmax + 2) * 4;
         if (need > lds_max) return false;
         p.Gkb = (int)G;
         p.nslot_kb = 1;
