@@ -1410,11 +1410,13 @@ __device__ __forceinline__ void argmax_accept(const uint16_t* logits, int M, int
     __syncthreads();
     if (!last) return;
     for (int m = tid; m < M; m += 256) {
+        /* the proposal and the key in flight together */
+        const int32_t prop = (proposals && m < M - 1) ? proposals[m] : 0;
         const uint64_t k = __hip_atomic_exchange(keys + m, 0ull, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
         const int32_t tok = k ? (int32_t)~(uint32_t)k : -1;
         if (tokens) tokens[m] = tok;
-        if (m < M - 1 && !(proposals && proposals[m] == tok)) atomicMin(&first_bad, m);
+        if (m < M - 1 && !(proposals && prop == tok)) atomicMin(&first_bad, m);
     }
     __syncthreads();
     if (tid == 0) {
