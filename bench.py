@@ -341,7 +341,7 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, one_graph=False):
     }
 
 
-def time_lm_head(torch, ctx, stream, dev, steps=20, nsets=2):
+def time_lm_head(torch, ctx, stream, dev, steps=20, nsets=4, reps=20):
     """The C5 LM head (M=8, 151936 x 5120, 4-bit g64) with the greedy accept, graph-replayed
     over rotated weights: fused (dfq_qmm_argmax_accept, no logits written) and as two calls
     (dfq_qmm to logits, then dfq_argmax_accept).  Per-call us."""
@@ -373,12 +373,13 @@ def time_lm_head(torch, ctx, stream, dev, steps=20, nsets=2):
         graph = ctx.graph_end(stream)
         with torch.cuda.stream(stream):
             graph.launch(stream)
-            out[form] = stats(time_replays(torch, stream, graph, steps, 10))["median"]
+            out[form] = stats(time_replays(torch, stream, graph, steps, reps))["median"]
         graph.close()
     nb = algorithmic_bytes(M, V, K)
     return {
         "workload": ("LM head M=8, 151936 x 5120 4-bit g64 bf16, with the greedy accept; "
-                     f"{nsets} rotated weight sets (880 MB)"),
+                     f"{nsets} rotated weight sets ({nsets * 440} MB), median of {reps} "
+                     f"replays of {steps} calls"),
         "fused_us": round(out["fused"], 2),
         "two_calls_us": round(out["two_calls"], 2),
         "ideal_us_at_8TBs": round(nb / (HBM_PEAK_GBS * 1e3), 2),
