@@ -29,6 +29,9 @@ struct Plan {
     int part_off = 0;   /* LDS offset of the per-unit partial tiles          */
     int cnt_off = 0;    /* LDS offset of the tile arrival counters           */
     int gen_off = 0;    /* LDS offset of the partial slots' generations      */
+    int tout_off = 0;   /* LDS offset of the finished tiles' fp32 sums        */
+    int key_off = 0;    /* LDS offset of the per-row greedy-accept keys      */
+    bool burst = false; /* tiles without a pair exchange leave at the end      */
     int ring = 0;       /* partial-tile slots (a ring over the take order)   */
     int umax = 0;       /* most units per workgroup                          */
     int lds_bytes = 0;  /* dynamic LDS requested per workgroup               */

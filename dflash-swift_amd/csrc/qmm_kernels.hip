@@ -638,57 +638,40 @@ __device__ __forceinline__ void publish(const QmmParams& p, const KBlock& kbk, i
     }
 }
 
-/* The publisher wave of a qmm_mt8 workgroup.  The streaming waves only sum a finished tile
- * into LDS and mark it kTileDone; this wave, which issues no weight loads, writes it out (y,
- * or the workspace fix-up of a tile shared with other workgroups or k-blocks) while the
- * streaming continues.  Global stores and atomics in the streaming waves would sit in the
- * same in-order vmcnt queue as their prefetch and make every later wait cover them.
- *
- * It polls the tile counters of its workgroup (one lane per tile, sleeping between empty
- * polls) until each of the ntl tiles has been written.  Every unit of [a, b) is taken by
- * exactly one streaming wave, so every tile reaches kTileDone and the loop ends. */
-/* Greedy-accept mode, after the publisher's last tile: its keys of each row (lane (q, n)
- * holds rows 4q..4q+3 of the columns it finished) are reduced over the 16 columns of the lane
- * group and folded into the workgroup group's keys with an agent-scope atomic max (16 groups
- * of workgroups, so that no key takes more than a sixteenth of the atomics).  Arrivals are
- * counted the same way: a counter per group, then one over the groups.  The last workgroup
- * takes every group's keys (exchanging them with zero), writes each row's token (the column
- * of its key, -1 for a row of NaN) and the accepted run -- the first verify row i < M-1 whose
- * token differs from proposals[i], or M-1 -- and re-arms the counters.  The keys are only
- * touched by agent-scope atomics, which complete (vmcnt) before the arrival is counted: no
- * cache write-back or invalidate. */
-template <int MT>
-__device__ void accept_finish(const QmmParams& p, uint64_t (&best)[4], int lane,
-                              uint32_t* wg_arrivals) {
-    const int q = lane >> 4, n = lane & 15;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int s = 8; s > 0; s >>= 1) {
-            const uint32_t lo = __shfl_xor((uint32_t)best[r], s, 16);
-            const uint32_t hi = __shfl_xor((uint32_t)(best[r] >> 32), s, 16);
-            const uint64_t o = ((uint64_t)hi << 32) | lo;
-            best[r] = o > best[r] ? o : best[r];
-        }
+/* Whether tile t of the range [a, b) (k-block of SS chunks) is finished by the pair exchange
+ * while the streaming goes on: it has exactly two parts in the whole split (a tile cut by the
+ * range, or any tile of a two-k-block split without a second pass).  Every other tile is
+ * written at the end of the workgroup: a whole tile to y, a part of a reduce split to its
+ * workspace slot. */
+__device__ __forceinline__ bool exchange_tile(const QmmParams& p, int t, int a, int b, int SS) {
+    const bool whole = max(a, t * SS) == t * SS && min(b, (t + 1) * SS) == (t + 1) * SS &&
+                       p.nkb == 1;
+    return !whole && !p.reduce;
+}
+
+/* Greedy-accept mode, once every output of the workgroup has been folded into its row's key
+ * in LDS (keys[m], zero at the start): wave 0 folds them into the workgroup group's keys with
+ * an agent-scope atomic max (16 groups of workgroups, so that no key takes more than a
+ * sixteenth of the atomics), waits for the maxima to complete (vmcnt) and counts the
+ * workgroup on one device-wide counter.  The last workgroup takes every group's keys
+ * (exchanging them with zero), writes each row's token (the column of its key, -1 for a row
+ * of NaN) and the accepted run -- the first verify row i < M-1 whose token differs from
+ * proposals[i], or M-1 -- and re-arms the counter.  The keys and the counter are only
+ * touched by agent-scope atomics, which complete before the arrival is counted: no cache
+ * write-back or invalidate. */
+__device__ void accept_finish(const QmmParams& p, const uint64_t* keys, int lane) {
     const int G = (int)gridDim.x, ng = min(16, G), grp = (int)blockIdx.x % ng;
-    if (n == 0 && lane < 32 * MT) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = 4 * q + r;
-            if (m < p.M && best[r])
-                __hip_atomic_fetch_max(p.am_keys + (size_t)grp * p.M + m, best[r],
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+    if (lane < p.M) {
+        const uint64_t k = keys[lane];
+        if (k)
+            __hip_atomic_fetch_max(p.am_keys + (size_t)grp * p.M + lane, k, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
     }
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the maxima have completed
     uint32_t last = 0;
-    if (lane == 0) {
-        /* the workgroup's publishers meet in LDS; the second counts the workgroup */
-        if (__hip_atomic_fetch_add(wg_arrivals, 1u, __ATOMIC_ACQ_REL,
-                                   __HIP_MEMORY_SCOPE_WORKGROUP) + 1u == (uint32_t)kPublishers)
-            last = __hip_atomic_fetch_add(p.am_count + 16 * 32, 1u, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT) + 1u == (uint32_t)G;
-    }
+    if (lane == 0)
+        last = __hip_atomic_fetch_add(p.am_count + 16 * 32, 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) + 1u == (uint32_t)G;
     if (!__builtin_amdgcn_readfirstlane(last)) return;
     bool bad = false;
     if (lane < p.M) {
@@ -714,55 +697,64 @@ __device__ void accept_finish(const QmmParams& p, uint64_t (&best)[4], int lane,
     }
 }
 
+/* The publisher wave of a qmm_mt8 workgroup: it finishes the pair-exchange tiles (a device-
+ * scope round trip each) while the streaming continues, and, unless the split writes its
+ * outputs at the end ("burst"), writes every other tile as it finishes.  The streaming waves
+ * only sum a finished tile into the LDS output area and mark it kTileDone.  Global stores and
+ * atomics in the streaming waves would sit in the same in-order vmcnt queue as their prefetch
+ * and make every later wait cover them.
+ *
+ * Tiles are taken in the order the take order completes them (the tile shared with the next
+ * workgroup first, then the first tile, ...), publisher pi taking ranks pi, pi + kPublishers,
+ * ..., so that the two shared tiles' exchanges run side by side.  It polls their counters (one
+ * lane per tile, sleeping between empty polls) until each has been published: every unit of
+ * [a, b) is taken by exactly one streaming wave, so every tile reaches kTileDone.  In greedy-
+ * accept mode its outputs' keys go to the rows' keys in LDS. */
 template <bool F16, int MT, bool AM>
 __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
-                               const KBlock& kbk, int lane, int wg, int pi) {
+                               const KBlock& kbk, int lane, int pi) {
     const int SS = kbk.SS;
     const int q = lane >> 4, n = lane & 15;
     const int ta = a / SS;
     const int ntl = (b > a) ? (b - 1) / SS - ta + 1 : 0;
     uint32_t* tcnt = (uint32_t*)(lds_base() + p.lds_cnt_off);
-    uint32_t* gen = (uint32_t*)(lds_base() + p.lds_gen_off);
-    const float* part = (const float*)(lds_base() + p.lds_part_off);
-    const int s1 = max(a, ((b - 1) / SS) * SS), nrot = b - s1;  // the take order (unit_of)
+    const float* tout = (const float*)(lds_base() + p.lds_tout_off);
     __syncthreads();  // the staging barrier of the streaming waves (tile counters zeroed)
     uint64_t best[4] = {0, 0, 0, 0};  // greedy-accept keys of rows 4q..4q+3
-    /* publisher pi takes the tiles pi, pi + kPublishers, ... of the workgroup */
-    const int nown = ntl > pi ? (ntl - pi + kPublishers - 1) / kPublishers : 0;
-    int remaining = nown;
+    auto tile_of = [&](int rk) { return rk == 0 ? ntl - 1 : rk - 1; };
+    const int nrank = ntl > pi ? (ntl - pi + kPublishers - 1) / kPublishers : 0;
+    int remaining = 0;
+    for (int base = 0; base < nrank; base += 64) {
+        const int rk = pi + (base + lane) * kPublishers;
+        const bool own = base + lane < nrank &&
+                         (!p.burst || exchange_tile(p, ta + tile_of(rk), a, b, SS));
+        remaining += __builtin_popcountll(__builtin_amdgcn_ballot_w64(own));
+    }
     while (remaining > 0) {
         int found = 0;
-        for (int base = 0; base < nown; base += 64) {
-            const int tl = pi + (base + lane) * kPublishers;
+        for (int base = 0; base < nrank; base += 64) {
+            const int rk = pi + (base + lane) * kPublishers;
             bool ready = false;
-            if (base + lane < nown)
-                ready = __hip_atomic_load(tcnt + tl, __ATOMIC_ACQUIRE,
+            if (base + lane < nrank && (!p.burst || exchange_tile(p, ta + tile_of(rk), a, b, SS)))
+                ready = __hip_atomic_load(tcnt + tile_of(rk), __ATOMIC_ACQUIRE,
                                           __HIP_MEMORY_SCOPE_WORKGROUP) == kTileDone;
             uint64_t m = __builtin_amdgcn_ballot_w64(ready);
             while (m) {
                 const int bit = __builtin_ctzll(m);
                 m &= m - 1;
-                const int tlb = pi + (base + bit) * kPublishers;
+                const int tlb = tile_of(pi + (base + bit) * kPublishers);
                 const int t = ta + tlb;
-                const int u0 = max(a, t * SS), u1 = min(b, (t + 1) * SS);
-                const int g0 = u0 >= s1 ? u0 - s1 : nrot + (u0 - a);  // take index of u0
-                const int sl0 = g0 % p.ring;
                 f32x4_t v = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (lane < 32 * MT) v = *(const f32x4_t*)(part + sl0 * (MT * 128) + tile_off(lane));
-                /* the tile's sum is read: its slot may take the unit p.ring takes later (LDS
-                 * operations of a wave complete in order, so the read precedes the release) */
-                if (lane == 0)
-                    __hip_atomic_store(gen + sl0, (uint32_t)(g0 + p.ring), __ATOMIC_RELEASE,
-                                       __HIP_MEMORY_SCOPE_WORKGROUP);
+                if (lane < 32 * MT) v = *(const f32x4_t*)(tout + tlb * (MT * 128) + tile_off(lane));
                 const int first = tile_first_owner(kbk, t);
-                if (u0 == t * SS && u1 == (t + 1) * SS && p.nkb == 1) {
-                    store_y<F16, AM>(p, t, lane, v, best);
-                } else if (p.reduce) {
-                    /* summed by the second pass: no round trip here */
-                    if (lane < 32 * MT) put_tile4(tile_slot(p, t, kb, cl - first, lane), v);
+                if (!exchange_tile(p, t, a, b, SS)) {
+                    if (!p.reduce || (max(a, t * SS) == t * SS && min(b, (t + 1) * SS) == (t + 1) * SS &&
+                                      p.nkb == 1))
+                        store_y<F16, AM>(p, t, lane, v, best);
+                    else if (lane < 32 * MT)  /* summed by the second pass: no round trip here */
+                        put_tile4(tile_slot(p, t, kb, cl - first, lane), v);
                 } else {
-                    publish<F16, AM>(p, kbk, t, kb * p.nslot_kb + (cl - first),
-                                     lane, v, best);
+                    publish<F16, AM>(p, kbk, t, kb * p.nslot_kb + (cl - first), lane, v, best);
                 }
                 if (lane == 0) tcnt[tlb] = kTileOut;
                 ++found;
@@ -771,8 +763,130 @@ __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
         remaining -= found;
         if (!found) __builtin_amdgcn_s_sleep(1);
     }
-    /* the word after the take counter (the streaming waves' tcnt + ntl, by their formula) */
-    if constexpr (AM) accept_finish<MT>(p, best, lane, tcnt + ((b - 1) / SS - ta + 1) + 1);
+    if constexpr (AM) {
+        /* the lane keys of rows 4q..4q+3, reduced over the 16 columns of the lane group,
+         * into the rows' keys in LDS */
+        uint64_t* keys = (uint64_t*)(lds_base() + p.lds_key_off);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int s = 8; s > 0; s >>= 1) {
+                const uint32_t lo = __shfl_xor((uint32_t)best[r], s, 16);
+                const uint32_t hi = __shfl_xor((uint32_t)(best[r] >> 32), s, 16);
+                const uint64_t o = ((uint64_t)hi << 32) | lo;
+                best[r] = o > best[r] ? o : best[r];
+            }
+        if (n == 0 && lane < 32 * MT)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (4 * q + r < p.M && best[r])
+                    __hip_atomic_fetch_max(keys + 4 * q + r, best[r], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+}
+
+/* The end of a workgroup, reached by every wave once its work is done: after a barrier (every
+ * tile summed into the LDS output area, every exchange tile published), all waves write the
+ * remaining tiles.  A whole tile goes to y as 16-byte rows of 8 outputs (plus the linear
+ * bias; the gate|up epilogue writes 8 outputs h = silu(g)*u per row), and, in greedy-accept
+ * mode, each row's outputs are folded into its key; a tile's part of a reduce split goes to
+ * its workspace slot.  Output stores happen here, after the streaming, so that they neither
+ * queue behind the weight loads nor hold ring slots. */
+template <bool F16, int MT, bool AM>
+__device__ void finish_wg(const QmmParams& p, const KBlock& kbk, int kb, int cl, int a, int b,
+                          int tid) {
+    __syncthreads();
+    /* opaque: nothing of the write-out is computed (and held in registers) before this point */
+    __asm__ volatile("" : "+v"(tid));
+    const int SS = kbk.SS;
+    uint64_t* keys = (uint64_t*)(lds_base() + p.lds_key_off);
+    if (b > a && p.burst) {
+        const int ta = a / SS, ntl = (b - 1) / SS - ta + 1;
+        const float* tout = (const float*)(lds_base() + p.lds_tout_off);
+        const int M = p.M;
+        const uint16_t* lb16 = (const uint16_t*)p.lbias;
+        /* whole tiles: items (tile, row, half of 8 columns), or (tile, row) for the epilogue */
+        const int per = p.epi ? M : 2 * M;
+        for (int i = tid; i < ntl * per; i += kBlock) {
+            const int tl = i / per, r = i - tl * per;
+            const int t = ta + tl;
+            if (!(max(a, t * SS) == t * SS && min(b, (t + 1) * SS) == (t + 1) * SS && p.nkb == 1))
+                continue;
+            const float* tb = tout + tl * (MT * 128);
+            uint16_t o[8];
+            if (p.epi) {
+                const int m = r;
+                const float* tr = tb + (m >> 3) * 128 + (m & 7);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    float g = tr[j * 8], u = tr[(8 + j) * 8];
+                    if (lb16) {
+                        g += elem_to_f32<F16>(lb16[t * 16 + j]);
+                        u += elem_to_f32<F16>(lb16[t * 16 + 8 + j]);
+                    }
+                    o[j] = silu_mul_round<F16>(g, u);
+                }
+                uint16_t* dst = (uint16_t*)p.y + (size_t)m * (p.N / 2) + t * 8;
+                if (((uintptr_t)dst & 15) == 0) {
+                    u32x4_t w;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) w[j] = (uint32_t)o[2 * j] | ((uint32_t)o[2 * j + 1] << 16);
+                    *(u32x4_t*)dst = w;
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) put16(dst + j, o[j]);
+                }
+            } else {
+                const int m = r >> 1, hh = r & 1;
+                const int c0 = t * 16 + hh * 8;
+                if (c0 >= p.N) continue;
+                const float* tr = tb + (m >> 3) * 128 + (hh * 8) * 8 + (m & 7);
+                uint64_t kbest = 0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int col = c0 + j;
+                    float v = tr[j * 8];
+                    if (lb16 && col < p.N) v += elem_to_f32<F16>(lb16[col]);
+                    o[j] = f32_to_out<F16>(v);
+                    if constexpr (AM)
+                        if (col < p.N) fold_key<F16>(kbest, o[j], col);
+                }
+                if (!AM || p.y) {
+                    uint16_t* dst = (uint16_t*)p.y + (size_t)m * p.N + c0;
+                    if (c0 + 8 <= p.N && ((uintptr_t)dst & 15) == 0) {
+                        u32x4_t w;
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            w[j] = (uint32_t)o[2 * j] | ((uint32_t)o[2 * j + 1] << 16);
+                        *(u32x4_t*)dst = w;
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 8; ++j)
+                            if (c0 + j < p.N) put16(dst + j, o[j]);
+                    }
+                }
+                if constexpr (AM)
+                    if (kbest)
+                        __hip_atomic_fetch_max(keys + m, kbest, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+        }
+        /* parts of a reduce split: each tile's fp32 part to its workspace slot */
+        if (p.reduce) {
+            for (int i = tid; i < ntl * 32 * MT; i += kBlock) {
+                const int tl = i / (32 * MT), li = i - tl * (32 * MT);
+                const int t = ta + tl;
+                if (max(a, t * SS) == t * SS && min(b, (t + 1) * SS) == (t + 1) * SS && p.nkb == 1)
+                    continue;  // whole: written to y above
+                put_tile4(tile_slot(p, t, kb, cl - tile_first_owner(kbk, t), li),
+                          *(const f32x4_t*)(tout + tl * (MT * 128) + tile_off(li)));
+            }
+        }
+    }
+    if constexpr (AM) {
+        __syncthreads();  // every output folded into its row's key
+        if ((tid >> 6) == 0) accept_finish(p, keys, tid & 63);
+    }
 }
 
 /* ---------------------------------------------------------------------------------- */
@@ -842,7 +956,8 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
     const int b = range_start(kbk, cl + 1);
 
     if (wave >= kWaves) {
-        publisher_wave<F16, MT, AM>(p, kb, cl, a, b, kbk, lane, wg, wave - kWaves);
+        publisher_wave<F16, MT, AM>(p, kb, cl, a, b, kbk, lane, wave - kWaves);
+        finish_wg<F16, MT, AM>(p, kbk, kb, cl, a, b, tid);
         return;
     }
 
@@ -948,6 +1063,7 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
     const int R = p.ring;
     float* xsum = (float*)(lds + p.lds_xsum_off);
     float* part = (float*)(lds + p.lds_part_off);
+    float* tout = (float*)(lds + p.lds_tout_off);
     uint32_t* gen = (uint32_t*)(lds + p.lds_gen_off);
     uint32_t* tcnt = (uint32_t*)(lds + p.lds_cnt_off);
     const int ta = a / SS;               // first tile touched by this workgroup
@@ -978,6 +1094,7 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
         if ((i & (XR - 1)) >= p.M) xsum[i] = 0.0f;
     for (int i = tid; i < ntl; i += kThreads) tcnt[i] = 0u;
     for (int i = tid; i < R; i += kThreads) gen[i] = (uint32_t)i;
+    if (tid < 16) ((uint64_t*)(lds + p.lds_key_off))[tid] = 0ull;  // greedy-accept row keys
     if (tid == 0) {
         *gcnt = (uint32_t)(kWaves * PF);
         gcnt[1] = 0u;  // the publishers' arrival count (greedy-accept mode)
@@ -1138,8 +1255,8 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
         }
         if (lane < 32 * MT) *(f32x4_t*)(part + sl * (MT * 128) + tile_off(lane)) = v;
         /* arrive at tile t; the wave that completes its units here sums them (in unit order)
-         * into the slot of the tile's first unit, releases the other slots, and hands the
-         * tile to the publisher wave */
+         * into the tile's block of the output area, releases all the tile's slots, and marks
+         * the tile done (for the publisher wave, or the write-out at the end) */
         const int u0 = max(a, t * SS), u1 = min(b, (t + 1) * SS);
         uint32_t old = 0;
         if (lane == 0)
@@ -1153,10 +1270,10 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
                 f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
                 for (int i = 0, s2 = sl0; i < u1 - u0; ++i, s2 = (s2 + 1 == R) ? 0 : s2 + 1)
                     sum += *(const f32x4_t*)(part + s2 * (MT * 128) + tile_off(lane));
-                *(f32x4_t*)(part + sl0 * (MT * 128) + tile_off(lane)) = sum;
+                *(f32x4_t*)(tout + (t - ta) * (MT * 128) + tile_off(lane)) = sum;
             }
             if (lane == 0) {
-                for (int i = 1; i < u1 - u0; ++i)
+                for (int i = 0; i < u1 - u0; ++i)
                     __hip_atomic_store(gen + (g0 + i) % R, (uint32_t)(g0 + i + R),
                                        __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
                 __hip_atomic_store(tcnt + (t - ta), kTileDone, __ATOMIC_RELEASE,
@@ -1227,6 +1344,7 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
         }
     }
     }
+    finish_wg<F16, MT, AM>(p, kbk, kb, cl, a, b, tid);
 }
 
 

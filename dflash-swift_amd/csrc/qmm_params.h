@@ -27,12 +27,17 @@
  *    cross-workgroup fix-ups happen early;
  *  - every unit's partial tile goes to a slot of an LDS ring over the take order (a slot is
  *    reused once its generation allows); the wave that completes a tile's
- *    units in this workgroup (an LDS arrival counter) sums the slots in unit order and marks
- *    the tile done; the workgroup's publisher wave then writes y, or, for a tile shared with
- *    other workgroups (or k-blocks), its part: with at most two parts per tile anywhere in
- *    the split, one 64-bit atomic exchange per element (the second arriver writes y);
- *    otherwise ("reduce" splits) a plain store into the tile's workspace slot, and a second
- *    kernel sums every tile's slots in a fixed order.
+ *    units in this workgroup (an LDS arrival counter) sums the slots in unit order into the
+ *    tile's block of an LDS output area, frees the tile's slots and marks the tile done;
+ *  - a tile with exactly two parts in the whole split (its units in two workgroups, or in
+ *    two k-blocks of an aligned split) is finished while the streaming goes on: the
+ *    workgroup's publisher wave exchanges its part with one 64-bit atomic per element (the
+ *    second arriver writes y);
+ *  - every other tile -- a whole tile for y, or, in "reduce" splits, a part for its
+ *    workspace slot, which a second kernel sums in a fixed order -- is written by the
+ *    publisher waves as it finishes, or ("burst" splits, where a workgroup holds many tiles)
+ *    by all waves at the end of the workgroup, after a barrier, with 16-byte row stores, so
+ *    that no output store interleaves with the weight stream.
  */
 typedef struct QmmParams {
     const void* x;          /* [M][K] activations, bf16 or fp16                      */
@@ -58,6 +63,11 @@ typedef struct QmmParams {
     int32_t lds_part_off;   /* byte offset of the per-unit partial tiles in LDS       */
     int32_t lds_cnt_off;    /* byte offset of the per-tile arrival counters in LDS    */
     int32_t lds_gen_off;    /* byte offset of the partial slots' generations in LDS   */
+    int32_t lds_tout_off;   /* byte offset of the finished tiles' fp32 sums in LDS, one
+                               [mt][n][8] block per tile the range touches            */
+    int32_t lds_key_off;    /* byte offset of 16 per-row 64-bit greedy-accept keys    */
+    int32_t burst;          /* 1: tiles without a pair exchange leave at the end of the
+                               workgroup; 0: the publisher waves write them as they finish */
     int32_t umax;           /* most units one workgroup holds                         */
     int32_t ring;           /* partial-tile slots in LDS (a ring over the take order) */
     uint32_t w_bytes;       /* size of w in bytes (< 2^31)                            */

@@ -164,6 +164,13 @@ static int tile_owners(int64_t t, int64_t SS, int64_t G, int64_t T) {
 /* Largest workgroup share (units) for which a narrow N is split into two k-blocks of one tile
  * per workgroup. */
 static constexpr int kShortSplitUnits = 24;
+/* Fewest tiles a workgroup touches for which its outputs are written at its end rather than
+ * as each tile finishes.  Stores from the publisher waves interleave with the weight stream;
+ * written at the end they do not, but the end then waits for every wave.  Measured on MI355X
+ * at M = 8, K = 5120 (us, at the end against as they finish): the LM head N = 151936 (38
+ * tiles) 83.3 against 90.7; gate|up N = 34816 (10) 25.25 against 25.55; N = 17408 (6) 16.54
+ * against 16.37; N = 7168 (3) 11.67 against 11.41. */
+static constexpr int kBurstTiles = 8;
 /* Most tiles per workgroup for which two k-blocks take an aligned split rather than
  * stream-K ranges with the second pass.  Every tile of an aligned split is finished by a
  * pair exchange of per-element device-scope atomics.  Measured on MI355X with 16 rows at
@@ -222,7 +229,10 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
             p.ring = (int)ring;
             p.gen_off = p.part_off + (int)ring * 512 * mt;
             p.cnt_off = p.gen_off + (int)ring * 4;
-            need = (size_t)p.cnt_off + (size_t)(ntl_max + 2) * 4;
+            /* then each touched tile's finished sum, and 16 per-row 64-bit keys */
+            p.tout_off = (int)(((size_t)p.cnt_off + (size_t)(ntl_max + 2) * 4 + 15) & ~(size_t)15);
+            p.key_off = p.tout_off + (int)ntl_max * 512 * mt;
+            need = (size_t)p.key_off + 16 * 8;
             if (need <= lds_max || G == U) break;
         }
         if (need > lds_max) return false;
@@ -234,6 +244,10 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
         /* At most two parts per tile: the pair exchange inside the kernel.  More: plain slot
          * stores and the fixed-order second kernel. */
         p.reduce = d > 1 ? (d > 2 || nslot > 1) : nslot > 2;
+        {
+            const int64_t umax = p.umax, ntl_max = (umax + ss_min - 1) / ss_min + 1;
+            p.burst = !p.reduce && ntl_max >= kBurstTiles;
+        }
         /* Ask for more than half the CU's LDS so that exactly one workgroup lands per CU. */
         const size_t want = std::max(need, lds_max / 2 + 256);
         p.lds_bytes = (int)std::min(want, lds_max);
@@ -270,7 +284,9 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
         p.ring = (int)std::min<int64_t>(p.umax, 4 * ss_max + 24);
         p.gen_off = p.part_off + p.ring * 512 * mt;
         p.cnt_off = p.gen_off + p.ring * 4;
-        const size_t need = (size_t)p.cnt_off + (size_t)(tmax + 2) * 4;
+        p.tout_off = (int)(((size_t)p.cnt_off + (size_t)(tmax + 2) * 4 + 15) & ~(size_t)15);
+        p.key_off = p.tout_off + (int)tmax * 512 * mt;
+        const size_t need = (size_t)p.key_off + 16 * 8;
         if (need > lds_max) return false;
         p.Gkb = (int)G;
         p.nslot_kb = 1;
@@ -636,6 +652,9 @@ static QmmParams fill_params(const Plan& pl, const void* x, const uint32_t* w,
     p.lds_part_off = pl.part_off;
     p.lds_cnt_off = pl.cnt_off;
     p.lds_gen_off = pl.gen_off;
+    p.lds_tout_off = pl.tout_off;
+    p.lds_key_off = pl.key_off;
+    p.burst = pl.burst ? 1 : 0;
     p.umax = pl.umax;
     p.ring = pl.ring;
     p.w_bytes = (uint32_t)((int64_t)N * K * bits / 8);
@@ -1010,21 +1029,21 @@ dfq_status dfq_graph_destroy(dfq_graph* gr) {
 
 /* The fields of a split as the debug calls report them. */
 static void plan_fields(const Plan& p, int* out) {
-    const int v[14] = {p.T,   p.SS,          p.nkb,           p.Gkb, p.nslot_kb, p.kr,
+    const int v[15] = {p.T,   p.SS,          p.nkb,           p.Gkb, p.nslot_kb, p.kr,
                        p.lds_bytes, p.need_ws ? 1 : 0, p.ch, p.umax, p.chunks,
-                       p.reduce ? 1 : 0, p.ring, p.aligned ? 1 : 0};
+                       p.reduce ? 1 : 0, p.ring, p.aligned ? 1 : 0, p.burst ? 1 : 0};
     std::memcpy(out, v, sizeof v);
 }
 
 /* Fills the work split the fast kernel uses for a shape: {T, SS, nkb, Gkb, nslot_kb, kr,
- * lds_bytes, need_ws, ch, umax, chunks, reduce, ring, aligned} (SS and kr of the largest
+ * lds_bytes, need_ws, ch, umax, chunks, reduce, ring, aligned, burst} (SS and kr of the largest
  * k-block). */
-dfq_status dfq_debug_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, int* out14) {
-    if (!out14) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
+dfq_status dfq_debug_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, int* out15) {
+    if (!out15) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
     Plan p;
     dfq_status s = get_plan(ctx, M, N, K, bits, gs, &p);
     if (s) return s;
-    plan_fields(p, out14);
+    plan_fields(p, out15);
     return DFQ_OK;
 }
 
@@ -1046,12 +1065,12 @@ dfq_status dfq_debug_read_stream(dfq_ctx* ctx, const void* src, size_t bytes, ui
 
 /* The same split computed without a device, for a given CU count and LDS limit. */
 dfq_status dfq_debug_make_plan(int M, int N, int K, int bits, int gs, int num_cus,
-                               size_t lds_max, int* out14) {
-    if (!out14) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
+                               size_t lds_max, int* out15) {
+    if (!out15) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");
     Plan p;
     if (!make_plan(M, N, K, bits, gs, num_cus, lds_max, &p))
         return fail(DFQ_ERR_UNSUPPORTED, "no work split");
-    plan_fields(p, out14);
+    plan_fields(p, out15);
     return DFQ_OK;
 }
 

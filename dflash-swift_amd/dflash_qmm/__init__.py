@@ -236,10 +236,10 @@ class Context:
                "dfq_workspace_clear")
 
     def plan(self, M, N, K, bits, gs) -> dict:
-        out = (ctypes.c_int * 14)()
+        out = (ctypes.c_int * 15)()
         _check(self.lib.dfq_debug_plan(self.handle, M, N, K, bits, gs, out), "dfq_debug_plan")
         keys = ["T", "SS", "nkb", "Gkb", "nslot_kb", "kr", "lds_bytes", "need_ws", "ch", "umax",
-                "chunks", "reduce", "ring", "aligned"]
+                "chunks", "reduce", "ring", "aligned", "burst"]
         return dict(zip(keys, list(out)))
 
     def read_stream(self, src, nbytes, sink, stream=None):

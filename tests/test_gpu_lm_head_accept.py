@@ -29,6 +29,9 @@ CASES = [
     (1, 32000, 4096, 4, 64, BF16, False, False),    # one row: nothing to accept
     (12, 20000, 1024, 4, 32, BF16, False, False),   # 12 rows, group 32
     (8, 3000, 640, 4, 64, BF16, True, False),       # K not 8 groups' worth: two calls
+    (8, 32768, 512, 4, 64, BF16, False, False),     # outputs written at the workgroup's end
+    (16, 32768, 512, 4, 64, F16, True, False),      # the same, 16 rows, fp16, linear bias
+    (3, 40000, 1024, 8, 64, BF16, False, False),    # the same, 8-bit, tiles cut by ranges
 ]
 
 
@@ -78,26 +81,29 @@ def test_fused_accept_matches_the_two_calls(ctx, M, V, K, bits, gs, dt, lb, word
             assert int(ws[:need - tail].count_nonzero().item()) == 0   # zero again
 
 
-def test_fused_accept_ties_and_nan_rows(ctx):
-    """x is made non-negative, so every logit is positive, and columns 100 and 5000 get the
+@pytest.mark.parametrize("V,K,far", [(8192, 1024, 5000), (32768, 512, 30000)])
+def test_fused_accept_ties_and_nan_rows(ctx, V, K, far):
+    """x is made non-negative, so every logit is positive, and columns 100 and `far` get the
     same codes and biases with every scale 0.5 (the others are ~0.02): in every row they are
     equal and the largest, and the first
     index, 100, wins although the two lie in tiles finished by different workgroups.  Row 3
-    of x is NaN: every logit of the row is NaN and its token is -1."""
+    of x is NaN: every logit of the row is NaN and its token is -1.  The second shape writes
+    its outputs (and folds their keys) at the end of each workgroup."""
     import torch
-    M, V, K = 8, 8192, 1024
+    M = 8
     c = make_case(M, V, K, bits=4, gs=64, seed=77)
     c.x = c.x & np.uint16(0x7FFF)
-    c.w[5000] = c.w[100]
+    c.w[far] = c.w[100]
     c.scales[100] = 0x3F00                                       # bf16 0.5
-    c.scales[5000] = 0x3F00
-    c.biases[5000] = c.biases[100]
+    c.scales[far] = 0x3F00
+    c.biases[far] = c.biases[100]
     x, w, s, b, _ = upload(c)
     x[3] = float("nan")
     announce("fused accept ties / NaN")
     logits, want_tok, _ = reference(ctx, torch, x, w, s, b, None, 4, 64, None)
     assert want_tok[3] == -1
     assert (want_tok[[0, 1, 2, 4, 5, 6, 7]] == 100).all()
+    assert ctx.plan(M, V, K, 4, 64)["burst"] == int(V == 32768)
     tokens, acc = ctx.qmm_argmax_accept(x, w, s, b, 4, 64)
     torch.cuda.synchronize()
     assert tokens.cpu().numpy().tolist() == want_tok.tolist()

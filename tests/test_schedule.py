@@ -20,12 +20,12 @@ import dflash_qmm
 
 def make_plan(M, N, K, bits, gs, cus=256, lds=163840):
     lib = dflash_qmm.load_library()
-    out = (ctypes.c_int * 14)()
+    out = (ctypes.c_int * 15)()
     rc = lib.dfq_debug_make_plan(M, N, K, bits, gs, cus, lds, out)
     if rc:
         return None
     keys = ["T", "SS", "nkb", "Gkb", "nslot_kb", "kr", "lds_bytes", "need_ws", "ch", "umax",
-            "chunks", "reduce", "ring", "aligned"]
+            "chunks", "reduce", "ring", "aligned", "burst"]
     return dict(zip(keys, list(out)))
 
 
@@ -141,9 +141,8 @@ def replay(p):
                     g0 = g_of[u0]
                     assert [g_of[uu] for uu in range(u0, u1)] == list(range(g0, g0 + u1 - u0))
                     units = {part[(g0 + i) % R] for i in range(u1 - u0)}
-                    for i in range(1, u1 - u0):               # the summing wave releases
-                        gen[(g0 + i) % R] = g0 + i + R
-                    gen[g0 % R] = g0 + R                      # the publisher, after reading
+                    for i in range(u1 - u0):                  # the summing wave releases every
+                        gen[(g0 + i) % R] = g0 + i + R        # slot (the sum is in the output area)
                     if u0 == t * SS and u1 == (t + 1) * SS and nkb == 1:
                         finalize(t, units)
                     else:
@@ -257,6 +256,21 @@ def test_narrow_n_splits_k_in_two_with_one_tile_per_workgroup():
     assert make_plan(8, 2048, 5120, 4, 64)["nkb"] == 1
     # long K: a workgroup's share would be too long; the reduce split stays
     assert make_plan(8, 1024, 32768, 4, 64)["reduce"] == 1
+
+
+def test_outputs_leave_at_the_end_where_workgroups_hold_many_tiles():
+    # the LM head (38 tiles a workgroup) and the C5 gate|up (10): outputs written at the end
+    # of each workgroup; the headline shape (6) and every reduce split: as each tile finishes
+    assert make_plan(8, 151936, 5120, 4, 64)["burst"] == 1
+    assert make_plan(8, 34816, 5120, 4, 64)["burst"] == 1
+    assert make_plan(1, 32768, 512, 4, 64)["burst"] == 1
+    assert make_plan(8, 17408, 5120, 4, 64)["burst"] == 0
+    assert make_plan(8, 7168, 5120, 4, 64)["burst"] == 0
+    for shape in [(8, 5120, 17408, 4, 64), (16, 17408, 5120, 4, 64), (16, 151936, 5120, 4, 64)]:
+        p = make_plan(*shape)
+        assert p["reduce"] == 1 and p["burst"] == 0, shape
+    # aligned and narrow splits pair every tile: nothing left for the end
+    assert make_plan(8, 1024, 5120, 4, 64)["burst"] == 0
 
 
 def test_sixteen_rows_fit_lds_with_two_row_tiles():
