@@ -192,6 +192,23 @@ def time_read(torch, ctx, stream, nbytes, nsets, steps, dev):
     return times
 
 
+def time_units(torch, ctx, stream, sets, M, steps, N=N_OUT, K=K_IN):
+    """The fast kernel's own loads with no compute (dfq_debug_read_units) over the rotated
+    weight sets of the matmul, `steps` launches per graph, replayed like it; per-launch us."""
+    sink = torch.zeros(12 * ctx.num_cus, dtype=torch.int32, device=sets[0][0].device)
+    torch.cuda.synchronize()
+    ctx.graph_begin(stream)
+    for i in range(steps):
+        w, s, b = sets[i % len(sets)]
+        ctx.read_units(w, s, b, M, N, K, sink, stream=stream)
+    graph = ctx.graph_end(stream)
+    with torch.cuda.stream(stream):
+        graph.launch(stream)
+        times = time_replays(torch, stream, graph, steps, replays_for(steps))
+    graph.close()
+    return times
+
+
 def time_copy(torch, stream, nbytes, nsets, steps):
     """A plain device copy moving `nbytes` per launch (nbytes/2 read, nbytes/2 written),
     rotated over buffers larger than the Infinity Cache and timed back to back like the
@@ -618,8 +635,9 @@ def main():
         rd = stats(time_read(torch, ctx, stream, nb8, args.sets, args.steps, dev))
         out["read_ceiling"] = {
             "workload": ("the library's plain streaming-read kernel (one workgroup of 8 waves "
-                         "per CU, contiguous 4 KB blocks) reading the M=8 call's algorithmic "
-                         "bytes per launch, rotated over buffers, replayed like the matmul"),
+                         "per CU, 4 KB blocks dealt to the waves round-robin, 32 KB in flight "
+                         "per CU) reading the M=8 call's algorithmic bytes per launch, rotated "
+                         "over buffers, replayed like the matmul"),
             "bytes_per_launch": nb8,
             "us_per_launch": round(rd["median"], 3),
             "p10": round(rd["p10"], 3),
@@ -629,6 +647,22 @@ def main():
         }
         print(f"[bench] read ceiling {nb8 / 1e6:.1f} MB: {rd['median']:.2f} us/launch, "
               f"{nb8 / rd['median'] / 1e3:.0f} GB/s", file=sys.stderr, flush=True)
+        ud = stats(time_units(torch, ctx, stream, sets, 8, args.steps))
+        wb = algorithmic_bytes(0)  # weights, scales and biases
+        out["unit_read"] = {
+            "workload": ("the fast kernel's own loads for M=8 with no compute "
+                         "(dfq_debug_read_units: its workgroup ranges, one unit of 16 columns x "
+                         "512 k in flight per wave, 12 waves per CU), over the same rotated "
+                         "weight sets"),
+            "bytes_per_launch": wb,
+            "us_per_launch": round(ud["median"], 3),
+            "p10": round(ud["p10"], 3),
+            "p90": round(ud["p90"], 3),
+            "gbs": round(wb / (ud["median"] * 1e-6) / 1e9, 1),
+            "matmul_frac_of_unit_read": round(ud["median"] / us[8], 4),
+        }
+        print(f"[bench] the kernel's own loads without compute: {ud['median']:.2f} us/launch",
+              file=sys.stderr, flush=True)
         uc_copy = time_copy(torch, stream, nb8, args.sets, args.steps)
         out["device_copy"] = {
             "workload": ("torch copy_ of half the M=8 call's algorithmic bytes into another "

@@ -89,6 +89,7 @@ struct dfq_ctx {
     hipFunction_t generic = nullptr;
     hipFunction_t fill = nullptr;
     hipFunction_t read_stream = nullptr; // the plain streaming read (bandwidth reference)
+    hipFunction_t read_units = nullptr;  // the fast kernel's own loads with no compute
     void* scratch = nullptr;             // the fixed scratch of dfq_qmm_noalloc (this device)
     std::mutex mu;
     std::unordered_map<PlanKey, dfq::Plan, PlanKeyHash> plans;
@@ -468,7 +469,8 @@ dfq_status dfq_init(int device, dfq_ctx** out) {
         (e = hipModuleGetFunction(&ctx->argmax_accept[0], ctx->module, "dfq_argmax_accept_bf16")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->argmax_accept[1], ctx->module, "dfq_argmax_accept_f16")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->fill, ctx->module, "dfq_fill_u32")) != hipSuccess ||
-        (e = hipModuleGetFunction(&ctx->read_stream, ctx->module, "dfq_read_stream")) != hipSuccess) {
+        (e = hipModuleGetFunction(&ctx->read_stream, ctx->module, "dfq_read_stream")) != hipSuccess ||
+        (e = hipModuleGetFunction(&ctx->read_units, ctx->module, "dfq_read_units_b4_g64")) != hipSuccess) {
         (void)hipModuleUnload(ctx->module);
         delete ctx;
         return hip_fail(e, "hipModuleGetFunction");
@@ -1061,6 +1063,30 @@ dfq_status dfq_debug_read_stream(dfq_ctx* ctx, const void* src, size_t bytes, ui
     hipError_t e = hipModuleLaunchKernel(ctx->read_stream, (unsigned)ctx->num_cus, 1, 1, 512, 1,
                                          1, 0, (hipStream_t)stream, args, nullptr);
     return e == hipSuccess ? DFQ_OK : hip_fail(e, "launch dfq_read_stream");
+}
+
+/* The fast kernel's own read of a 4-bit group-64 shape with a one-k-block split: the same
+ * workgroup ranges and loads, no compute; sink receives 12 words per workgroup (12 *
+ * dfq_num_cus suffices).  w, scales and biases as for dfq_qmm. */
+dfq_status dfq_debug_read_units(dfq_ctx* ctx, const uint32_t* w, const void* scales,
+                                const void* biases, int M, int N, int K, uint32_t* sink,
+                                void* stream) {
+    if (!ctx || !w || !scales || !biases || !sink)
+        return fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
+    dfq_status s = check_fast_args(ctx, M, N, K, 4, 64, DFQ_BF16, DFQ_BF16, DFQ_BF16);
+    if (s) return s;
+    Plan pl;
+    if ((s = get_plan(ctx, M, N, K, 4, 64, &pl))) return s;
+    if (pl.nkb != 1 || pl.ch != 8 / 2 || pl.Gkb > ctx->num_cus)
+        return fail(DFQ_ERR_UNSUPPORTED,
+                    "the unit read covers one-k-block splits of 8-group chunks over the CUs");
+    DeviceGuard g(ctx->device);
+    QmmParams p = fill_params(pl, nullptr, w, scales, biases, nullptr, nullptr, M, N, K, 4, 64,
+                              nullptr);
+    void* args[] = {&p, &sink};
+    hipError_t e = hipModuleLaunchKernel(ctx->read_units, (unsigned)pl.Gkb, 1, 1, 768, 1, 1, 0,
+                                         (hipStream_t)stream, args, nullptr);
+    return e == hipSuccess ? DFQ_OK : hip_fail(e, "launch dfq_read_units");
 }
 
 /* The same split computed without a device, for a given CU count and LDS limit. */

@@ -127,6 +127,7 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         "dfq_debug_plan": ([P, I, I, I, I, I, ctypes.POINTER(I)], I),
         "dfq_debug_make_plan": ([I, I, I, I, I, I, S, ctypes.POINTER(I)], I),
         "dfq_debug_read_stream": ([P, P, S, P, P], I),
+        "dfq_debug_read_units": ([P, P, P, P, I, I, I, P, P], I),
         "dfq_linear_describe": ([P, ctypes.POINTER(_LinearDesc)], I),
         "dfq_checkpoint_open": ([ctypes.c_char_p, PP], I), "dfq_checkpoint_close": ([P], I),
         "dfq_checkpoint_format": ([P], ctypes.c_char_p),
@@ -241,6 +242,13 @@ class Context:
         keys = ["T", "SS", "nkb", "Gkb", "nslot_kb", "kr", "lds_bytes", "need_ws", "ch", "umax",
                 "chunks", "reduce", "ring", "aligned", "burst"]
         return dict(zip(keys, list(out)))
+
+    def read_units(self, w, scales, biases, M, N, K, sink, stream=None):
+        """One launch of the fast kernel's own loads for a 4-bit g64 shape (one-k-block
+        splits), with no compute; sink holds 12 * num_cus uint32."""
+        _check(self.lib.dfq_debug_read_units(self.handle, _ptr(w), _ptr(scales), _ptr(biases),
+                                             M, N, K, _ptr(sink), _stream(stream)),
+               "dfq_debug_read_units")
 
     def read_stream(self, src, nbytes, sink, stream=None):
         """One launch of the plain streaming read of nbytes of src (the bandwidth reference);
