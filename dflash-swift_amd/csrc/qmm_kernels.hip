@@ -1272,13 +1272,21 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
                     sum += *(const f32x4_t*)(part + s2 * (MT * 128) + tile_off(lane));
                 *(f32x4_t*)(tout + (t - ta) * (MT * 128) + tile_off(lane)) = sum;
             }
-            if (lane == 0) {
-                for (int i = 0; i < u1 - u0; ++i)
-                    __hip_atomic_store(gen + (g0 + i) % R, (uint32_t)(g0 + i + R),
-                                       __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            /* The slots' reads above complete before any slot is handed on.  Then each lane
+             * releases one slot (a tile has at most R units in a range, so its slots wrap
+             * at most once): one store instruction instead of a per-slot loop of modulo
+             * arithmetic and waits on the completing wave, which issues its next unit only
+             * after this (the headline call measured 16.25-16.47 -> 16.06-16.09 us, the LM
+             * head 82.9 -> 82.1 us). */
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            for (int i = lane; i < u1 - u0; i += 64) {
+                const int s2 = sl0 + i;
+                __hip_atomic_store(gen + (s2 >= R ? s2 - R : s2), (uint32_t)(g0 + i + R),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+            if (lane == 0)
                 __hip_atomic_store(tcnt + (t - ta), kTileDone, __ATOMIC_RELEASE,
                                    __HIP_MEMORY_SCOPE_WORKGROUP);
-            }
         }
     };
 
