@@ -908,11 +908,11 @@ __device__ void finish_wg(const QmmParams& p, const KBlock& kbk, int kb, int cl,
  * slot. */
 template <bool F16>
 __device__ __forceinline__ void reduce_tile(const QmmParams& p, int t, int lane) {
-    int parts = 0;
-    for (int kb = 0; kb < p.nkb; ++kb) {
-        parts += tile_owners(kblock(p, kb), t);
-    }
-    if (parts <= 1) return;
+    /* A tile of a several-k-block split has a part in every k-block.  With one k-block, a tile
+     * inside one workgroup's range was written by the main kernel.  (Counting the parts over
+     * every k-block put each k-block's split arithmetic, several integer divisions, before
+     * the first load: C3 19.7-20.3 -> 18.6-19.0 us.) */
+    if (p.nkb == 1 && tile_owners(kblock(p, 0), t) <= 1) return;
     f32x4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
     if (lane < 32 * p.mt) {
         const int S = p.nkb * p.nslot_kb, stride = p.mt * 128;
@@ -1616,6 +1616,16 @@ extern "C" __global__ void __launch_bounds__(256) dfq_argmax_accept_f16(
  * k-blocks, or tiles spread over three or more workgroups): one wave per 16-column tile. */
 template <bool F16>
 __device__ __forceinline__ void qmm_reduce(const QmmParams& p) {
+    /* Every parameter the pass reads, fetched in one go: left to itself the compiler fetches
+     * each where it is first used, three dependent scalar round trips before the first slot
+     * load (C3 18.6 -> 18.5 us, M=16 20.9 -> 20.2 us). */
+    int nkb = p.nkb, nslot = p.nslot_kb, mt = p.mt, M = p.M, N = p.N, epi = p.epi, T = p.T;
+    int chunks = p.chunks, Gkb = p.Gkb, al = p.aligned;
+    const void* y = p.y;
+    const void* lb = p.lbias;
+    const float* sl = p.slots;
+    __asm__ volatile("" ::"s"(nkb), "s"(nslot), "s"(mt), "s"(M), "s"(N), "s"(epi), "s"(T),
+                     "s"(chunks), "s"(Gkb), "s"(al), "s"(y), "s"(lb), "s"(sl));
     reduce_tile<F16>(p, blockIdx.x, threadIdx.x);
 }
 
