@@ -165,12 +165,15 @@ static int tile_owners(int64_t t, int64_t SS, int64_t G, int64_t T) {
 /* Largest workgroup share (units) for which a narrow N is split into two k-blocks of one tile
  * per workgroup. */
 static constexpr int kShortSplitUnits = 24;
-/* Fewest tiles a workgroup touches for which its outputs are written at its end rather than
- * as each tile finishes.  Stores from the publisher waves interleave with the weight stream;
- * written at the end they do not, but the end then waits for every wave.  Measured on MI355X
- * at M = 8, K = 5120 (us, at the end against as they finish): the LM head N = 151936 (38
- * tiles) 83.3 against 90.7; gate|up N = 34816 (10) 25.25 against 25.55; N = 17408 (6) 16.54
- * against 16.37; N = 7168 (3) 11.67 against 11.41. */
+/* Fewest tiles a workgroup touches for which its outputs (whole tiles to y, or the parts of a
+ * reduce split to their workspace slots) are written at its end rather than as each tile
+ * finishes.  Stores from the publisher waves interleave with the weight stream; written at
+ * the end they do not, but the end then waits for every wave.  Measured on MI355X at M = 8,
+ * K = 5120 (us, at the end against as they finish): the LM head N = 151936 (38 tiles) 83.3
+ * against 90.7; gate|up N = 34816 (10) 25.25 against 25.55; N = 17408 (6) 16.54 against
+ * 16.37; N = 7168 (3) 11.67 against 11.41.  The 16-row reduce split at N = 17408 (10 tiles
+ * in each of two k-blocks): 19.8-20.2 against 20.0-20.8; 12 rows 18.9-19.0 against
+ * 19.3-19.6. */
 static constexpr int kBurstTiles = 8;
 /* Most tiles per workgroup for which two k-blocks take an aligned split rather than
  * stream-K ranges with the second pass.  Every tile of an aligned split is finished by a
@@ -247,7 +250,7 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
         p.reduce = d > 1 ? (d > 2 || nslot > 1) : nslot > 2;
         {
             const int64_t umax = p.umax, ntl_max = (umax + ss_min - 1) / ss_min + 1;
-            p.burst = !p.reduce && ntl_max >= kBurstTiles;
+            p.burst = ntl_max >= kBurstTiles;
         }
         /* Ask for more than half the CU's LDS so that exactly one workgroup lands per CU. */
         const size_t want = std::max(need, lds_max / 2 + 256);

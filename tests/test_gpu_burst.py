@@ -1,11 +1,14 @@
 """Splits whose workgroups hold many tiles write their outputs at the end of the workgroup
 ("burst"): every tile without a pair exchange goes from the LDS output area to y, with
 16-byte row stores where a row's 8 columns are aligned and in range and element stores
-elsewhere, after the streaming.  These shapes take that path (asserted from the plan) at
-sizes the oracle checks in seconds: every row count 1..16, bf16 and fp16, 4- and 8-bit, a
-linear bias, N that is not a multiple of 16 or of 8 (element stores), and the gate|up
-epilogue; each against the fp64 oracle within the parity bar and bit-identical on a repeat
-call.  The fused greedy accept at burst shapes is in test_gpu_lm_head_accept.py.
+elsewhere, after the streaming; in a reduce split (two k-blocks of 9..16 rows) each tile's
+part goes to its workspace slot at that point instead, for the second pass.  These shapes
+take that path (asserted from the plan) at sizes the oracle checks in seconds: every row
+count 1..16, bf16 and fp16, 4- and 8-bit, group 32, 64 and 128, a linear bias, N that is not
+a multiple of 16 or of 8 (element stores), and the gate|up epilogue; each against the fp64
+oracle within the parity bar and bit-identical on a repeat call (which also shows the
+workspace left zero).  The fused greedy accept at burst shapes is in
+test_gpu_lm_head_accept.py.
 """
 import numpy as np
 import pytest
@@ -18,23 +21,29 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-2
 
 CASES = [
-    # (M, N, K, bits, gs, dtype, linear bias)
-    (1, 32768, 512, 4, 64, BF16, False),
-    (8, 32768, 512, 4, 64, BF16, True),
-    (16, 32768, 512, 4, 64, F16, False),     # two row tiles
-    (12, 33000, 512, 4, 64, BF16, True),     # last tile 8 columns wide
-    (8, 33003, 512, 4, 64, BF16, False),     # rows not 16-byte aligned: element stores
-    (5, 40000, 1024, 8, 64, F16, True),      # 8-bit, two chunks per tile
-    (8, 36000, 1024, 4, 32, BF16, False),    # group 32
-    (3, 40000, 2048, 8, 128, BF16, True),    # 8-bit g128
+    # (M, N, K, bits, gs, dtype, linear bias, reduce split)
+    (1, 32768, 512, 4, 64, BF16, False, 0),
+    (8, 32768, 512, 4, 64, BF16, True, 0),
+    (16, 32768, 512, 4, 64, F16, False, 0),     # two row tiles
+    (12, 33000, 512, 4, 64, BF16, True, 0),     # last tile 8 columns wide
+    (8, 33003, 512, 4, 64, BF16, False, 0),     # rows not 16-byte aligned: element stores
+    (5, 40000, 1024, 8, 64, F16, True, 0),      # 8-bit, two chunks per tile
+    (8, 36000, 1024, 4, 32, BF16, False, 0),    # group 32
+    (3, 40000, 2048, 8, 128, BF16, True, 0),    # 8-bit g128
+    # two k-blocks of stream-K ranges: parts to the workspace at the end, second pass
+    (16, 40000, 4096, 4, 64, BF16, True, 1),
+    (16, 40000, 4096, 8, 64, F16, False, 1),
+    (13, 40000, 4096, 4, 32, BF16, False, 1),   # group 32, one super-step per chunk half
+    (16, 40000, 4096, 4, 128, F16, True, 1),    # g128
+    (12, 40000, 6144, 4, 64, BF16, False, 1),
 ]
 
 
-@pytest.mark.parametrize("M,N,K,bits,gs,dt,lb", CASES)
-def test_burst_split_matches_oracle_and_repeats(ctx, oracle, M, N, K, bits, gs, dt, lb):
+@pytest.mark.parametrize("M,N,K,bits,gs,dt,lb,red", CASES)
+def test_burst_split_matches_oracle_and_repeats(ctx, oracle, M, N, K, bits, gs, dt, lb, red):
     import torch
     plan = ctx.plan(M, N, K, bits, gs)
-    assert plan["burst"] == 1 and plan["reduce"] == 0, plan
+    assert plan["burst"] == 1 and plan["reduce"] == red, plan
     c = make_case(M, N, K, bits=bits, gs=gs, xdt=dt, seed=3 * M + N + K, lbias=lb)
     x, w, s, b, lbias = upload(c)
     announce(f"burst qmm M={M} N={N} K={K} bits={bits} gs={gs} dt={dt} plan={plan}")
@@ -54,7 +63,8 @@ def deinterleave(torch, y, H):
 
 
 @pytest.mark.parametrize("M,H,K,dt,lb", [(8, 16384, 512, BF16, True), (16, 16384, 512, F16, False),
-                                         (1, 20000, 512, BF16, False)])
+                                         (1, 20000, 512, BF16, False),
+                                         (16, 20000, 4096, BF16, True)])  # reduce split
 def test_burst_gate_up_epilogue(ctx, oracle, M, H, K, dt, lb):
     import torch
     assert ctx.plan(M, 2 * H, K, 4, 64)["burst"] == 1
