@@ -17,7 +17,10 @@ Method:
     algorithmic bytes per launch over the same rotation, timed the same way: the
     single-launch read rate this memory system reaches with no compute;
   * the CPU baseline is the oracle's fp32 restatement of MLX's CPU algorithm (dequantise a
-    group, multiply-accumulate), OpenMP over the host cores, timed on a bounded sample.
+    group, multiply-accumulate), OpenMP over the host cores, timed on a bounded sample;
+  * the 64-layer verify forward (c5_chain*) is timed with one HIP graph per layer and as one
+    graph; the per-layer form once more in a child process with the HIP runtime's graph
+    packet capture off (c5_chain_fused_no_packet_capture).
 
 --profile-timed dispatches the matmul only as graph replays (one warm-up replay, then the
 timed ones), so that `rocprofv3 --kernel-trace --stats` averages the calls the figures time.
@@ -358,6 +361,27 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, one_graph=False):
     }
 
 
+def c5_child(form, env_extra, timeout=600):
+    """chain_c5 of one form in a child process started with extra environment variables.
+    The HIP runtime reads them once, when it starts, so they cannot change inside this
+    process.  DEBUG_CLR_GRAPH_PACKET_CAPTURE=0 turns off the runtime's pre-recorded packets
+    for graph launches; with them, each of the 64 layer graphs starts several microseconds
+    after the previous one ends, without them the layer graphs follow each other as the
+    kernels of one graph do.  Returns the child's figures, or what went wrong."""
+    import subprocess
+    env = dict(os.environ)
+    env.update(env_extra)
+    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--c5-only", form], env=env,
+                       capture_output=True, text=True, timeout=timeout)
+    for line in r.stdout.splitlines():
+        if line.startswith("{"):
+            d = json.loads(line)["c5_" + form]
+            d["environment"] = env_extra
+            return d
+    return {"error": f"child exited with {r.returncode}", "stderr_tail": r.stderr[-400:],
+            "environment": env_extra}
+
+
 def time_lm_head(torch, ctx, stream, dev, steps=20, nsets=4, reps=20):
     """The C5 LM head (M=8, 151936 x 5120, 4-bit g64) with the greedy accept, graph-replayed
     over rotated weights: fused (dfq_qmm_argmax_accept, no logits written) and as two calls
@@ -686,7 +710,13 @@ def main():
         torch.cuda.empty_cache()
         out["c5_chain_fused"] = chain_c5(torch, ctx, dev, fused=True)
         out["c5_chain_fused_one_graph"] = chain_c5(torch, ctx, dev, fused=True, one_graph=True)
-        for key in ("c5_chain", "c5_chain_fused", "c5_chain_fused_one_graph"):
+        torch.cuda.empty_cache()
+        out["c5_chain_fused_no_packet_capture"] = c5_child(
+            "fused", {"DEBUG_CLR_GRAPH_PACKET_CAPTURE": "0"})
+        for key in ("c5_chain", "c5_chain_fused", "c5_chain_fused_one_graph",
+                    "c5_chain_fused_no_packet_capture"):
+            if "us_per_forward" not in out[key]:
+                continue
             print(f"[bench] {key}: {out[key]['us_per_forward']} us/forward "
                   f"(ideal {out[key]['ideal_us_at_8TBs']})", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
