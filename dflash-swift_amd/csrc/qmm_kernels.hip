@@ -557,7 +557,7 @@ __device__ __forceinline__ void store_y(const QmmParams& p, int t, int lane, f32
  * XCDs' L2s without a whole-cache write-back or invalidate). */
 template <bool F16, bool AM>
 __device__ __forceinline__ void publish(const QmmParams& p, const KBlock& kbk, int t,
-                                        int slot, int lane, f32x4_t v, uint64_t (&best)[4]) {
+                                        int lane, f32x4_t v, uint64_t (&best)[4]) {
     const int q = lane >> 4, n = lane & 15;
     const bool act = lane < 32 * p.mt;  // lanes holding the tile
     const int nwg = tile_owners(kbk, t);
@@ -746,15 +746,14 @@ __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
                 const int t = ta + tlb;
                 f32x4_t v = {0.0f, 0.0f, 0.0f, 0.0f};
                 if (lane < 32 * MT) v = *(const f32x4_t*)(tout + tlb * (MT * 128) + tile_off(lane));
-                const int first = tile_first_owner(kbk, t);
                 if (!exchange_tile(p, t, a, b, SS)) {
                     if (!p.reduce || (max(a, t * SS) == t * SS && min(b, (t + 1) * SS) == (t + 1) * SS &&
                                       p.nkb == 1))
                         store_y<F16, AM>(p, t, lane, v, best);
                     else if (lane < 32 * MT)  /* summed by the second pass: no round trip here */
-                        put_tile4(tile_slot(p, t, kb, cl - first, lane), v);
+                        put_tile4(tile_slot(p, t, kb, cl - tile_first_owner(kbk, t), lane), v);
                 } else {
-                    publish<F16, AM>(p, kbk, t, kb * p.nslot_kb + (cl - first), lane, v, best);
+                    publish<F16, AM>(p, kbk, t, lane, v, best);
                 }
                 if (lane == 0) tcnt[tlb] = kTileOut;
                 ++found;
