@@ -539,6 +539,19 @@ __device__ __forceinline__ void store_y(const QmmParams& p, int t, int lane, f32
     }
 }
 
+/* Two fp32 values in one 64-bit exchange word, each as the bitwise complement of its bits, so
+ * that a word is zero only when empty: both values would have to be 0xFFFFFFFF, a NaN
+ * payload that bf16/fp16 arithmetic does not produce and that is mapped to another NaN. */
+__device__ __forceinline__ uint64_t pair_word(float a, float b) {
+    uint32_t x = __float_as_uint(a), y = __float_as_uint(b);
+    if (x == 0xFFFFFFFFu) x = 0xFFC00000u;
+    if (y == 0xFFFFFFFFu) y = 0xFFC00000u;
+    return (uint64_t)~x | ((uint64_t)~y << 32);
+}
+__device__ __forceinline__ float pair_value(uint64_t w, int e) {
+    return __uint_as_float(~(uint32_t)(w >> (32 * e)));
+}
+
 /* Contribute a partial tile to the workspace.
  *
  * Two contributors (the usual case: a tile split between two workgroups): every two
@@ -569,27 +582,28 @@ __device__ __forceinline__ void publish(const QmmParams& p, const KBlock& kbk, i
     uint32_t* base = (uint32_t*)p.slots + (size_t)t * p.nkb * p.nslot_kb * p.mt * 128;
     if (total == 2 && p.epi) {
         /* the gate|up epilogue needs g and u of one element summed by the same contributor:
-         * lanes n < 8 hold g and take u from lane n + 8; each element has a u word (the
-         * slot lane n + 8 would use) and a g word.  u goes in first; once that has
-         * completed, g is exchanged, and the contributor that gets back a tagged g finishes:
-         * the other's u is in its u word by then (deposited before the other's g), or came
-         * back from our own u exchange (then our u sits in the word and is cleared).  Every
-         * word is zero again afterwards. */
+         * lanes n < 8 hold g and take u from lane n + 8; each pair of elements has a u word
+         * and a g word.  u goes in first; once that has completed, g is exchanged, and the
+         * contributor that gets back a non-zero g word finishes: the other's u is in its u
+         * word by then (deposited before the other's g), or came back from our own u
+         * exchange (then our u sits in the word and is cleared).  Every word is zero again
+         * afterwards. */
         f32x4_t u;
 #pragma unroll
         for (int r = 0; r < 4; ++r) u[r] = dpp_f32<0x128>(v[r]);
         if (!act || n >= 8) return;
-        uint64_t* sg = (uint64_t*)base + tile_off(lane);
-        uint64_t* su = sg + 64;
-        uint64_t ou[4], og[4];
+        /* two values per word, as bit complements (see below): g words, then u words */
+        uint64_t* sg = (uint64_t*)base + (tile_off(lane) >> 1);
+        uint64_t* su = sg + 32;
+        uint64_t ou[2], og[2];
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            ou[r] = __hip_atomic_exchange(su + r, (1ull << 32) | __float_as_uint(u[r]),
+        for (int h = 0; h < 2; ++h)
+            ou[h] = __hip_atomic_exchange(su + h, pair_word(u[2 * h], u[2 * h + 1]),
                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            og[r] = __hip_atomic_exchange(sg + r, (1ull << 32) | __float_as_uint(v[r]),
+        for (int h = 0; h < 2; ++h)
+            og[h] = __hip_atomic_exchange(sg + h, pair_word(v[2 * h], v[2 * h + 1]),
                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const int H = p.N / 2;
         float lbg = 0.0f, lbu = 0.0f;
@@ -598,43 +612,37 @@ __device__ __forceinline__ void publish(const QmmParams& p, const KBlock& kbk, i
             lbu = elem_to_f32<F16>(((const uint16_t*)p.lbias)[t * 16 + n + 8]);
         }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            if (!(og[r] >> 32)) continue;
-            float up;
-            if (ou[r] >> 32) {
-                up = __uint_as_float((uint32_t)ou[r]);
-                __hip_atomic_store(su + r, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int h = 0; h < 2; ++h) {
+            if (!og[h]) continue;
+            uint64_t upw;
+            if (ou[h]) {
+                upw = ou[h];
+                __hip_atomic_store(su + h, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             } else {
-                up = __uint_as_float((uint32_t)__hip_atomic_exchange(
-                    su + r, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+                upw = __hip_atomic_exchange(su + h, 0ull, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
             }
-            const float g = v[r] + __uint_as_float((uint32_t)og[r]);
-            const int m = 4 * q + r;
-            if (m < p.M)
-                put16((uint16_t*)p.y + (size_t)m * H + t * 8 + n,
-                           silu_mul_round<F16>(g + lbg, u[r] + up + lbu));
-            __hip_atomic_store(sg + r, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int r = 2 * h + e;
+                const float g = v[r] + pair_value(og[h], e);
+                const int m = 4 * q + r;
+                if (m < p.M)
+                    put16((uint16_t*)p.y + (size_t)m * H + t * 8 + n,
+                          silu_mul_round<F16>(g + lbg, u[r] + pair_value(upw, e) + lbu));
+            }
+            __hip_atomic_store(sg + h, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         return;
     }
     if (total != 2 || !act) return;  // one part: stored by the caller; more: reduce splits
     const int col = t * 16 + n;
-    /* two values per 64-bit word, each as its bitwise complement, so that zero means empty:
-     * a word is zero only if both values are 0xFFFFFFFF, a NaN payload that bf16/fp16
-     * arithmetic does not produce (and that is mapped to another NaN here) */
     uint64_t* sl = (uint64_t*)base + (tile_off(lane) >> 1);
-    uint32_t bits[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        bits[r] = __float_as_uint(v[r]);
-        if (bits[r] == 0xFFFFFFFFu) bits[r] = 0xFFC00000u;
-    }
     uint64_t old[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
-        old[h] = __hip_atomic_exchange(
-            sl + h, (uint64_t)~bits[2 * h] | ((uint64_t)~bits[2 * h + 1] << 32),
-            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        old[h] = __hip_atomic_exchange(sl + h, pair_word(v[2 * h], v[2 * h + 1]),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     float lb = 0.0f;
     if (p.lbias && col < p.N) lb = elem_to_f32<F16>(((const uint16_t*)p.lbias)[col]);
 #pragma unroll
@@ -644,7 +652,7 @@ __device__ __forceinline__ void publish(const QmmParams& p, const KBlock& kbk, i
         for (int e = 0; e < 2; ++e) {
             const int r = 2 * h + e;
             const int m = 4 * q + r;
-            const float sum = v[r] + __uint_as_float(~(uint32_t)(old[h] >> (32 * e)));
+            const float sum = v[r] + pair_value(old[h], e);
             if (m < p.M && col < p.N) {
                 const uint16_t o = f32_to_out<F16>(sum + lb);
                 if (!AM || p.y) put16((uint16_t*)p.y + (size_t)m * p.N + col, o);
