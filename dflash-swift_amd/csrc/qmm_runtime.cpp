@@ -175,13 +175,14 @@ static constexpr int kShortSplitUnits = 24;
  * in each of two k-blocks): 19.8-20.2 against 20.0-20.8; 12 rows 18.9-19.0 against
  * 19.3-19.6. */
 static constexpr int kBurstTiles = 8;
-/* Most tiles per workgroup for which two k-blocks take an aligned split rather than
- * stream-K ranges with the second pass.  Every tile of an aligned split is finished by a
- * pair exchange of per-element device-scope atomics.  Measured on MI355X with 16 rows at
- * K = 5120 (us, aligned against the second pass): N = 1024 (one tile per workgroup) 8.2
- * against 9.6; N = 5120 (three) 12.2 against 12.1; N = 7168 (four) 13.8 against 13.7;
- * N = 17408 (nine) 24.4 against 20.7. */
-static constexpr int kAlignedMaxTiles = 2;
+/* Most tiles per workgroup for which two k-blocks take an aligned split rather than stream-K
+ * ranges with the second pass.  Measured on MI355X with 9..16 rows (us, aligned against the
+ * second pass), the exchange at two values per atomic: N = 5120, K = 5120 (three tiles a
+ * workgroup) 11.0 against 12.2; N = 7168 (four) 12.0 against 13.9; N = 17408 (nine)
+ * 18.8-19.1 against 19.3-19.7, and 12 rows 18.5 against 19.0; N = 40000, K = 4096 (twenty)
+ * 29.6 against 28.8-29.3; N = 60000 (thirty) 42.5 against 38.9-39.3; N = 80000 (forty) 54.2
+ * against 48.6-48.8. */
+static constexpr int kAlignedMaxTiles = 12;
 
 bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_max, Plan* pl) {
     const int kss = kss_for(bits, gs);
@@ -306,8 +307,11 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
     for (int d = std::min(DFQ_MIN_KBLOCKS, chunks); d <= chunks; ++d) {
         if (!split(d, num_cus / d, pl)) continue;
         /* Two k-blocks of stream-K ranges give tiles three or four parts (second pass); whole
-         * tiles per workgroup give two, finished in the kernel, which pays where each
-         * workgroup holds few tiles. */
+         * tiles per workgroup give two, finished in the kernel by the pair exchange, at the
+         * price of up to one tile of imbalance; taken where its LDS fits (one output block
+         * per tile a workgroup holds) and a workgroup holds few enough tiles (with one value
+         * per atomic the exchange lost from four tiles on: N = 17408 at 16 rows, 24.4
+         * against 20.7 us). */
         Plan al;
         if (pl->reduce && d == 2 && split_aligned(num_cus / 2, &al) &&
             (T + al.Gkb - 1) / al.Gkb <= kAlignedMaxTiles) {
