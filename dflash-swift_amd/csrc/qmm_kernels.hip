@@ -552,6 +552,65 @@ __device__ __forceinline__ float pair_value(uint64_t w, int e) {
     return __uint_as_float(~(uint32_t)(w >> (32 * e)));
 }
 
+/* One two-party exchange of the plain path at the words sl[0..1] (two elements each), for
+ * the words with go[h] set: the party that gets back a non-zero word adds the other's pair
+ * into w, zeroes the word and keeps go[h]; the other clears go[h]. */
+__device__ __forceinline__ void pair_exchange(uint64_t* sl, bool (&go)[2], f32x4_t& w) {
+    uint64_t old[2] = {0, 0};
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+        if (go[h])
+            old[h] = __hip_atomic_exchange(sl + h, pair_word(w[2 * h], w[2 * h + 1]),
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        go[h] = old[h] != 0;
+        if (!go[h]) continue;
+        w[2 * h] += pair_value(old[h], 0);
+        w[2 * h + 1] += pair_value(old[h], 1);
+        __hip_atomic_store(sl + h, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+/* The same for the gate|up epilogue, which needs g and u of one element summed by the same
+ * party: each pair of elements has a g word sg[h] and a u word su[h].  u goes in first; once
+ * that has completed, g is exchanged, and the party that gets back a non-zero g word
+ * finishes: the other's u is in its u word by then (deposited before the other's g), or came
+ * back from our own u exchange (then our u sits in the word and is cleared). */
+__device__ __forceinline__ void pair_exchange_gu(uint64_t* sg, uint64_t* su, bool (&go)[2],
+                                                 f32x4_t& g, f32x4_t& u) {
+    uint64_t ou[2] = {0, 0}, og[2] = {0, 0};
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+        if (go[h])
+            ou[h] = __hip_atomic_exchange(su + h, pair_word(u[2 * h], u[2 * h + 1]),
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+        if (go[h])
+            og[h] = __hip_atomic_exchange(sg + h, pair_word(g[2 * h], g[2 * h + 1]),
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        go[h] = og[h] != 0;
+        if (!go[h]) continue;
+        uint64_t upw;
+        if (ou[h]) {
+            upw = ou[h];
+            __hip_atomic_store(su + h, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            upw = __hip_atomic_exchange(su + h, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            g[2 * h + e] += pair_value(og[h], e);
+            u[2 * h + e] += pair_value(upw, e);
+        }
+        __hip_atomic_store(sg + h, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 /* Contribute a partial tile to the workspace.
  *
  * Two contributors (the usual case: a tile split between two workgroups): every two
@@ -563,7 +622,14 @@ __device__ __forceinline__ float pair_value(uint64_t w, int e) {
  * one value halve the device-scope atomics and resets: the headline call measured 15.87 ->
  * 15.58 us, N = 1024 (every tile exchanged) 7.86 -> 7.64 us.
  *
- * Tiles with more contributors belong to reduce splits, which store their parts with no
+ * Three contributors in an aligned split of three k-blocks (whole tiles per workgroup):
+ * k-blocks 0 and 1 exchange at the tile's first word set, and whoever completes a word
+ * carries the pair's sum into the second set, where k-block 2's part waits or arrives; the
+ * second arrival there writes y.  The sum is (A + B) + C whatever the order of arrival, so
+ * the result does not depend on timing.  This replaces the second pass of such splits: the
+ * down projection (M=8, N=5120, K=17408) measured 18.3-18.5 -> 16.9-17.1 us.
+ *
+ * Other tiles with more contributors belong to reduce splits, which store their parts with no
  * round trip and leave the sum to the second pass (a per-tile arrival counter here costs
  * the publisher two memory round trips per tile under full HBM load, which made such
  * splits 1.7-2.2x slower than the second pass).
@@ -572,39 +638,30 @@ __device__ __forceinline__ float pair_value(uint64_t w, int e) {
  * these partials: every access to a slot is an agent-scope atomic (coherent across the
  * XCDs' L2s without a whole-cache write-back or invalidate). */
 template <bool F16, bool AM>
-__device__ __forceinline__ void publish(const QmmParams& p, const KBlock& kbk, int t,
+__device__ __forceinline__ void publish(const QmmParams& p, const KBlock& kbk, int t, int kb,
                                         int lane, f32x4_t v, uint64_t (&best)[4]) {
     const int q = lane >> 4, n = lane & 15;
     const bool act = lane < 32 * p.mt;  // lanes holding the tile
     const int nwg = tile_owners(kbk, t);
     const uint32_t total = (uint32_t)(p.nkb * nwg);
-    /* the tile's workspace area: nkb*nslot_kb slots of mt*128 floats */
+    /* one part: stored by the caller; more than two outside an aligned split: reduce splits */
+    const bool chain = total == 3 && p.aligned;
+    if (total != 2 && !chain) return;
+    /* the tile's workspace area: nkb*nslot_kb slots of mt*128 floats.  A lane's pairs sit at
+     * two words of the first set (64*mt words); a chain's second exchange uses the second */
     uint32_t* base = (uint32_t*)p.slots + (size_t)t * p.nkb * p.nslot_kb * p.mt * 128;
-    if (total == 2 && p.epi) {
-        /* the gate|up epilogue needs g and u of one element summed by the same contributor:
-         * lanes n < 8 hold g and take u from lane n + 8; each pair of elements has a u word
-         * and a g word.  u goes in first; once that has completed, g is exchanged, and the
-         * contributor that gets back a non-zero g word finishes: the other's u is in its u
-         * word by then (deposited before the other's g), or came back from our own u
-         * exchange (then our u sits in the word and is cleared).  Every word is zero again
-         * afterwards. */
+    uint64_t* s1 = (uint64_t*)base + (tile_off(lane) >> 1);
+    uint64_t* s2 = s1 + 64 * p.mt;
+    bool go[2] = {true, true};
+    if (p.epi) {
+        /* lanes n < 8 hold g and take u from lane n + 8 (g words, then u words) */
         f32x4_t u;
 #pragma unroll
         for (int r = 0; r < 4; ++r) u[r] = dpp_f32<0x128>(v[r]);
         if (!act || n >= 8) return;
-        /* two values per word, as bit complements (see below): g words, then u words */
-        uint64_t* sg = (uint64_t*)base + (tile_off(lane) >> 1);
-        uint64_t* su = sg + 32;
-        uint64_t ou[2], og[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-            ou[h] = __hip_atomic_exchange(su + h, pair_word(u[2 * h], u[2 * h + 1]),
-                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-            og[h] = __hip_atomic_exchange(sg + h, pair_word(v[2 * h], v[2 * h + 1]),
-                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        f32x4_t g = v;
+        if (!chain || kb < 2) pair_exchange_gu(s1, s1 + 32, go, g, u);
+        if (chain) pair_exchange_gu(s2, s2 + 32, go, g, u);
         const int H = p.N / 2;
         float lbg = 0.0f, lbu = 0.0f;
         if (p.lbias) {
@@ -612,54 +669,29 @@ __device__ __forceinline__ void publish(const QmmParams& p, const KBlock& kbk, i
             lbu = elem_to_f32<F16>(((const uint16_t*)p.lbias)[t * 16 + n + 8]);
         }
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            if (!og[h]) continue;
-            uint64_t upw;
-            if (ou[h]) {
-                upw = ou[h];
-                __hip_atomic_store(su + h, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            } else {
-                upw = __hip_atomic_exchange(su + h, 0ull, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-            }
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const int r = 2 * h + e;
-                const float g = v[r] + pair_value(og[h], e);
-                const int m = 4 * q + r;
-                if (m < p.M)
-                    put16((uint16_t*)p.y + (size_t)m * H + t * 8 + n,
-                          silu_mul_round<F16>(g + lbg, u[r] + pair_value(upw, e) + lbu));
-            }
-            __hip_atomic_store(sg + h, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int r = 0; r < 4; ++r) {
+            const int m = 4 * q + r;
+            if (go[r >> 1] && m < p.M)
+                put16((uint16_t*)p.y + (size_t)m * H + t * 8 + n,
+                      silu_mul_round<F16>(g[r] + lbg, u[r] + lbu));
         }
         return;
     }
-    if (total != 2 || !act) return;  // one part: stored by the caller; more: reduce splits
+    if (!act) return;
+    f32x4_t w = v;
+    if (!chain || kb < 2) pair_exchange(s1, go, w);
+    if (chain) pair_exchange(s2, go, w);
     const int col = t * 16 + n;
-    uint64_t* sl = (uint64_t*)base + (tile_off(lane) >> 1);
-    uint64_t old[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-        old[h] = __hip_atomic_exchange(sl + h, pair_word(v[2 * h], v[2 * h + 1]),
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     float lb = 0.0f;
     if (p.lbias && col < p.N) lb = elem_to_f32<F16>(((const uint16_t*)p.lbias)[col]);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        if (!old[h]) continue;  // first to arrive: the other part finishes
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const int r = 2 * h + e;
-            const int m = 4 * q + r;
-            const float sum = v[r] + pair_value(old[h], e);
-            if (m < p.M && col < p.N) {
-                const uint16_t o = f32_to_out<F16>(sum + lb);
-                if (!AM || p.y) put16((uint16_t*)p.y + (size_t)m * p.N + col, o);
-                if constexpr (AM) fold_key<F16>(best[r], o, col);
-            }
+    for (int r = 0; r < 4; ++r) {
+        const int m = 4 * q + r;
+        if (go[r >> 1] && m < p.M && col < p.N) {
+            const uint16_t o = f32_to_out<F16>(w[r] + lb);
+            if (!AM || p.y) put16((uint16_t*)p.y + (size_t)m * p.N + col, o);
+            if constexpr (AM) fold_key<F16>(best[r], o, col);
         }
-        __hip_atomic_store(sl + h, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -778,7 +810,7 @@ __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
                     else if (lane < 32 * MT)  /* summed by the second pass: no round trip here */
                         put_tile4(tile_slot(p, t, kb, cl - tile_first_owner(kbk, t), lane), v);
                 } else {
-                    publish<F16, AM>(p, kbk, t, lane, v, best);
+                    publish<F16, AM>(p, kbk, t, kb, lane, v, best);
                 }
                 if (lane == 0) tcnt[tlb] = kTileOut;
                 ++found;

@@ -262,13 +262,14 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
         *out = p;
         return true;
     };
-    /* Two k-blocks whose workgroups take whole tiles (an "aligned" split of G0 workgroups per
-     * k-block, at most one per tile): every tile then has one part per k-block, finished by
-     * the pair exchange, so no second pass is needed, at the price of up to one tile of
-     * imbalance between workgroups. */
-    auto split_aligned = [&](int64_t G0, Plan* out) -> bool {
-        if (chunks < 2) return false;
-        const int ss_max = (chunks + 1) / 2;
+    /* dd = 2 or 3 k-blocks whose workgroups take whole tiles (an "aligned" split of G0
+     * workgroups per k-block, at most one per tile): every tile then has one part per
+     * k-block, finished by the pair exchange (a chain of two exchanges for three parts), so
+     * no second pass is needed, at the price of up to one tile of imbalance between
+     * workgroups. */
+    auto split_aligned = [&](int dd, int64_t G0, Plan* out) -> bool {
+        if (chunks < dd) return false;
+        const int ss_max = (chunks + dd - 1) / dd;
         const int kr = ss_max * kch;
         if ((int64_t)M * (kr / 8) > (int64_t)kMaxStageItems * kThreads) return false;
         const int64_t G = std::min<int64_t>(std::max<int64_t>(1, G0), T);
@@ -279,7 +280,7 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
         p.ch = ch;
         p.T = T;
         p.chunks = chunks;
-        p.nkb = 2;
+        p.nkb = dd;
         p.kr = kr;
         p.SS = ss_max;
         p.rs = 2 * kr + 16;
@@ -300,20 +301,20 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
         p.lds_bytes = (int)std::min(std::max(need, lds_max / 2 + 256), lds_max);
         p.lds_need = (int)need;
         p.need_ws = true;
-        p.ws_bytes = (size_t)T * 2 * mt * 128 * 4;
+        p.ws_bytes = (size_t)T * dd * mt * 128 * 4;
         *out = p;
         return true;
     };
     for (int d = std::min(DFQ_MIN_KBLOCKS, chunks); d <= chunks; ++d) {
         if (!split(d, num_cus / d, pl)) continue;
-        /* Two k-blocks of stream-K ranges give tiles three or four parts (second pass); whole
-         * tiles per workgroup give two, finished in the kernel by the pair exchange, at the
-         * price of up to one tile of imbalance; taken where its LDS fits (one output block
-         * per tile a workgroup holds) and a workgroup holds few enough tiles (with one value
-         * per atomic the exchange lost from four tiles on: N = 17408 at 16 rows, 24.4
-         * against 20.7 us). */
+        /* Two or three k-blocks of stream-K ranges give tiles three or more parts (second
+         * pass); whole tiles per workgroup give one per k-block, finished in the kernel by the
+         * pair exchange, at the price of up to one tile of imbalance; taken where its LDS fits
+         * (one output block per tile a workgroup holds) and a workgroup holds few enough
+         * tiles (with one value per atomic the exchange lost from four tiles on: N = 17408 at
+         * 16 rows, 24.4 against 20.7 us). */
         Plan al;
-        if (pl->reduce && d == 2 && split_aligned(num_cus / 2, &al) &&
+        if (pl->reduce && (d == 2 || d == 3) && split_aligned(d, num_cus / d, &al) &&
             (T + al.Gkb - 1) / al.Gkb <= kAlignedMaxTiles) {
             *pl = al;
             return true;

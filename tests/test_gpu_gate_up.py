@@ -28,6 +28,8 @@ CASES = [
     (6, 2048, 2048, 8, 128, F16, True),     # 8-bit g128
     (16, 1024, 1024, 4, 32, BF16, True),    # 4-bit g32, two row tiles
     (1, 4096, 4096, 4, 64, F16, False),     # one row
+    (8, 2560, 17408, 4, 64, BF16, True),    # three k-blocks of whole tiles: chained exchange
+    (7, 512, 16384, 8, 64, F16, False),     # the same, one tile per workgroup
 ]
 
 

@@ -32,6 +32,7 @@ CASES = [
     (8, 32768, 512, 4, 64, BF16, False, False),     # outputs written at the workgroup's end
     (16, 32768, 512, 4, 64, F16, True, False),      # the same, 16 rows, fp16, linear bias
     (3, 40000, 1024, 8, 64, BF16, False, False),    # the same, 8-bit, tiles cut by ranges
+    (8, 5000, 17408, 4, 64, BF16, True, False),     # three k-blocks: chained pair exchange
 ]
 
 

@@ -123,11 +123,32 @@ def test_narrow_n_split_matches_oracle_and_repeats(ctx, oracle, M, N, K, bits, g
         assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
 
 
+# Three k-blocks of whole tiles (1..8 rows at K of 15360..17408): every tile has three parts,
+# summed by a chain of two pair exchanges, no second pass.  Ragged N, one and four tiles per
+# workgroup, 8-bit fp16, group 32, and group 128 with five chunks a k-block.
+THREE_BLOCK_CASES = [
+    (8, 1000, 16384, 4, 64, BF16),
+    (6, 5000, 17408, 8, 64, F16),
+    (7, 777, 16896, 4, 32, BF16),
+    (8, 3000, 15360, 4, 128, F16),
+]
+
+
 @pytest.mark.parametrize("M,N,K,bits,gs,dt", ALIGNED_CASES)
 def test_aligned_split_matches_oracle_and_repeats(ctx, oracle, M, N, K, bits, gs, dt):
+    check_aligned(ctx, oracle, M, N, K, bits, gs, dt, 2)
+
+
+@pytest.mark.parametrize("M,N,K,bits,gs,dt", THREE_BLOCK_CASES)
+def test_three_block_aligned_split_matches_oracle_and_repeats(ctx, oracle, M, N, K, bits, gs,
+                                                              dt):
+    check_aligned(ctx, oracle, M, N, K, bits, gs, dt, 3)
+
+
+def check_aligned(ctx, oracle, M, N, K, bits, gs, dt, nkb):
     import torch
     p = ctx.plan(M, N, K, bits, gs)
-    assert p["aligned"] == 1 and p["nkb"] == 2 and p["reduce"] == 0, p
+    assert p["aligned"] == 1 and p["nkb"] == nkb and p["reduce"] == 0, p
     c = make_case(M, N, K, bits=bits, gs=gs, xdt=dt, seed=11 * M + N + K + bits + gs,
                   lbias=(N % 2 == 1))
     announce(f"aligned M={M} N={N} K={K} bits={bits} gs={gs} dt={dt}")

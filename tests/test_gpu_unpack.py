@@ -13,7 +13,8 @@ words or groups cannot hide under a tolerance.
 Covered: every bits x group size x dtype in the 1..8-row form with 8-group chunks (c8), the
 9..16-row form (mt16) and one-super-step chunks (c1), plus the narrow split (two k-blocks,
 one tile per workgroup, pair exchange), the aligned split (two k-blocks of whole tiles per
-workgroup) and a reduce split (several k-blocks, second pass).
+workgroup), three k-blocks of whole tiles (chained pair exchange) and a reduce split
+(several k-blocks, second pass).
 """
 import numpy as np
 import pytest
@@ -119,7 +120,19 @@ def test_unpack_is_exact_in_a_reduce_split(ctx, bits, gs, dt, M):
     """Several k-blocks and workgroups per tile, summed by the second pass: every k of the
     first, a middle and the last chunk."""
     ck = chunk_k(bits, gs)
-    K = 32 * ck
-    pos = list(range(ck)) + list(range(15 * ck, 16 * ck)) + list(range(31 * ck, 32 * ck))
+    K = 48 * ck
+    pos = list(range(ck)) + list(range(23 * ck, 24 * ck)) + list(range(47 * ck, 48 * ck))
     run_one_hot(ctx, 48, K, bits, gs, dt, M, pos, seed=bits * 5000 + gs + dt,
                 expect_plan={"reduce": 1})
+
+
+@pytest.mark.parametrize("bits,gs,dt,M", [(4, 64, BF16, 8), (8, 64, F16, 7)])
+def test_unpack_is_exact_in_the_three_block_aligned_split(ctx, bits, gs, dt, M):
+    """Three k-blocks of whole tiles per workgroup, summed by a chain of two pair exchanges:
+    every k of the first chunk of each k-block and of the last chunk (K = 32 chunks)."""
+    ck = chunk_k(bits, gs)
+    K = 32 * ck
+    pos = (list(range(ck)) + list(range(10 * ck, 11 * ck)) + list(range(21 * ck, 22 * ck))
+           + list(range(31 * ck, 32 * ck)))
+    run_one_hot(ctx, 48, K, bits, gs, dt, M, pos, seed=bits * 7000 + gs + dt,
+                expect_plan={"nkb": 3, "aligned": 1, "reduce": 0})

@@ -92,7 +92,13 @@ def replay(p):
         for t in range(T):
             parts_of[t] = parts_of.get(t, 0) + tile_owners(p, kb, t)
     max_parts = max(parts_of.values())
-    assert p["reduce"] == int(max_parts > 2), (max_parts, p["reduce"])
+    # aligned splits (two or three k-blocks) finish every tile in the kernel, by the pair
+    # exchange or a chain of two of them; other splits with three or more parts take the
+    # second pass
+    if p["aligned"]:
+        assert nkb in (2, 3) and max_parts == nkb and not p["reduce"], (max_parts, p)
+    else:
+        assert p["reduce"] == int(max_parts > 2), (max_parts, p["reduce"])
 
     def finalize(t, units):
         assert t not in y_writes, f"tile {t} written twice"
@@ -201,6 +207,7 @@ EXTRA_SHAPES = ([(m, n, k, 4, 64) for m in (8, 16) for (n, k) in
                   (34816, 5120))]
                 + _unpack_test_shapes()
                 + [(16, 4096, 5120, 8, 64), (6, 1024, 5120, 4, 128), (3, 40, 256, 4, 32)]
+                + [(8, 1024, 17408, 4, 64), (8, 1000, 16384, 4, 64), (6, 5120, 17408, 8, 64)]
                 + ALIGNED_SHAPES)
 
 
@@ -249,7 +256,21 @@ def test_planner_respects_lds_and_staging_limits():
 def test_long_k_uses_few_uneven_k_blocks():
     # K = 17408 at M = 8: 34 chunks of 512 k; three k-blocks of 11-12 chunks fit LDS
     p = make_plan(8, 5120, 17408, 4, 64)
-    assert p["nkb"] == 3 and p["chunks"] == 34 and p["reduce"] == 1
+    assert p["nkb"] == 3 and p["chunks"] == 34 and p["SS"] == 12
+
+
+def test_three_k_blocks_take_whole_tiles_up_to_twelve_a_workgroup():
+    """Three k-blocks of whole tiles per workgroup finish every tile with a chain of two pair
+    exchanges, no second pass: the down projection (four tiles a workgroup) and narrow N.
+    From thirteen tiles a workgroup on the stream-K split with the second pass stays."""
+    for shape, tiles in [((8, 5120, 17408, 4, 64), 4), ((8, 1024, 17408, 4, 64), 1),
+                         ((8, 1000, 16384, 4, 64), 1), ((6, 5120, 17408, 8, 64), 4)]:
+        p = make_plan(*shape)
+        assert (p["nkb"], p["aligned"], p["reduce"], p["nslot_kb"]) == (3, 1, 0, 1), (shape, p)
+        assert -(-p["T"] // p["Gkb"]) == tiles and 3 * p["Gkb"] <= 256, (shape, p)
+        assert p["lds_bytes"] <= 163840
+    p = make_plan(8, 17408, 17408, 4, 64)
+    assert (p["nkb"], p["aligned"], p["reduce"]) == (3, 0, 1), p
 
 
 def test_narrow_n_splits_k_in_two_with_one_tile_per_workgroup():
@@ -265,14 +286,14 @@ def test_narrow_n_splits_k_in_two_with_one_tile_per_workgroup():
 
 def test_outputs_leave_at_the_end_where_workgroups_hold_many_tiles():
     # the LM head (38 tiles a workgroup) and the C5 gate|up (10): outputs written at the end
-    # of each workgroup; the headline shape (6) and C3 (5 per k-block): as each tile finishes
+    # of each workgroup; the headline shape (6) and C3 (4 per k-block): as each tile finishes
     assert make_plan(8, 151936, 5120, 4, 64)["burst"] == 1
     assert make_plan(8, 34816, 5120, 4, 64)["burst"] == 1
     assert make_plan(1, 32768, 512, 4, 64)["burst"] == 1
     assert make_plan(8, 17408, 5120, 4, 64)["burst"] == 0
     assert make_plan(8, 7168, 5120, 4, 64)["burst"] == 0
     p = make_plan(8, 5120, 17408, 4, 64)
-    assert p["reduce"] == 1 and p["burst"] == 0
+    assert p["aligned"] == 1 and p["burst"] == 0
     # reduce splits holding many tiles per workgroup leave their parts at the end too
     for shape in [(16, 40000, 4096, 4, 64), (12, 40000, 6144, 4, 64), (16, 151936, 5120, 4, 64)]:
         p = make_plan(*shape)
