@@ -83,7 +83,17 @@ constexpr int kThreads = kWaves * 64;        // streaming threads
 #endif
 constexpr int kPublishers = DFQ_PUBLISHERS;
 constexpr int kBlock = kThreads + 64 * kPublishers;  // + the publisher waves
-constexpr int kMaxStageItems = 96 / DFQ_WAVES;  // 16-byte x chunks staged per thread
+/* x is staged by the first 8 waves only (two per SIMD).  A workgroup's waves start over
+ * about 1 us, and staging is VALU-bound: spread over all 12 streaming waves, the last waves
+ * to start finish it last and hold up the staging barrier.  With the late waves free of it
+ * they only issue their first weights.  Measured on MI355X at M = 8 (us, against staging
+ * on all 12 waves): N = 17408, K = 5120 15.16 against 15.44; gate|up N = 34816 23.25 against
+ * 23.6; N = 5120, K = 17408 15.98 against 16.2; N = K = 5120 9.67 against 9.85; 16 rows at
+ * N = 17408 18.62 against 18.84; one row and N = 7168 within noise; one row at N = K = 4096
+ * (eight units a workgroup, one per staging wave) 7.20 against 7.05. */
+constexpr int kStageThreads = 8 * 64;
+constexpr int kMaxStageItems = 96 * 64 / kStageThreads;  // 16-byte x chunks staged per thread
+static_assert(kThreads >= kStageThreads, "the staging waves are streaming waves");
 
 /* The dynamic LDS block of a qmm_mt8 workgroup (its layout is fixed by the host plan). */
 __device__ __forceinline__ uint8_t* lds_base() {
@@ -1023,7 +1033,7 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
     const int k0 = kbk.c0 * (CH * C::KSS);  // first k of this k-block
 
     /* ---- x staging loads go out first (their wait must not cover the weight prefetch).
-     * Item c (16 bytes, 8 elements) of the M x kr block goes to thread c % kThreads, so each
+     * Item c (16 bytes, 8 elements) of the M x kr block goes to thread c % kStageThreads, so each
      * load instruction reads 1 KB of consecutive x; rounds past the last item are skipped
      * and lanes past it reload the last one. */
     const int CPR = kr / 8;  // 16-byte chunks per row of the k-block
@@ -1032,12 +1042,13 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
      * staging is VALU-bound, so no 64-bit address arithmetic per item) */
     const uint8_t* xb = (const uint8_t*)p.x + (size_t)k0 * 2;
     const uint32_t xrow = (uint32_t)p.K * 2u;
-    /* (row, chunk) of item tid + i * kThreads, stepped without a per-item division */
-    const int dr = kThreads / CPR, dcc = kThreads - dr * CPR;  // wave-uniform
+    /* (row, chunk) of item tid + i * kStageThreads, stepped without a per-item division */
+    const int dr = kStageThreads / CPR, dcc = kStageThreads - dr * CPR;  // wave-uniform
     uint32_t xo[kMaxStageItems];  // LDS offset of the item, (1 + row) * RS + chunk * 16
     int xs[kMaxStageItems];       // its group-sum slot, or -1 past the last item
     u32x4_t xv[kMaxStageItems];
     auto stage_loads = [&]() {
+        if (tid >= kStageThreads) return;
         int r = tid / CPR, cc = tid - r * CPR;
 #pragma unroll
         for (int i = 0; i < kMaxStageItems; ++i) {
@@ -1045,7 +1056,7 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
             const int rr = in ? r : p.M - 1, c2 = in ? cc : CPR - 1;
             xo[i] = __umul24((uint32_t)(1 + rr), (uint32_t)p.lds_row_stride) + (uint32_t)c2 * 16u;
             xs[i] = in ? (cc / (GS / 8)) * XR + r : -1;
-            if (i * kThreads < items)
+            if (i * kStageThreads < items)
                 xv[i] = *(const u32x4_t*)(xb + (__umul24((uint32_t)rr, xrow) + (uint32_t)c2 * 16u));
             r += dr;
             cc += dcc;
@@ -1085,9 +1096,9 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
     const uint8_t* sbytes = (const uint8_t*)p.scales;
     const uint8_t* bbytes = (const uint8_t*)p.biases;
 
-    /* last unit fetched.  A wave that gets no unit still fetches one, never used: the first
-     * unit of the range, or the k-block's last unit for an empty range (which can sit past
-     * the last unit when a small k-block has fewer units than workgroups). */
+    /* last unit fetched (the clamped reload past the end of the range fetches it again): the
+     * first unit of the range, or the k-block's last unit for an empty range (a small
+     * k-block can have fewer units than workgroups). */
     int lu = min(a, p.T * SS - 1);
     auto issue = [&](int slot, int g) {
         sg[slot] = g;
@@ -1134,7 +1145,7 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
     auto stage_finish = [&]() {
 #pragma unroll
     for (int i = 0; i < kMaxStageItems; ++i) {
-        if (i * kThreads < items) {
+        if (tid < kStageThreads && i * kStageThreads < items) {
             float sm = chunk_dot<F16>(xv[i], 0.0f);
             sm += dpp_f32<0xB1>(sm);             // lanes ^1 (quad_perm 1,0,3,2)
             sm += dpp_f32<0x4E>(sm);             // lanes ^2 (quad_perm 2,3,0,1)
@@ -1158,6 +1169,15 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
     __builtin_amdgcn_sched_barrier(0);
     };
     auto issue_first = [&]() {
+        if (wave * PF >= L) {
+            /* no unit for this wave (takes only grow): it never enters the streaming loop, so
+             * it fetches nothing, rather than queueing a load ahead of the waves that do
+             * have units (waves that stage no x get here first).  One row at N = K = 4096
+             * (eight units a workgroup): 7.20 against 7.34 us. */
+#pragma unroll
+            for (int i = 0; i < PF; ++i) sg[i] = wave * PF + i;
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < PF; ++i) {
             issue(i, wave * PF + i);

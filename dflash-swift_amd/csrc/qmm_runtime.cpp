@@ -54,7 +54,7 @@ constexpr int kThreads = kWaves * 64;             // qmm_mt8 streaming threads
 #define DFQ_PUBLISHERS 2               // must match the kernels' build
 #endif
 constexpr int kBlockThreads = kThreads + 64 * DFQ_PUBLISHERS;  // + the publisher waves
-constexpr int kMaxStageItems = 96 / DFQ_WAVES;    // must match qmm_kernels.hip
+constexpr int64_t kStageItems = 96 * 64;           // x items a workgroup stages (as the kernels)
 
 struct PlanKey {
     int M, N, K, bits, gs;
@@ -204,7 +204,7 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
     auto split = [&](int d, int64_t G0, Plan* out) -> bool {
         const int ss_max = (chunks + d - 1) / d, ss_min = chunks / d;
         const int kr = ss_max * kch;
-        if ((int64_t)M * (kr / 8) > (int64_t)kMaxStageItems * kThreads) return false;
+        if ((int64_t)M * (kr / 8) > kStageItems) return false;
         Plan p{};
         p.kss = kss;
         p.mt = mt;
@@ -271,7 +271,7 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
         if (chunks < dd) return false;
         const int ss_max = (chunks + dd - 1) / dd;
         const int kr = ss_max * kch;
-        if ((int64_t)M * (kr / 8) > (int64_t)kMaxStageItems * kThreads) return false;
+        if ((int64_t)M * (kr / 8) > kStageItems) return false;
         const int64_t G = std::min<int64_t>(std::max<int64_t>(1, G0), T);
         const int64_t tmax = (T + G - 1) / G;
         Plan p{};
