@@ -90,7 +90,8 @@ constexpr int kBlock = kThreads + 64 * kPublishers;  // + the publisher waves
  * on all 12 waves): N = 17408, K = 5120 15.16 against 15.44; gate|up N = 34816 23.25 against
  * 23.6; N = 5120, K = 17408 15.98 against 16.2; N = K = 5120 9.67 against 9.85; 16 rows at
  * N = 17408 18.62 against 18.84; one row and N = 7168 within noise; one row at N = K = 4096
- * (eight units a workgroup, one per staging wave) 7.20 against 7.05. */
+ * (eight units a workgroup: the four waves with none fetch an unused unit, now ahead of the
+ * staging waves' weights) 7.35 against 7.05. */
 constexpr int kStageThreads = 8 * 64;
 constexpr int kMaxStageItems = 96 * 64 / kStageThreads;  // 16-byte x chunks staged per thread
 static_assert(kThreads >= kStageThreads, "the staging waves are streaming waves");
@@ -1096,9 +1097,11 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
     const uint8_t* sbytes = (const uint8_t*)p.scales;
     const uint8_t* bbytes = (const uint8_t*)p.biases;
 
-    /* last unit fetched (the clamped reload past the end of the range fetches it again): the
-     * first unit of the range, or the k-block's last unit for an empty range (a small
-     * k-block can have fewer units than workgroups). */
+    /* last unit fetched.  A wave that gets no unit still fetches one, never used: the first
+     * unit of the range, or the k-block's last unit for an empty range (which can sit past
+     * the last unit when a small k-block has fewer units than workgroups).  Skipping that
+     * fetch measured 1.1 us slower at 16 rows and 0.2 us at 8 (the loop's code changes),
+     * for 0.18 us at one row and N = K = 4096 (eight units a workgroup). */
     int lu = min(a, p.T * SS - 1);
     auto issue = [&](int slot, int g) {
         sg[slot] = g;
@@ -1169,15 +1172,6 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
     __builtin_amdgcn_sched_barrier(0);
     };
     auto issue_first = [&]() {
-        if (wave * PF >= L) {
-            /* no unit for this wave (takes only grow): it never enters the streaming loop, so
-             * it fetches nothing, rather than queueing a load ahead of the waves that do
-             * have units (waves that stage no x get here first).  One row at N = K = 4096
-             * (eight units a workgroup): 7.20 against 7.34 us. */
-#pragma unroll
-            for (int i = 0; i < PF; ++i) sg[i] = wave * PF + i;
-            return;
-        }
 #pragma unroll
         for (int i = 0; i < PF; ++i) {
             issue(i, wave * PF + i);
