@@ -30,6 +30,7 @@ CASES = [
     (1, 4096, 4096, 4, 64, F16, False),     # one row
     (8, 2560, 17408, 4, 64, BF16, True),    # three k-blocks of whole tiles: chained exchange
     (7, 512, 16384, 8, 64, F16, False),     # the same, one tile per workgroup
+    (16, 1504, 7680, 4, 64, BF16, True),    # the same with two row tiles
 ]
 
 

@@ -33,6 +33,7 @@ CASES = [
     (16, 32768, 512, 4, 64, F16, True, False),      # the same, 16 rows, fp16, linear bias
     (3, 40000, 1024, 8, 64, BF16, False, False),    # the same, 8-bit, tiles cut by ranges
     (8, 5000, 17408, 4, 64, BF16, True, False),     # three k-blocks: chained pair exchange
+    (16, 3000, 7680, 4, 64, F16, False, False),     # the same with two row tiles
 ]
 
 

@@ -123,7 +123,7 @@ def test_narrow_n_split_matches_oracle_and_repeats(ctx, oracle, M, N, K, bits, g
         assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
 
 
-# Three k-blocks of whole tiles (1..8 rows at K of 15360..17408): every tile has three parts,
+# Three k-blocks of whole tiles (1..8 rows at K of 15360..17408, 9..16 rows from K = 7680): every tile has three parts,
 # summed by a chain of two pair exchanges, no second pass.  Ragged N, one and four tiles per
 # workgroup, 8-bit fp16, group 32, and group 128 with five chunks a k-block.
 THREE_BLOCK_CASES = [
@@ -131,6 +131,9 @@ THREE_BLOCK_CASES = [
     (6, 5000, 17408, 8, 64, F16),
     (7, 777, 16896, 4, 32, BF16),
     (8, 3000, 15360, 4, 128, F16),
+    (12, 1024, 9216, 4, 64, BF16),           # two row tiles: 9..16 rows
+    (16, 3000, 7680, 4, 64, F16),
+    (13, 777, 9216, 4, 128, BF16),
 ]
 
 

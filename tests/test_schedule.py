@@ -207,7 +207,8 @@ EXTRA_SHAPES = ([(m, n, k, 4, 64) for m in (8, 16) for (n, k) in
                   (34816, 5120))]
                 + _unpack_test_shapes()
                 + [(16, 4096, 5120, 8, 64), (6, 1024, 5120, 4, 128), (3, 40, 256, 4, 32)]
-                + [(8, 1024, 17408, 4, 64), (8, 1000, 16384, 4, 64), (6, 5120, 17408, 8, 64)]
+                + [(8, 1024, 17408, 4, 64), (8, 1000, 16384, 4, 64), (6, 5120, 17408, 8, 64),
+                   (16, 3000, 7680, 4, 64), (13, 777, 9216, 4, 128)]
                 + ALIGNED_SHAPES)
 
 
@@ -261,10 +262,12 @@ def test_long_k_uses_few_uneven_k_blocks():
 
 def test_three_k_blocks_take_whole_tiles_up_to_twelve_a_workgroup():
     """Three k-blocks of whole tiles per workgroup finish every tile with a chain of two pair
-    exchanges, no second pass: the down projection (four tiles a workgroup) and narrow N.
+    exchanges, no second pass: the down projection (four tiles a workgroup), narrow N, and
+    9..16 rows from K = 7680.
     From thirteen tiles a workgroup on the stream-K split with the second pass stays."""
     for shape, tiles in [((8, 5120, 17408, 4, 64), 4), ((8, 1024, 17408, 4, 64), 1),
-                         ((8, 1000, 16384, 4, 64), 1), ((6, 5120, 17408, 8, 64), 4)]:
+                         ((8, 1000, 16384, 4, 64), 1), ((6, 5120, 17408, 8, 64), 4),
+                         ((16, 3000, 7680, 4, 64), 3), ((12, 1024, 9216, 4, 64), 1)]:
         p = make_plan(*shape)
         assert (p["nkb"], p["aligned"], p["reduce"], p["nslot_kb"]) == (3, 1, 0, 1), (shape, p)
         assert -(-p["T"] // p["Gkb"]) == tiles and 3 * p["Gkb"] <= 256, (shape, p)
