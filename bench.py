@@ -3,24 +3,29 @@
 
 Workload (the headline configuration): y[M,17408] = x[M,5120] . dequant(W)^T, W 4-bit
 group 64 in MLX's affine layout, bf16 activations / scales / biases / output, M swept over
-1, 2, 4, 6, 8 (and 16).  A "step" is one call at M = 8 (a verify pass's width).
+1..6, 8 (and 16).  A "step" is one call at M = 8 (a verify pass's width).
 
 Method:
   * 8 distinct weight sets (~400 MB, more than the 256 MB Infinity Cache) are rotated so
-    every call streams its weights from HBM;
-  * the `steps` calls of one M are captured into one HIP graph on a non-default stream and
+    every call streams its weights from HBM: a graph holds whole cycles through every set
+    (at least `steps` calls), so 350 MB of other weights pass between two uses of one set,
+    also across the boundary between replays;
+  * the calls of one M are captured into one HIP graph on a non-default stream and
     replayed R >= 10 times (at least 200 calls); HIP events on that stream bracket each
-    replay, so a replay's time / steps is the back-to-back time per call including launch
+    replay, so a replay's time / calls is the back-to-back time per call including launch
     gaps; us_per_call is the median over the replays, with p10 / p90 beside it;
   * algorithmic bytes per call = N*K*bits/8 + 2*N*(K/gs)*2 + M*K*2 + M*N*2;
   * read_ceiling: the library's plain streaming-read kernel moving the M=8 call's
     algorithmic bytes per launch over the same rotation, timed the same way: the
     single-launch read rate this memory system reaches with no compute;
+  * generic: the stock-path stand-in (dfq_qmm_fallback) at 1..5 rows beside the fast
+    kernel, the rows below the drop-in window's lower bound;
   * the CPU baseline is the oracle's fp32 restatement of MLX's CPU algorithm (dequantise a
-    group, multiply-accumulate), OpenMP over the host cores, timed on a bounded sample;
-  * the 64-layer verify forward (c5_chain*) is timed with one HIP graph per layer and as one
-    graph; the per-layer form once more in a child process with the HIP runtime's graph
-    packet capture off (c5_chain_fused_no_packet_capture).
+    group, multiply-accumulate), OpenMP over the host cores, timed on a bounded sample: an
+    MLX-semantics CPU restatement, not MLX;
+  * the 64-layer verify forward (c5_chain*) is timed with one HIP graph per layer, launched
+    one by one or composed into one launch, and as one captured graph; c5_rows times the
+    composed fused forward at every verify width of the reference's --rows sweep.
 
 --profile-timed dispatches the matmul only as graph replays (one warm-up replay, then the
 timed ones), so that `rocprofv3 --kernel-trace --stats` averages the calls the figures time.
@@ -39,6 +44,7 @@ sys.path.insert(0, os.path.join(ROOT, "dflash-swift_amd"))
 
 N_OUT, K_IN, BITS, GS = 17408, 5120, 4, 64
 HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 << 20   # MI355X Infinity Cache: a weight set re-read sooner could hit it
 # rocprofv3 summary of the M=8 launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated); the
 # roofline's measured-traffic figure is read from its "traffic_bytes_per_launch:" line.
 PROFILE = os.path.join(ROOT, "profiles", "qmm_mt8_b4g64_bf16_k5120_n17408.md")
@@ -110,10 +116,28 @@ def time_replays(torch, stream, graph, steps, reps):
     return [e0.elapsed_time(e1) * 1000.0 / steps for e0, e1 in events]
 
 
+def rotation(nsets, steps, set_bytes):
+    """The calls one graph captures over `nsets` rotated weight sets of `set_bytes` each: the
+    fewest whole cycles through every set that hold at least `steps` calls, so that every set
+    is used equally often and the bytes read between two uses of one set -- within a replay
+    and across the boundary into the next replay, which starts again at set 0 -- are always
+    (nsets - 1) * set_bytes."""
+    calls = -(-max(1, steps) // nsets) * nsets
+    return {"calls_per_graph": calls, "sets_touched": nsets,
+            "min_reuse_bytes": (nsets - 1) * set_bytes}
+
+
+def set_bytes_of(sets):
+    w, s, b = sets[0]
+    return sum(t.numel() * t.element_size() for t in (w, s, b))
+
+
 def time_m(torch, ctx, stream, sets, M, steps, warmup, N, K, bits, gs, ws, wsb, f16=False,
            x_sd=1.0):
-    """Per-call microseconds (one figure per replay) of `steps` graph-replayed calls at row
-    count M, over replays_for(steps) replays (fp16 throughout with f16, else bf16)."""
+    """Per-call microseconds (one figure per replay) of graph-replayed calls at row count M
+    (fp16 throughout with f16, else bf16): the graph holds rotation(...)["calls_per_graph"]
+    calls, at least `steps`, cycling through every weight set; replays_for(steps) replays,
+    each divided by the calls it holds."""
     import dflash_qmm
     dev = sets[0][0].device
     g = torch.Generator(device=dev)
@@ -129,15 +153,16 @@ def time_m(torch, ctx, stream, sets, M, steps, warmup, N, K, bits, gs, ws, wsb, 
             ctx.qmm_raw(x, w, s, b, y, M, N, K, bits, gs, B, B, B, ws=ws, ws_bytes=wsb,
                         stream=stream)
 
+    calls = rotation(len(sets), steps, 0)["calls_per_graph"]
     torch.cuda.synchronize()
     ctx.graph_begin(stream)
-    issue(steps, 0)
+    issue(calls, 0)
     graph = ctx.graph_end(stream)
     with torch.cuda.stream(stream):
         if not GRAPH_ONLY:
             issue(warmup, 1)           # eager warm-up (also checks the eager path)
         graph.launch(stream)           # graph warm-up
-        times = time_replays(torch, stream, graph, steps, replays_for(steps))
+        times = time_replays(torch, stream, graph, calls, replays_for(steps))
     graph.close()
     return times
 
@@ -160,7 +185,7 @@ def time_configs(torch, ctx, stream, dev, steps, warmup):
     out = {}
     for (name, M, N, K, bits, gs, f16, x_sd, s_sd) in CONFIGS:
         nb = algorithmic_bytes(M, N, K, bits, gs)
-        nsets = max(2, -(-400_000_000 // (N * K * bits // 8)))
+        nsets = max(2, -(-400_000_000 // algorithmic_bytes(0, N, K, bits, gs)))
         sets = make_sets(torch, nsets, N, K, bits, gs, dev, seed=3,
                          dtype=torch.float16 if f16 else torch.bfloat16, scale_sd=s_sd)
         wsb = ctx.workspace_bytes(M, N, K, bits, gs)
@@ -171,7 +196,8 @@ def time_configs(torch, ctx, stream, dev, steps, warmup):
                      "p90": round(d["p90"], 3), "bytes": nb,
                      "gbs": round(nb / (d["median"] * 1e-6) / 1e9, 1),
                      "frac": round(nb / (d["median"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                     "rotated_sets": nsets}
+                     "rotated_sets": nsets,
+                     **rotation(nsets, steps, set_bytes_of(sets))}
         print(f"[bench] {name}: {d['median']:.2f} us/call, {out[name]['gbs']:.0f} GB/s",
               file=sys.stderr, flush=True)
         del sets
@@ -183,14 +209,15 @@ def time_read(torch, ctx, stream, nbytes, nsets, steps, dev):
     `nbytes`, `steps` launches per graph, replayed like the matmul; per-launch us."""
     bufs = [torch.ones(nbytes // 4, dtype=torch.int32, device=dev) for _ in range(nsets)]
     sink = torch.zeros(8 * ctx.num_cus, dtype=torch.int32, device=dev)
+    calls = rotation(nsets, steps, nbytes)["calls_per_graph"]
     torch.cuda.synchronize()
     ctx.graph_begin(stream)
-    for i in range(steps):
+    for i in range(calls):
         ctx.read_stream(bufs[i % nsets], nbytes, sink, stream=stream)
     graph = ctx.graph_end(stream)
     with torch.cuda.stream(stream):
         graph.launch(stream)
-        times = time_replays(torch, stream, graph, steps, replays_for(steps))
+        times = time_replays(torch, stream, graph, calls, replays_for(steps))
     graph.close()
     return times
 
@@ -199,17 +226,47 @@ def time_units(torch, ctx, stream, sets, M, steps, N=N_OUT, K=K_IN):
     """The fast kernel's own loads with no compute (dfq_debug_read_units) over the rotated
     weight sets of the matmul, `steps` launches per graph, replayed like it; per-launch us."""
     sink = torch.zeros(12 * ctx.num_cus, dtype=torch.int32, device=sets[0][0].device)
+    calls = rotation(len(sets), steps, 0)["calls_per_graph"]
     torch.cuda.synchronize()
     ctx.graph_begin(stream)
-    for i in range(steps):
+    for i in range(calls):
         w, s, b = sets[i % len(sets)]
         ctx.read_units(w, s, b, M, N, K, sink, stream=stream)
     graph = ctx.graph_end(stream)
     with torch.cuda.stream(stream):
         graph.launch(stream)
-        times = time_replays(torch, stream, graph, steps, replays_for(steps))
+        times = time_replays(torch, stream, graph, calls, replays_for(steps))
     graph.close()
     return times
+
+
+def time_generic(torch, ctx, stream, sets, rows=(1, 2, 3, 4, 5), calls=None, reps=10):
+    """The stock-path stand-in (dfq_qmm_fallback: one wave per output, W re-read for every
+    row) on the headline shape at each of `rows`, over the rotated weight sets, one graph of
+    whole cycles through the sets replayed `reps` times; median per-call us."""
+    import dflash_qmm
+    dev = sets[0][0].device
+    B = dflash_qmm.BF16
+    calls = calls or len(sets)
+    out = {}
+    for M in rows:
+        g = torch.Generator(device=dev)
+        g.manual_seed(100 + M)
+        x = torch.randn(M, K_IN, device=dev, generator=g).to(torch.bfloat16)
+        y = torch.empty(M, N_OUT, device=dev, dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        ctx.graph_begin(stream)
+        for i in range(calls):
+            w, s, b = sets[i % len(sets)]
+            ctx.fallback_raw(x, w, s, b, y, M, N_OUT, K_IN, BITS, GS, B, B, B, stream=stream)
+        graph = ctx.graph_end(stream)
+        with torch.cuda.stream(stream):
+            graph.launch(stream)
+            d = stats(time_replays(torch, stream, graph, calls, reps))
+        graph.close()
+        out[str(M)] = round(d["median"], 2)
+        print(f"[bench] generic M={M}: {d['median']:.1f} us/call", file=sys.stderr, flush=True)
+    return out
 
 
 def time_copy(torch, stream, nbytes, nsets, steps):
@@ -244,15 +301,11 @@ C5_FUSED = [(7168, 5120), (5120, 5120), (34816, 5120), (5120, 17408)]
 C5_LM_HEAD = (151936, 5120)
 
 
-def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, one_graph=False):
-    """The C5 verify forward at M=8: `layers` layers of seven 4-bit g64 matmuls (or, fused,
-    q|k|v, o, gate|up with the SiLU-mul epilogue, down), then the lm_head and the greedy
-    accept; distinct random weights per layer (about 11.6 GiB, so every layer streams from
-    HBM).  Each layer is captured as one HIP graph (the configuration's form), or with
-    one_graph the whole forward, lm_head and accept included, as a single graph.  Returns
-    the figures of one form."""
-    import dflash_qmm
-    M = 8
+def c5_weights(torch, dev, fused, layers=64):
+    """Distinct random 4-bit g64 weights for every layer of the C5 verify forward (about
+    11.6 GiB, so every layer streams from HBM) and the LM head: codes uniform, scales
+    |N(0, 0.02)|, biases N(0, 0.01), bf16.  Fused: q|k|v, o, gate|up (interleaved by 8 rows
+    for the SiLU-mul epilogue), down; else the seven projections."""
     g = torch.Generator(device=dev)
     g.manual_seed(5)
 
@@ -264,6 +317,28 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, one_graph=False):
         return w, s, b
 
     layer = C5_FUSED if fused else C5_LAYER
+    return {"fused": fused, "layers": layers, "layer": layer,
+            "lw": [[weights(N, K) for (N, K) in layer] for _ in range(layers)],
+            "lm": weights(*C5_LM_HEAD)}
+
+
+C5_FORMS = {
+    "per_layer": "one HIP graph per layer, launched one after the other",
+    "composed": "one HIP graph per layer, the 64 composed into one launch (dfq_graph_compose)",
+    "one_graph": "the forward captured as one HIP graph",
+}
+
+
+def chain_c5(torch, ctx, dev, W, M=8, form="per_layer", forwards=10):
+    """The C5 verify forward at M rows over the weights W (c5_weights): every layer's
+    projections, then the LM head with the greedy accept (only M + 1 ints leave the device).
+    Each layer is captured as one HIP graph (the configuration's form); `form` says how the
+    forward launches them (C5_FORMS).  One untimed forward, then `forwards` timed ones, each
+    between its own HIP events; figures are the median with p10 / p90."""
+    import dflash_qmm
+    fused, layers, layer = W["fused"], W["layers"], W["layer"]
+    g = torch.Generator(device=dev)
+    g.manual_seed(6)
     shapes = layer + [C5_LM_HEAD]
     wsb = max(ctx.workspace_bytes(M, N, K, 4, 64) for (N, K) in shapes)
     ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
@@ -282,22 +357,16 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, one_graph=False):
         kinds = ["qmm"] * len(layer)
     stream = torch.cuda.Stream(device=dev)
     B = dflash_qmm.BF16
-    graphs = []
-    lw = [[weights(N, K) for (N, K) in layer] for _ in range(layers)]
-    wlm, slm, blm = weights(*C5_LM_HEAD)
-    proposals = torch.zeros(M - 1, dtype=torch.int32, device=dev)
+    wlm, slm, blm = W["lm"]
+    proposals = torch.zeros(max(1, M - 1), dtype=torch.int32, device=dev)
     tokens = torch.empty(M, dtype=torch.int32, device=dev)
     accepted = torch.empty(1, dtype=torch.int32, device=dev)
     acc_ws = torch.zeros(ctx.qmm_argmax_accept_workspace_bytes(M, *C5_LM_HEAD, 4, 64),
                          dtype=torch.uint8, device=dev)
-    torch.cuda.synchronize()
-    if one_graph:
-        ctx.graph_begin(stream)
-    for li in range(layers):
-        wl = lw[li]
+
+    def enqueue_layer(li):
+        wl = W["lw"][li]
         layer_in = x if li == 0 else outs[-1]
-        if not one_graph:
-            ctx.graph_begin(stream)
         for j, (N, K) in enumerate(layer):
             inp = layer_in if srcs[j] is None else outs[srcs[j]]
             w, s, b = wl[j]
@@ -306,80 +375,91 @@ def chain_c5(torch, ctx, dev, layers=64, reps=5, fused=False, one_graph=False):
             else:
                 ctx.qmm_raw(inp, w, s, b, outs[j], M, N, K, 4, 64, B, B, B, ws=ws,
                             ws_bytes=ws.numel(), stream=stream)
-        if not one_graph:
-            graphs.append(ctx.graph_end(stream))
 
     def lm_only():
-        """the lm_head fused with the greedy accept: only M + 1 ints leave the device"""
-        ctx.qmm_argmax_accept(outs[-1], wlm, slm, blm, 4, 64, proposals=proposals,
-                              tokens=tokens, accepted=accepted, ws=acc_ws, stream=stream)
+        ctx.qmm_argmax_accept(outs[-1], wlm, slm, blm, 4, 64,
+                              proposals=proposals if M > 1 else None, tokens=tokens,
+                              accepted=accepted, ws=acc_ws, stream=stream)
 
-    if one_graph:
+    torch.cuda.synchronize()
+    graphs, launch = [], []
+    if form == "one_graph":
+        ctx.graph_begin(stream)
+        for li in range(layers):
+            enqueue_layer(li)
         lm_only()
-        graphs.append(ctx.graph_end(stream))
+        launch = [ctx.graph_end(stream)]
+    else:
+        for li in range(layers):
+            ctx.graph_begin(stream)
+            enqueue_layer(li)
+            graphs.append(ctx.graph_end(stream))
+        launch = [ctx.graph_compose(graphs)] if form == "composed" else graphs
 
     def forward():
-        for gr in graphs:
+        for gr in launch:
             gr.launch(stream)
-        if not one_graph:
+        if form != "one_graph":
             lm_only()
 
     def timed(fn, n):
         with torch.cuda.stream(stream):
             fn()
             torch.cuda.synchronize()
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            for _ in range(n):
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(n)]
+            for e0, e1 in ev:
+                e0.record(stream)
                 fn()
-            e1.record(stream)
+                e1.record(stream)
             torch.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1000.0 / n
+        return [e0.elapsed_time(e1) * 1000.0 for e0, e1 in ev]
 
-    total = timed(forward, reps)
-    lm = timed(lm_only, 20)
-    for gr in graphs:
+    fw = stats(timed(forward, forwards))
+    lm = stats(timed(lm_only, 20))
+    for gr in set(graphs) | set(launch):
         gr.close()
     layer_bytes = sum(algorithmic_bytes(M, N, K) for (N, K) in C5_LAYER)   # the same fused
     total_bytes = layers * layer_bytes + algorithmic_bytes(M, *C5_LM_HEAD)
     ideal = total_bytes / (HBM_PEAK_GBS * 1e3)
+    total = fw["median"]
     return {
-        "workload": (f"M=8 verify forward: {layers} layers x "
+        "workload": (f"M={M} verify forward: {layers} layers x "
                      + ("(q|k|v, o, gate|up with silu*up epilogue, down)" if fused
                         else "(q,k,v,o,gate,up,down)")
-                     + " + lm_head + greedy accept, 4-bit g64 bf16, "
-                     + ("one HIP graph per forward" if one_graph else "one HIP graph per layer")),
+                     + " + lm_head + greedy accept, 4-bit g64 bf16, " + C5_FORMS[form]),
         "us_per_forward": round(total, 1),
+        "p10": round(fw["p10"], 1),
+        "p90": round(fw["p90"], 1),
+        "forwards": fw["replays"],
         "ideal_us_at_8TBs": round(ideal, 1),
         "frac_of_ideal": round(ideal / total, 4),
         "bytes_per_forward": total_bytes,
-        "layer_us": round((total - lm) / layers, 2),
+        "layer_us": round((total - lm["median"]) / layers, 2),
         "layer_ideal_us": round(layer_bytes / (HBM_PEAK_GBS * 1e3), 2),
-        "lm_head_accept_us": round(lm, 2),
+        "lm_head_accept_us": round(lm["median"], 2),
         "lm_head_ideal_us": round(algorithmic_bytes(M, *C5_LM_HEAD) / (HBM_PEAK_GBS * 1e3), 2),
     }
 
 
-def c5_child(form, env_extra, timeout=600):
-    """chain_c5 of one form in a child process started with extra environment variables.
-    The HIP runtime reads them once, when it starts, so they cannot change inside this
-    process.  DEBUG_CLR_GRAPH_PACKET_CAPTURE=0 turns off the runtime's pre-recorded packets
-    for graph launches; with them, each of the 64 layer graphs starts several microseconds
-    after the previous one ends, without them the layer graphs follow each other as the
-    kernels of one graph do.  Returns the child's figures, or what went wrong."""
-    import subprocess
-    env = dict(os.environ)
-    env.update(env_extra)
-    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--c5-only", form], env=env,
-                       capture_output=True, text=True, timeout=timeout)
-    for line in r.stdout.splitlines():
-        if line.startswith("{"):
-            d = json.loads(line)["c5_" + form]
-            d["environment"] = env_extra
-            return d
-    return {"error": f"child exited with {r.returncode}", "stderr_tail": r.stderr[-400:],
-            "environment": env_extra}
+# Verify widths of the forward-cost curve (the reference's dflash-bench --rows sweep).
+C5_ROWS = [1, 2, 4, 5, 6, 8, 9, 12, 16]
+
+
+def c5_rows(torch, ctx, dev, W, rows=C5_ROWS, form="composed", forwards=10):
+    """The fused verify forward's cost at each verify width, and its ratio to one row."""
+    out = {}
+    for M in rows:
+        r = chain_c5(torch, ctx, dev, W, M=M, form=form, forwards=forwards)
+        out[str(M)] = {"us_per_forward": r["us_per_forward"], "p10": r["p10"], "p90": r["p90"]}
+        print(f"[bench] c5 rows M={M}: {r['us_per_forward']} us/forward", file=sys.stderr,
+              flush=True)
+    base = out[str(rows[0])]["us_per_forward"]
+    for M in rows:
+        out[str(M)]["ratio_to_m1"] = round(out[str(M)]["us_per_forward"] / base, 4)
+    return {"workload": ("fused verify forward (64 layers + LM head + greedy accept, 4-bit g64 "
+                         "bf16), " + C5_FORMS[form] + f", median of {forwards} forwards per width"),
+            "rows": out}
 
 
 def time_lm_head(torch, ctx, stream, dev, steps=20, nsets=4, reps=20):
@@ -452,6 +532,7 @@ def cpu_baseline(seconds):
         "us_per_call": round(us, 1),
         "cores": orc.num_threads(),
         "kind": "port",
+        "label": "MLX-semantics CPU restatement, not MLX",
         "sample": (f"M=8 K=5120 4-bit g64 bf16, {n_sample} of 17408 output rows, {calls} calls "
                    f"in {el:.1f}s, scaled to all rows"),
     }
@@ -533,7 +614,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--sets", type=int, default=8, help="rotated weight sets")
-    ap.add_argument("--ms", default="1,2,4,6,8,16")
+    ap.add_argument("--ms", default="1,2,3,4,5,6,8,16")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-chain", action="store_true",
@@ -542,7 +623,12 @@ def main():
                     help="skip the other benchmark configurations (C1, C3, C4)")
     ap.add_argument("--no-reference", action="store_true",
                     help="skip the read-ceiling and device-copy reference legs")
-    ap.add_argument("--c5-only", choices=["separate", "fused", "fused_one_graph"],
+    ap.add_argument("--no-generic", action="store_true",
+                    help="skip the stock-path stand-in's timing at 1..5 rows")
+    ap.add_argument("--no-rows", action="store_true",
+                    help="skip the verify forward's cost at each width (c5_rows)")
+    ap.add_argument("--c5-only", choices=["separate", "fused", "fused_composed",
+                                          "fused_one_graph"],
                     default=None,
                     help="only time this form of the 64-layer verify forward (for profiling) "
                          "and print its figures")
@@ -590,8 +676,11 @@ def main():
         return
     ctx = dflash_qmm.Context(0)
     if args.c5_only:
-        r = chain_c5(torch, ctx, dev, fused=args.c5_only.startswith("fused"),
-                     one_graph=args.c5_only == "fused_one_graph")
+        fused = args.c5_only.startswith("fused")
+        form = {"separate": "per_layer", "fused": "per_layer", "fused_composed": "composed",
+                "fused_one_graph": "one_graph"}[args.c5_only]
+        W = c5_weights(torch, dev, fused)
+        r = chain_c5(torch, ctx, dev, W, form=form)
         print(json.dumps({"c5_" + args.c5_only: r}), flush=True)
         ctx.close()
         return
@@ -640,6 +729,8 @@ def main():
             "M_sweep": ms,
             "rotated_weight_sets": args.sets,
             "replays_per_M": replays_for(args.steps),
+            "rotation": rotation(args.sets, args.steps, set_bytes_of(sets)),
+            "mall_bytes": MALL_BYTES,
         },
         "us_per_call": {str(m): round(us[m], 3) for m in ms},
         "us_per_call_p10": {str(m): round(dist[m]["p10"], 3) for m in ms},
@@ -697,6 +788,15 @@ def main():
         }
         print(f"[bench] device copy moving {nb8 / 1e6:.1f} MB: {uc_copy:.2f} us/copy",
               file=sys.stderr, flush=True)
+    if not args.no_generic:
+        gen = time_generic(torch, ctx, stream, sets)
+        out["generic"] = {
+            "workload": ("dfq_qmm_fallback, the stock-path stand-in a swapped layer falls "
+                         "through to below the window's lower bound, on the headline shape; "
+                         "us per call beside the fast kernel's at the same rows"),
+            "us_per_call": gen,
+            "fast_us_per_call": {k: round(us[int(k)], 3) for k in gen if int(k) in us},
+        }
     del sets
     torch.cuda.empty_cache()
     if not args.no_configs:
@@ -706,19 +806,22 @@ def main():
         out["lm_head_accept"] = time_lm_head(torch, ctx, stream, dev)
         print(f"[bench] lm_head + accept: fused {out['lm_head_accept']['fused_us']} us, two "
               f"calls {out['lm_head_accept']['two_calls_us']} us", file=sys.stderr, flush=True)
-        out["c5_chain"] = chain_c5(torch, ctx, dev)
+        W = c5_weights(torch, dev, fused=False)
+        out["c5_chain"] = chain_c5(torch, ctx, dev, W, form="per_layer")
+        del W
         torch.cuda.empty_cache()
-        out["c5_chain_fused"] = chain_c5(torch, ctx, dev, fused=True)
-        out["c5_chain_fused_one_graph"] = chain_c5(torch, ctx, dev, fused=True, one_graph=True)
-        torch.cuda.empty_cache()
-        out["c5_chain_fused_no_packet_capture"] = c5_child(
-            "fused", {"DEBUG_CLR_GRAPH_PACKET_CAPTURE": "0"})
-        for key in ("c5_chain", "c5_chain_fused", "c5_chain_fused_one_graph",
-                    "c5_chain_fused_no_packet_capture"):
-            if "us_per_forward" not in out[key]:
-                continue
+        W = c5_weights(torch, dev, fused=True)
+        for key, form in (("c5_chain_fused", "per_layer"), ("c5_chain_fused_composed", "composed"),
+                          ("c5_chain_fused_one_graph", "one_graph")):
+            out[key] = chain_c5(torch, ctx, dev, W, form=form)
+        for key in ("c5_chain", "c5_chain_fused", "c5_chain_fused_composed",
+                    "c5_chain_fused_one_graph"):
             print(f"[bench] {key}: {out[key]['us_per_forward']} us/forward "
                   f"(ideal {out[key]['ideal_us_at_8TBs']})", file=sys.stderr, flush=True)
+        if not args.no_rows:
+            out["c5_rows"] = c5_rows(torch, ctx, dev, W)
+        del W
+        torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)

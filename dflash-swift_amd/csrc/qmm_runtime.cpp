@@ -1026,6 +1026,42 @@ dfq_status dfq_graph_launch(dfq_graph* gr, void* stream) {
     return e == hipSuccess ? DFQ_OK : hip_fail(e, "hipGraphLaunch");
 }
 
+dfq_status dfq_graph_compose(dfq_ctx* ctx, dfq_graph* const* parts, int n, dfq_graph** out) {
+    if (!ctx || !out || (n > 0 && !parts)) return fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    if (n < 1) return fail(DFQ_ERR_INVALID_ARGUMENT, "no graphs to compose");
+    for (int i = 0; i < n; ++i) {
+        if (!parts[i] || !parts[i]->graph)
+            return fail(DFQ_ERR_INVALID_ARGUMENT, "graph %d is null", i);
+        if (parts[i]->device != ctx->device)
+            return fail(DFQ_ERR_INVALID_ARGUMENT, "graph %d was captured on device %d, not %d", i,
+                        parts[i]->device, ctx->device);
+    }
+    DeviceGuard g(ctx->device);
+    auto* gr = new dfq_graph();
+    gr->device = ctx->device;
+    hipError_t e = hipGraphCreate(&gr->graph, 0);
+    if (e != hipSuccess) {
+        delete gr;
+        return hip_fail(e, "hipGraphCreate");
+    }
+    hipGraphNode_t prev = nullptr;
+    for (int i = 0; i < n && e == hipSuccess; ++i) {
+        hipGraphNode_t node = nullptr;
+        e = hipGraphAddChildGraphNode(&node, gr->graph, prev ? &prev : nullptr, prev ? 1 : 0,
+                                      parts[i]->graph);
+        prev = node;
+    }
+    if (e == hipSuccess) e = hipGraphInstantiate(&gr->exec, gr->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(gr->graph);
+        delete gr;
+        return hip_fail(e, "compose graphs");
+    }
+    *out = gr;
+    return DFQ_OK;
+}
+
 dfq_status dfq_graph_destroy(dfq_graph* gr) {
     if (!gr) return DFQ_OK;
     DeviceGuard g(gr->device);

@@ -115,6 +115,7 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         "dfq_qmm_argmax_accept": ([P, P, P, P, P, P, P, I, I, I, I, I, I, P, P, P, P, S, P],
                                   I),
         "dfq_graph_launch": ([P, P], I), "dfq_graph_destroy": ([P], I),
+        "dfq_graph_compose": ([P, PP, I, PP], I),
         "dfq_linear_create": ([P, ctypes.POINTER(_LinearDesc), PP], I),
         "dfq_small_m_linear_create": ([P, PP], I), "dfq_linear_destroy": ([P], I),
         "dfq_linear_is_small_m": ([P], I), "dfq_linear_output_dtype": ([P, I], I),
@@ -427,6 +428,14 @@ class Context:
         g = ctypes.c_void_p()
         _check(self.lib.dfq_graph_end(self.handle, _stream(stream), ctypes.byref(g)),
                "dfq_graph_end")
+        return Graph(self.lib, g)
+
+    def graph_compose(self, graphs) -> "Graph":
+        """One graph running `graphs` in order (dfq_graph_compose); they stay usable."""
+        arr = (ctypes.c_void_p * len(graphs))(*[gr.handle.value for gr in graphs])
+        g = ctypes.c_void_p()
+        _check(self.lib.dfq_graph_compose(self.handle, arr, len(graphs), ctypes.byref(g)),
+               "dfq_graph_compose")
         return Graph(self.lib, g)
 
 

@@ -175,6 +175,15 @@ dfq_status dfq_graph_begin(dfq_ctx* ctx, void* stream);
 dfq_status dfq_graph_end(dfq_ctx* ctx, void* stream, dfq_graph** out);
 dfq_status dfq_graph_launch(dfq_graph* graph, void* stream);
 dfq_status dfq_graph_destroy(dfq_graph* graph);
+/* One graph that runs the n captured graphs parts[0..n-1] one after the other (each as a
+ * child-graph node depending on the previous one), instantiated once: the verify forward's
+ * per-layer graphs launched as one.  The parts are copied in; they stay valid and owned by
+ * the caller.  Launched graphs follow each other with a gap of several microseconds on
+ * MI355X (the runtime's graph launch), the kernels of one graph do not: 64 layer graphs
+ * composed run as fast as the forward captured as one graph.  No counterpart in the
+ * reference (DFlashSpeculativeGenerator.swift:389-398 issues one lazy MLX graph per
+ * forward). */
+dfq_status dfq_graph_compose(dfq_ctx* ctx, dfq_graph* const* parts, int n, dfq_graph** out);
 
 /* h[m][n] = silu(gu[m][n]) * gu[m][N + n] for the fused gate||up projection's output
  * gu[M][2N] (row pitch 2N elements): the activation between gate||up and down in a layer

@@ -50,6 +50,64 @@ def test_graph_replays_match_eager(ctx):
     g.close()
 
 
+def test_composed_layer_graphs_match_eager(ctx):
+    """Three layers captured one graph each, chained through their inputs (each layer reads
+    the previous layer's output), composed into one graph (dfq_graph_compose): every replay
+    equals the eager chain, with eager work and synchronisations between replays, and the
+    parts still replay on their own afterwards."""
+    dev = "cuda"
+    K = 1024
+    chain = []
+    x0 = upload(make_case(8, K, K, bits=4, gs=64, seed=70))[0]
+    for i, N in enumerate((K, 2048, K)):
+        kin = K if i != 2 else 2048
+        c = make_case(8, N, kin, bits=4, gs=64, seed=71 + i)
+        _, w, s, b, _ = upload(c)
+        chain.append((w, s, b, torch.empty(8, N, dtype=torch.bfloat16, device=dev), kin, N))
+    need = max(ctx.workspace_bytes(8, N, kin, 4, 64) for (_, _, _, _, kin, N) in chain)
+    ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.Stream()
+
+    def layer(i):
+        w, s, b, y, kin, N = chain[i]
+        inp = x0 if i == 0 else chain[i - 1][3]
+        ctx.qmm(inp, w, s, b, 4, 64, out=y, ws=ws, stream=stream)
+
+    announce("composed graphs: eager reference")
+    with torch.cuda.stream(stream):
+        for i in range(3):
+            layer(i)
+    torch.cuda.synchronize()
+    eager = [c[3].clone() for c in chain]
+    parts = []
+    for i in range(3):
+        ctx.graph_begin(stream)
+        layer(i)
+        parts.append(ctx.graph_end(stream))
+    fwd = ctx.graph_compose(parts)
+    for rep in range(3):
+        announce(f"composed graphs: replay {rep}")
+        for c in chain:
+            c[3].fill_(5.0)
+        torch.cuda.synchronize()
+        fwd.launch(stream)
+        torch.cuda.synchronize()
+        for i, (e, c) in enumerate(zip(eager, chain)):
+            assert torch.equal(e.view(torch.int16), c[3].view(torch.int16)), (rep, i)
+    announce("composed graphs: parts on their own")
+    for c in chain:
+        c[3].fill_(5.0)
+    torch.cuda.synchronize()
+    for gr in parts:
+        gr.launch(stream)
+    torch.cuda.synchronize()
+    for e, c in zip(eager, chain):
+        assert torch.equal(e.view(torch.int16), c[3].view(torch.int16))
+    fwd.close()
+    for gr in parts:
+        gr.close()
+
+
 def test_one_workspace_serves_every_shape(ctx):
     """Each call leaves the workspace zero, so shapes can alternate on one workspace."""
     shapes = [(8, 48, 16384), (1, 5000, 12288), (8, 17408, 5120), (8, 48, 16384)]

@@ -393,3 +393,4 @@ def test_prefetch_addresses_stay_in_bounds(shape):
                 lane_s = 0 if ch > 1 else (4 if gps == 4 else 0)
                 last_s = ((row0 + rmax) * GPR + kc // gs) * 2 + lane_s + sv
                 assert last_s <= N * GPR * 2, (kb, cl, u)
+
