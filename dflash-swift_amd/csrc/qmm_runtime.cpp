@@ -93,6 +93,14 @@ struct dfq_ctx {
     void* scratch = nullptr;             // the fixed scratch of dfq_qmm_noalloc (this device)
     std::mutex mu;
     std::unordered_map<PlanKey, dfq::Plan, PlanKeyHash> plans;
+    /* Splits that dfq_qmm_noalloc computed for shapes the cache above does not hold: a table
+     * allocated with the context and filled without allocating (the oldest entry goes when
+     * it is full), so that a no-allocation caller plans each shape once, not on every call. */
+    static constexpr int kFixedPlans = 64;
+    PlanKey fixed_key[kFixedPlans] = {};
+    dfq::Plan fixed_plan[kFixedPlans];
+    int fixed_used = 0;
+    int fixed_next = 0;
 };
 
 struct dfq_graph {
@@ -334,7 +342,8 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
 }
 
 /* The split for a shape, from the context's cache; a shape with none is cached too (T == 0).
- * cache = false (the no-allocation path) computes a missing split without storing it. */
+ * cache = false (the no-allocation path) looks in the cache, then in the context's fixed
+ * table, and stores a split it had to compute in that table, which allocates nothing. */
 static bool find_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, Plan* out,
                       bool cache = true) {
     PlanKey key{M, N, K, bits, gs};
@@ -342,12 +351,26 @@ static bool find_plan(dfq_ctx* ctx, int M, int N, int K, int bits, int gs, Plan*
     auto it = ctx->plans.find(key);
     if (it != ctx->plans.end()) {
         *out = it->second;
-    } else {
-        Plan p;
-        if (!make_plan(M, N, K, bits, gs, ctx->num_cus, ctx->lds_max, &p)) p = Plan{};
-        if (cache) ctx->plans.emplace(key, p);
-        *out = p;
+        return out->T > 0;
     }
+    if (!cache)
+        for (int i = 0; i < ctx->fixed_used; ++i)
+            if (ctx->fixed_key[i] == key) {
+                *out = ctx->fixed_plan[i];
+                return out->T > 0;
+            }
+    Plan p;
+    if (!make_plan(M, N, K, bits, gs, ctx->num_cus, ctx->lds_max, &p)) p = Plan{};
+    if (cache) {
+        ctx->plans.emplace(key, p);
+    } else {
+        const int slot = ctx->fixed_used < dfq_ctx::kFixedPlans
+                             ? ctx->fixed_used++
+                             : ctx->fixed_next++ % dfq_ctx::kFixedPlans;
+        ctx->fixed_key[slot] = key;
+        ctx->fixed_plan[slot] = p;
+    }
+    *out = p;
     return out->T > 0;
 }
 
@@ -755,8 +778,25 @@ dfq_status dfq_qmm_noalloc(dfq_ctx* ctx, const void* x, const uint32_t* w, const
                     "M=%d N=%d K=%d needs %zu bytes of workspace; the fixed scratch of "
                     "dfq_qmm_noalloc holds %zu (use dfq_qmm with a workspace)",
                     M, N, K, need, (size_t)DFQ_SCRATCH_MAX_BYTES);
-    return qmm_any(ctx, x, w, scales, biases, lbias, y, M, N, K, bits, gs, xdt, sdt, ydt,
-                   ctx->scratch, DFQ_SCRATCH_MAX_BYTES, stream, 0, false);
+    s = qmm_any(ctx, x, w, scales, biases, lbias, y, M, N, K, bits, gs, xdt, sdt, ydt,
+                ctx->scratch, DFQ_SCRATCH_MAX_BYTES, stream, 0, false);
+    if (s && need) {
+        /* A call of several launches that failed after its first one was queued (the second
+         * pass, or the second 8-row pass) can leave partial sums in the scratch, which every
+         * later call on this GPU would read as exchange words: clear what the shape uses,
+         * behind whatever was queued.  The first error is the one reported. */
+        const std::string first = g_last_error;
+        DeviceGuard g(ctx->device);
+        uint32_t* p = (uint32_t*)ctx->scratch;
+        uint32_t v = 0;
+        uint64_t count = (need + 3) / 4;
+        void* args[] = {&p, &v, &count};
+        unsigned grid = (unsigned)std::min<uint64_t>((count + 255) / 256, 4096);
+        (void)hipModuleLaunchKernel(ctx->fill, grid, 1, 1, 256, 1, 1, 0, (hipStream_t)stream,
+                                    args, nullptr);
+        g_last_error = first;
+    }
+    return s;
 }
 
 dfq_status dfq_qmm_silu_gate_up(dfq_ctx* ctx, const void* x, const uint32_t* w_gu,

@@ -217,7 +217,13 @@ dfq_status dfq_model_destroy(dfq_model* model) {
 
 dfq_status dfq_model_set_leaf(dfq_model* model, const char* path, dfq_linear* lin) {
     if (!model || !path || !lin) return dfq::fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
-    model->owned.emplace_back(lin);
+    /* A handle the model already owns (set at another path, as a tied layer is, or one that
+     * dfq_model_leaf returned) is only pointed at again: owning it twice would free it twice
+     * when the model is destroyed. */
+    bool owned = false;
+    for (const auto& o : model->owned)
+        if (o.get() == lin) owned = true;
+    if (!owned) model->owned.emplace_back(lin);
     model->leaves[path] = lin;
     return DFQ_OK;
 }

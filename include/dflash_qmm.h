@@ -128,8 +128,11 @@ dfq_status dfq_qmm(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* s
  * hipFree or host allocation) and returns DFQ_ERR_WORKSPACE for a shape whose workspace
  * (dfq_qmm_workspace_bytes) is larger.  Every call on one GPU shares that array: calls that
  * overlap on one GPU (other streams, other threads, other contexts) race, so serialise
- * them.  Each call leaves the array zero, as dfq_qmm leaves its workspace.  Same arguments,
- * results and errors as dfq_qmm otherwise (bit-identical outputs). */
+ * them.  Each call leaves the array zero, as dfq_qmm leaves its workspace; a call that fails
+ * after queueing a launch queues a clear of the bytes its shape uses.  The work split of a
+ * shape is planned once per context: shapes dfq_qmm has not met go to a fixed table of 64
+ * entries made with the context.  Same arguments, results and errors as dfq_qmm otherwise
+ * (bit-identical outputs). */
 #define DFQ_SCRATCH_MAX_BYTES ((size_t)64 << 20)
 dfq_status dfq_qmm_noalloc(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
                            const void* biases, const void* linear_bias, void* y, int M, int N,
@@ -274,7 +277,9 @@ dfq_status dfq_linear_workspace_bytes(dfq_linear* lin, int rows, size_t* bytes);
 /* A module tree reduced to what the swap needs: named leaf layers. */
 dfq_status dfq_model_create(dfq_model** out);
 dfq_status dfq_model_destroy(dfq_model* model);
-/* Adds (or replaces) the leaf at `path`; the model takes ownership of `lin`. */
+/* Adds (or replaces) the leaf at `path`; the model takes ownership of `lin`.  A handle the
+ * model already owns (set at another path, as for a tied layer, or returned by
+ * dfq_model_leaf) may be set again: it stays owned once and is freed once. */
 dfq_status dfq_model_set_leaf(dfq_model* model, const char* path, dfq_linear* lin);
 /* The leaf at `path` (NULL if none) as a borrowed handle: never pass it to
  * dfq_linear_destroy.  It stays valid until dfq_model_destroy, also after the leaf is

@@ -121,3 +121,39 @@ def test_leaf_views_do_not_own_the_model_leaves():
         assert model.projection.is_small_m and model.other.is_small_m
         gc.collect()
     assert enable_small_m_quantized_matmul(model) == 0
+
+
+def test_a_leaf_set_at_two_paths_is_owned_once():
+    """A tied layer: one handle set at two paths, and a handle that dfq_model_leaf returned set
+    again.  The model must free each handle once (run in a child process with glibc's heap
+    checks on, where a double free aborts)."""
+    import subprocess
+    import sys
+    code = r'''
+import ctypes, dflash_qmm
+lib = dflash_qmm.load_library()
+fake = 1 << 40
+d = dflash_qmm._LinearDesc(fake, fake, fake, None, 4096, 1024, 4, 64, 1, dflash_qmm.BF16)
+h = ctypes.c_void_p()
+assert lib.dfq_linear_create(None, ctypes.byref(d), ctypes.byref(h)) == 0
+m = ctypes.c_void_p()
+assert lib.dfq_model_create(ctypes.byref(m)) == 0
+assert lib.dfq_model_set_leaf(m, b"model.embed.proj", h) == 0
+assert lib.dfq_model_set_leaf(m, b"lm_head.proj", h) == 0
+lib.dfq_model_leaf.restype = ctypes.c_void_p
+again = lib.dfq_model_leaf(m, b"lm_head.proj")
+assert again == h.value
+assert lib.dfq_model_set_leaf(m, b"tied.again", ctypes.c_void_p(again)) == 0
+assert lib.dfq_model_leaf_count(m) == 3
+assert lib.dfq_enable_small_m_quantized_matmul(m) == 3
+assert lib.dfq_model_destroy(m) == 0
+print("ok")
+'''
+    import os
+    env = dict(os.environ, MALLOC_CHECK_="3")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env["PYTHONPATH"] = os.pathsep.join([os.path.join(root, "dflash-swift_amd"),
+                                         env.get("PYTHONPATH", "")])
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0 and "ok" in r.stdout, (r.returncode, r.stderr[-600:])

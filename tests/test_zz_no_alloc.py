@@ -5,8 +5,6 @@ only the workspace differs) on calls in a row of decreasing size, which also sho
 scratch is left zero for the next call; a shape whose workspace exceeds the scratch is
 refused before any launch.
 """
-import ctypes
-
 import numpy as np
 import pytest
 
@@ -27,33 +25,57 @@ def noalloc(ctx, c, x, w, s, b, lb, y, stream=None):
     return rc
 
 
-# decreasing in size; the first three need a workspace (pair exchange, reduce split, narrow
-# split), the fourth a reduce split of 16 rows, the last one none
+# decreasing in size (M, N, K, bits, gs, dtype, linear bias, split the planner must give):
+#   the headline shape: one k-block, the pair exchange of tiles shared by two workgroups;
+#   a 16-row reduce split: parts in workspace slots, summed and re-zeroed by the second pass;
+#   the down projection: three k-blocks of whole tiles, a chain of two pair exchanges;
+#   16 rows of 8-bit: two k-blocks, each tile in one workgroup of each, paired;
+#   a narrow N at six rows: two k-blocks of one tile per workgroup;
+#   a tiny shape that needs no workspace
 CASES = [
-    (8, 17408, 5120, 4, 64, BF16, False),
-    (8, 5120, 17408, 4, 64, BF16, True),
-    (16, 4096, 5120, 8, 64, F16, False),
-    (6, 1024, 5120, 4, 128, BF16, True),
-    (3, 40, 256, 4, 32, F16, False),
+    (8, 17408, 5120, 4, 64, BF16, False, dict(nkb=1, reduce=0)),
+    (16, 40000, 4096, 4, 64, BF16, False, dict(reduce=1)),
+    (8, 5120, 17408, 4, 64, BF16, True, dict(nkb=3, aligned=1, reduce=0)),
+    (16, 4096, 5120, 8, 64, F16, False, dict(nkb=2, reduce=0, nslot_kb=1)),
+    (6, 1024, 5120, 4, 128, BF16, True, dict(nkb=2, reduce=0)),
+    (3, 40, 256, 4, 32, F16, False, dict(need_ws=0)),
 ]
 
 
-def test_noalloc_matches_qmm_on_calls_in_a_row(ctx):
+@pytest.fixture
+def fresh():
+    """A context of its own, whose split cache no other test has filled."""
     import torch
-    for i, (M, N, K, bits, gs, dt, lbias) in enumerate(CASES):
+    c = dflash_qmm.Context(0)
+    yield c
+    torch.cuda.synchronize()
+    c.close()
+
+
+def test_noalloc_matches_qmm_on_calls_in_a_row(fresh):
+    """Each shape goes through dfq_qmm_noalloc before dfq_qmm has planned it on this context
+    (the split comes from the no-allocation table), then through dfq_qmm on a fresh workspace:
+    bit-identical."""
+    import torch
+    ctx = fresh
+    for i, (M, N, K, bits, gs, dt, lbias, want_plan) in enumerate(CASES):
         c = make_case(M, N, K, bits=bits, gs=gs, xdt=dt, seed=900 + i, lbias=lbias)
-        need = ctx.workspace_bytes(M, N, K, bits, gs)
-        assert need <= SCRATCH_MAX
         x, w, s, b, lb = upload(c)
-        announce(f"noalloc call {i}: M={M} N={N} K={K} bits={bits} gs={gs} ws={need}")
-        want = ctx.qmm(x, w, s, b, bits, gs, lbias=lb)
-        got = torch.empty_like(want)
+        tdt = torch.bfloat16 if dt == BF16 else torch.float16
+        got = torch.empty(M, N, dtype=tdt, device="cuda")
+        announce(f"noalloc call {i}: M={M} N={N} K={K} bits={bits} gs={gs}, before dfq_qmm")
         rc = noalloc(ctx, c, x, w, s, b, lb, got)
         assert rc == 0, ctx.lib.dfq_last_error()
+        plan = ctx.plan(M, N, K, bits, gs)
+        assert all(plan[k] == v for k, v in want_plan.items()), (i, plan)
+        need = ctx.workspace_bytes(M, N, K, bits, gs)
+        assert need <= SCRATCH_MAX
+        announce(f"noalloc call {i}: dfq_qmm, workspace {need}")
+        want = ctx.qmm(x, w, s, b, bits, gs, lbias=lb)
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"call {i}"
-    # the same first shape once more, after the others: the scratch was left re-armed
-    M, N, K, bits, gs, dt, lbias = CASES[0]
+    # the first shape once more, after the others: the scratch was left re-armed
+    M, N, K, bits, gs, dt, lbias, _ = CASES[0]
     c = make_case(M, N, K, bits=bits, gs=gs, xdt=dt, seed=900)
     x, w, s, b, _ = upload(c)
     announce("noalloc repeat of call 0")
@@ -68,9 +90,9 @@ def test_noalloc_refuses_a_shape_past_the_scratch(ctx):
     """600000 x 5120 at 16 rows needs more workspace than the scratch holds: refused with
     DFQ_ERR_WORKSPACE before any launch (the pointers are never dereferenced)."""
     M, N, K = 16, 600000, 5120
-    assert ctx.workspace_bytes(M, N, K, 4, 64) > SCRATCH_MAX
     fake = 1 << 40
     rc = ctx.lib.dfq_qmm_noalloc(ctx.handle, fake, fake, fake, fake, None, fake, M, N, K, 4,
                                  64, BF16, BF16, BF16, None)
     assert rc == 3, ctx.lib.dfq_last_error()
     assert b"scratch" in ctx.lib.dfq_last_error()
+    assert ctx.workspace_bytes(M, N, K, 4, 64) > SCRATCH_MAX
