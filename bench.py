@@ -18,8 +18,9 @@ Method:
   * read_ceiling: the library's plain streaming-read kernel moving the M=8 call's
     algorithmic bytes per launch over the same rotation, timed the same way: the
     single-launch read rate this memory system reaches with no compute;
-  * generic: the stock-path stand-in (dfq_qmm_fallback) at 1..5 rows beside the fast
-    kernel, the rows below the drop-in window's lower bound;
+  * stock: the stock path a swapped layer falls through to (dfq_qmm_fallback, a GEMV) beside
+    the fast kernel at 1..8 rows, and the fewest rows at which the fast kernel wins (the
+    drop-in window's lower bound on this chip); at one row also for C1;
   * the CPU baseline is the oracle's fp32 restatement of MLX's CPU algorithm (dequantise a
     group, multiply-accumulate), OpenMP over the host cores, timed on a bounded sample: an
     MLX-semantics CPU restatement, not MLX;
@@ -192,12 +193,18 @@ def time_configs(torch, ctx, stream, dev, steps, warmup):
         ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
         d = stats(time_m(torch, ctx, stream, sets, M, steps, warmup, N, K, bits, gs, ws,
                          ws.numel(), f16=f16, x_sd=x_sd))
+        if M == 1:  # below the window: the stock path a swapped layer takes at one row
+            stock1 = time_stock(torch, ctx, stream, sets, [1], N, K, bits, gs, f16,
+                                steps=steps)["1"]
         out[name] = {"us_per_call": round(d["median"], 3), "p10": round(d["p10"], 3),
                      "p90": round(d["p90"], 3), "bytes": nb,
                      "gbs": round(nb / (d["median"] * 1e-6) / 1e9, 1),
                      "frac": round(nb / (d["median"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                      "rotated_sets": nsets,
                      **rotation(nsets, steps, set_bytes_of(sets))}
+        if M == 1:
+            out[name]["stock_us_per_call"] = stock1
+            out[name]["stock_gbs"] = round(nb / (stock1 * 1e-6) / 1e9, 1)
         print(f"[bench] {name}: {d['median']:.2f} us/call, {out[name]['gbs']:.0f} GB/s",
               file=sys.stderr, flush=True)
         del sets
@@ -240,32 +247,35 @@ def time_units(torch, ctx, stream, sets, M, steps, N=N_OUT, K=K_IN):
     return times
 
 
-def time_generic(torch, ctx, stream, sets, rows=(1, 2, 3, 4, 5), calls=None, reps=10):
-    """The stock-path stand-in (dfq_qmm_fallback: one wave per output, W re-read for every
-    row) on the headline shape at each of `rows`, over the rotated weight sets, one graph of
-    whole cycles through the sets replayed `reps` times; median per-call us."""
+def time_stock(torch, ctx, stream, sets, rows, N=N_OUT, K=K_IN, bits=BITS, gs=GS, f16=False,
+               steps=20, reps=10):
+    """The stock path a swapped layer falls through to (dfq_qmm_fallback: its GEMV, one launch
+    per 4 rows) at each of `rows`, over the rotated weight sets, timed like the fast kernel;
+    median per-call us."""
     import dflash_qmm
     dev = sets[0][0].device
-    B = dflash_qmm.BF16
-    calls = calls or len(sets)
+    B = dflash_qmm.F16 if f16 else dflash_qmm.BF16
+    tdt = torch.float16 if f16 else torch.bfloat16
+    calls = rotation(len(sets), steps, 0)["calls_per_graph"]
     out = {}
     for M in rows:
         g = torch.Generator(device=dev)
         g.manual_seed(100 + M)
-        x = torch.randn(M, K_IN, device=dev, generator=g).to(torch.bfloat16)
-        y = torch.empty(M, N_OUT, device=dev, dtype=torch.bfloat16)
+        x = torch.randn(M, K, device=dev, generator=g).to(tdt)
+        y = torch.empty(M, N, device=dev, dtype=tdt)
         torch.cuda.synchronize()
         ctx.graph_begin(stream)
         for i in range(calls):
             w, s, b = sets[i % len(sets)]
-            ctx.fallback_raw(x, w, s, b, y, M, N_OUT, K_IN, BITS, GS, B, B, B, stream=stream)
+            ctx.fallback_raw(x, w, s, b, y, M, N, K, bits, gs, B, B, B, stream=stream)
         graph = ctx.graph_end(stream)
         with torch.cuda.stream(stream):
             graph.launch(stream)
             d = stats(time_replays(torch, stream, graph, calls, reps))
         graph.close()
-        out[str(M)] = round(d["median"], 2)
-        print(f"[bench] generic M={M}: {d['median']:.1f} us/call", file=sys.stderr, flush=True)
+        out[str(M)] = round(d["median"], 3)
+        print(f"[bench] stock M={M} N={N} K={K}: {d['median']:.2f} us/call", file=sys.stderr,
+              flush=True)
     return out
 
 
@@ -623,8 +633,8 @@ def main():
                     help="skip the other benchmark configurations (C1, C3, C4)")
     ap.add_argument("--no-reference", action="store_true",
                     help="skip the read-ceiling and device-copy reference legs")
-    ap.add_argument("--no-generic", action="store_true",
-                    help="skip the stock-path stand-in's timing at 1..5 rows")
+    ap.add_argument("--no-stock", action="store_true",
+                    help="skip the stock path's timing beside the fast kernel")
     ap.add_argument("--no-rows", action="store_true",
                     help="skip the verify forward's cost at each width (c5_rows)")
     ap.add_argument("--c5-only", choices=["separate", "fused", "fused_composed",
@@ -788,14 +798,15 @@ def main():
         }
         print(f"[bench] device copy moving {nb8 / 1e6:.1f} MB: {uc_copy:.2f} us/copy",
               file=sys.stderr, flush=True)
-    if not args.no_generic:
-        gen = time_generic(torch, ctx, stream, sets)
-        out["generic"] = {
-            "workload": ("dfq_qmm_fallback, the stock-path stand-in a swapped layer falls "
-                         "through to below the window's lower bound, on the headline shape; "
-                         "us per call beside the fast kernel's at the same rows"),
-            "us_per_call": gen,
-            "fast_us_per_call": {k: round(us[int(k)], 3) for k in gen if int(k) in us},
+    if not args.no_stock:
+        st = time_stock(torch, ctx, stream, sets, [m for m in ms if m <= 8], steps=args.steps)
+        out["stock"] = {
+            "workload": ("dfq_qmm_fallback, the stock path a swapped layer falls through to "
+                         "below the window's lower bound (its GEMV, one launch per 4 rows), "
+                         "on the headline shape, rotated and replayed like the fast kernel"),
+            "us_per_call": st,
+            "fast_us_per_call": {k: round(us[int(k)], 3) for k in st},
+            "fast_wins_from_rows": min([int(k) for k in st if us[int(k)] < st[k]], default=None),
         }
     del sets
     torch.cuda.empty_cache()

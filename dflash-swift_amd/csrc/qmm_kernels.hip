@@ -1443,6 +1443,211 @@ __device__ __forceinline__ void store_any(void* ptr, int dt, size_t i, float f) 
     else ((uint16_t*)ptr)[i] = f32_to_out<false>(f);
 }
 
+/* ---------------------------------------------------------------------------------- */
+/* The stock path for few rows: a GEMV (qmv)                                            */
+/* ---------------------------------------------------------------------------------- */
+
+/* MLX's stock op runs a GEMV (qmv) below about 13 rows (README.md:19-21 of the reference):
+ * one pass over each weight row per call, at HBM speed for one row.  This is that path for
+ * up to 4 rows a launch (more rows take one launch per 4), written for CDNA4: no MFMA, no
+ * split of K across workgroups, nothing shared between workgroups.
+ *
+ *  - x (all M rows, pre-permuted into the nibble order of the codes, as the fast kernel keeps
+ *    it) and its per-chunk sums are staged in LDS once per workgroup, one workgroup per CU.
+ *  - A wave takes 4 weight rows at a time (groups of the workgroup's rows, the first by wave
+ *    index, then from an LDS counter) and walks K in steps: lane l holds the 16 bytes of codes
+ *    of chunk l + 64 j of each row (32 k at 4 bits, 16 at 8), so each load instruction reads
+ *    1 KB of one row.  The next step's codes, scales and biases are in flight while a step is
+ *    computed (two register sets).
+ *  - A chunk lies in one quantisation group: acc += s * sum x (MAGIC + q) + (b - MAGIC s) *
+ *    sum x, with sum x (MAGIC + q) from v_dot2 on the exact 16-bit codes and the chunk's
+ *    staged x sum.
+ *  - At the end of a row group every lane holds partial sums; a DPP and cross-row reduction
+ *    gives each output, which goes to an LDS block; the workgroup writes its rows' outputs
+ *    after all its groups, so no store joins the loads' queue. */
+constexpr int kQmvWaves = 8;  // waves per workgroup
+constexpr int kQmvRows = 4;   // weight rows a wave works on at once
+
+template <bool F16>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    if constexpr (F16)
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a),
+                                      __builtin_bit_cast(f16x2_t, b), c, false);
+    else
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                               __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+/* The sum of v over the 64 lanes, in every lane: the four DPP steps of a 16-lane row, then
+ * the rows combined. */
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_f32<0xB1>(v);   // quad_perm 1,0,3,2
+    v += dpp_f32<0x4E>(v);   // quad_perm 2,3,0,1
+    v += dpp_f32<0x141>(v);  // row_half_mirror
+    v += dpp_f32<0x140>(v);  // row_mirror
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+template <int BITS, int GS, bool F16, int MM>
+__device__ __forceinline__ void qmv(const QmvParams& p) {
+    constexpr int KPL = 128 / BITS;  // k a lane covers per step (16 bytes of codes)
+    constexpr int IPC = KPL / 8;     // 16-byte x items per lane chunk
+    constexpr int R = kQmvRows;
+    static_assert(KPL <= GS, "a lane chunk lies in one group");
+    uint8_t* lds = lds_base();
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int M = p.M, N = p.N, K = p.K;
+    const int nchunk = K / KPL;
+    const int nsteps = (nchunk + 63) / 64;
+    const int bid = blockIdx.x;
+    const int base = N / p.G, rem = N - base * p.G;
+    const int row_lo = bid * base + min(bid, rem);
+    const int nrows = base + (bid < rem ? 1 : 0);
+    const int ngroups = (nrows + R - 1) / R;
+    float* xsum = (float*)(lds + p.lds_xsum_off);
+    float* out = (float*)(lds + p.lds_out_off);
+    uint32_t* gcnt = (uint32_t*)(lds + p.lds_cnt_off);
+
+    /* x to LDS (item = 8 consecutive k), pre-permuted, and each lane chunk's sum: the IPC
+     * items of a chunk sit in aligned neighbouring lanes */
+    {
+        const int ipr = K / 8;
+        const uint8_t* xg = (const uint8_t*)p.x;
+        for (int it = tid; it < M * ipr; it += kQmvWaves * 64) {
+            const int m = it / ipr, kk = it - m * ipr;
+            const uint32_t off = ((uint32_t)m * (uint32_t)K + (uint32_t)kk * 8u) * 2u;
+            const u32x4_t v = *(const u32x4_t*)(xg + off);
+            float sm = chunk_dot<F16>(v, 0.0f);
+            sm += dpp_f32<0xB1>(sm);                         // lanes ^1
+            if constexpr (IPC == 4) sm += dpp_f32<0x4E>(sm);  // lanes ^2
+            *(u32x4_t*)(lds + off) = (BITS == 4) ? nibble_permute(v) : v;
+            if ((it & (IPC - 1)) == 0) xsum[m * nchunk + kk / IPC] = sm;
+        }
+        if (tid == 0) *gcnt = (uint32_t)kQmvWaves;  // groups below kQmvWaves go by wave index
+    }
+    __syncthreads();
+
+    uint32_t magic = F16 ? 0x64006400u : 0x43004300u;
+    uint32_t nmask = 0x000F000Fu;
+    __asm__ volatile("" : "+v"(magic));  // opaque: keep in a VGPR (see nibble_operand)
+    __asm__ volatile("" : "+s"(nmask));  // opaque: keep in an SGPR
+    constexpr float kOff = (BITS == 4) ? (F16 ? 1024.0f : 128.0f) : 0.0f;
+    const uint8_t* wg = (const uint8_t*)p.w;
+    const uint16_t* sg = (const uint16_t*)p.scales;
+    const uint16_t* bg = (const uint16_t*)p.biases;
+    const uint32_t RB = (uint32_t)K * BITS / 8u;
+    const uint32_t GPR = (uint32_t)(K / GS);
+
+    int grp = wave;
+    while (grp < ngroups) {
+        /* the next group's index, taken now and needed after this group */
+        uint32_t gn = 0;
+        if (lane == 0)
+            gn = __hip_atomic_fetch_add(gcnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        uint32_t rowoff[R], sboff[R];  // a row's first code byte and first scale (clamped rows)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t row = (uint32_t)(row_lo + min(grp * R + r, nrows - 1));
+            rowoff[r] = row * RB;
+            sboff[r] = row * GPR;
+        }
+        float acc[R][MM];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int m = 0; m < MM; ++m) acc[r][m] = 0.0f;
+        u32x4_t wA[R], wB[R];
+        uint32_t sA[R], bA[R], sB[R], bB[R];
+        /* step j's codes, scales and biases; a lane past the row's last chunk reloads it */
+        auto load = [&](u32x4_t (&wv)[R], uint32_t (&sv)[R], uint32_t (&bv)[R], int j) {
+            const uint32_t c = (uint32_t)min(lane + 64 * j, nchunk - 1);
+            const uint32_t g = c * KPL / GS;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                wv[r] = *(const u32x4_t*)(wg + rowoff[r] + c * 16u);
+                sv[r] = sg[sboff[r] + g];
+                bv[r] = bg[sboff[r] + g];
+            }
+        };
+        auto compute = [&](const u32x4_t (&wv)[R], const uint32_t (&sv)[R],
+                           const uint32_t (&bv)[R], int j) {
+            const int c0 = lane + 64 * j;
+            const bool act = c0 < nchunk;
+            const int c = act ? c0 : nchunk - 1;
+            float s[R], bp[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                s[r] = act ? elem_to_f32<F16>(sv[r]) : 0.0f;
+                const float b = act ? elem_to_f32<F16>(bv[r]) : 0.0f;
+                bp[r] = (kOff != 0.0f) ? __builtin_fmaf(-kOff, s[r], b) : b;
+            }
+#pragma unroll
+            for (int m = 0; m < MM; ++m) {
+                if (m >= M) break;
+                const uint8_t* xp = lds + ((uint32_t)m * (uint32_t)K + (uint32_t)c * KPL) * 2u;
+                u32x4_t xv[IPC];
+#pragma unroll
+                for (int i = 0; i < IPC; ++i) xv[i] = *(const u32x4_t*)(xp + i * 16);
+                const float X = xsum[m * nchunk + c];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    float P = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < IPC; ++i) {
+                        u32x4_t B;
+                        if constexpr (BITS == 4) B = nibble_operand<F16>(wv[r][i], nmask, magic);
+                        else B = byte_operand<F16>(wv[r][2 * i], wv[r][2 * i + 1]);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const uint32_t xe = xv[i][e], be = B[e];
+                            P = dot2<F16>(xe, be, P);
+                        }
+                    }
+                    acc[r][m] = __builtin_fmaf(s[r], P, acc[r][m]);
+                    acc[r][m] = __builtin_fmaf(bp[r], X, acc[r][m]);
+                }
+                __builtin_amdgcn_sched_barrier(0);  // one x row at a time
+            }
+        };
+        load(wA, sA, bA, 0);
+        for (int j = 0; j < nsteps; j += 2) {
+            __builtin_amdgcn_sched_barrier(0);
+            load(wB, sB, bB, min(j + 1, nsteps - 1));  // always issued: exact vmcnt waits
+            __builtin_amdgcn_sched_barrier(0);
+            compute(wA, sA, bA, j);
+            if (j + 1 >= nsteps) break;
+            __builtin_amdgcn_sched_barrier(0);
+            load(wA, sA, bA, min(j + 2, nsteps - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            compute(wB, sB, bB, j + 1);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int rr = grp * R + r;
+#pragma unroll
+            for (int m = 0; m < MM; ++m) {
+                if (m >= M) break;
+                const float v = wave_sum(acc[r][m]);
+                if (lane == 0 && rr < nrows) out[m * p.rows_max + rr] = v;
+            }
+        }
+        grp = (int)__builtin_amdgcn_readfirstlane(gn);
+    }
+    __syncthreads();
+    /* the workgroup's outputs, plus the linear bias, rounded once */
+    const uint16_t* lb = (const uint16_t*)p.lbias;
+    uint16_t* y = (uint16_t*)p.y;
+    for (int i = tid; i < M * nrows; i += kQmvWaves * 64) {
+        const int m = i / nrows, rr = i - m * nrows;
+        float v = out[m * p.rows_max + rr];
+        if (lb) v += elem_to_f32<F16>(lb[row_lo + rr]);
+        y[(size_t)m * N + row_lo + rr] = f32_to_out<F16>(v);
+    }
+}
+
 }  // namespace
 
 /* One 64-lane wave per output element (blockIdx.x = column n, blockIdx.y = row m). */
@@ -1743,3 +1948,26 @@ DFQ_MT8_FORMAT(4, 128, true, f16)
 DFQ_MT8_FORMAT(8, 32, true, f16)
 DFQ_MT8_FORMAT(8, 64, true, f16)
 DFQ_MT8_FORMAT(8, 128, true, f16)
+
+/* The stock path's few-row GEMV, per format: one row (decode) and up to four. */
+#define DFQ_QMV_KERNEL(BITS, GS, F16, NAME, MM)                                                \
+    extern "C" __global__ void __launch_bounds__(kQmvWaves * 64)                               \
+        dfq_qmv_b##BITS##_g##GS##_##NAME##_m##MM(QmvParams p) {                               \
+        qmv<BITS, GS, F16, MM>(p);                                                             \
+    }
+#define DFQ_QMV_FORMAT(BITS, GS, F16, NAME) \
+    DFQ_QMV_KERNEL(BITS, GS, F16, NAME, 1)  \
+    DFQ_QMV_KERNEL(BITS, GS, F16, NAME, 4)
+
+DFQ_QMV_FORMAT(4, 32, false, bf16)
+DFQ_QMV_FORMAT(4, 64, false, bf16)
+DFQ_QMV_FORMAT(4, 128, false, bf16)
+DFQ_QMV_FORMAT(8, 32, false, bf16)
+DFQ_QMV_FORMAT(8, 64, false, bf16)
+DFQ_QMV_FORMAT(8, 128, false, bf16)
+DFQ_QMV_FORMAT(4, 32, true, f16)
+DFQ_QMV_FORMAT(4, 64, true, f16)
+DFQ_QMV_FORMAT(4, 128, true, f16)
+DFQ_QMV_FORMAT(8, 32, true, f16)
+DFQ_QMV_FORMAT(8, 64, true, f16)
+DFQ_QMV_FORMAT(8, 128, true, f16)

@@ -94,6 +94,24 @@ typedef struct QmmGenericParams {
     int32_t xdt, sdt, ydt;  /* 0 bf16, 1 fp16, 2 fp32 */
 } QmmGenericParams;
 
+/* Parameters of the stock path's few-row GEMV (qmv): one dtype for x, scales, biases and y,
+ * at most 4 rows a launch.  Workgroup b owns output rows [b*base + min(b, rem), +base +
+ * (b < rem)) of base = N / G, rem = N % G; its waves take groups of rows from an LDS counter. */
+typedef struct QmvParams {
+    const void* x;          /* [M][K]                                                 */
+    const uint32_t* w;      /* [N][K*bits/32]                                         */
+    const void* scales;     /* [N][K/gs]                                              */
+    const void* biases;     /* [N][K/gs]                                              */
+    const void* lbias;      /* [N] or NULL                                            */
+    void* y;                /* [M][N]                                                 */
+    int32_t M, N, K;
+    int32_t G;              /* workgroups                                             */
+    int32_t rows_max;       /* most rows one workgroup owns                           */
+    int32_t lds_xsum_off;   /* byte offset of the per-chunk x sums [M][K/kpl] fp32    */
+    int32_t lds_cnt_off;    /* byte offset of the row-group take counter              */
+    int32_t lds_out_off;    /* byte offset of the workgroup's outputs [M][rows_max] fp32 */
+} QmvParams;
+
 /* Logits per block of dfq_argmax_accept: 256 threads x two 16-byte loads of 8 logits. */
 #define DFQ_ACCEPT_CHUNK 4096
 

@@ -86,6 +86,7 @@ struct dfq_ctx {
     hipFunction_t reduce[2] = {};        // second pass of reduce splits [bf16/f16]
     hipFunction_t silu_mul[2] = {};      // SiLU-mul of a fused gate||up output [bf16/f16]
     hipFunction_t argmax_accept[2] = {}; // greedy accept of a verify pass [bf16/f16]
+    hipFunction_t qmv[2][3][2][2] = {};  // stock-path GEMV [bits][gs][bf16/f16][rows 1 / <= 4]
     hipFunction_t generic = nullptr;
     hipFunction_t fill = nullptr;
     hipFunction_t read_stream = nullptr; // the plain streaming read (bandwidth reference)
@@ -467,6 +468,14 @@ dfq_status dfq_init(int device, dfq_ctx** out) {
                     snprintf(name, sizeof name, "dfq_qmm_mt8_b%d_g%d_%s_%s", kBits[b], kGs[g2],
                              kDt[d], kCh[c]);
                     if ((e = hipModuleGetFunction(&ctx->mt8[b][g2][d][c], ctx->module, name)) !=
+                        hipSuccess) {
+                        (void)hipModuleUnload(ctx->module);
+                        delete ctx;
+                        return hip_fail(e, name);
+                    }
+                    snprintf(name, sizeof name, "dfq_qmv_b%d_g%d_%s_m%d", kBits[b], kGs[g2],
+                             kDt[d], c == 0 ? 1 : 4);
+                    if ((e = hipModuleGetFunction(&ctx->qmv[b][g2][d][c], ctx->module, name)) !=
                         hipSuccess) {
                         (void)hipModuleUnload(ctx->module);
                         delete ctx;
@@ -986,6 +995,75 @@ dfq_status dfq_qmm_argmax_accept(dfq_ctx* ctx, const void* x, const uint32_t* w,
                              align256((size_t)16 * M * 8) + align256(kAcceptCountBytes), stream);
 }
 
+/* Workgroups and LDS layout of the stock path's GEMV for a shape of at most 4 rows; false
+ * where its x (M x K, pre-permuted, and the per-chunk sums) and outputs would not fit in LDS. */
+static constexpr int kQmvRows = 4;    // weight rows a wave works on at once (as the kernels)
+static constexpr int kQmvWaves = 8;   // waves per workgroup (as the kernels)
+static bool qmv_layout(const dfq_ctx* ctx, int M, int N, int K, int bits, QmvParams* p,
+                       size_t* lds) {
+    const int kpl = 128 / bits;  // k per lane chunk
+    if (M < 1 || M > 4 || K % kpl) return false;
+    /* one workgroup per CU, each with at least a row group per wave.  Measured on MI355X at
+     * one row (us; this form against unit-balanced splits of 1, 2 or 4 rows a unit, 2 to 6
+     * units in flight, 8 or 16 waves a CU, the first units issued before the staging):
+     * N = 17408, K = 5120: 15.5 against 16.2-20.0; N = 151936: 90.8 against 92-131; N = K =
+     * 5120: 8.2 against 8.4-9.6; N = K = 4096 (fp16): 6.3 against 6.1-6.6. */
+    const int G = std::max(1, std::min(ctx->num_cus, (N + kQmvRows * kQmvWaves - 1) /
+                                                         (kQmvRows * kQmvWaves)));
+    const int rows_max = (N + G - 1) / G;
+    const size_t xbytes = (size_t)M * K * 2;
+    const size_t xsum_off = (xbytes + 15) & ~(size_t)15;
+    const size_t cnt_off = xsum_off + (size_t)M * (K / kpl) * 4;
+    const size_t out_off = (cnt_off + 16 + 15) & ~(size_t)15;
+    const size_t need = out_off + (size_t)M * rows_max * 4;
+    if (need > ctx->lds_max) return false;
+    p->M = M;
+    p->N = N;
+    p->K = K;
+    p->G = G;
+    p->rows_max = rows_max;
+    p->lds_xsum_off = (int)xsum_off;
+    p->lds_cnt_off = (int)cnt_off;
+    p->lds_out_off = (int)out_off;
+    *lds = need;
+    return true;
+}
+
+/* The stock path as MLX takes it for few rows: its GEMV, one launch per 4 rows, for one dtype
+ * of x, scales, biases and y (bf16 or fp16), 4- or 8-bit codes, group 32, 64 or 128, K a
+ * multiple of one lane's chunk, and x of 4 rows in LDS; DFQ_ERR_UNSUPPORTED otherwise (the
+ * per-element path then takes the call). */
+static dfq_status qmv_any(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
+                          const void* biases, const void* lbias, void* y, int M, int N, int K,
+                          int bits, int gs, dfq_dtype dt, hipStream_t stream) {
+    if ((bits != 4 && bits != 8) || (gs != 32 && gs != 64 && gs != 128) ||
+        (dt != DFQ_BF16 && dt != DFQ_F16) || !aligned(x, 16) || !aligned(w, 16) ||
+        !aligned(scales, 2) || !aligned(biases, 2) || !aligned(y, 2) ||
+        (int64_t)N * K * bits / 8 >= (int64_t)1 << 32)
+        return DFQ_ERR_UNSUPPORTED;
+    QmvParams p{};
+    size_t lds = 0;
+    if (!qmv_layout(ctx, std::min(M, 4), N, K, bits, &p, &lds)) return DFQ_ERR_UNSUPPORTED;
+    const int bi = bits == 4 ? 0 : 1, gi = gs == 32 ? 0 : gs == 64 ? 1 : 2;
+    const int di = dt == DFQ_BF16 ? 0 : 1;
+    for (int m0 = 0; m0 < M; m0 += 4) {
+        const int mc = std::min(4, M - m0);
+        if (!qmv_layout(ctx, mc, N, K, bits, &p, &lds)) return DFQ_ERR_UNSUPPORTED;
+        p.x = (const char*)x + (size_t)m0 * K * 2;
+        p.w = w;
+        p.scales = scales;
+        p.biases = biases;
+        p.lbias = lbias;
+        p.y = (char*)y + (size_t)m0 * N * 2;
+        void* args[] = {&p};
+        hipError_t e = hipModuleLaunchKernel(ctx->qmv[bi][gi][di][mc == 1 ? 0 : 1],
+                                             (unsigned)p.G, 1, 1, kQmvWaves * 64, 1, 1,
+                                             (unsigned)lds, stream, args, nullptr);
+        if (e != hipSuccess) return hip_fail(e, "launch dfq_qmv");
+    }
+    return DFQ_OK;
+}
+
 dfq_status dfq_qmm_fallback(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
                             const void* biases, const void* lbias, void* y, int M, int N, int K,
                             int bits, int gs, dfq_dtype xdt, dfq_dtype sdt, dfq_dtype ydt,
@@ -1005,6 +1083,11 @@ dfq_status dfq_qmm_fallback(dfq_ctx* ctx, const void* x, const uint32_t* w, cons
             return fail(DFQ_ERR_INVALID_ARGUMENT, "bad dtype");
     if (!aligned(w, 4)) return fail(DFQ_ERR_INVALID_ARGUMENT, "w must be 4-byte aligned");
     DeviceGuard g(ctx->device);
+    if (xdt == sdt && sdt == ydt) {
+        const dfq_status s = qmv_any(ctx, x, w, scales, biases, lbias, y, M, N, K, bits, gs, xdt,
+                                     (hipStream_t)stream);
+        if (s != DFQ_ERR_UNSUPPORTED) return s;
+    }
     QmmGenericParams p{};
     p.x = x;
     p.w = w;
@@ -1174,6 +1257,21 @@ dfq_status dfq_debug_read_units(dfq_ctx* ctx, const uint32_t* w, const void* sca
 }
 
 /* The same split computed without a device, for a given CU count and LDS limit. */
+/* Launches of the stock path's GEMV for a shape with x, scales and y all of `dt` and 16-byte
+ * aligned arrays: one per 4 rows, or 0 where the per-element path takes the call. */
+dfq_status dfq_debug_stock_gemv_launches(dfq_ctx* ctx, int M, int N, int K, int bits, int gs,
+                                         dfq_dtype dt, int* launches) {
+    if (!ctx || !launches) return fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
+    QmvParams p{};
+    size_t lds = 0;
+    const bool ok = (bits == 4 || bits == 8) && (gs == 32 || gs == 64 || gs == 128) &&
+                    (dt == DFQ_BF16 || dt == DFQ_F16) && M >= 1 &&
+                    (int64_t)N * K * bits / 8 < (int64_t)1 << 32 &&
+                    qmv_layout(ctx, std::min(M, 4), N, K, bits, &p, &lds);
+    *launches = ok ? (M + 3) / 4 : 0;
+    return DFQ_OK;
+}
+
 dfq_status dfq_debug_make_plan(int M, int N, int K, int bits, int gs, int num_cus,
                                size_t lds_max, int* out15) {
     if (!out15) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");

@@ -127,6 +127,7 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         "dfq_enable_small_m_quantized_matmul": ([P], I),
         "dfq_debug_plan": ([P, I, I, I, I, I, ctypes.POINTER(I)], I),
         "dfq_debug_make_plan": ([I, I, I, I, I, I, S, ctypes.POINTER(I)], I),
+        "dfq_debug_stock_gemv_launches": ([P, I, I, I, I, I, I, ctypes.POINTER(I)], I),
         "dfq_debug_read_stream": ([P, P, S, P, P], I),
         "dfq_debug_read_units": ([P, P, P, P, I, I, I, P, P], I),
         "dfq_linear_describe": ([P, ctypes.POINTER(_LinearDesc)], I),
@@ -243,6 +244,14 @@ class Context:
         keys = ["T", "SS", "nkb", "Gkb", "nslot_kb", "kr", "lds_bytes", "need_ws", "ch", "umax",
                 "chunks", "reduce", "ring", "aligned", "burst"]
         return dict(zip(keys, list(out)))
+
+    def stock_gemv_launches(self, M, N, K, bits, gs, dt=BF16) -> int:
+        """GEMV launches the stock path makes for a shape (0: the per-element path)."""
+        n = ctypes.c_int(-1)
+        _check(self.lib.dfq_debug_stock_gemv_launches(self.handle, M, N, K, bits, gs, dt,
+                                                      ctypes.byref(n)),
+               "dfq_debug_stock_gemv_launches")
+        return n.value
 
     def read_units(self, w, scales, biases, M, N, K, sink, stream=None):
         """One launch of the fast kernel's own loads for a 4-bit g64 shape (one-k-block
@@ -461,7 +470,7 @@ class Graph:
 class SmallMQuantizedMatmul:
     """The reference enum's statics (SmallMQuantizedMatmul.swift:29-49, 193-207)."""
 
-    minimum_rows = 6
+    minimum_rows = 2   # DFQ_MINIMUM_ROWS: this chip's crossover (the reference's is 6)
     maximum_rows = 16
     rows_per_tile = 8
     minimum_output_features = 4096

@@ -50,7 +50,14 @@ typedef struct dfq_ctx dfq_ctx;
 typedef struct dfq_graph dfq_graph;
 
 /* ---- the eligibility window (SmallMQuantizedMatmul.swift:29-49) -------------------- */
-#define DFQ_MINIMUM_ROWS 6               /* :32 minimumRows                              */
+/* :32 minimumRows, "a constant of (chip x MLX version)" (:29-31): the fewest rows for which
+ * the fast kernel clearly beats the stock path the layer falls through to, MLX's GEMV on the
+ * reference's Apple GPU (6 there).  On MI355X the stock path is dfq_qmm_fallback's GEMV;
+ * measured against it (us, stock / fast kernel), one row is a draw -- 4096 x 4096:
+ * 6.3 / 7.4, 5120 x 5120: 8.2 / 9.7, 17408 x 5120: 15.5 / 15.3, 5120 x 17408: 16.0 / 15.9,
+ * 151936 x 5120: 90.8 / 78.8 -- and two rows are the first clear win (17408 x 5120:
+ * 18.3 / 15.0, 5120 x 17408: 19.9 / 15.7, 151936 x 5120: 100.7 / 79.3). */
+#define DFQ_MINIMUM_ROWS 2
 #define DFQ_MAXIMUM_ROWS 16              /* :36 maximumRows                              */
 #define DFQ_ROWS_PER_TILE 8              /* :39 rowsPerTile (also read by the generator's
                                             width snapping, DFlashSpeculativeGenerator.swift
@@ -159,10 +166,14 @@ dfq_status dfq_qmm_silu_gate_up(dfq_ctx* ctx, const void* x, const uint32_t* w_g
 dfq_status dfq_interleave_gate_up(dfq_ctx* ctx, const void* gate, const void* up, void* out,
                                   int H, size_t row_bytes, void* stream);
 
-/* The generic path: any M >= 1, bits 2/4/8, any group size dividing K; x and scales may
- * differ in dtype (y dtype follows MLX promotion: equal -> same, else fp32).  Re-reads W
- * for every row.  Stands in for the stock op MLX falls back to,
- * QuantizedLinear.callAsFunction -> quantizedMatmul (reached at SmallMQuantizedMatmul.swift:265). */
+/* The stock path: any M >= 1, bits 2/4/8, any group size dividing K; x and scales may
+ * differ in dtype (y dtype follows MLX promotion: equal -> same, else fp32).  Stands in for
+ * the stock op MLX falls back to, QuantizedLinear.callAsFunction -> quantizedMatmul (reached
+ * at SmallMQuantizedMatmul.swift:265), which runs a GEMV for few rows.  Where x, scales and y
+ * share bf16 or fp16, bits are 4 or 8, the group 32, 64 or 128 and 4 rows of x fit in LDS, it
+ * runs as that GEMV, one launch per 4 rows (each weight row read once a launch); otherwise
+ * one wave per output element, re-reading W for every row.  No workspace; asynchronous on
+ * `stream`. */
 dfq_status dfq_qmm_fallback(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
                             const void* biases, const void* linear_bias, void* y, int M, int N,
                             int K, int bits, int group_size, dfq_dtype x_dtype,

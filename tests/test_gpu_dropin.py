@@ -46,12 +46,12 @@ def assert_agrees(ctx, bits, rows):
     assert diff <= TOL * max(mag, 1.0), f"{bits}-bit M={rows}: {diff} at {mag}"
 
 
-@pytest.mark.parametrize("rows", range(6, 17))
+@pytest.mark.parametrize("rows", range(2, 17))
 def test_4bit_matches_stock(ctx, rows):
     assert_agrees(ctx, 4, rows)
 
 
-@pytest.mark.parametrize("rows", range(6, 17))
+@pytest.mark.parametrize("rows", range(2, 17))
 def test_8bit_matches_stock(ctx, rows):
     assert_agrees(ctx, 8, rows)
 
@@ -74,9 +74,11 @@ def test_ineligible_shape_returns_the_stock_result(ctx):
 
 
 def test_row_counts_outside_the_window_return_the_stock_result(ctx):
+    """One row (below this chip's crossover, where the stock GEMV is as fast) and more than
+    16 rows (more than two row tiles) fall through unchanged, bit for bit."""
     stock = make_layer(ctx, 4)
     fast = SmallMQuantizedLinear(stock)
-    for rows in [1, 3, 5, 17, 24, 32]:
+    for rows in [1, 17, 24, 32]:
         x = make_input(rows)
         announce(f"dropin rows outside window {rows}")
         assert torch.equal(stock(x), fast(x)), f"M={rows}"

@@ -394,3 +394,42 @@ def test_prefetch_addresses_stay_in_bounds(shape):
                 last_s = ((row0 + rmax) * GPR + kc // gs) * 2 + lane_s + sv
                 assert last_s <= N * GPR * 2, (kb, cl, u)
 
+
+
+
+QMV_WAVES, QMV_ROWS = 8, 4   # the stock-path GEMV's waves per workgroup and rows per group
+
+
+@pytest.mark.parametrize("shape", [(17408, 5120, 4), (4096, 4096, 4), (151936, 5120, 4),
+                                   (5120, 17408, 4), (1, 256, 4), (3, 2048, 4), (37, 2560, 4),
+                                   (1000, 5120, 8), (257, 768, 8), (5120, 5120, 8),
+                                   (130, 2560, 4), (40, 640, 8), (100000, 256, 4)])
+def test_stock_gemv_split_writes_every_row_once(shape):
+    """The stock-path GEMV's split (qmv_layout and the kernel): workgroup b owns rows
+    [b*base + min(b, rem), ...); groups of 4 of its rows go to its waves (the first
+    QMV_WAVES by index, the rest from a counter starting there), so every group is taken
+    once whatever the order; loads stay in bounds (rows clamped to the workgroup's last, the
+    chunk to the row's last)."""
+    N, K, bits = shape
+    kpl = 128 // bits
+    nchunk = K // kpl
+    nsteps = -(-nchunk // 64)
+    G = max(1, min(256, -(-N // (QMV_ROWS * QMV_WAVES))))
+    base, rem = divmod(N, G)
+    written = []
+    for b in range(G):
+        lo, nrows = b * base + min(b, rem), base + (1 if b < rem else 0)
+        ngroups = -(-nrows // QMV_ROWS)
+        takes = list(range(min(QMV_WAVES, ngroups))) + list(range(QMV_WAVES, ngroups))
+        assert sorted(takes) == list(range(ngroups))
+        for g in takes:
+            for r in range(QMV_ROWS):
+                row = lo + min(g * QMV_ROWS + r, nrows - 1)
+                assert lo <= row < lo + nrows <= N
+                if g * QMV_ROWS + r < nrows:
+                    written.append(lo + g * QMV_ROWS + r)
+            for j in range(nsteps + 1):          # the clamped reload past the last step
+                for lane in (0, 63):
+                    c = min(lane + 64 * min(j, nsteps - 1), nchunk - 1)
+                    assert 0 <= c < nchunk and (c * kpl) // 32 < K // 32
+    assert sorted(written) == list(range(N))
