@@ -24,14 +24,25 @@ public struct DFQError: Error, CustomStringConvertible {
     public let call: String
     public let message: String
 
+    public init(status: dfq_status, call: String, message: String) {
+        self.status = status
+        self.call = call
+        self.message = message
+    }
+
+    /// The error of the failed call `call`, with the library's message for it (read on the
+    /// thread that made the call).
+    public init(status: dfq_status, call: String) {
+        self.init(status: status, call: call, message: String(cString: dfq_last_error()))
+    }
+
     public var description: String { "\(call): status \(status.rawValue): \(message)" }
 }
 
+/// Throws the call's error unless it returned DFQ_OK.
 @inline(__always)
-func check(_ status: dfq_status, _ call: String) throws {
-    if status != DFQ_OK {
-        throw DFQError(status: status, call: call, message: String(cString: dfq_last_error()))
-    }
+public func check(_ status: dfq_status, _ call: String) throws {
+    if status != DFQ_OK { throw DFQError(status: status, call: call) }
 }
 
 /// Failures inside a forward are programming or device errors with no recovery path; the
@@ -95,25 +106,68 @@ extension DeviceArray {
     }
 }
 
-/// Device memory allocated by this module (layer outputs, the accept's buffers).
+/// Device memory allocated by this module (layer outputs), taken from and returned to its
+/// context's pool: no device allocation or free happens on a warm forward path.
 public final class DeviceBuffer: DeviceArray {
     public let deviceAddress: UnsafeMutableRawPointer
     public let shape: [Int]
     public let dtype: DeviceDType
     let context: HIPContext
+    private let bytes: Int
 
     public init(context: HIPContext, shape: [Int], dtype: DeviceDType) throws {
-        var p: UnsafeMutableRawPointer?
-        try check(dfq_malloc(context.handle, max(1, shape.reduce(1, *) * dtype.size), &p),
-                  "dfq_malloc")
-        self.deviceAddress = p!
+        let bytes = DevicePool.sizeClass(max(1, shape.reduce(1, *) * dtype.size))
+        self.deviceAddress = try context.pool.take(bytes)
+        self.bytes = bytes
         self.shape = shape
         self.dtype = dtype
         self.context = context
     }
 
     deinit {
-        _ = dfq_free(context.handle, deviceAddress)
+        context.pool.give(deviceAddress, bytes)
+    }
+}
+
+/// A stream-ordered cache of device blocks for one context.  Every call of a context runs on
+/// its one stream, so a block handed back when its last user's array goes away can serve the
+/// next array at once: any kernel that writes it through the new array is queued after every
+/// kernel that used it through the old one.  Blocks come in power-of-two sizes from 256
+/// bytes up and go back to the device only when the context ends.  Used from one thread at
+/// a time, as the generator serialises its work on one queue
+/// (DFlashSpeculativeGenerator.swift:93-99).  For eager forwards: a captured HIP graph
+/// keeps the addresses it recorded, so code that captures the layers' calls manages those
+/// buffers itself (the C ABI's dfq_graph_* over caller-owned memory).
+final class DevicePool {
+    private let handle: OpaquePointer
+    private var free: [Int: [UnsafeMutableRawPointer]] = [:]
+    private var all: [UnsafeMutableRawPointer] = []
+
+    init(handle: OpaquePointer) { self.handle = handle }
+
+    static func sizeClass(_ bytes: Int) -> Int {
+        var c = 256
+        while c < bytes { c <<= 1 }
+        return c
+    }
+
+    func take(_ bytes: Int) throws -> UnsafeMutableRawPointer {
+        if let p = free[bytes]?.popLast() { return p }
+        var p: UnsafeMutableRawPointer?
+        try check(dfq_malloc(handle, bytes, &p), "dfq_malloc")
+        all.append(p!)
+        return p!
+    }
+
+    func give(_ p: UnsafeMutableRawPointer, _ bytes: Int) {
+        free[bytes, default: []].append(p)
+    }
+
+    /// Frees every block; the stream must be idle.
+    func drain() {
+        for p in all { _ = dfq_free(handle, p) }
+        all = []
+        free = [:]
     }
 }
 
@@ -142,6 +196,13 @@ public final class HIPContext {
     /// context goes, since work queued on the stream may still use them.  Raw, not
     /// DeviceBuffer, so that they hold no reference back to the context.
     private var workspaces: [(UnsafeMutableRawPointer, Int)] = []
+    /// Device blocks of the arrays this context's layers return.
+    let pool: DevicePool
+    /// The greedy accept's device buffers for a verify width: its workspace (zero at rest:
+    /// cleared once when made, every call leaves it zero), the tokens with the accepted count
+    /// behind them, and the proposals.  Raw for the same reason as the workspaces.
+    var acceptBuffers: [Int: (ws: UnsafeMutableRawPointer, wsBytes: Int,
+                              out: UnsafeMutableRawPointer, props: UnsafeMutableRawPointer)] = [:]
 
     /// The context layers use unless they are given one.
     public static let shared: HIPContext = {
@@ -164,11 +225,18 @@ public final class HIPContext {
         }
         self.handle = h!
         self.stream = s
+        self.pool = DevicePool(handle: h!)
     }
 
     deinit {
         _ = dfq_stream_sync(handle, stream)
         for (p, _) in workspaces { _ = dfq_free(handle, p) }
+        for b in acceptBuffers.values {
+            _ = dfq_free(handle, b.ws)
+            _ = dfq_free(handle, b.out)
+            _ = dfq_free(handle, b.props)
+        }
+        pool.drain()
         _ = dfq_stream_destroy(handle, stream)
         _ = dfq_destroy(handle)
     }
@@ -245,8 +313,9 @@ open class Module {
 
 /// MLX's QuantizedLinear over device arrays: weight uint32 [out][in * bits / 32] (element 0 in
 /// the low bits), scales and biases [out][in / groupSize], an optional linear bias [out].
-/// Every forward runs the generic path (dfq_qmm_fallback), the stand-in for MLX's stock
-/// quantizedMatmul that SmallMQuantizedLinear falls through to (SmallMQuantizedMatmul.swift:265).
+/// Every forward runs the stock path (dfq_qmm_fallback: a GEMV for few rows), the stand-in
+/// for MLX's quantizedMatmul that SmallMQuantizedLinear falls through to
+/// (SmallMQuantizedMatmul.swift:265).
 open class QuantizedLinear: Module {
     public enum Mode: Equatable { case affine, mxfp4 }
 
@@ -318,8 +387,9 @@ enum SmallMQuantizedMatmul {
     static let inputFeatureMultiple = Int(DFQ_INPUT_FEATURE_MULTIPLE)
     static let requiredGroupSize = Int(DFQ_REQUIRED_GROUP_SIZE)
 
-    /// Can this layer's shape and quantisation format run on the kernel at all?  The static
-    /// half of the test, answered once when the model is swapped.
+    /// The gate's shape-and-format half (affine with biases, 4 or 8 bits, group 64, at least
+    /// 4096 outputs, inputs a multiple of 512), which no row count changes: the swap asks it
+    /// once per layer, the forward never.
     static func isEligible(_ layer: QuantizedLinear) -> Bool {
         let (outputFeatures, inputFeatures) = layer.shape
         return dfq_is_eligible(Int32(outputFeatures), Int32(inputFeatures), Int32(layer.bits),
@@ -327,7 +397,7 @@ enum SmallMQuantizedMatmul {
                                layer.biases == nil ? 0 : 1) == 1
     }
 
-    /// MMA tiles of 8 rows a pass of `rows` rows pays for: one up to eight, two beyond.
+    /// Row tiles of `rowsPerTile` a launch of `rows` rows computes: 1 for 1...8, 2 for 9...16.
     static func tiles(for rows: Int) -> Int { Int(dfq_tiles_for(Int32(rows))) }
 
     /// y[rows, N] = x[rows, K] . dequant(w)^T (+ bias), bf16, on the fast kernel.  No padding
@@ -359,17 +429,20 @@ enum SmallMQuantizedMatmul {
 
 // MARK: - The drop-in layer
 
-/// A ``QuantizedLinear`` that routes verify-width forwards through the MI355X kernel and
-/// everything else through the stock path (SmallMQuantizedMatmul.swift:234-293).
+/// The drop-in layer (SmallMQuantizedMatmul.swift:234-293): the same arrays as the layer it
+/// wraps; a forward whose row count lies in the window goes to the MI355X kernel, any other
+/// forward to the stock path, unchanged.
 public final class SmallMQuantizedLinear: QuantizedLinear {
 
-    /// Whether this layer's shape and format are ones the kernel can handle at all, settled
-    /// once here (:236-240).  Also false for rows the fast kernel has no split for (weights of
-    /// 2 GiB or more), which fall through like any ineligible call.
+    /// The gate's static half for this layer, computed when the layer is built (:236-240),
+    /// so that a caller who wraps an ineligible layer by hand still gets the stock result.
     private let kernelEligible: Bool
+    /// Row counts of the window the fast kernel has a work split for at this shape (none for
+    /// weights of 2 GiB or more); other rows take the stock path like an ineligible call.
     private let kernelRows: Set<Int>
 
-    /// Wraps an existing layer, sharing its arrays: no weights are copied (:243-252).
+    /// The drop-in over `other`'s own weight, scale, bias and linear-bias arrays: nothing is
+    /// copied, so swapping adds no weight memory (:243-252).
     public init(_ other: QuantizedLinear) {
         let eligible = SmallMQuantizedMatmul.isEligible(other)
         var fits = Set<Int>()
@@ -392,8 +465,8 @@ public final class SmallMQuantizedLinear: QuantizedLinear {
     public override func callAsFunction(_ x: DeviceArray) -> DeviceArray {
         let shape = x.shape
         let rows = shape.dropLast().reduce(1, *)
-        // bf16 only: the kernel's output is bf16, so any other input dtype would change this
-        // layer's output type (:258-266).
+        // The kernel writes bf16 from bf16 inputs.  An fp16 input, whose stock result MLX
+        // promotes to fp32, must keep getting exactly that, so it falls through (:258-266).
         guard kernelEligible,
             rows >= SmallMQuantizedMatmul.minimumRows,
             rows <= SmallMQuantizedMatmul.maximumRows,
@@ -414,11 +487,12 @@ public final class SmallMQuantizedLinear: QuantizedLinear {
     }
 }
 
-/// Swaps every eligible ``QuantizedLinear`` in `model` for a ``SmallMQuantizedLinear``
-/// (SmallMQuantizedMatmul.swift:303-317).  Opt-in: the swapped layers' numerics change by a
-/// bf16 ulp or two.
+/// Replaces each leaf of `model` that is a ``QuantizedLinear`` passing the static gate, and
+/// is not already a drop-in, by a ``SmallMQuantizedLinear`` over the same arrays
+/// (SmallMQuantizedMatmul.swift:303-317).  The caller opts in: the kernel sums in another
+/// order than the stock path, so swapped layers' outputs move by about one bf16 ulp.
 ///
-/// - Returns: how many layers were swapped.
+/// - Returns: the number of leaves replaced (0 on a second call).
 @discardableResult
 public func enableSmallMQuantizedMatmul(in model: Module) -> Int {
     let updates = model
@@ -432,6 +506,45 @@ public func enableSmallMQuantizedMatmul(in model: Module) -> Int {
         }
     model.update(modules: updates)
     return updates.count
+}
+
+// MARK: - The fused MLP
+
+extension HIPContext {
+    /// At load: `out` gets the gate and up arrays interleaved in blocks of 8 rows (rows
+    /// 16t...16t+7 are gate rows 8t...8t+7, rows 16t+8...16t+15 the matching up rows), the
+    /// layout of gateUpSiLU's weights.  Call it for the weight (rowBytes = K * bits / 8), the
+    /// scales and the biases (rowBytes = K / groupSize * 2) and a linear bias (2).
+    public func interleaveGateUp(gate: UnsafeRawPointer, up: UnsafeRawPointer,
+                                 out: UnsafeMutableRawPointer, hidden: Int,
+                                 rowBytes: Int) throws {
+        try check(dfq_interleave_gate_up(handle, gate, up, out, Int32(hidden), rowBytes,
+                                         stream), "dfq_interleave_gate_up")
+    }
+
+    /// Per verify pass: h[rows, hidden] = silu(x . Wg^T) * (x . Wu^T) in one launch over the
+    /// interleaved gate|up arrays (the MLP of DFlashDecoderLayer.swift:26 before its down
+    /// projection); x is bf16 [rows, K].
+    public func gateUpSiLU(x: DeviceArray, weight: DeviceArray, scales: DeviceArray,
+                           biases: DeviceArray, hidden: Int, bits: Int,
+                           groupSize: Int) throws -> DeviceArray {
+        let inputFeatures = x.shape[x.shape.count - 1]
+        let rows = x.count / inputFeatures
+        var need = 0
+        try check(dfq_qmm_workspace_bytes(handle, Int32(rows), Int32(2 * hidden),
+                                          Int32(inputFeatures), Int32(bits), Int32(groupSize),
+                                          &need), "dfq_qmm_workspace_bytes")
+        let ws = workspace(need)
+        let h = try DeviceBuffer(context: self, shape: [rows, hidden], dtype: .bfloat16)
+        try check(dfq_qmm_silu_gate_up(handle, x.deviceAddress,
+                                       weight.deviceAddress.assumingMemoryBound(to: UInt32.self),
+                                       scales.deviceAddress, biases.deviceAddress, nil,
+                                       h.deviceAddress, Int32(rows), Int32(hidden),
+                                       Int32(inputFeatures), Int32(bits), Int32(groupSize),
+                                       DFQ_BF16, ws?.0, ws?.1 ?? 0, stream),
+                  "dfq_qmm_silu_gate_up")
+        return h
+    }
 }
 
 // MARK: - The verify round's greedy accept
@@ -452,38 +565,45 @@ public func greedyAccept(lmHead: QuantizedLinear, hidden: DeviceArray,
         throw DFQError(status: DFQ_ERR_UNSUPPORTED, call: "greedyAccept",
                        message: "the LM head must be affine-quantised with biases")
     }
-    var need = 0
-    try check(dfq_qmm_argmax_accept_workspace_bytes(h, Int32(rows), Int32(vocab),
-                                                    Int32(inputFeatures), Int32(lmHead.bits),
-                                                    Int32(lmHead.groupSize), &need),
-              "dfq_qmm_argmax_accept_workspace_bytes")
-    let ws = try DeviceBuffer(context: context, shape: [max(1, (need + 3) / 4)], dtype: .float32)
-    try check(dfq_workspace_clear(h, ws.deviceAddress, ws.count * 4, context.stream),
-              "dfq_workspace_clear")
-    let out = try DeviceBuffer(context: context, shape: [rows + 1], dtype: .uint32)
-    let props = try DeviceBuffer(context: context, shape: [max(1, proposals.count)],
-                                 dtype: .uint32)
+    /* the buffers of this verify width, made once per context: the workspace (in 4-byte
+     * words, cleared when made; every call leaves it zero), the tokens followed by the
+     * accepted count, and the proposals */
+    if context.acceptBuffers[rows] == nil {
+        var need = 0
+        try check(dfq_qmm_argmax_accept_workspace_bytes(h, Int32(rows), Int32(vocab),
+                                                        Int32(inputFeatures), Int32(lmHead.bits),
+                                                        Int32(lmHead.groupSize), &need),
+                  "dfq_qmm_argmax_accept_workspace_bytes")
+        let wsBytes = max(1, (need + 3) / 4) * 4
+        var ws: UnsafeMutableRawPointer?, out: UnsafeMutableRawPointer?
+        var props: UnsafeMutableRawPointer?
+        try check(dfq_malloc(h, wsBytes, &ws), "dfq_malloc")
+        try check(dfq_malloc(h, (rows + 1) * 4, &out), "dfq_malloc")
+        try check(dfq_malloc(h, max(1, rows - 1) * 4, &props), "dfq_malloc")
+        try check(dfq_workspace_clear(h, ws, wsBytes, context.stream), "dfq_workspace_clear")
+        context.acceptBuffers[rows] = (ws!, wsBytes, out!, props!)
+    }
+    let b = context.acceptBuffers[rows]!
     if !proposals.isEmpty {
         try proposals.withUnsafeBytes {
-            try check(dfq_memcpy_h2d(h, props.deviceAddress, $0.baseAddress, $0.count,
-                                     context.stream), "dfq_memcpy_h2d")
+            try check(dfq_memcpy_h2d(h, b.props, $0.baseAddress, $0.count, context.stream),
+                      "dfq_memcpy_h2d")
         }
     }
-    let tokens = out.deviceAddress.assumingMemoryBound(to: Int32.self)
+    let tokens = b.out.assumingMemoryBound(to: Int32.self)
     let proposalsOnDevice: UnsafePointer<Int32>? =
-        proposals.isEmpty ? nil : UnsafePointer(props.deviceAddress.assumingMemoryBound(to: Int32.self))
+        proposals.isEmpty ? nil : UnsafePointer(b.props.assumingMemoryBound(to: Int32.self))
     try check(dfq_qmm_argmax_accept(h, hidden.deviceAddress,
                                     lmHead.weight.deviceAddress.assumingMemoryBound(to: UInt32.self),
                                     lmHead.scales.deviceAddress, biases.deviceAddress,
                                     lmHead.bias?.deviceAddress, nil, Int32(rows), Int32(vocab),
                                     Int32(inputFeatures), Int32(lmHead.bits),
                                     Int32(lmHead.groupSize), hidden.dtype.dfq, proposalsOnDevice,
-                                    tokens, tokens + rows, ws.deviceAddress, ws.count * 4,
-                                    context.stream),
+                                    tokens, tokens + rows, b.ws, b.wsBytes, context.stream),
               "dfq_qmm_argmax_accept")
     var host = [Int32](repeating: 0, count: rows + 1)
     try host.withUnsafeMutableBytes {
-        try check(dfq_memcpy_d2h(h, $0.baseAddress, out.deviceAddress, $0.count, context.stream),
+        try check(dfq_memcpy_d2h(h, $0.baseAddress, b.out, $0.count, context.stream),
                   "dfq_memcpy_d2h")
     }
     return (Array(host[0..<rows]), Int(host[rows]))

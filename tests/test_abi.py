@@ -127,3 +127,51 @@ def test_swift_shim_calls_match_the_header():
     consts = set(re.findall(r"\b(DFQ_[A-Z_]+)\b", src))
     for c in consts:
         assert re.search(r"\b%s\b" % c, hdr), c
+
+
+INTEGRATION = os.path.join(ROOT, "INTEGRATION.md")
+
+
+def _swift_blocks():
+    text = open(INTEGRATION).read()
+    return re.findall(r"```swift\n(.*?)```", text, flags=re.S)
+
+
+def test_integration_swift_snippets_match_the_header_and_the_package():
+    """The Swift snippets of INTEGRATION.md compile against what exists: every dfq_* call
+    names a function the header declares, with its number of arguments; every DFQ_ constant
+    is the header's; every call of the package's own API (greedyAccept, the fused-MLP
+    helpers, DFQError, QuantizedLinear ...) uses labels the package declares; and members
+    read off a context are ones HIPContext has."""
+    blocks = _swift_blocks()
+    assert len(blocks) >= 4
+    code = "\n".join(re.sub(r"//[^\n]*", "", b) for b in blocks)
+    hdr = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    arity = dict(_calls(hdr, r"\b(dfq_[a-z0-9_]+)"))
+    calls = _calls(code, r"\b(dfq_[a-z0-9_]+)")
+    assert calls
+    for name, n in calls:
+        assert name in arity, name
+        assert n == arity[name], (name, n, arity[name])
+    for c in set(re.findall(r"\b(DFQ_[A-Z_]+)\b", code)):
+        assert re.search(r"\b%s\b" % c, hdr), c
+    pkg = re.sub(r"//[^\n]*", "", open(SWIFT).read())
+    # labelled calls: name(label: ...) must match a declaration's first label
+    for name, label in re.findall(r"\b([a-zA-Z][A-Za-z0-9]*)\(\s*([a-z][A-Za-z0-9]*):", code):
+        if name.startswith("dfq_"):
+            continue
+        decl = re.search(r"(?:func|init|class|struct)\s+%s\b" % name, pkg) or \
+            (name in ("DFQError", "QuantizedLinear", "SmallMQuantizedLinear", "HIPContext",
+                      "DeviceBuffer") and re.search(r"\b%s\b" % name, pkg))
+        assert decl, name
+        if name in ("DFQError", "QuantizedLinear", "HIPContext", "DeviceBuffer"):
+            inits = re.findall(r"init\(([a-z][A-Za-z0-9]*)\s*:", pkg)
+            assert label in inits, (name, label)
+        else:
+            m = re.search(r"func\s+%s\(\s*([a-z][A-Za-z0-9]*)" % name, pkg)
+            assert m and m.group(1) == label, (name, label)
+    # members read off a HIPContext value named ctx or context
+    members = set(re.findall(r"\b(?:ctx|context)\.([a-zA-Z][A-Za-z0-9]*)", code))
+    ctx_src = pkg[pkg.index("public final class HIPContext"):]
+    for m in members:
+        assert re.search(r"(?:let|var|func)\s+%s\b" % m, ctx_src), m
