@@ -134,11 +134,12 @@ def set_bytes_of(sets):
 
 
 def time_m(torch, ctx, stream, sets, M, steps, warmup, N, K, bits, gs, ws, wsb, f16=False,
-           x_sd=1.0):
+           x_sd=1.0, packed=None):
     """Per-call microseconds (one figure per replay) of graph-replayed calls at row count M
     (fp16 throughout with f16, else bf16): the graph holds rotation(...)["calls_per_graph"]
     calls, at least `steps`, cycling through every weight set; replays_for(steps) replays,
-    each divided by the calls it holds."""
+    each divided by the calls it holds.  With `packed` (the sets in the packed layout,
+    Context.pack), the calls are dfq_qmm_packed over those instead."""
     import dflash_qmm
     dev = sets[0][0].device
     g = torch.Generator(device=dev)
@@ -150,6 +151,10 @@ def time_m(torch, ctx, stream, sets, M, steps, warmup, N, K, bits, gs, ws, wsb, 
 
     def issue(count, start):
         for i in range(count):
+            if packed is not None:
+                ctx.qmm_packed_raw(x, packed[(start + i) % len(packed)], y, M, ws=ws,
+                                   ws_bytes=wsb, stream=stream)
+                continue
             w, s, b = sets[(start + i) % len(sets)]
             ctx.qmm_raw(x, w, s, b, y, M, N, K, bits, gs, B, B, B, ws=ws, ws_bytes=wsb,
                         stream=stream)
@@ -229,14 +234,18 @@ def time_read(torch, ctx, stream, nbytes, nsets, steps, dev):
     return times
 
 
-def time_units(torch, ctx, stream, sets, M, steps, N=N_OUT, K=K_IN):
-    """The fast kernel's own loads with no compute (dfq_debug_read_units) over the rotated
-    weight sets of the matmul, `steps` launches per graph, replayed like it; per-launch us."""
+def time_units(torch, ctx, stream, sets, M, steps, N=N_OUT, K=K_IN, packed=None):
+    """The fast kernel's own loads with no compute (dfq_debug_read_units, or
+    dfq_debug_read_units_packed over `packed`) over the rotated weight sets of the matmul,
+    `steps` launches per graph, replayed like it; per-launch us."""
     sink = torch.zeros(12 * ctx.num_cus, dtype=torch.int32, device=sets[0][0].device)
     calls = rotation(len(sets), steps, 0)["calls_per_graph"]
     torch.cuda.synchronize()
     ctx.graph_begin(stream)
     for i in range(calls):
+        if packed is not None:
+            ctx.read_units_packed(packed[i % len(packed)].data, M, N, K, sink, stream=stream)
+            continue
         w, s, b = sets[i % len(sets)]
         ctx.read_units(w, s, b, M, N, K, sink, stream=stream)
     graph = ctx.graph_end(stream)
@@ -332,6 +341,13 @@ def c5_weights(torch, dev, fused, layers=64):
             "lm": weights(*C5_LM_HEAD)}
 
 
+def pack_c5(ctx, W):
+    """The same weights in the packed layout (Context.pack), for the packed forward."""
+    return {**W, "packed": True,
+            "lw": [[ctx.pack(w, s, b, 4, 64) for (w, s, b) in lw] for lw in W["lw"]],
+            "lm": ctx.pack(*W["lm"], 4, 64)}
+
+
 C5_FORMS = {
     "per_layer": "one HIP graph per layer, launched one after the other",
     "composed": "one HIP graph per layer, the 64 composed into one launch (dfq_graph_compose)",
@@ -367,7 +383,7 @@ def chain_c5(torch, ctx, dev, W, M=8, form="per_layer", forwards=10):
         kinds = ["qmm"] * len(layer)
     stream = torch.cuda.Stream(device=dev)
     B = dflash_qmm.BF16
-    wlm, slm, blm = W["lm"]
+    packed = W.get("packed", False)
     proposals = torch.zeros(max(1, M - 1), dtype=torch.int32, device=dev)
     tokens = torch.empty(M, dtype=torch.int32, device=dev)
     accepted = torch.empty(1, dtype=torch.int32, device=dev)
@@ -379,6 +395,13 @@ def chain_c5(torch, ctx, dev, W, M=8, form="per_layer", forwards=10):
         layer_in = x if li == 0 else outs[-1]
         for j, (N, K) in enumerate(layer):
             inp = layer_in if srcs[j] is None else outs[srcs[j]]
+            if packed:
+                if kinds[j] == "qmm_silu_gate_up":
+                    ctx.qmm_silu_gate_up_packed(inp, wl[j], out=outs[j], ws=ws, stream=stream)
+                else:
+                    ctx.qmm_packed_raw(inp, wl[j], outs[j], M, ws=ws, ws_bytes=ws.numel(),
+                                       stream=stream)
+                continue
             w, s, b = wl[j]
             if kinds[j] == "qmm_silu_gate_up":
                 ctx.qmm_silu_gate_up(inp, w, s, b, 4, 64, out=outs[j], ws=ws, stream=stream)
@@ -387,6 +410,12 @@ def chain_c5(torch, ctx, dev, W, M=8, form="per_layer", forwards=10):
                             ws_bytes=ws.numel(), stream=stream)
 
     def lm_only():
+        if packed:
+            ctx.qmm_argmax_accept_packed(outs[-1], W["lm"],
+                                         proposals=proposals if M > 1 else None, tokens=tokens,
+                                         accepted=accepted, ws=acc_ws, stream=stream)
+            return
+        wlm, slm, blm = W["lm"]
         ctx.qmm_argmax_accept(outs[-1], wlm, slm, blm, 4, 64,
                               proposals=proposals if M > 1 else None, tokens=tokens,
                               accepted=accepted, ws=acc_ws, stream=stream)
@@ -437,7 +466,8 @@ def chain_c5(torch, ctx, dev, W, M=8, form="per_layer", forwards=10):
         "workload": (f"M={M} verify forward: {layers} layers x "
                      + ("(q|k|v, o, gate|up with silu*up epilogue, down)" if fused
                         else "(q,k,v,o,gate,up,down)")
-                     + " + lm_head + greedy accept, 4-bit g64 bf16, " + C5_FORMS[form]),
+                     + " + lm_head + greedy accept, 4-bit g64 bf16"
+                     + (" in the packed layout" if packed else "") + ", " + C5_FORMS[form]),
         "us_per_forward": round(total, 1),
         "p10": round(fw["p10"], 1),
         "p90": round(fw["p90"], 1),
@@ -488,13 +518,17 @@ def time_lm_head(torch, ctx, stream, dev, steps=20, nsets=4, reps=20):
                          ctx.workspace_bytes(M, V, K, 4, 64)), dtype=torch.uint8, device=dev)
     acc_ws = torch.zeros(256, dtype=torch.uint8, device=dev)
     B = dflash_qmm.BF16
+    packed = [ctx.pack(w, s, b, 4, 64) for (w, s, b) in sets]
     out = {}
-    for form in ("fused", "two_calls"):
+    for form in ("fused", "fused_packed", "two_calls"):
         torch.cuda.synchronize()
         ctx.graph_begin(stream)
         for i in range(steps):
             w, s, b = sets[i % nsets]
-            if form == "fused":
+            if form == "fused_packed":
+                ctx.qmm_argmax_accept_packed(x, packed[i % nsets], proposals=props,
+                                             tokens=tokens, accepted=acc, ws=ws, stream=stream)
+            elif form == "fused":
                 ctx.qmm_argmax_accept(x, w, s, b, 4, 64, proposals=props, tokens=tokens,
                                       accepted=acc, ws=ws, stream=stream)
             else:
@@ -512,6 +546,7 @@ def time_lm_head(torch, ctx, stream, dev, steps=20, nsets=4, reps=20):
                      f"{nsets} rotated weight sets ({nsets * 440} MB), median of {reps} "
                      f"replays of {steps} calls"),
         "fused_us": round(out["fused"], 2),
+        "fused_packed_us": round(out["fused_packed"], 2),
         "two_calls_us": round(out["two_calls"], 2),
         "ideal_us_at_8TBs": round(nb / (HBM_PEAK_GBS * 1e3), 2),
         "fused_gbs": round(nb / (out["fused"] * 1e-6) / 1e9, 1),
@@ -637,8 +672,10 @@ def main():
                     help="skip the stock path's timing beside the fast kernel")
     ap.add_argument("--no-rows", action="store_true",
                     help="skip the verify forward's cost at each width (c5_rows)")
+    ap.add_argument("--no-packed", action="store_true",
+                    help="skip the packed-layout legs (dfq_qmm_packed and its fused forms)")
     ap.add_argument("--c5-only", choices=["separate", "fused", "fused_composed",
-                                          "fused_one_graph"],
+                                          "fused_one_graph", "fused_composed_packed"],
                     default=None,
                     help="only time this form of the 64-layer verify forward (for profiling) "
                          "and print its figures")
@@ -688,8 +725,11 @@ def main():
     if args.c5_only:
         fused = args.c5_only.startswith("fused")
         form = {"separate": "per_layer", "fused": "per_layer", "fused_composed": "composed",
-                "fused_one_graph": "one_graph"}[args.c5_only]
+                "fused_one_graph": "one_graph",
+                "fused_composed_packed": "composed"}[args.c5_only]
         W = c5_weights(torch, dev, fused)
+        if args.c5_only.endswith("_packed"):
+            W = pack_c5(ctx, W)
         r = chain_c5(torch, ctx, dev, W, form=form)
         print(json.dumps({"c5_" + args.c5_only: r}), flush=True)
         ctx.close()
@@ -798,6 +838,31 @@ def main():
         }
         print(f"[bench] device copy moving {nb8 / 1e6:.1f} MB: {uc_copy:.2f} us/copy",
               file=sys.stderr, flush=True)
+    if not args.no_packed:
+        psets = [ctx.pack(w, s, b, BITS, GS) for (w, s, b) in sets]
+        pdist = {m: stats(time_m(torch, ctx, stream, sets, m, args.steps, args.warmup, N_OUT,
+                                 K_IN, BITS, GS, ws, ws.numel(), packed=psets)) for m in ms}
+        pud = stats(time_units(torch, ctx, stream, sets, 8, args.steps, packed=psets))
+        pus = {m: pdist[m]["median"] for m in ms}
+        out["packed"] = {
+            "workload": ("the same calls over the same rotated weight sets in the packed "
+                         "layout (dfq_pack_weights once at load, then dfq_qmm_packed): each "
+                         "unit of 16 rows x 8 groups is one contiguous piece, its codes in the "
+                         "order the lanes load them, then its scales and biases"),
+            "us_per_call": {str(m): round(pus[m], 3) for m in ms},
+            "us_per_call_p10": {str(m): round(pdist[m]["p10"], 3) for m in ms},
+            "us_per_call_p90": {str(m): round(pdist[m]["p90"], 3) for m in ms},
+            "gbs_by_M": {str(m): round(algorithmic_bytes(m) / (pus[m] * 1e-6) / 1e9, 1)
+                         for m in ms},
+            "faster_than_mlx_layout_us": {str(m): round(us[m] - pus[m], 3) for m in ms},
+            "unit_read_us": round(pud["median"], 3),
+            "unit_read_p10": round(pud["p10"], 3),
+            "unit_read_p90": round(pud["p90"], 3),
+        }
+        print(f"[bench] packed layout: M=8 {pus[8]:.2f} us/call ({us[8] - pus[8]:+.2f} us "
+              f"faster), its own loads {pud['median']:.2f} us/launch", file=sys.stderr,
+              flush=True)
+        del psets
     if not args.no_stock:
         st = time_stock(torch, ctx, stream, sets, [m for m in ms if m <= 8], steps=args.steps)
         out["stock"] = {
@@ -831,6 +896,14 @@ def main():
                   f"(ideal {out[key]['ideal_us_at_8TBs']})", file=sys.stderr, flush=True)
         if not args.no_rows:
             out["c5_rows"] = c5_rows(torch, ctx, dev, W)
+        if not args.no_packed:
+            WP = pack_c5(ctx, W)
+            for key, form in (("c5_chain_fused_composed_packed", "composed"),
+                              ("c5_chain_fused_one_graph_packed", "one_graph")):
+                out[key] = chain_c5(torch, ctx, dev, WP, form=form)
+                print(f"[bench] {key}: {out[key]['us_per_forward']} us/forward",
+                      file=sys.stderr, flush=True)
+            del WP
         del W
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline:

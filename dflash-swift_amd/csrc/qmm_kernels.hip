@@ -1002,9 +1002,10 @@ __device__ __forceinline__ void reduce_tile(const QmmParams& p, int t, int lane)
     store_y<F16>(p, t, lane, sum, unused);
 }
 
-template <int BITS, int GS, bool F16, int CH, int PF, int MT, bool AM = false>
+template <int BITS, int GS, bool F16, int CH, int PF, int MT, bool AM = false, bool PK = false>
 __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
     using C = Cfg<BITS, GS>;
+    static_assert(!PK || CH > 1, "the packed layout holds 8-group chunks");
     constexpr int XR = 8 * MT;  // rows of x sums per group in LDS
     static_assert(CH == 1 || CH * C::GPS == 8, "chunk = one super-step or 8 groups");
     uint8_t* lds = lds_base();
@@ -1112,6 +1113,22 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
         const int rl = (row0 + 16 <= p.N) ? n : min(n, p.N - 1 - row0);
         const uint32_t vw = (uint32_t)rl * RB + lane_w;
         const uint32_t vs = (uint32_t)rl * GPR * 2u + lane_s;
+        if constexpr (PK) {
+            /* the packed unit: its codes as CH * NS pieces of 1 KB (this lane's 16 bytes of
+             * piece i at i * 1024 + lane * 16), then 512 bytes of its rows' scales and biases
+             * (this lane's at ((q & 1) * 16 + n) * 16); past row N the pack holds zeros */
+            constexpr uint32_t kCodeBytes = 16u * CH * C::KSS * BITS / 8u;
+            const uint8_t* ub =
+                wbytes + ((size_t)t * p.chunks + kbk.c0 + c) * (kCodeBytes + 512u);
+            rsb[slot] = *(const SV*)(ub + kCodeBytes + (uint32_t)((q & 1) * 16 + n) * 16u);
+#pragma unroll
+            for (int j = 0; j < CH; ++j)
+#pragma unroll
+                for (int s = 0; s < C::NS; ++s)
+                    rw[slot][j][s] =
+                        *(const u32x4_t*)(ub + (j * C::NS + s) * 1024 + (uint32_t)lane * 16u);
+            return;
+        }
         const uint8_t* sbb = (q & 1) ? bbytes : sbytes;
         const int kc = k0 + c * (CH * C::KSS);  // first k of the chunk
         const uint8_t* wb = wbytes + (size_t)row0 * RB + kc * BITS / 8;
@@ -1676,6 +1693,44 @@ extern "C" __global__ void __launch_bounds__(64) dfq_qmm_generic(QmmGenericParam
     }
 }
 
+/* The packed layout of a 4/8-bit weight with its scales and biases, for 8-group chunks:
+ * unit (t, c) -- 16 rows of tile t, chunk c of K (8 groups) -- at (t * chunks + c) * ub
+ * bytes, ub = cb + 512.  Its codes are cb / 1024 pieces of 1 KB: byte 16 * l of piece i holds
+ * the 16 bytes lane l = 16 q + n loads for piece i from the MLX layout (row 16 t + n, bytes
+ * 64 i + 16 q of the chunk's codes).  Then 512 bytes: for qq = 0 (scales) and 1 (biases) and
+ * each row n, the 8 groups' 16 bytes at (16 qq + n) * 16.  Rows past N are zeros.  One thread
+ * per 16-byte piece; a pure byte permutation of the MLX arrays. */
+extern "C" __global__ void __launch_bounds__(256) dfq_pack_weights(
+    const uint8_t* w, const uint8_t* scales, const uint8_t* biases, uint8_t* packed, int N,
+    int K, int bits, int gs, uint64_t pieces) {
+    const uint32_t chunk_k = 8u * (uint32_t)gs;            // k of a chunk (8 groups)
+    const uint32_t cb = 16u * chunk_k * (uint32_t)bits / 8u;  // code bytes of a unit
+    const uint32_t ppu = (cb + 512u) / 16u;                // 16-byte pieces of a unit
+    const uint32_t chunks = (uint32_t)K / chunk_k;
+    const size_t rb = (size_t)K * bits / 8;                // bytes per weight row
+    const size_t sb = (size_t)(K / gs) * 2;                // bytes per scale row
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < pieces;
+         i += (uint64_t)gridDim.x * 256) {
+        const uint64_t u = i / ppu;
+        const uint32_t r = (uint32_t)(i - u * ppu);
+        const uint32_t t = (uint32_t)(u / chunks), c = (uint32_t)(u - (uint64_t)t * chunks);
+        u32x4_t v = {0u, 0u, 0u, 0u};
+        if (r < cb / 16u) {
+            const uint32_t piece = r / 64u, l = r % 64u, q = l >> 4, n = l & 15u;
+            const uint32_t row = t * 16u + n;
+            if ((int)row < N)
+                v = *(const u32x4_t*)(w + row * rb + (size_t)c * chunk_k * bits / 8 +
+                                      piece * 64u + q * 16u);
+        } else {
+            const uint32_t k = r - cb / 16u, qq = k >> 4, n = k & 15u;
+            const uint32_t row = t * 16u + n;
+            if ((int)row < N)
+                v = *(const u32x4_t*)((qq ? biases : scales) + row * sb + (size_t)c * 16u);
+        }
+        *(u32x4_t*)(packed + i * 16u) = v;
+    }
+}
+
 /* Fill n uint32 words with v (workspace re-arm; no memset node is ever captured). */
 extern "C" __global__ void __launch_bounds__(256) dfq_fill_u32(uint32_t* ptr, uint32_t v,
                                                                 uint64_t count) {
@@ -1722,6 +1777,41 @@ extern "C" __global__ void __launch_bounds__(768) dfq_read_units_b4_g64(QmmParam
         for (; u < b; u += 12) {
 #pragma unroll
             for (int j = 0; j < 1 + CH; ++j) acc ^= r[j];
+            if (u + 12 >= b) break;
+            __builtin_amdgcn_sched_barrier(0);
+            load(u + 12);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    const uint32_t v = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+    if (lane == 0) sink[blockIdx.x * 12 + wave] = v;
+}
+
+/* The same read over a packed weight array: unit (t, c) is 4608 contiguous bytes at
+ * (t * chunks + c) * 4608 -- its codes as four 1 KB pieces (load j of lane l at j * 1024 +
+ * l * 16), then its 16 rows' scales and biases (512 bytes: lane (q, n) at ((q & 1) * 16 + n) *
+ * 16) -- in the unpacked read's ranges, order and depth. */
+extern "C" __global__ void __launch_bounds__(768) dfq_read_units_packed_b4_g64(QmmParams p,
+                                                                                uint32_t* sink) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int q = lane >> 4, n = lane & 15;
+    const KBlock kbk = kblock(p, 0);
+    const int a = range_start(kbk, blockIdx.x), b = range_start(kbk, blockIdx.x + 1);
+    const uint8_t* pk = (const uint8_t*)p.w;
+    u32x4_t acc = {0u, 0u, 0u, 0u};
+    u32x4_t r[5];
+    auto load = [&](int u) {
+        const uint8_t* ub = pk + (size_t)u * 4608;  // one k-block: u = t * chunks + c
+        r[0] = *(const u32x4_t*)(ub + 4096 + ((q & 1) * 16 + n) * 16);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r[1 + j] = *(const u32x4_t*)(ub + j * 1024 + lane * 16);
+    };
+    int u = a + wave;
+    if (u < b) {
+        load(u);
+        for (; u < b; u += 12) {
+#pragma unroll
+            for (int j = 0; j < 5; ++j) acc ^= r[j];
             if (u + 12 >= b) break;
             __builtin_amdgcn_sched_barrier(0);
             load(u + 12);
@@ -1922,19 +2012,28 @@ constexpr int prefetch_depth() {
     return d < 1 ? 1 : (d > 8 ? 8 : d);
 }
 
-#define DFQ_MT8_KERNEL(BITS, GS, F16, NAME, CHN, CH, MTN, MT, AM, SFX)                     \
+#define DFQ_MT8_KERNEL(BITS, GS, F16, NAME, CHN, CH, MTN, MT, AM, PK, SFX)                 \
     extern "C" __global__ void __launch_bounds__(kBlock)                                     \
         dfq_qmm_##MTN##_b##BITS##_g##GS##_##NAME##_##CHN##SFX(QmmParams p) {                  \
-        qmm_mt8<BITS, GS, F16, CH, prefetch_depth<BITS, GS, CH>(), MT, AM>(p, blockIdx.x);    \
+        qmm_mt8<BITS, GS, F16, CH, prefetch_depth<BITS, GS, CH>(), MT, AM, PK>(p, blockIdx.x); \
     }
 /* per format: one super-step or 8-group chunks at up to 8 rows; 8-group chunks at up to 16;
- * and the greedy-accept forms (_am) of the 8-group-chunk kernels */
+ * the greedy-accept forms (_am) of the 8-group-chunk kernels; and all of the 8-group-chunk
+ * kernels again over the packed layout (_pk) */
 #define DFQ_MT8_FORMAT(BITS, GS, F16, NAME)                                                    \
-    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c1, 1, mt8, 1, false, )                               \
-    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt8, 1, false, )        \
-    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt16, 2, false, )       \
-    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt8, 1, true, _am)      \
-    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt16, 2, true, _am)
+    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c1, 1, mt8, 1, false, false, )                        \
+    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt8, 1, false, false, ) \
+    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt16, 2, false, false, )\
+    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt8, 1, true, false, _am)\
+    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt16, 2, true, false,    \
+                   _am)                                                                        \
+    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt8, 1, false, true, _pk)\
+    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt16, 2, false, true,    \
+                   _pk)                                                                        \
+    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt8, 1, true, true,      \
+                   _am_pk)                                                                     \
+    DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt16, 2, true, true,     \
+                   _am_pk)
 
 DFQ_MT8_FORMAT(4, 32, false, bf16)
 DFQ_MT8_FORMAT(4, 64, false, bf16)

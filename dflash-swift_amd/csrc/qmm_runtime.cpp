@@ -83,6 +83,9 @@ struct dfq_ctx {
     hipFunction_t mt8[2][3][2][2] = {};  // [bits 4/8][gs 32/64/128][bf16/f16][chunk 1/8 groups]
     hipFunction_t mt16[2][3][2] = {};    // up to 16 rows, 8-group chunks [bits][gs][bf16/f16]
     hipFunction_t am[2][3][2][2] = {};   // greedy-accept forms, 8-group chunks [..][rows 8/16]
+    hipFunction_t pk[2][3][2][2] = {};   // over the packed layout [bits][gs][dt][rows 8/16]
+    hipFunction_t pk_am[2][3][2][2] = {};  // greedy-accept forms over the packed layout
+    hipFunction_t pack = nullptr;        // MLX arrays -> the packed layout
     hipFunction_t reduce[2] = {};        // second pass of reduce splits [bf16/f16]
     hipFunction_t silu_mul[2] = {};      // SiLU-mul of a fused gate||up output [bf16/f16]
     hipFunction_t argmax_accept[2] = {}; // greedy accept of a verify pass [bf16/f16]
@@ -91,6 +94,7 @@ struct dfq_ctx {
     hipFunction_t fill = nullptr;
     hipFunction_t read_stream = nullptr; // the plain streaming read (bandwidth reference)
     hipFunction_t read_units = nullptr;  // the fast kernel's own loads with no compute
+    hipFunction_t read_units_packed = nullptr;  // the same over the packed layout
     void* scratch = nullptr;             // the fixed scratch of dfq_qmm_noalloc (this device)
     std::mutex mu;
     std::unordered_map<PlanKey, dfq::Plan, PlanKeyHash> plans;
@@ -491,13 +495,18 @@ dfq_status dfq_init(int device, dfq_ctx** out) {
                         return hip_fail(e, name);
                     }
                     for (int t = 0; t < 2; ++t) {
-                        snprintf(name, sizeof name, "dfq_qmm_mt%d_b%d_g%d_%s_c8_am", 8 * (t + 1),
-                                 kBits[b], kGs[g2], kDt[d]);
-                        if ((e = hipModuleGetFunction(&ctx->am[b][g2][d][t], ctx->module,
-                                                      name)) != hipSuccess) {
-                            (void)hipModuleUnload(ctx->module);
-                            delete ctx;
-                            return hip_fail(e, name);
+                        hipFunction_t* dst[3] = {&ctx->am[b][g2][d][t], &ctx->pk[b][g2][d][t],
+                                                 &ctx->pk_am[b][g2][d][t]};
+                        static const char* kSfx[3] = {"_am", "_pk", "_am_pk"};
+                        for (int f = 0; f < 3; ++f) {
+                            snprintf(name, sizeof name, "dfq_qmm_mt%d_b%d_g%d_%s_c8%s",
+                                     8 * (t + 1), kBits[b], kGs[g2], kDt[d], kSfx[f]);
+                            if ((e = hipModuleGetFunction(dst[f], ctx->module, name)) !=
+                                hipSuccess) {
+                                (void)hipModuleUnload(ctx->module);
+                                delete ctx;
+                                return hip_fail(e, name);
+                            }
                         }
                     }
                 }
@@ -509,8 +518,11 @@ dfq_status dfq_init(int device, dfq_ctx** out) {
         (e = hipModuleGetFunction(&ctx->argmax_accept[0], ctx->module, "dfq_argmax_accept_bf16")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->argmax_accept[1], ctx->module, "dfq_argmax_accept_f16")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->fill, ctx->module, "dfq_fill_u32")) != hipSuccess ||
+        (e = hipModuleGetFunction(&ctx->pack, ctx->module, "dfq_pack_weights")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->read_stream, ctx->module, "dfq_read_stream")) != hipSuccess ||
-        (e = hipModuleGetFunction(&ctx->read_units, ctx->module, "dfq_read_units_b4_g64")) != hipSuccess) {
+        (e = hipModuleGetFunction(&ctx->read_units, ctx->module, "dfq_read_units_b4_g64")) != hipSuccess ||
+        (e = hipModuleGetFunction(&ctx->read_units_packed, ctx->module,
+                                  "dfq_read_units_packed_b4_g64")) != hipSuccess) {
         (void)hipModuleUnload(ctx->module);
         delete ctx;
         return hip_fail(e, "hipModuleGetFunction");
@@ -717,10 +729,14 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
                              const void* biases, const void* lbias, void* y, int M, int N, int K,
                              int bits, int gs, dfq_dtype dt, void* ws, size_t wsb,
                              hipStream_t stream, int epi = 0, bool cache = true,
-                             const AcceptArgs* acc = nullptr) {
+                             const AcceptArgs* acc = nullptr, bool packed = false) {
     Plan pl;
     dfq_status s = get_plan(ctx, M, N, K, bits, gs, &pl, cache);
     if (s) return s;
+    if (packed && pl.ch == 1)
+        return fail(DFQ_ERR_UNSUPPORTED,
+                    "the packed layout holds chunks of 8 groups: K=%d is not a multiple of %d", K,
+                    8 * gs);
     if (acc && (pl.reduce || epi || pl.ch == 1))
         return fail(DFQ_ERR_STATE,
                     "greedy-accept mode needs 8-group chunks and a split without a second pass");
@@ -744,7 +760,9 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
     const int di = dt == DFQ_BF16 ? 0 : 1;
     void* args[] = {&p};
     const int ci = pl.ch > 1 ? 1 : 0;
-    hipFunction_t fn = acc           ? ctx->am[bi][gi][di][pl.mt - 1]
+    hipFunction_t fn = packed ? (acc ? ctx->pk_am[bi][gi][di][pl.mt - 1]
+                                     : ctx->pk[bi][gi][di][pl.mt - 1])
+                       : acc           ? ctx->am[bi][gi][di][pl.mt - 1]
                        : pl.mt == 2 ? ctx->mt16[bi][gi][di]
                                     : ctx->mt8[bi][gi][di][ci];
     hipError_t e = hipModuleLaunchKernel(fn, (unsigned)(pl.nkb * pl.Gkb), 1, 1, kBlockThreads, 1,
@@ -762,7 +780,8 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
 static dfq_status qmm_any(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
                           const void* biases, const void* lbias, void* y, int M, int N, int K,
                           int bits, int gs, dfq_dtype xdt, dfq_dtype sdt, dfq_dtype ydt, void* ws,
-                          size_t wsb, void* stream, int epi, bool cache = true);
+                          size_t wsb, void* stream, int epi, bool cache = true,
+                          bool packed = false);
 
 dfq_status dfq_qmm(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
                    const void* biases, const void* lbias, void* y, int M, int N, int K, int bits,
@@ -808,6 +827,62 @@ dfq_status dfq_qmm_noalloc(dfq_ctx* ctx, const void* x, const uint32_t* w, const
     return s;
 }
 
+/* ---- the packed layout -------------------------------------------------------------- */
+
+dfq_status dfq_packed_bytes(int N, int K, int bits, int gs, size_t* bytes) {
+    if (!bytes) return fail(DFQ_ERR_INVALID_ARGUMENT, "null bytes");
+    *bytes = 0;
+    if (N < 1 || K < 1) return fail(DFQ_ERR_INVALID_ARGUMENT, "N and K must be >= 1");
+    if (bits != 4 && bits != 8) return fail(DFQ_ERR_UNSUPPORTED, "bits must be 4 or 8");
+    if (gs != 32 && gs != 64 && gs != 128)
+        return fail(DFQ_ERR_UNSUPPORTED, "group size must be 32, 64 or 128");
+    if (K % (8 * gs))
+        return fail(DFQ_ERR_UNSUPPORTED,
+                    "the packed layout holds chunks of 8 groups: K=%d is not a multiple of %d", K,
+                    8 * gs);
+    const size_t unit = (size_t)16 * 8 * gs * bits / 8 + 512;
+    *bytes = (size_t)((N + 15) / 16) * (K / (8 * gs)) * unit;
+    return DFQ_OK;
+}
+
+dfq_status dfq_pack_weights(dfq_ctx* ctx, const uint32_t* w, const void* scales,
+                            const void* biases, int N, int K, int bits, int gs, void* packed,
+                            void* stream) {
+    if (!ctx || !w || !scales || !biases || !packed)
+        return fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
+    size_t bytes = 0;
+    dfq_status s = dfq_packed_bytes(N, K, bits, gs, &bytes);
+    if (s) return s;
+    if (!aligned(w, 16) || !aligned(scales, 16) || !aligned(biases, 16) || !aligned(packed, 256))
+        return fail(DFQ_ERR_INVALID_ARGUMENT,
+                    "w, scales and biases must be 16-byte aligned, packed 256-byte");
+    DeviceGuard g(ctx->device);
+    uint64_t pieces = bytes / 16;
+    void* args[] = {(void*)&w, (void*)&scales, (void*)&biases, &packed, &N, &K, &bits, &gs,
+                    &pieces};
+    const unsigned grid = (unsigned)std::min<uint64_t>((pieces + 255) / 256, 65536);
+    hipError_t e = hipModuleLaunchKernel(ctx->pack, grid, 1, 1, 256, 1, 1, 0,
+                                         (hipStream_t)stream, args, nullptr);
+    return e == hipSuccess ? DFQ_OK : hip_fail(e, "launch dfq_pack_weights");
+}
+
+dfq_status dfq_qmm_packed(dfq_ctx* ctx, const void* x, const void* packed, const void* lbias,
+                          void* y, int M, int N, int K, int bits, int gs, dfq_dtype dt, void* ws,
+                          size_t wsb, void* stream) {
+    return qmm_any(ctx, x, (const uint32_t*)packed, nullptr, nullptr, lbias, y, M, N, K, bits,
+                   gs, dt, dt, dt, ws, wsb, stream, 0, true, true);
+}
+
+dfq_status dfq_qmm_silu_gate_up_packed(dfq_ctx* ctx, const void* x, const void* packed_gu,
+                                       const void* linear_bias_gu, void* h, int M, int H, int K,
+                                       int bits, int gs, dfq_dtype dtype, void* ws, size_t wsb,
+                                       void* stream) {
+    if (H < 8 || H % 8)
+        return fail(DFQ_ERR_UNSUPPORTED, "the gate|up epilogue needs H a multiple of 8 (got %d)", H);
+    return qmm_any(ctx, x, (const uint32_t*)packed_gu, nullptr, nullptr, linear_bias_gu, h, M,
+                   2 * H, K, bits, gs, dtype, dtype, dtype, ws, wsb, stream, 1, true, true);
+}
+
 dfq_status dfq_qmm_silu_gate_up(dfq_ctx* ctx, const void* x, const uint32_t* w_gu,
                                 const void* scales_gu, const void* biases_gu,
                                 const void* linear_bias_gu, void* h, int M, int H, int K,
@@ -838,20 +913,26 @@ dfq_status dfq_interleave_gate_up(dfq_ctx* ctx, const void* gate, const void* up
 static dfq_status qmm_any(dfq_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
                           const void* biases, const void* lbias, void* y, int M, int N, int K,
                           int bits, int gs, dfq_dtype xdt, dfq_dtype sdt, dfq_dtype ydt, void* ws,
-                          size_t wsb, void* stream, int epi, bool cache) {
+                          size_t wsb, void* stream, int epi, bool cache, bool packed) {
     dfq_status s = check_fast_args(ctx, M, N, K, bits, gs, xdt, sdt, ydt);
     if (s) return s;
-    if (!x || !w || !scales || !biases || !y)
+    if (!x || !w || (!packed && (!scales || !biases)) || !y)
         return fail(DFQ_ERR_INVALID_ARGUMENT, "null x, w, scales, biases or y");
-    if (!aligned(x, 16) || !aligned(w, 16) || !aligned(scales, 4) || !aligned(biases, 4) ||
-        !aligned(y, 2) || (lbias && !aligned(lbias, 2)))
+    if (!aligned(x, 16) || !aligned(w, packed ? 256 : 16) ||
+        (!packed && (!aligned(scales, 4) || !aligned(biases, 4))) || !aligned(y, 2) ||
+        (lbias && !aligned(lbias, 2)))
         return fail(DFQ_ERR_INVALID_ARGUMENT,
-                    "x and w must be 16-byte aligned, scales/biases 4-byte aligned");
+                    "x and w must be 16-byte aligned (a packed weight 256-byte), scales/biases "
+                    "4-byte aligned");
     DeviceGuard g(ctx->device);
     const size_t esz = 2;
     if (one_pass(ctx, M, N, K, bits, gs, cache))
         return launch_mt8(ctx, x, w, scales, biases, lbias, y, M, N, K, bits, gs, xdt, ws, wsb,
-                          (hipStream_t)stream, epi, cache);
+                          (hipStream_t)stream, epi, cache, nullptr, packed);
+    if (packed)
+        return fail(DFQ_ERR_UNSUPPORTED,
+                    "the packed layout holds chunks of 8 groups: K=%d is not a multiple of %d", K,
+                    8 * gs);
     /* 9..16 rows with one-super-step chunks: two passes of up to 8 rows over the weights. */
     const size_t ypitch = (size_t)(epi ? N / 2 : N) * esz;
     for (int m0 = 0; m0 < M; m0 += 8) {
@@ -949,19 +1030,22 @@ dfq_status dfq_qmm_argmax_accept_workspace_bytes(dfq_ctx* ctx, int M, int V, int
     return qmm_accept_layout(ctx, M, V, K, bits, gs, &fused, &qws, bytes);
 }
 
-dfq_status dfq_qmm_argmax_accept(dfq_ctx* ctx, const void* x, const uint32_t* w,
-                                 const void* scales, const void* biases, const void* lbias,
-                                 void* logits, int M, int V, int K, int bits, int gs,
-                                 dfq_dtype dt, const int32_t* proposals, int32_t* tokens,
-                                 int32_t* accepted, void* ws, size_t wsb, void* stream) {
+static dfq_status qmm_argmax_accept(dfq_ctx* ctx, const void* x, const uint32_t* w,
+                                    const void* scales, const void* biases, const void* lbias,
+                                    void* logits, int M, int V, int K, int bits, int gs,
+                                    dfq_dtype dt, const int32_t* proposals, int32_t* tokens,
+                                    int32_t* accepted, void* ws, size_t wsb, void* stream,
+                                    bool packed) {
     dfq_status s = check_fast_args(ctx, M, V, K, bits, gs, dt, dt, dt);
     if (s) return s;
-    if (!x || !w || !scales || !biases)
+    if (!x || !w || (!packed && (!scales || !biases)))
         return fail(DFQ_ERR_INVALID_ARGUMENT, "null x, w, scales or biases");
-    if (!aligned(x, 16) || !aligned(w, 16) || !aligned(scales, 4) || !aligned(biases, 4) ||
+    if (!aligned(x, 16) || !aligned(w, packed ? 256 : 16) ||
+        (!packed && (!aligned(scales, 4) || !aligned(biases, 4))) ||
         (logits && !aligned(logits, 2)) || (lbias && !aligned(lbias, 2)))
         return fail(DFQ_ERR_INVALID_ARGUMENT,
-                    "x and w must be 16-byte aligned, scales/biases 4-byte aligned");
+                    "x and w must be 16-byte aligned (a packed weight 256-byte), scales/biases "
+                    "4-byte aligned");
     bool fused;
     size_t qws, total;
     if ((s = qmm_accept_layout(ctx, M, V, K, bits, gs, &fused, &qws, &total))) return s;
@@ -981,7 +1065,7 @@ dfq_status dfq_qmm_argmax_accept(dfq_ctx* ctx, const void* x, const uint32_t* w,
         acc.tokens = tokens;
         acc.accepted = accepted;
         return launch_mt8(ctx, x, w, scales, biases, lbias, logits, M, V, K, bits, gs, dt, ws,
-                          qws, (hipStream_t)stream, 0, true, &acc);
+                          qws, (hipStream_t)stream, 0, true, &acc, packed);
     }
     /* a split with a second pass: the logits first (to `logits` or the workspace), then the
      * accept kernel over them, its keys and counter in the accept region */
@@ -989,10 +1073,29 @@ dfq_status dfq_qmm_argmax_accept(dfq_ctx* ctx, const void* x, const uint32_t* w,
                       : (void*)(base + qws + align256((size_t)16 * M * 8) +
                                 align256(kAcceptCountBytes));
     if ((s = qmm_any(ctx, x, w, scales, biases, lbias, lg, M, V, K, bits, gs, dt, dt, dt, ws,
-                     qws, stream, 0)))
+                     qws, stream, 0, true, packed)))
         return s;
     return dfq_argmax_accept(ctx, lg, M, V, dt, proposals, tokens, accepted, keys,
                              align256((size_t)16 * M * 8) + align256(kAcceptCountBytes), stream);
+}
+
+dfq_status dfq_qmm_argmax_accept(dfq_ctx* ctx, const void* x, const uint32_t* w,
+                                 const void* scales, const void* biases, const void* lbias,
+                                 void* logits, int M, int V, int K, int bits, int gs,
+                                 dfq_dtype dt, const int32_t* proposals, int32_t* tokens,
+                                 int32_t* accepted, void* ws, size_t wsb, void* stream) {
+    return qmm_argmax_accept(ctx, x, w, scales, biases, lbias, logits, M, V, K, bits, gs, dt,
+                             proposals, tokens, accepted, ws, wsb, stream, false);
+}
+
+dfq_status dfq_qmm_argmax_accept_packed(dfq_ctx* ctx, const void* x, const void* packed,
+                                        const void* lbias, void* logits, int M, int V, int K,
+                                        int bits, int gs, dfq_dtype dt, const int32_t* proposals,
+                                        int32_t* tokens, int32_t* accepted, void* ws, size_t wsb,
+                                        void* stream) {
+    return qmm_argmax_accept(ctx, x, (const uint32_t*)packed, nullptr, nullptr, lbias, logits,
+                             M, V, K, bits, gs, dt, proposals, tokens, accepted, ws, wsb, stream,
+                             true);
 }
 
 /* Workgroups and LDS layout of the stock path's GEMV for a shape of at most 4 rows; false
@@ -1256,7 +1359,28 @@ dfq_status dfq_debug_read_units(dfq_ctx* ctx, const uint32_t* w, const void* sca
     return e == hipSuccess ? DFQ_OK : hip_fail(e, "launch dfq_read_units");
 }
 
-/* The same split computed without a device, for a given CU count and LDS limit. */
+/* The same unit read over a packed weight array: unit (t, c) of the split's 4608 bytes at
+ * packed + (t * chunks + c) * 4608, its codes as 4 x 1 KB (instruction j, lane l at j*1024 +
+ * l*16) and its scales and biases as 512 bytes; sink receives 12 * dfq_num_cus words. */
+dfq_status dfq_debug_read_units_packed(dfq_ctx* ctx, const void* packed, int M, int N, int K,
+                                       uint32_t* sink, void* stream) {
+    if (!ctx || !packed || !sink) return fail(DFQ_ERR_INVALID_ARGUMENT, "null argument");
+    dfq_status s = check_fast_args(ctx, M, N, K, 4, 64, DFQ_BF16, DFQ_BF16, DFQ_BF16);
+    if (s) return s;
+    Plan pl;
+    if ((s = get_plan(ctx, M, N, K, 4, 64, &pl))) return s;
+    if (pl.nkb != 1 || pl.ch != 8 / 2 || pl.Gkb > ctx->num_cus)
+        return fail(DFQ_ERR_UNSUPPORTED,
+                    "the unit read covers one-k-block splits of 8-group chunks over the CUs");
+    DeviceGuard g(ctx->device);
+    QmmParams p = fill_params(pl, nullptr, (const uint32_t*)packed, nullptr, nullptr, nullptr,
+                              nullptr, M, N, K, 4, 64, nullptr);
+    void* args[] = {&p, &sink};
+    hipError_t e = hipModuleLaunchKernel(ctx->read_units_packed, (unsigned)pl.Gkb, 1, 1, 768, 1,
+                                         1, 0, (hipStream_t)stream, args, nullptr);
+    return e == hipSuccess ? DFQ_OK : hip_fail(e, "launch dfq_read_units_packed");
+}
+
 /* Launches of the stock path's GEMV for a shape with x, scales and y all of `dt` and 16-byte
  * aligned arrays: one per 4 rows, or 0 where the per-element path takes the call. */
 dfq_status dfq_debug_stock_gemv_launches(dfq_ctx* ctx, int M, int N, int K, int bits, int gs,
@@ -1272,6 +1396,7 @@ dfq_status dfq_debug_stock_gemv_launches(dfq_ctx* ctx, int M, int N, int K, int 
     return DFQ_OK;
 }
 
+/* The same split computed without a device, for a given CU count and LDS limit. */
 dfq_status dfq_debug_make_plan(int M, int N, int K, int bits, int gs, int num_cus,
                                size_t lds_max, int* out15) {
     if (!out15) return fail(DFQ_ERR_INVALID_ARGUMENT, "null out");

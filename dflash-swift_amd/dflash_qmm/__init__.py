@@ -23,7 +23,8 @@ import ctypes
 import os
 
 __all__ = [
-    "BF16", "F16", "F32", "DfqError", "Context", "SmallMQuantizedMatmul", "QuantizedLinear",
+    "BF16", "F16", "F32", "DfqError", "Context", "PackedWeight", "SmallMQuantizedMatmul",
+    "QuantizedLinear",
     "SmallMQuantizedLinear", "Model", "enable_small_m_quantized_matmul", "library_path",
     "load_library",
 ]
@@ -116,6 +117,12 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
                                   I),
         "dfq_graph_launch": ([P, P], I), "dfq_graph_destroy": ([P], I),
         "dfq_graph_compose": ([P, PP, I, PP], I),
+        "dfq_packed_bytes": ([I, I, I, I, Z], I),
+        "dfq_pack_weights": ([P, P, P, P, I, I, I, I, P, P], I),
+        "dfq_qmm_packed": ([P, P, P, P, P, I, I, I, I, I, I, P, S, P], I),
+        "dfq_qmm_silu_gate_up_packed": ([P, P, P, P, P, I, I, I, I, I, I, P, S, P], I),
+        "dfq_qmm_argmax_accept_packed": ([P, P, P, P, P, I, I, I, I, I, I, P, P, P, P, S, P],
+                                         I),
         "dfq_linear_create": ([P, ctypes.POINTER(_LinearDesc), PP], I),
         "dfq_small_m_linear_create": ([P, PP], I), "dfq_linear_destroy": ([P], I),
         "dfq_linear_is_small_m": ([P], I), "dfq_linear_output_dtype": ([P, I], I),
@@ -128,6 +135,7 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         "dfq_debug_plan": ([P, I, I, I, I, I, ctypes.POINTER(I)], I),
         "dfq_debug_make_plan": ([I, I, I, I, I, I, S, ctypes.POINTER(I)], I),
         "dfq_debug_stock_gemv_launches": ([P, I, I, I, I, I, I, ctypes.POINTER(I)], I),
+        "dfq_debug_read_units_packed": ([P, P, I, I, I, P, P], I),
         "dfq_debug_read_stream": ([P, P, S, P, P], I),
         "dfq_debug_read_units": ([P, P, P, P, I, I, I, P, P], I),
         "dfq_linear_describe": ([P, ctypes.POINTER(_LinearDesc)], I),
@@ -259,6 +267,12 @@ class Context:
         _check(self.lib.dfq_debug_read_units(self.handle, _ptr(w), _ptr(scales), _ptr(biases),
                                              M, N, K, _ptr(sink), _stream(stream)),
                "dfq_debug_read_units")
+
+    def read_units_packed(self, packed, M, N, K, sink, stream=None):
+        """The unit read over a packed array of 4608-byte units (4-bit g64, one k-block)."""
+        _check(self.lib.dfq_debug_read_units_packed(self.handle, _ptr(packed), M, N, K,
+                                                    _ptr(sink), _stream(stream)),
+               "dfq_debug_read_units_packed")
 
     def read_stream(self, src, nbytes, sink, stream=None):
         """One launch of the plain streaming read of nbytes of src (the bandwidth reference);
@@ -400,6 +414,73 @@ class Context:
                "dfq_argmax_accept")
         return tokens, accepted
 
+    # ---- the packed layout ---------------------------------------------------------------
+    def pack(self, w, scales, biases, bits, gs, stream=None) -> "PackedWeight":
+        """The weight, scales and biases of an MLX layer in the packed layout
+        (dfq_pack_weights): a new device buffer; the MLX arrays are left as they are."""
+        import torch
+        N = w.shape[0]
+        K = w.shape[1] * 32 // bits
+        nb = ctypes.c_size_t()
+        _check(self.lib.dfq_packed_bytes(N, K, bits, gs, ctypes.byref(nb)), "dfq_packed_bytes")
+        buf = torch.empty(nb.value, dtype=torch.uint8, device=w.device)
+        _check(self.lib.dfq_pack_weights(self.handle, _ptr(w), _ptr(scales), _ptr(biases), N, K,
+                                         bits, gs, _ptr(buf), _stream(stream)),
+               "dfq_pack_weights")
+        return PackedWeight(buf, N, K, bits, gs, dtype_code(scales))
+
+    def qmm_packed_raw(self, x, pw, y, M, lbias=None, ws=None, ws_bytes=0, stream=None):
+        _check(self.lib.dfq_qmm_packed(self.handle, _ptr(x), _ptr(pw.data), _ptr(lbias), _ptr(y),
+                                       M, pw.N, pw.K, pw.bits, pw.gs, pw.dtype, _ptr(ws),
+                                       ws_bytes, _stream(stream)), "dfq_qmm_packed")
+
+    def qmm_packed(self, x, pw, lbias=None, out=None, ws=None, stream=None):
+        """y = x @ dequant(W).T from a packed weight (pack)."""
+        import torch
+        M = x.shape[0]
+        if out is None:
+            out = torch.empty((M, pw.N), dtype=x.dtype, device=x.device)
+        if ws is None:
+            ws = self.workspace(self.workspace_bytes(M, pw.N, pw.K, pw.bits, pw.gs), stream)
+        self.qmm_packed_raw(x, pw, out, M, lbias=lbias, ws=ws,
+                            ws_bytes=ws.numel() if ws is not None else 0, stream=stream)
+        return out
+
+    def qmm_silu_gate_up_packed(self, x, pw, lbias=None, out=None, ws=None, stream=None):
+        """qmm_silu_gate_up over a packed interleaved gate|up weight (N = 2H rows)."""
+        import torch
+        M, K = x.shape
+        H = pw.N // 2
+        if out is None:
+            out = torch.empty((M, H), dtype=x.dtype, device=x.device)
+        if ws is None:
+            ws = self.workspace(self.workspace_bytes(M, pw.N, K, pw.bits, pw.gs), stream)
+        _check(self.lib.dfq_qmm_silu_gate_up_packed(
+            self.handle, _ptr(x), _ptr(pw.data), _ptr(lbias), _ptr(out), M, H, K, pw.bits,
+            pw.gs, pw.dtype, _ptr(ws), ws.numel() if ws is not None else 0, _stream(stream)),
+            "dfq_qmm_silu_gate_up_packed")
+        return out
+
+    def qmm_argmax_accept_packed(self, x, pw, proposals=None, lbias=None, logits=None,
+                                 tokens=None, accepted=None, ws=None, stream=None):
+        """qmm_argmax_accept over a packed LM-head weight."""
+        import torch
+        M, K = x.shape
+        dev = x.device
+        if tokens is None:
+            tokens = torch.empty(M, dtype=torch.int32, device=dev)
+        if accepted is None:
+            accepted = torch.empty(1, dtype=torch.int32, device=dev)
+        if ws is None:
+            need = self.qmm_argmax_accept_workspace_bytes(M, pw.N, K, pw.bits, pw.gs)
+            ws = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+            self.workspace_clear(ws, ws.numel(), stream=stream)
+        _check(self.lib.dfq_qmm_argmax_accept_packed(
+            self.handle, _ptr(x), _ptr(pw.data), _ptr(lbias), _ptr(logits), M, pw.N, K,
+            pw.bits, pw.gs, pw.dtype, _ptr(proposals), _ptr(tokens), _ptr(accepted), _ptr(ws),
+            ws.numel(), _stream(stream)), "dfq_qmm_argmax_accept_packed")
+        return tokens, accepted
+
     def qmm_argmax_accept_workspace_bytes(self, M, V, K, bits, gs) -> int:
         b = ctypes.c_size_t()
         _check(self.lib.dfq_qmm_argmax_accept_workspace_bytes(self.handle, M, V, K, bits, gs,
@@ -446,6 +527,13 @@ class Context:
         _check(self.lib.dfq_graph_compose(self.handle, arr, len(graphs), ctypes.byref(g)),
                "dfq_graph_compose")
         return Graph(self.lib, g)
+
+
+class PackedWeight:
+    """A weight in the packed layout (Context.pack): its device bytes and format."""
+
+    def __init__(self, data, N, K, bits, gs, dtype):
+        self.data, self.N, self.K, self.bits, self.gs, self.dtype = data, N, K, bits, gs, dtype
 
 
 class Graph:

@@ -199,6 +199,44 @@ dfq_status dfq_graph_destroy(dfq_graph* graph);
  * forward). */
 dfq_status dfq_graph_compose(dfq_ctx* ctx, dfq_graph* const* parts, int n, dfq_graph** out);
 
+/* ---- the packed layout ---------------------------------------------------------------- */
+/* A weight prepared once at load for the fast kernel: the MLX arrays (codes, scales, biases)
+ * of 16 output rows by 8 quantisation groups, the unit one lane group of the kernel loads,
+ * stored as one contiguous piece -- the codes as the kernel's lanes load them (1 KB per load
+ * instruction), then the rows' scales and biases (512 bytes) -- in tile-major order, rows past
+ * N zero.  The kernel then reads each unit as whole cache lines instead of 16 rows' pieces of
+ * the weight and 32 pieces of the two 16-bit arrays: on MI355X the kernel's own loads of the
+ * 17408 x 5120 4-bit weight take 10.6 us packed against 11.4 us in the MLX layout, and of the
+ * 151936 x 5120 LM head 72 us against 82-85 us.  Results are bit-identical to the MLX layout's
+ * (the same values reach the same registers).  No counterpart in the reference, which reads
+ * MLX's arrays in place (SmallMQuantizedMatmul.swift:127-129, 140); the packed copy holds the
+ * same bytes as those arrays (rounded up to whole tiles of 16 rows), so a loader that packs
+ * and drops them uses no extra memory.
+ *
+ * dfq_packed_bytes: its size for an N x K weight (K a multiple of 8 groups; 4 or 8 bits;
+ * groups of 32, 64 or 128).  dfq_pack_weights: builds it on `stream` from 16-byte aligned MLX
+ * arrays into a 256-byte aligned buffer.  dfq_qmm_packed, dfq_qmm_silu_gate_up_packed and
+ * dfq_qmm_argmax_accept_packed: dfq_qmm, dfq_qmm_silu_gate_up and dfq_qmm_argmax_accept over
+ * it (one dtype for x, scales, biases and the outputs; the same workspaces). */
+dfq_status dfq_packed_bytes(int N, int K, int bits, int group_size, size_t* bytes);
+dfq_status dfq_pack_weights(dfq_ctx* ctx, const uint32_t* w, const void* scales,
+                            const void* biases, int N, int K, int bits, int group_size,
+                            void* packed, void* stream);
+dfq_status dfq_qmm_packed(dfq_ctx* ctx, const void* x, const void* packed,
+                          const void* linear_bias, void* y, int M, int N, int K, int bits,
+                          int group_size, dfq_dtype dtype, void* workspace,
+                          size_t workspace_bytes, void* stream);
+dfq_status dfq_qmm_silu_gate_up_packed(dfq_ctx* ctx, const void* x, const void* packed_gu,
+                                       const void* linear_bias_gu, void* h, int M, int H, int K,
+                                       int bits, int group_size, dfq_dtype dtype,
+                                       void* workspace, size_t workspace_bytes, void* stream);
+dfq_status dfq_qmm_argmax_accept_packed(dfq_ctx* ctx, const void* x, const void* packed,
+                                        const void* linear_bias, void* logits, int M, int V,
+                                        int K, int bits, int group_size, dfq_dtype dtype,
+                                        const int32_t* proposals, int32_t* tokens,
+                                        int32_t* accepted, void* workspace,
+                                        size_t workspace_bytes, void* stream);
+
 /* h[m][n] = silu(gu[m][n]) * gu[m][N + n] for the fused gate||up projection's output
  * gu[M][2N] (row pitch 2N elements): the activation between gate||up and down in a layer
  * chain.  bf16 or fp16, computed in fp32 (silu(g) = g / (1 + e^-g)) and rounded once.  No

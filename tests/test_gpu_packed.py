@@ -1,0 +1,140 @@
+"""The packed weight layout (dfq_pack_weights) and the fast kernel over it.
+
+The pack is a byte permutation of the MLX arrays; it is checked byte for byte against a numpy
+restatement of the layout (pack_reference below).  The kernels over it load the same values
+into the same registers as over the MLX layout, so dfq_qmm_packed, dfq_qmm_silu_gate_up_packed
+and dfq_qmm_argmax_accept_packed must equal dfq_qmm, dfq_qmm_silu_gate_up and
+dfq_qmm_argmax_accept bit for bit -- the MLX-layout kernels are pinned against the oracle by
+the parity, one-hot and accept tests -- across formats, dtypes, 1..16 rows, ragged N (the
+pack's zero rows past N) and every split (one k-block, narrow, aligned, three k-blocks,
+reduce, outputs written at the end of the workgroup).
+"""
+import numpy as np
+import pytest
+
+from gpu_util import announce, upload
+from oracle.qmm_oracle import BF16, F16, make_case
+
+pytestmark = pytest.mark.gpu
+
+
+def pack_reference(w_words, s_bits, b_bits, N, K, bits, gs):
+    """The packed layout on the CPU: unit (t, c) of 16 rows x 8 groups at (t*chunks + c) *
+    ub; piece i of its codes holds, at 16 * (16 q + n), bytes 64 i + 16 q of the chunk's codes
+    of row 16 t + n; then scales (qq = 0) and biases (qq = 1) of row n at (16 qq + n) * 16;
+    rows past N zero."""
+    ck = 8 * gs
+    cb = 16 * ck * bits // 8
+    chunks, T = K // ck, -(-N // 16)
+    wb = np.zeros((T * 16, K * bits // 8), dtype=np.uint8)
+    wb[:N] = np.ascontiguousarray(w_words).view(np.uint8).reshape(N, -1)
+    sb = np.zeros((T * 16, K // gs * 2), dtype=np.uint8)
+    bb = np.zeros_like(sb)
+    sb[:N] = np.ascontiguousarray(s_bits).view(np.uint8).reshape(N, -1)
+    bb[:N] = np.ascontiguousarray(b_bits).view(np.uint8).reshape(N, -1)
+    out = np.zeros((T, chunks, cb + 512), dtype=np.uint8)
+    for t in range(T):
+        rows = slice(16 * t, 16 * t + 16)
+        for c in range(chunks):
+            codes = wb[rows, c * cb // 16:(c + 1) * cb // 16]          # [16 n][cb/16]
+            pieces = codes.reshape(16, cb // 1024, 4, 16)               # [n][i][q][16]
+            out[t, c, :cb] = pieces.transpose(1, 2, 0, 3).reshape(-1)   # [i][q][n][16]
+            out[t, c, cb:cb + 256] = sb[rows, c * 16:(c + 1) * 16].reshape(-1)
+            out[t, c, cb + 256:] = bb[rows, c * 16:(c + 1) * 16].reshape(-1)
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("N,K,bits,gs,dt", [(40, 512, 4, 64, BF16), (33, 1024, 8, 64, F16),
+                                            (16, 256, 4, 32, BF16), (50, 2048, 4, 128, F16),
+                                            (17, 1024, 8, 128, BF16), (100, 768, 8, 32, BF16)])
+def test_pack_matches_the_layout(ctx, N, K, bits, gs, dt):
+    import torch
+    c = make_case(1, N, K, bits=bits, gs=gs, xdt=dt, seed=N + K)
+    _, w, s, b, _ = upload(c)
+    announce(f"pack N={N} K={K} bits={bits} gs={gs}")
+    pw = ctx.pack(w, s, b, bits, gs)
+    torch.cuda.synchronize()
+    got = pw.data.cpu().numpy()
+    want = pack_reference(c.w, c.scales, c.biases, N, K, bits, gs)
+    assert got.size == want.size
+    assert np.array_equal(got, want)
+
+
+def _eq(a, b):
+    import torch
+    return torch.equal(a.contiguous().view(torch.int16), b.contiguous().view(torch.int16))
+
+
+CASES = [  # (M, N, K, bits, gs, dtype, linear bias)
+    (8, 17408, 5120, 4, 64, BF16, False),   # the headline: one k-block, pair exchange
+    (1, 17408, 5120, 4, 64, BF16, False),
+    (16, 17408, 5120, 4, 64, BF16, False),  # two row tiles, aligned two-k-block split
+    (8, 5120, 17408, 4, 64, BF16, True),    # three k-blocks of whole tiles
+    (8, 1024, 5120, 4, 64, BF16, False),    # narrow: two k-blocks, one tile each
+    (12, 40000, 4096, 4, 64, F16, False),   # 12 rows, pair exchange
+    (8, 1024, 32768, 4, 64, BF16, True),    # the reduce split's second pass
+    (8, 7168, 5120, 8, 64, BF16, False),
+    (5, 5120, 5120, 4, 32, BF16, True),
+    (16, 333, 1024, 4, 128, F16, False),    # ragged N: zero rows past N in the last tile
+    (7, 130, 1024, 8, 128, BF16, True),
+    (3, 200, 512, 8, 32, F16, False),
+    (8, 32768, 512, 4, 64, BF16, False),    # outputs written at the end of the workgroup
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_packed_kernel_equals_the_mlx_layout(ctx, case):
+    import torch
+    M, N, K, bits, gs, dt, lb = case
+    c = make_case(M, N, K, bits=bits, gs=gs, xdt=dt, seed=M + N + K, lbias=lb,
+                  words=N * K > 4_000_000)
+    x, w, s, b, lbias = upload(c)
+    announce(f"packed qmm M={M} N={N} K={K} bits={bits} gs={gs} plan={ctx.plan(M, N, K, bits, gs)}")
+    pw = ctx.pack(w, s, b, bits, gs)
+    want = ctx.qmm(x, w, s, b, bits, gs, lbias=lbias)
+    got = ctx.qmm_packed(x, pw, lbias=lbias)
+    again = ctx.qmm_packed(x, pw, lbias=lbias)
+    torch.cuda.synchronize()
+    assert _eq(got, want) and _eq(again, want)
+
+
+def test_packed_gate_up_epilogue_equals_the_mlx_layout(ctx):
+    import torch
+    H, K = 2048, 5120
+    cg = make_case(8, H, K, bits=4, gs=64, seed=5, words=True)
+    cu = make_case(8, H, K, bits=4, gs=64, seed=6, words=True)
+    x, wg, sg, bg, _ = upload(cg)
+    _, wu, su, bu, _ = upload(cu)
+    w_gu, s_gu, b_gu = (ctx.interleave_gate_up(a, b) for a, b in ((wg, wu), (sg, su), (bg, bu)))
+    announce("packed gate|up epilogue")
+    want = ctx.qmm_silu_gate_up(x, w_gu, s_gu, b_gu, 4, 64)
+    got = ctx.qmm_silu_gate_up_packed(x, ctx.pack(w_gu, s_gu, b_gu, 4, 64))
+    torch.cuda.synchronize()
+    assert _eq(got, want)
+
+
+@pytest.mark.parametrize("M,V,K", [(8, 151936, 5120), (16, 32768, 512), (5, 3000, 2048)])
+def test_packed_lm_head_accept_equals_the_mlx_layout(ctx, M, V, K):
+    import torch
+    c = make_case(M, V, K, bits=4, gs=64, seed=M + V, words=V * K > 4_000_000)
+    x, w, s, b, _ = upload(c)
+    props = torch.zeros(max(1, M - 1), dtype=torch.int32, device="cuda")
+    announce(f"packed accept M={M} V={V} K={K}")
+    pw = ctx.pack(w, s, b, 4, 64)
+    lg_a = torch.empty(M, V, dtype=torch.bfloat16, device="cuda")
+    lg_b = torch.empty_like(lg_a)
+    ta, aa = ctx.qmm_argmax_accept(x, w, s, b, 4, 64, proposals=props, logits=lg_a)
+    tb, ab = ctx.qmm_argmax_accept_packed(x, pw, proposals=props, logits=lg_b)
+    tc, ac = ctx.qmm_argmax_accept_packed(x, pw, proposals=props)   # no logits written
+    torch.cuda.synchronize()
+    assert _eq(lg_a, lg_b)
+    assert torch.equal(ta, tb) and torch.equal(ta, tc)
+    assert int(aa.item()) == int(ab.item()) == int(ac.item())
+
+
+def test_packed_refuses_k_without_whole_chunks(ctx):
+    import ctypes
+    nb = ctypes.c_size_t(7)
+    assert ctx.lib.dfq_packed_bytes(64, 640, 4, 64, ctypes.byref(nb)) != 0 and nb.value == 0
+    assert ctx.lib.dfq_packed_bytes(64, 1024, 4, 64, ctypes.byref(nb)) == 0
+    assert nb.value == 4 * 2 * (4096 + 512)
