@@ -610,9 +610,24 @@ dfq_status dfq_checkpoint_upload(dfq_ctx* ctx, dfq_checkpoint* ck, const char* n
     return copy_pieces(ck, pieces, t.nbytes, (hipStream_t)stream);
 }
 
-dfq_status dfq_checkpoint_load_model(dfq_ctx* ctx, dfq_checkpoint* ck, dfq_model* model,
-                                     int (*want)(const char* prefix, void* user), void* user,
-                                     void* stream, int* loaded) {
+/* Whether layer L loads into the packed layout: an affine 4/8-bit layer with biases whose
+ * scales are bf16 or fp16, K a whole number of 8-group chunks, and a fast-kernel split at
+ * every row count of a launch (1..16). */
+static bool packs(dfq_ctx* ctx, const Layer& L) {
+    size_t nb = 0;
+    if (L.b < 0 || (L.dtype != DFQ_BF16 && L.dtype != DFQ_F16) ||
+        dfq_packed_bytes(L.out_features, L.in_features, L.bits, L.group_size, &nb) != DFQ_OK)
+        return false;
+    for (int r = 1; r <= DFQ_MAXIMUM_ROWS; ++r)
+        if (!dfq_qmm_supported(ctx, r, L.out_features, L.in_features, L.bits, L.group_size,
+                               L.dtype, L.dtype, L.dtype))
+            return false;
+    return true;
+}
+
+static dfq_status load_model(dfq_ctx* ctx, dfq_checkpoint* ck, dfq_model* model,
+                             int (*want)(const char* prefix, void* user), void* user,
+                             void* stream, int* loaded, bool pack) {
     if (loaded) *loaded = 0;
     if (!ctx || !ck || !model) return fail(DFQ_ERR_INVALID_ARGUMENT, "null ctx, checkpoint or model");
     std::vector<const Layer*> sel;
@@ -623,27 +638,57 @@ dfq_status dfq_checkpoint_load_model(dfq_ctx* ctx, dfq_checkpoint* ck, dfq_model
         sel.push_back(&L);
     }
     if (sel.empty()) return DFQ_OK;
-    /* one allocation, each tensor at a 256-byte aligned offset */
+    /* One allocation, each array at a 256-byte aligned offset: a packed layer's packed weight
+     * (slot 0) and linear bias (slot 3); any other layer's weight, scales, biases and bias as
+     * stored.  A packed layer's three MLX tensors pass through a device staging buffer, a
+     * batch of layers at a time, and are packed from there. */
     struct Slot {
         int tensor;
         size_t at;
     };
+    const auto up = [](size_t n) { return (n + 255) & ~(size_t)255; };
     std::vector<std::vector<Slot>> slots(sel.size());
-    size_t total = 0;
-    for (size_t i = 0; i < sel.size(); ++i)
-        for (int ti : {sel[i]->w, sel[i]->s, sel[i]->b, sel[i]->bias}) {
+    std::vector<char> packed(sel.size(), 0);
+    size_t total = 0, stage_max = 0, stage_all = 0;
+    for (size_t i = 0; i < sel.size(); ++i) {
+        const Layer& L = *sel[i];
+        packed[i] = pack && packs(ctx, L);
+        if (packed[i]) {
+            size_t nb = 0;
+            (void)dfq_packed_bytes(L.out_features, L.in_features, L.bits, L.group_size, &nb);
+            slots[i] = {{-1, total}, {-1, 0}, {-1, 0}, {L.bias, 0}};
+            total += up(nb);
+            if (L.bias >= 0) {
+                slots[i][3].at = total;
+                total += up(ck->tensors[L.bias].nbytes);
+            }
+            const size_t sb = up(ck->tensors[L.w].nbytes) + up(ck->tensors[L.s].nbytes) +
+                              up(ck->tensors[L.b].nbytes);
+            stage_max = std::max(stage_max, sb);
+            stage_all += sb;
+            continue;
+        }
+        for (int ti : {L.w, L.s, L.b, L.bias}) {
             if (ti < 0) {
                 slots[i].push_back({-1, 0});
                 continue;
             }
             slots[i].push_back({ti, total});
-            total += (ck->tensors[ti].nbytes + 255) & ~(size_t)255;
+            total += up(ck->tensors[ti].nbytes);
         }
+    }
     dfq::DeviceScope g(ctx);
     void* arena = nullptr;
+    void* stage = nullptr;
+    const size_t stage_bytes = std::max(stage_max, std::min(stage_all, (size_t)1 << 30));
     hipError_t e = hipMalloc(&arena, total);
     if (e != hipSuccess)
         return fail(DFQ_ERR_HIP, "device allocation of %zu bytes: %s", total, hipGetErrorString(e));
+    if (stage_all && (e = hipMalloc(&stage, stage_bytes)) != hipSuccess) {
+        (void)hipFree(arena);
+        return fail(DFQ_ERR_HIP, "packing stage of %zu bytes: %s", stage_bytes,
+                    hipGetErrorString(e));
+    }
     std::vector<Piece> pieces;
     for (auto& ls : slots)
         for (const Slot& s : ls)
@@ -651,7 +696,43 @@ dfq_status dfq_checkpoint_load_model(dfq_ctx* ctx, dfq_checkpoint* ck, dfq_model
                 const Tensor& t = ck->tensors[s.tensor];
                 pieces.push_back({t.shard, t.offset, t.nbytes, (char*)arena + s.at});
             }
-    dfq_status st = copy_pieces(ck, pieces, total, (hipStream_t)stream);
+    dfq_status st = pieces.empty() ? DFQ_OK : copy_pieces(ck, pieces, total, (hipStream_t)stream);
+    /* packed layers: fill the stage with as many as fit, pack them, repeat (copy_pieces
+     * returns once its copies are done; the packs run on the same stream before the next
+     * batch's copies overwrite the stage) */
+    for (size_t i = 0; st == DFQ_OK && i < sel.size();) {
+        std::vector<Piece> batch;
+        std::vector<std::pair<size_t, size_t>> layers;  // (layer, stage offset)
+        size_t fill = 0;
+        for (; i < sel.size(); ++i) {
+            if (!packed[i]) continue;
+            const Layer& L = *sel[i];
+            const size_t sb = up(ck->tensors[L.w].nbytes) + up(ck->tensors[L.s].nbytes) +
+                              up(ck->tensors[L.b].nbytes);
+            if (fill + sb > stage_bytes) break;
+            layers.push_back({i, fill});
+            for (int ti : {L.w, L.s, L.b}) {
+                const Tensor& t = ck->tensors[ti];
+                batch.push_back({t.shard, t.offset, t.nbytes, (char*)stage + fill});
+                fill += up(t.nbytes);
+            }
+        }
+        if (batch.empty()) break;
+        st = copy_pieces(ck, batch, fill, (hipStream_t)stream);
+        for (size_t k = 0; st == DFQ_OK && k < layers.size(); ++k) {
+            const Layer& L = *sel[layers[k].first];
+            char* base = (char*)stage + layers[k].second;
+            const size_t ws = up(ck->tensors[L.w].nbytes), ss = up(ck->tensors[L.s].nbytes);
+            st = dfq_pack_weights(ctx, (const uint32_t*)base, base + ws, base + ws + ss,
+                                  L.out_features, L.in_features, L.bits, L.group_size,
+                                  (char*)arena + slots[layers[k].first][0].at, stream);
+        }
+    }
+    if (stage) {
+        if ((e = hipStreamSynchronize((hipStream_t)stream)) != hipSuccess && st == DFQ_OK)
+            st = fail(DFQ_ERR_HIP, "packing: %s", hipGetErrorString(e));
+        (void)hipFree(stage);
+    }
     std::vector<dfq_linear*> lins;
     for (size_t i = 0; st == DFQ_OK && i < sel.size(); ++i) {
         const Layer& L = *sel[i];
@@ -659,9 +740,6 @@ dfq_status dfq_checkpoint_load_model(dfq_ctx* ctx, dfq_checkpoint* ck, dfq_model
             return slots[i][k].tensor < 0 ? nullptr : (char*)arena + slots[i][k].at;
         };
         dfq_linear_desc d{};
-        d.weight = (const uint32_t*)at(0);
-        d.scales = at(1);
-        d.biases = at(2);
         d.bias = at(3);
         d.out_features = L.out_features;
         d.in_features = L.in_features;
@@ -670,7 +748,14 @@ dfq_status dfq_checkpoint_load_model(dfq_ctx* ctx, dfq_checkpoint* ck, dfq_model
         d.mode_affine = 1;
         d.dtype = L.dtype;
         dfq_linear* lin = nullptr;
-        st = dfq_linear_create(ctx, &d, &lin);
+        if (packed[i]) {
+            st = dfq::make_packed_linear(ctx, d, (char*)arena + slots[i][0].at, &lin);
+        } else {
+            d.weight = (const uint32_t*)at(0);
+            d.scales = at(1);
+            d.biases = at(2);
+            st = dfq_linear_create(ctx, &d, &lin);
+        }
         if (st == DFQ_OK) lins.push_back(lin);
     }
     if (st != DFQ_OK) {
@@ -686,6 +771,18 @@ dfq_status dfq_checkpoint_load_model(dfq_ctx* ctx, dfq_checkpoint* ck, dfq_model
         }
     if (loaded) *loaded = (int)sel.size();
     return DFQ_OK;
+}
+
+dfq_status dfq_checkpoint_load_model(dfq_ctx* ctx, dfq_checkpoint* ck, dfq_model* model,
+                                     int (*want)(const char* prefix, void* user), void* user,
+                                     void* stream, int* loaded) {
+    return load_model(ctx, ck, model, want, user, stream, loaded, false);
+}
+
+dfq_status dfq_checkpoint_load_model_packed(dfq_ctx* ctx, dfq_checkpoint* ck, dfq_model* model,
+                                            int (*want)(const char* prefix, void* user),
+                                            void* user, void* stream, int* loaded) {
+    return load_model(ctx, ck, model, want, user, stream, loaded, true);
 }
 
 }  // extern "C"

@@ -61,6 +61,10 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
 /* The device address of the fixed scratch array (qmm_scratch.hip) on `device`, which must be
  * current; taken and cleared once per device. */
 dfq_status scratch_setup(int device, void** out);
+/* A layer whose only copy of the weight is `packed` (the packed layout, in memory the caller
+ * keeps alive); d carries its shape, format, dtype and linear bias, and no MLX arrays. */
+dfq_status make_packed_linear(dfq_ctx* ctx, const dfq_linear_desc& d, const void* packed,
+                              dfq_linear** out);
 dfq_status check_fast_args(const dfq_ctx* ctx, int M, int N, int K, int bits, int gs,
                            dfq_dtype xdt, dfq_dtype sdt, dfq_dtype ydt);
 

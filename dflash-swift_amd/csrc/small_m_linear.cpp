@@ -14,8 +14,17 @@
  *                                                returns the count
  *
  * The module tree is reduced to what the swap needs: named leaf layers.  Layers hold
- * device pointers owned by the caller; nothing is copied.  Errors are status codes.
+ * device pointers owned by the caller; nothing is copied, except by the opt-in
+ * dfq_small_m_linear_pack.  Errors are status codes.
+ *
+ * A layer may also hold its weight in the packed layout (dfq_pack_weights): as a copy made by
+ * dfq_small_m_linear_pack next to the MLX arrays, which the stock path keeps reading; or as
+ * its only copy, loaded so by dfq_checkpoint_load_model_packed, when the stock path is the
+ * fast kernel over that layout (16 rows a launch), there being no MLX arrays to hand to a
+ * stock op.
  */
+#include <hip/hip_runtime.h>
+
 #include <algorithm>
 #include <atomic>
 #include <map>
@@ -37,21 +46,47 @@ struct SmallMQuantizedMatmul {
     static constexpr int inputFeatureMultiple = DFQ_INPUT_FEATURE_MULTIPLE;
     static constexpr int requiredGroupSize = DFQ_REQUIRED_GROUP_SIZE;
 
-    static bool isEligible(const dfq_linear_desc& d) {
+    static bool isEligible(const dfq_linear_desc& d, bool hasBiases) {
         return dfq_is_eligible(d.out_features, d.in_features, d.bits, d.group_size,
-                               d.mode_affine, d.biases != nullptr) != 0;
+                               d.mode_affine, hasBiases) != 0;
     }
     static int tiles(int rows) { return dfq_tiles_for(rows); }
+};
+
+/* A weight in the packed layout.  `owned` (a copy made by dfq_small_m_linear_pack) is freed
+ * with the last layer that shares it; a loader's packed weight lives in its arena. */
+struct PackedWeight {
+    const void* ptr = nullptr;
+    void* owned = nullptr;
+    int device = -1;
+    PackedWeight() = default;
+    PackedWeight(const PackedWeight&) = delete;
+    PackedWeight& operator=(const PackedWeight&) = delete;
+    ~PackedWeight() {
+        if (!owned) return;
+        int prev = -1;
+        if (hipGetDevice(&prev) == hipSuccess && prev != device) (void)hipSetDevice(device);
+        (void)hipFree(owned);
+        if (prev >= 0 && prev != device) (void)hipSetDevice(prev);
+    }
 };
 
 /* MLX's QuantizedLinear reduced to its arrays and call. */
 class QuantizedLinear {
 public:
-    QuantizedLinear(dfq_ctx* ctx, const dfq_linear_desc& d) : ctx_(ctx), d_(d) {}
+    QuantizedLinear(dfq_ctx* ctx, const dfq_linear_desc& d,
+                    std::shared_ptr<PackedWeight> packed = nullptr)
+        : ctx_(ctx), d_(d), packed_(std::move(packed)) {}
     virtual ~QuantizedLinear() = default;
 
     const dfq_linear_desc& desc() const { return d_; }
     dfq_ctx* ctx() const { return ctx_; }
+    const std::shared_ptr<PackedWeight>& packed() const { return packed_; }
+    void setPacked(std::shared_ptr<PackedWeight> pw) { packed_ = std::move(pw); }
+    /* Only the packed copy: no MLX arrays (dfq_checkpoint_load_model_packed). */
+    bool packedOnly() const { return packed_ && !d_.weight; }
+    bool hasBiases() const { return d_.biases != nullptr || packedOnly(); }
+    bool eligible() const { return SmallMQuantizedMatmul::isEligible(d_, hasBiases()); }
     virtual bool isSmallM() const { return false; }
 
     /* The stock op's result dtype: MLX promotion of the input with the scales. */
@@ -61,9 +96,8 @@ public:
 
     virtual dfq_status callAsFunction(const void* x, dfq_dtype xdt, int rows, void* y,
                                       void* ws, size_t wsb, void* stream, int* took) {
-        (void)ws;
-        (void)wsb;
         if (took) *took = 0;
+        if (packedOnly()) return packedSlices(x, xdt, rows, y, ws, wsb, stream);
         if (!d_.biases)
             return dfq::fail(DFQ_ERR_UNSUPPORTED, "the generic path needs affine biases");
         return dfq_qmm_fallback(ctx_, x, d_.weight, d_.scales, d_.biases, d_.bias, y, rows,
@@ -72,14 +106,46 @@ public:
     }
 
     virtual dfq_status workspaceBytes(int rows, size_t* bytes) const {
-        (void)rows;
         *bytes = 0;
+        if (!packedOnly()) return DFQ_OK;
+        /* the stock path of a packed-only layer: launches of up to 16 rows */
+        for (int r : {std::min(rows, kSlice), rows % kSlice}) {
+            size_t b = 0;
+            if (r < 1) continue;
+            dfq_status s = dfq_qmm_workspace_bytes(ctx_, r, d_.out_features, d_.in_features,
+                                                   d_.bits, d_.group_size, &b);
+            if (s) return s;
+            *bytes = std::max(*bytes, b);
+        }
         return DFQ_OK;
     }
 
 protected:
+    static constexpr int kSlice = DFQ_MAXIMUM_ROWS;
+
+    /* The fast kernel over the packed copy, up to 16 rows a launch: the stock path of a layer
+     * that has no MLX arrays (x, scales and y in the one dtype the pack holds). */
+    dfq_status packedSlices(const void* x, dfq_dtype xdt, int rows, void* y, void* ws,
+                            size_t wsb, void* stream) const {
+        if (xdt != d_.dtype)
+            return dfq::fail(DFQ_ERR_UNSUPPORTED,
+                             "a packed layer takes x in the dtype of its scales (%d), not %d",
+                             (int)d_.dtype, (int)xdt);
+        const size_t xrow = (size_t)d_.in_features * 2, yrow = (size_t)d_.out_features * 2;
+        for (int r0 = 0; r0 < rows; r0 += kSlice) {
+            const int r = std::min(kSlice, rows - r0);
+            dfq_status s = dfq_qmm_packed(ctx_, (const char*)x + r0 * xrow, packed_->ptr, d_.bias,
+                                          (char*)y + r0 * yrow, r, d_.out_features,
+                                          d_.in_features, d_.bits, d_.group_size, d_.dtype, ws,
+                                          wsb, stream);
+            if (s) return s;
+        }
+        return DFQ_OK;
+    }
+
     dfq_ctx* ctx_;
     dfq_linear_desc d_;
+    std::shared_ptr<PackedWeight> packed_;
 };
 
 /* SmallMQuantizedLinear: shares the wrapped layer's arrays (:243-252) and settles
@@ -87,8 +153,8 @@ protected:
 class SmallMQuantizedLinear final : public QuantizedLinear {
 public:
     explicit SmallMQuantizedLinear(const QuantizedLinear& other)
-        : QuantizedLinear(other.ctx(), other.desc()),
-          kernelEligible_(SmallMQuantizedMatmul::isEligible(other.desc())) {
+        : QuantizedLinear(other.ctx(), other.desc(), other.packed()),
+          kernelEligible_(other.eligible()) {
         /* The reference gate says nothing of the kernel's own limits (weights under 2 GiB,
          * a work split for the shape).  Rows the fast kernel cannot take fall through to the
          * stock op like any other ineligible call (:254-266), decided once here. */
@@ -104,7 +170,7 @@ public:
     bool takesKernel(dfq_dtype xdt, int rows) const {
         return kernelEligible_ && rows >= SmallMQuantizedMatmul::minimumRows &&
                rows <= SmallMQuantizedMatmul::maximumRows && ((rowsFit_ >> rows) & 1u) &&
-               xdt == DFQ_BF16 && d_.biases != nullptr && d_.dtype == DFQ_BF16;
+               xdt == DFQ_BF16 && hasBiases() && d_.dtype == DFQ_BF16;
     }
 
     dfq_status callAsFunction(const void* x, dfq_dtype xdt, int rows, void* y, void* ws,
@@ -112,6 +178,10 @@ public:
         if (!takesKernel(xdt, rows))
             return QuantizedLinear::callAsFunction(x, xdt, rows, y, ws, wsb, stream, took);
         if (took) *took = 1;
+        if (packed_)
+            return dfq_qmm_packed(ctx_, x, packed_->ptr, d_.bias, y, rows, d_.out_features,
+                                  d_.in_features, d_.bits, d_.group_size, DFQ_BF16, ws, wsb,
+                                  stream);
         return dfq_qmm(ctx_, x, d_.weight, d_.scales, d_.biases, d_.bias, y, rows,
                        d_.out_features, d_.in_features, d_.bits, d_.group_size, DFQ_BF16,
                        DFQ_BF16, DFQ_BF16, ws, wsb, stream);
@@ -119,7 +189,7 @@ public:
 
     dfq_status workspaceBytes(int rows, size_t* bytes) const override {
         *bytes = 0;
-        if (!takesKernel(DFQ_BF16, rows)) return DFQ_OK;
+        if (!takesKernel(DFQ_BF16, rows)) return QuantizedLinear::workspaceBytes(rows, bytes);
         return dfq_qmm_workspace_bytes(ctx_, rows, d_.out_features, d_.in_features, d_.bits,
                                        d_.group_size, bytes);
     }
@@ -144,6 +214,16 @@ struct dfq_model {
     std::map<std::string, dfq_linear*> leaves;
     std::vector<std::unique_ptr<dfq_linear>> owned;
 };
+
+dfq_status dfq::make_packed_linear(dfq_ctx* ctx, const dfq_linear_desc& d, const void* packed,
+                                   dfq_linear** out) {
+    if (!packed || !out || d.weight || d.scales || d.biases)
+        return dfq::fail(DFQ_ERR_INVALID_ARGUMENT, "a packed layer has no MLX arrays");
+    auto pw = std::make_shared<dflash::PackedWeight>();
+    pw->ptr = packed;
+    *out = new dfq_linear{std::make_shared<dflash::QuantizedLinear>(ctx, d, std::move(pw))};
+    return DFQ_OK;
+}
 
 extern "C" {
 
@@ -183,6 +263,41 @@ dfq_status dfq_linear_destroy(dfq_linear* lin) {
 }
 
 int dfq_linear_is_small_m(const dfq_linear* lin) { return lin && lin->impl->isSmallM(); }
+
+const void* dfq_linear_packed(const dfq_linear* lin) {
+    return lin && lin->impl->packed() ? lin->impl->packed()->ptr : nullptr;
+}
+
+dfq_status dfq_small_m_linear_pack(dfq_linear* lin, void* stream) {
+    if (!lin) return dfq::fail(DFQ_ERR_INVALID_ARGUMENT, "null layer");
+    auto& L = *lin->impl;
+    if (!L.isSmallM())
+        return dfq::fail(DFQ_ERR_INVALID_ARGUMENT,
+                         "only a SmallMQuantizedLinear takes a packed copy");
+    if (L.packed()) return DFQ_OK;
+    if (!L.ctx()) return dfq::fail(DFQ_ERR_STATE, "layer was created without a context");
+    const dfq_linear_desc& d = L.desc();
+    if (!L.eligible() || !d.biases || d.dtype != DFQ_BF16)
+        return dfq::fail(DFQ_ERR_UNSUPPORTED,
+                         "a packed copy serves the fast kernel's bf16 calls of an eligible layer");
+    size_t bytes = 0;
+    dfq_status s = dfq_packed_bytes(d.out_features, d.in_features, d.bits, d.group_size, &bytes);
+    if (s) return s;
+    auto pw = std::make_shared<dflash::PackedWeight>();
+    pw->device = dfq::ctx_device(L.ctx());
+    dfq::DeviceScope g(L.ctx());
+    hipError_t e = hipMalloc(&pw->owned, bytes);
+    if (e != hipSuccess)
+        return dfq::fail(DFQ_ERR_HIP, "packed copy of %zu bytes: %s", bytes, hipGetErrorString(e));
+    pw->ptr = pw->owned;
+    s = dfq_pack_weights(L.ctx(), d.weight, d.scales, d.biases, d.out_features, d.in_features,
+                         d.bits, d.group_size, pw->owned, stream);
+    if (s) return s;
+    if ((e = hipStreamSynchronize((hipStream_t)stream)) != hipSuccess)
+        return dfq::fail(DFQ_ERR_HIP, "packing: %s", hipGetErrorString(e));
+    L.setPacked(std::move(pw));
+    return DFQ_OK;
+}
 
 dfq_dtype dfq_linear_output_dtype(const dfq_linear* lin, dfq_dtype x_dtype) {
     /* Both paths return MLX's promotion of (x, scales): the kernel path only runs when
@@ -247,7 +362,7 @@ int dfq_enable_small_m_quantized_matmul(dfq_model* model) {
     for (auto& kv : model->leaves) {
         const auto& leaf = kv.second->impl;
         if (leaf->isSmallM()) continue;                                       // :309
-        if (!dflash::SmallMQuantizedMatmul::isEligible(leaf->desc())) continue; // :310-311
+        if (!leaf->eligible()) continue;                                      // :310-311
         auto* swapped_leaf =                                                   // :313
             new dfq_linear{std::make_shared<dflash::SmallMQuantizedLinear>(*leaf)};
         model->owned.emplace_back(swapped_leaf);

@@ -150,6 +150,8 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         "dfq_checkpoint_layer_count": ([P], I),
         "dfq_checkpoint_layer": ([P, I, ctypes.POINTER(_LayerInfo)], I),
         "dfq_checkpoint_load_model": ([P, P, P, _WANT_FN, P, P, ctypes.POINTER(I)], I),
+        "dfq_checkpoint_load_model_packed": ([P, P, P, _WANT_FN, P, P, ctypes.POINTER(I)], I),
+        "dfq_small_m_linear_pack": ([P, P], I), "dfq_linear_packed": ([P], P),
         "dfq_qmm_silu_gate_up": ([P, P, P, P, P, P, P, I, I, I, I, I, I, P, S, P], I),
         "dfq_interleave_gate_up": ([P, P, P, P, I, S, P], I),
     }
@@ -611,6 +613,11 @@ class QuantizedLinear:
         return bool(self.lib.dfq_linear_is_small_m(self._h))
 
     @property
+    def packed(self):
+        """Device address of the layer's weight in the packed layout, or None."""
+        return self.lib.dfq_linear_packed(self._h) or None
+
+    @property
     def shape(self):
         return (self.out_features, self.in_features)
 
@@ -658,6 +665,12 @@ class SmallMQuantizedLinear(QuantizedLinear):
                "dfq_small_m_linear_create")
         super().__init__(other.ctx, other.weight, other.scales, other.biases, other.bias,
                          other.group_size, other.bits, other.mode, _handle=h)
+
+    def pack(self, stream=None):
+        """A packed copy of the weight for the fast kernel's calls (dfq_small_m_linear_pack)."""
+        _check(self.lib.dfq_small_m_linear_pack(self._h, _stream(stream)),
+               "dfq_small_m_linear_pack")
+        return self
 
 
 class Model:
@@ -814,15 +827,16 @@ class Checkpoint:
         return out
 
     def load_model(self, ctx: Context, want=None, model: "Model | None" = None,
-                   stream=None) -> "Model":
+                   stream=None, packed=False) -> "Model":
         """Load the quantised layers (those want(prefix) accepts) into device memory as
-        stock QuantizedLinear leaves of `model` (a new Model if None)."""
+        stock QuantizedLinear leaves of `model` (a new Model if None); with packed, the
+        layers the packed layout serves load in it (dfq_checkpoint_load_model_packed)."""
         model = model if model is not None else Model()
         cb = _WANT_FN(lambda p, _u: int(bool(want(p.decode())))) if want else _WANT_FN()
         n = ctypes.c_int(0)
-        _check(self.lib.dfq_checkpoint_load_model(ctx.handle, self._h, model._h, cb, None,
-                                                  _stream(stream), ctypes.byref(n)),
-               "dfq_checkpoint_load_model")
+        fn = "dfq_checkpoint_load_model_packed" if packed else "dfq_checkpoint_load_model"
+        _check(getattr(self.lib, fn)(ctx.handle, self._h, model._h, cb, None, _stream(stream),
+                                     ctypes.byref(n)), fn)
         model._ctx = ctx
         model._keep.append(self)
         for L in self.layers():

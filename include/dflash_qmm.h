@@ -311,6 +311,17 @@ dfq_status dfq_small_m_linear_create(dfq_linear* other, dfq_linear** out);
 dfq_status dfq_linear_destroy(dfq_linear* lin);
 /* 1 if `lin` is a SmallMQuantizedLinear. */
 int dfq_linear_is_small_m(const dfq_linear* lin);
+/* Gives a SmallMQuantizedLinear a copy of its weight in the packed layout (dfq_pack_weights),
+ * which its fast-kernel calls then read (bit-identical results); the stock path keeps reading
+ * the MLX arrays, so the layer holds its weight twice.  The copy belongs to the layer (freed
+ * with it and with every handle sharing it) and is built on `stream`; returns when done.
+ * DFQ_ERR_UNSUPPORTED for a layer whose calls never take the fast kernel (not eligible, not
+ * bf16) or whose format has no packed form (the layer is left as it was);
+ * DFQ_ERR_INVALID_ARGUMENT for a stock layer.  A second call does nothing.  No counterpart
+ * in the reference, which reads MLX's arrays in place (SmallMQuantizedMatmul.swift:245-248). */
+dfq_status dfq_small_m_linear_pack(dfq_linear* lin, void* stream);
+/* The layer's weight in the packed layout, or NULL if it has none. */
+const void* dfq_linear_packed(const dfq_linear* lin);
 /* The dtype callAsFunction returns for input dtype x_dtype. */
 dfq_dtype dfq_linear_output_dtype(const dfq_linear* lin, dfq_dtype x_dtype);
 /* callAsFunction (:254-292): y[rows][out] for x[rows][in]; rows = product of the leading
@@ -412,6 +423,19 @@ dfq_status dfq_checkpoint_layer(const dfq_checkpoint* ck, int index, dfq_layer_i
 dfq_status dfq_checkpoint_load_model(dfq_ctx* ctx, dfq_checkpoint* ck, dfq_model* model,
                                      int (*want)(const char* prefix, void* user), void* user,
                                      void* stream, int* loaded);
+/* dfq_checkpoint_load_model with every chosen layer that the packed layout serves (an affine
+ * layer with biases, 4 or 8 bits, bf16 or fp16 scales, K a multiple of 8 groups, a fast-kernel
+ * split at 1..16 rows) written into the allocation in that layout instead of MLX's: the same
+ * bytes (rows rounded up to 16), through a device staging buffer of up to 1 GiB (or the
+ * largest such layer) that is freed before it returns.  Other layers load as stored.  A
+ * packed layer has no MLX arrays (dfq_linear_describe gives NULL weight, scales and biases;
+ * dfq_linear_packed gives its weight): its stock path is the fast kernel over the packed
+ * layout, 16 rows a launch, with x in the dtype of its scales; swapped, it takes the window
+ * like any SmallMQuantizedLinear.  No counterpart in the reference, whose loader fills MLX
+ * arrays (mlx-swift-lm loadModel, reached at Sources/dflash-bench/main.swift:26). */
+dfq_status dfq_checkpoint_load_model_packed(dfq_ctx* ctx, dfq_checkpoint* ck, dfq_model* model,
+                                            int (*want)(const char* prefix, void* user),
+                                            void* user, void* stream, int* loaded);
 /* The arrays and shape of a layer (for layers the caller did not create itself). */
 dfq_status dfq_linear_describe(const dfq_linear* lin, dfq_linear_desc* out);
 

@@ -138,3 +138,137 @@ def test_packed_refuses_k_without_whole_chunks(ctx):
     assert ctx.lib.dfq_packed_bytes(64, 640, 4, 64, ctypes.byref(nb)) != 0 and nb.value == 0
     assert ctx.lib.dfq_packed_bytes(64, 1024, 4, 64, ctypes.byref(nb)) == 0
     assert nb.value == 4 * 2 * (4096 + 512)
+
+
+# ---- the drop-in layer over the packed layout ------------------------------------------------
+
+CK_LAYERS = [
+    # (prefix, N, K, bits, gs, linear bias, scale dtype)
+    ("model.layers.0.self_attn.q_proj", 4096, 1024, 4, 64, False, BF16),
+    ("model.layers.0.self_attn.o_proj", 4100, 2048, 4, 64, True, BF16),   # ragged last tile
+    ("model.layers.0.mlp.down_proj", 4096, 1024, 8, 64, False, BF16),
+    ("model.layers.1.mlp.gate_proj", 4096, 512, 4, 32, False, BF16),      # g32: never swapped
+    ("model.layers.1.mlp.up_proj", 4096, 1024, 4, 64, True, F16),         # fp16 scales
+    ("model.layers.1.mlp.down_proj", 4096, 320, 4, 64, False, BF16),      # 5 groups: as stored
+]
+
+
+def _build_checkpoint(tmp_path):
+    from ckpt_util import write_model_dir
+    layers, q = [], {"group_size": 64, "bits": 4}
+    for i, (prefix, N, K, bits, gs, lb, sdt) in enumerate(CK_LAYERS):
+        c = make_case(8, N, K, bits=bits, gs=gs, xdt=BF16, sdt=sdt, seed=200 + i, lbias=lb)
+        layers.append((prefix, c, lb))
+        if bits != 4 or gs != 64:
+            q[prefix] = {"bits": bits, "group_size": gs}
+    write_model_dir(tmp_path, layers, q, shards=2)
+    return {p: c for p, c, _ in layers}
+
+
+def _d2h(ctx, addr, nbytes):
+    out = np.empty(nbytes, dtype=np.uint8)
+    import dflash_qmm
+    dflash_qmm._check(ctx.lib.dfq_memcpy_d2h(ctx.handle, out.ctypes.data, addr, nbytes, None),
+                      "d2h")
+    return out
+
+
+def _slices(ctx, c, x):
+    """The fast kernel over the MLX arrays, 16 rows a launch (what a packed layer's stock
+    path computes)."""
+    import torch
+    _, w, s, b, lb = upload(c)
+    return torch.cat([ctx.qmm(x[r:r + 16], w, s, b, c.bits, c.gs, lbias=lb)
+                      for r in range(0, x.shape[0], 16)])
+
+
+def test_checkpoint_loads_packed_and_matches_the_mlx_layout(ctx, tmp_path):
+    import torch
+    import dflash_qmm
+    from gpu_util import to_dev16
+    cases = _build_checkpoint(tmp_path)
+    ck = dflash_qmm.Checkpoint(str(tmp_path))
+    announce("checkpoint load, MLX layout and packed")
+    plain = ck.load_model(ctx)
+    packed = ck.load_model(ctx, packed=True)
+    assert len(plain) == len(packed) == len(CK_LAYERS)
+    packs = {p for (p, N, K, bits, gs, lb, sdt) in CK_LAYERS if K % (8 * gs) == 0}
+    for (prefix, N, K, bits, gs, lb, sdt) in CK_LAYERS:
+        leaf = packed.leaf(prefix)
+        assert (leaf.packed is not None) == (prefix in packs), prefix
+        if prefix not in packs:
+            continue
+        assert leaf.weight is None and leaf.scales is None and leaf.biases is None
+        assert (leaf.bias is not None) == lb
+        c = cases[prefix]
+        nb = ctypes_size(ctx, N, K, bits, gs)
+        want = pack_reference(c.w, c.scales, c.biases, N, K, bits, gs)
+        assert nb == want.size and np.array_equal(_d2h(ctx, leaf.packed, nb), want), prefix
+    assert dflash_qmm.enable_small_m_quantized_matmul(plain) == \
+        dflash_qmm.enable_small_m_quantized_matmul(packed) == 4
+    for (prefix, N, K, bits, gs, lb, sdt) in CK_LAYERS:
+        c = cases[prefix]
+        a, p = plain.leaf(prefix), packed.leaf(prefix)
+        assert a.is_small_m == p.is_small_m
+        for rows in (1, 2, 8, 16, 17, 33):
+            x = to_dev16(make_case(rows, N, K, bits=bits, gs=gs, xdt=sdt, seed=rows).x, sdt)
+            announce(f"packed leaf {prefix} rows={rows}")
+            ya, yp = a(x), p(x)
+            took_a, took_p = a.last_took_kernel, p.last_took_kernel
+            torch.cuda.synchronize()
+            assert took_a == took_p
+            if prefix not in packs or took_p:
+                assert _eq(ya, yp), (prefix, rows)       # the same path, the same kernel
+            else:
+                assert _eq(yp, _slices(ctx, c, x)), (prefix, rows)
+                rel = float(((yp.float() - ya.float()).abs().max() /
+                             ya.float().abs().max().clamp_min(1.0)).item())
+                assert rel <= 1e-2, (prefix, rows, rel)  # the stock path, another kernel
+    up = packed.leaf("model.layers.1.mlp.up_proj")
+    with pytest.raises(dflash_qmm.DfqError):            # fp16 scales take fp16 x
+        up(torch.zeros(2, 1024, dtype=torch.bfloat16, device="cuda"))
+    del a, p, up, leaf, plain, packed
+    import gc
+    gc.collect()
+    ck.close()
+
+
+def ctypes_size(ctx, N, K, bits, gs):
+    import ctypes
+    nb = ctypes.c_size_t()
+    assert ctx.lib.dfq_packed_bytes(N, K, bits, gs, ctypes.byref(nb)) == 0
+    return nb.value
+
+
+def test_small_m_layer_takes_a_packed_copy(ctx):
+    import torch
+    import dflash_qmm
+    c = make_case(8, 4096, 2048, bits=4, gs=64, seed=31, lbias=True)
+    x8, w, s, b, lb = upload(c)
+    stock = dflash_qmm.QuantizedLinear(ctx, w, s, b, lb, group_size=64, bits=4)
+    with pytest.raises(dflash_qmm.DfqError):
+        stock_h = dflash_qmm.SmallMQuantizedLinear.pack(stock)  # a stock layer has no copy
+        del stock_h
+    lay = dflash_qmm.SmallMQuantizedLinear(stock)
+    x1 = x8[:1].contiguous()
+    announce("small-M layer before the packed copy")
+    before8, before1 = lay(x8), lay(x1)
+    assert lay.packed is None
+    lay.pack()
+    lay.pack()                                           # a second call does nothing
+    addr = lay.packed
+    assert addr is not None and lay.packed == addr
+    announce("small-M layer over its packed copy")
+    after8, after1 = lay(x8), lay(x1)
+    torch.cuda.synchronize()
+    assert _eq(before8, after8) and lay.last_took_kernel is False   # rows=1: the stock path
+    assert _eq(before1, after1)
+    model = dflash_qmm.Model(layer=lay)                  # the model's handle shares the copy
+    assert model.leaf("layer").packed == addr
+    g32 = make_case(8, 4096, 512, bits=4, gs=32, seed=32)
+    _, w2, s2, b2, _ = upload(g32)
+    not_eligible = dflash_qmm.SmallMQuantizedLinear(
+        dflash_qmm.QuantizedLinear(ctx, w2, s2, b2, group_size=32, bits=4))
+    with pytest.raises(dflash_qmm.DfqError):
+        not_eligible.pack()
+    assert not_eligible.packed is None

@@ -14,7 +14,8 @@ Covered: every bits x group size x dtype in the 1..8-row form with 8-group chunk
 9..16-row form (mt16) and one-super-step chunks (c1), plus the narrow split (two k-blocks,
 one tile per workgroup, pair exchange), the aligned split (two k-blocks of whole tiles per
 workgroup), three k-blocks of whole tiles (chained pair exchange) and a reduce split
-(several k-blocks, second pass).
+(several k-blocks, second pass); and the same over the packed layout (dfq_pack_weights,
+dfq_qmm_packed) for every format at 1..8 and 9..16 rows and in each split.
 """
 import numpy as np
 import pytest
@@ -36,8 +37,9 @@ def chunk_k(bits, gs):
     return 8 * gs  # 8 groups: the chunk of the c8 kernels
 
 
-def run_one_hot(ctx, N, K, bits, gs, dt, M, positions, seed, expect_plan=None):
-    """y for one-hot rows at `positions` (M per call) against the exact dequant columns."""
+def run_one_hot(ctx, N, K, bits, gs, dt, M, positions, seed, expect_plan=None, packed=False):
+    """y for one-hot rows at `positions` (M per call) against the exact dequant columns;
+    with `packed`, through the packed layout."""
     import torch
     if expect_plan is not None:
         p = ctx.plan(M, N, K, bits, gs)
@@ -54,9 +56,14 @@ def run_one_hot(ctx, N, K, bits, gs, dt, M, positions, seed, expect_plan=None):
     x = torch.zeros(len(pos), K, dtype=tdt, device="cuda")
     x[torch.arange(len(pos), device="cuda"), torch.from_numpy(pos).cuda()] = 1.0
     y = torch.empty(len(pos), N, dtype=tdt, device="cuda")
-    announce(f"one-hot bits={bits} gs={gs} dt={dt} M={M} N={N} K={K} calls={calls}")
+    announce(f"one-hot bits={bits} gs={gs} dt={dt} M={M} N={N} K={K} calls={calls} "
+             f"packed={packed}")
+    pw = ctx.pack(wd, sd, bd, bits, gs) if packed else None
     for c in range(calls):
-        ctx.qmm(x[c * M:(c + 1) * M], wd, sd, bd, bits, gs, out=y[c * M:(c + 1) * M])
+        if packed:
+            ctx.qmm_packed(x[c * M:(c + 1) * M], pw, out=y[c * M:(c + 1) * M])
+        else:
+            ctx.qmm(x[c * M:(c + 1) * M], wd, sd, bd, bits, gs, out=y[c * M:(c + 1) * M])
     torch.cuda.synchronize()
     got = y.view(torch.int16).cpu().numpy().view(np.uint16)
     want = to_bits(deq[:, pos].T, dt)
@@ -136,3 +143,30 @@ def test_unpack_is_exact_in_the_three_block_aligned_split(ctx, bits, gs, dt, M):
            + list(range(31 * ck, 32 * ck)))
     run_one_hot(ctx, 48, K, bits, gs, dt, M, pos, seed=bits * 7000 + gs + dt,
                 expect_plan={"nkb": 3, "aligned": 1, "reduce": 0})
+
+
+@pytest.mark.parametrize("bits,gs,dt", FORMATS)
+@pytest.mark.parametrize("M", [8, 16])
+def test_unpack_is_exact_over_the_packed_layout(ctx, bits, gs, dt, M):
+    """The packed layout, 1..8 and 9..16 rows: every k of two chunks, ragged N."""
+    K = 2 * chunk_k(bits, gs)
+    run_one_hot(ctx, 40, K, bits, gs, dt, M, range(K), seed=bits * 7000 + gs + dt + M,
+                packed=True)
+
+
+@pytest.mark.parametrize("bits,gs,dt,M,N,chunks,plan", [
+    (4, 64, BF16, 8, 64, 8, {"nkb": 2, "reduce": 0, "nslot_kb": 1}),    # narrow
+    (8, 64, F16, 12, 256, 10, {"nkb": 2, "aligned": 1, "reduce": 0}),   # aligned
+    (4, 64, BF16, 8, 48, 64, {"reduce": 1}),                           # reduce
+])
+def test_unpack_is_exact_over_the_packed_layout_in_each_split(ctx, bits, gs, dt, M, N, chunks,
+                                                              plan):
+    """The packed layout in the narrow, aligned and reduce splits: every k of the first, a
+    middle and the last chunk."""
+    ck = chunk_k(bits, gs)
+    K = chunks * ck
+    mid = chunks // 2
+    pos = list(range(ck)) + list(range(mid * ck, (mid + 1) * ck)) + \
+        list(range((chunks - 1) * ck, chunks * ck))
+    run_one_hot(ctx, N, K, bits, gs, dt, M, pos, seed=bits * 8000 + gs + dt, expect_plan=plan,
+                packed=True)
