@@ -92,8 +92,9 @@ constexpr int kBlock = kThreads + 64 * kPublishers;  // + the publisher waves
  * N = 17408 18.62 against 18.84; one row and N = 7168 within noise; one row at N = K = 4096
  * (eight units a workgroup: the four waves with none fetch an unused unit, now ahead of the
  * staging waves' weights) 7.35 against 7.05. */
-constexpr int kStageThreads = 8 * 64;
-constexpr int kMaxStageItems = 96 * 64 / kStageThreads;  // 16-byte x chunks staged per thread
+constexpr int kStageThreads = DFQ_STAGE_THREADS;
+constexpr int kMaxStageItems = DFQ_STAGE_ITEMS;  // 16-byte x chunks staged per thread
+static_assert(kStageThreads == 8 * 64, "x is staged by the first eight waves");
 static_assert(kThreads >= kStageThreads, "the staging waves are streaming waves");
 
 /* The dynamic LDS block of a qmm_mt8 workgroup (its layout is fixed by the host plan). */
@@ -1035,38 +1036,32 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
     const int k0 = kbk.c0 * (CH * C::KSS);  // first k of this k-block
 
     /* ---- x staging loads go out first (their wait must not cover the weight prefetch).
-     * Item c (16 bytes, 8 elements) of the M x kr block goes to thread c % kStageThreads, so each
-     * load instruction reads 1 KB of consecutive x; rounds past the last item are skipped
-     * and lanes past it reload the last one. */
-    const int CPR = kr / 8;  // 16-byte chunks per row of the k-block
-    const int items = p.M * CPR;
+     * Row sr of the k-block's x goes to the TPR threads sr*TPR .. +TPR-1 (a multiple of GS/8,
+     * M*TPR <= kStageThreads): thread sr*TPR + sc takes the 16-byte chunks sc, sc + TPR,
+     * sc + 2 TPR, ... of the row, so an item's global and LDS addresses and its group-sum
+     * slot step by constants, and a group's GS/8 chunks sit in aligned neighbouring lanes.
+     * A thread's last item past the row's end reloads the row's last chunk (and stores the
+     * same value again); threads past row M stage nothing. */
+    const int CPR = kr / 8;                  // 16-byte chunks per row of the k-block
+    const int TPR = DFQ_STAGE_TPR(p.M, GS);  // wave-uniform
+    const int NI = (CPR + TPR - 1) / TPR;    // items per staging thread (the host plan
+                                             // keeps it within kMaxStageItems)
+    const int sr = tid / TPR;
+    const int sc = tid - sr * TPR;
+    const bool stager = tid < kStageThreads && sr < p.M;
     /* the k-block's x as a uniform base plus 32-bit per-lane offsets (24-bit multiplies:
      * staging is VALU-bound, so no 64-bit address arithmetic per item) */
     const uint8_t* xb = (const uint8_t*)p.x + (size_t)k0 * 2;
-    const uint32_t xrow = (uint32_t)p.K * 2u;
-    /* (row, chunk) of item tid + i * kStageThreads, stepped without a per-item division */
-    const int dr = kStageThreads / CPR, dcc = kStageThreads - dr * CPR;  // wave-uniform
-    uint32_t xo[kMaxStageItems];  // LDS offset of the item, (1 + row) * RS + chunk * 16
-    int xs[kMaxStageItems];       // its group-sum slot, or -1 past the last item
+    const uint32_t xrow_off = __umul24((uint32_t)sr, (uint32_t)p.K * 2u);
     u32x4_t xv[kMaxStageItems];
     auto stage_loads = [&]() {
-        if (tid >= kStageThreads) return;
-        int r = tid / CPR, cc = tid - r * CPR;
+        if (!stager) return;
 #pragma unroll
-        for (int i = 0; i < kMaxStageItems; ++i) {
-            const bool in = r < p.M;
-            const int rr = in ? r : p.M - 1, c2 = in ? cc : CPR - 1;
-            xo[i] = __umul24((uint32_t)(1 + rr), (uint32_t)p.lds_row_stride) + (uint32_t)c2 * 16u;
-            xs[i] = in ? (cc / (GS / 8)) * XR + r : -1;
-            if (i * kStageThreads < items)
-                xv[i] = *(const u32x4_t*)(xb + (__umul24((uint32_t)rr, xrow) + (uint32_t)c2 * 16u));
-            r += dr;
-            cc += dcc;
-            if (cc >= CPR) {
-                cc -= CPR;
-                ++r;
+        for (int i = 0; i < kMaxStageItems; ++i)
+            if (i < NI) {
+                const uint32_t c = (uint32_t)min(sc + i * TPR, CPR - 1);
+                xv[i] = *(const u32x4_t*)(xb + (xrow_off + c * 16u));
             }
-        }
         __builtin_amdgcn_sched_barrier(0);
     };
     /* x goes out before the split's scalar arithmetic, which overlaps its latency */
@@ -1158,22 +1153,26 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
     uint32_t* gcnt = tcnt + ntl;
     const int GK = kr / GS;  // groups in the k-block
     /* per item: pre-permute into the MFMA k order, and sum its 8 elements; the GS/8 items
-     * of a group sit in aligned neighbouring lanes (all real or all past the end, as CPR is
-     * a multiple of GS/8) and are summed with DPP.  Lanes past the last item rewrite the
-     * last item with its own value; only the group sums need a mask. */
+     * of a group sit in aligned neighbouring lanes of one row (all real or all past the
+     * row's end, as CPR and TPR are multiples of GS/8) and are summed with DPP; the group's
+     * first lane stores the sum. */
     const bool leader = (tid & (GS / 8 - 1)) == 0;
     auto stage_finish = [&]() {
+    if (stager) {
+        const uint32_t lrow = __umul24((uint32_t)(1 + sr), (uint32_t)p.lds_row_stride);
 #pragma unroll
-    for (int i = 0; i < kMaxStageItems; ++i) {
-        if (tid < kStageThreads && i * kStageThreads < items) {
-            float sm = chunk_dot<F16>(xv[i], 0.0f);
-            sm += dpp_f32<0xB1>(sm);             // lanes ^1 (quad_perm 1,0,3,2)
-            sm += dpp_f32<0x4E>(sm);             // lanes ^2 (quad_perm 2,3,0,1)
-            if constexpr (GS >= 64) sm += dpp_f32<0x104>(sm);   // + lane+4 (row_shl:4)
-            if constexpr (GS >= 128) sm += dpp_f32<0x108>(sm);  // + lane+8 (row_shl:8)
-            const u32x4_t v = (BITS == 4) ? nibble_permute(xv[i]) : xv[i];
-            *(u32x4_t*)(lds + xo[i]) = v;
-            if (leader && xs[i] >= 0) xsum[xs[i]] = sm;
+        for (int i = 0; i < kMaxStageItems; ++i) {
+            if (i < NI) {
+                const int c = sc + i * TPR;
+                float sm = chunk_dot<F16>(xv[i], 0.0f);
+                sm += dpp_f32<0xB1>(sm);             // lanes ^1 (quad_perm 1,0,3,2)
+                sm += dpp_f32<0x4E>(sm);             // lanes ^2 (quad_perm 2,3,0,1)
+                if constexpr (GS >= 64) sm += dpp_f32<0x104>(sm);   // + lane+4 (row_shl:4)
+                if constexpr (GS >= 128) sm += dpp_f32<0x108>(sm);  // + lane+8 (row_shl:8)
+                const u32x4_t v = (BITS == 4) ? nibble_permute(xv[i]) : xv[i];
+                *(u32x4_t*)(lds + lrow + (uint32_t)min(c, CPR - 1) * 16u) = v;
+                if (leader && c < CPR) xsum[(c / (GS / 8)) * XR + sr] = sm;
+            }
         }
     }
     for (int c = tid; c < CPR; c += kThreads) *(u32x4_t*)(lds + c * 16) = u32x4_t{0, 0, 0, 0};

@@ -54,7 +54,12 @@ constexpr int kThreads = kWaves * 64;             // qmm_mt8 streaming threads
 #define DFQ_PUBLISHERS 2               // must match the kernels' build
 #endif
 constexpr int kBlockThreads = kThreads + 64 * DFQ_PUBLISHERS;  // + the publisher waves
-constexpr int64_t kStageItems = 96 * 64;           // x items a workgroup stages (as the kernels)
+/* Whether the x of a k-block of kr elements at M rows fits the kernel's staging: each
+ * staging thread holds at most DFQ_STAGE_ITEMS 16-byte chunks of its row. */
+static bool stage_fits(int M, int kr, int gs) {
+    const int tpr = DFQ_STAGE_TPR(M, gs);
+    return tpr > 0 && (kr / 8 + tpr - 1) / tpr <= DFQ_STAGE_ITEMS;
+}
 
 struct PlanKey {
     int M, N, K, bits, gs;
@@ -217,7 +222,7 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
     auto split = [&](int d, int64_t G0, Plan* out) -> bool {
         const int ss_max = (chunks + d - 1) / d, ss_min = chunks / d;
         const int kr = ss_max * kch;
-        if ((int64_t)M * (kr / 8) > kStageItems) return false;
+        if (!stage_fits(M, kr, gs)) return false;
         Plan p{};
         p.kss = kss;
         p.mt = mt;
@@ -284,7 +289,7 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
         if (chunks < dd) return false;
         const int ss_max = (chunks + dd - 1) / dd;
         const int kr = ss_max * kch;
-        if ((int64_t)M * (kr / 8) > kStageItems) return false;
+        if (!stage_fits(M, kr, gs)) return false;
         const int64_t G = std::min<int64_t>(std::max<int64_t>(1, G0), T);
         const int64_t tmax = (T + G - 1) / G;
         Plan p{};
