@@ -57,6 +57,8 @@ private:
     int dev_ = -1;
 };
 int kss_for(int bits, int gs);
+/* Groups of a chunk of the c8 kernels (and of a unit of the packed layout). */
+int chunk_groups(int bits, int gs);
 bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_max, Plan* pl);
 /* The device address of the fixed scratch array (qmm_scratch.hip) on `device`, which must be
  * current; taken and cleared once per device. */

@@ -120,6 +120,10 @@ struct Cfg {
     static constexpr int NOPS = (BITS == 4) ? 4 * NS : 2 * NS;  // MFMA B operands
     static constexpr int NOW = (BITS == 4) ? NOPS : 2 * NOPS;   // operand words
     static constexpr int CPS = KSS / 8;       // 8-element chunks per super-step
+    /* groups of a unit of the packed layout, and of the chunks the 1..8-row kernels take
+     * where K allows: 8, one 16-byte scale load per lane; 16 for 4-bit group 32 (two loads,
+     * the c16 kernels), so that a unit holds 4 KB of codes as at group 64 rather than 2 KB */
+    static constexpr int CG = (BITS == 4 && GS == 32) ? 16 : 8;
 
     /* chunk index (within the super-step) read by lane group q for operand o is
      * base_chunk(q) + delta_chunk(o); the group (within the super-step) that lane group q
@@ -1008,7 +1012,9 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
     using C = Cfg<BITS, GS>;
     static_assert(!PK || CH > 1, "the packed layout holds 8-group chunks");
     constexpr int XR = 8 * MT;  // rows of x sums per group in LDS
-    static_assert(CH == 1 || CH * C::GPS == 8, "chunk = one super-step or 8 groups");
+    static_assert(CH == 1 || CH * C::GPS == 8 || CH * C::GPS == C::CG,
+                  "chunk = one super-step, 8 groups or CG groups");
+    constexpr int SB = (CH > 1) ? CH * C::GPS / 8 : 1;  // 16-byte scale (bias) loads a unit
     uint8_t* lds = lds_base();
 
     const int tid = threadIdx.x;
@@ -1087,7 +1093,7 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
     const uint32_t lane_s = (CH > 1) ? 0u : (C::GPS == 4 ? 4u * (q >> 1) : 0u);
     using SV = typename std::conditional<(CH > 1), u32x4_t, uint32_t>::type;
     u32x4_t rw[PF][CH][C::NS];
-    SV rsb[PF];  // scale words (lane rows 0, 2) or bias words (rows 1, 3) of the slot's unit
+    SV rsb[PF][SB];  // scale words (lane rows 0, 2) or bias words (rows 1, 3) of the slot's unit
     int sg[PF];  // the unit (as a take index) each slot holds; >= L: none
     const uint8_t* wbytes = (const uint8_t*)p.w;
     const uint8_t* sbytes = (const uint8_t*)p.scales;
@@ -1109,19 +1115,30 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
         const uint32_t vw = (uint32_t)rl * RB + lane_w;
         const uint32_t vs = (uint32_t)rl * GPR * 2u + lane_s;
         if constexpr (PK) {
-            /* the packed unit: its codes as CH * NS pieces of 1 KB (this lane's 16 bytes of
-             * piece i at i * 1024 + lane * 16), then 512 bytes of its rows' scales and biases
-             * (this lane's at ((q & 1) * 16 + n) * 16); past row N the pack holds zeros */
-            constexpr uint32_t kCodeBytes = 16u * CH * C::KSS * BITS / 8u;
-            const uint8_t* ub =
-                wbytes + ((size_t)t * p.chunks + kbk.c0 + c) * (kCodeBytes + 512u);
-            rsb[slot] = *(const SV*)(ub + kCodeBytes + (uint32_t)((q & 1) * 16 + n) * 16u);
+            /* the packed unit of CG groups, which holds RH of this kernel's chunks (part hh
+             * of it is this chunk): its codes as pieces of 1 KB (this lane's 16 bytes of piece
+             * i at i * 1024 + lane * 16; the chunk's pieces from hh * CH * NS), then its rows'
+             * scales and biases, 16 * PSB bytes a row (this lane's h-th 16 bytes of the chunk
+             * at (q & 1) * 256 PSB + n * 16 PSB + 16 (hh SB + h)); past row N the pack holds
+             * zeros */
+            constexpr int RH = C::CG / (CH * C::GPS);
+            constexpr int PSB = C::CG / 8;
+            constexpr uint32_t kCodeBytes = 16u * C::CG * GS * BITS / 8u;
+            const int kc = kbk.c0 + c;
+            const int hh = kc % RH;
+            const uint8_t* ub = wbytes + ((size_t)t * (p.chunks / RH) + kc / RH) *
+                                             (kCodeBytes + 512u * PSB);
+#pragma unroll
+            for (int h = 0; h < SB; ++h)
+                rsb[slot][h] = *(const SV*)(ub + kCodeBytes +
+                                            (uint32_t)((q & 1) * 256 * PSB + n * 16 * PSB +
+                                                       16 * (hh * SB + h)));
 #pragma unroll
             for (int j = 0; j < CH; ++j)
 #pragma unroll
                 for (int s = 0; s < C::NS; ++s)
-                    rw[slot][j][s] =
-                        *(const u32x4_t*)(ub + (j * C::NS + s) * 1024 + (uint32_t)lane * 16u);
+                    rw[slot][j][s] = *(const u32x4_t*)(ub + (hh * CH * C::NS + j * C::NS + s) * 1024 +
+                                                       (uint32_t)lane * 16u);
             return;
         }
         const uint8_t* sbb = (q & 1) ? bbytes : sbytes;
@@ -1129,7 +1146,8 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
         const uint8_t* wb = wbytes + (size_t)row0 * RB + kc * BITS / 8;
         const size_t so = ((size_t)row0 * GPR + kc / GS) * 2;
         /* scales / biases first: they are split (a cross-lane swap) before the first MFMA */
-        rsb[slot] = *(const SV*)(sbb + so + vs);
+#pragma unroll
+        for (int h = 0; h < SB; ++h) rsb[slot][h] = *(const SV*)(sbb + so + vs + 16u * h);
 #pragma unroll
         for (int j = 0; j < CH; ++j)
 #pragma unroll
@@ -1231,14 +1249,25 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
     auto process = [&](const int i, const int g) {
         const int u = unit_of(g);
         const int t = u / SS, cc = u - t * SS;
+        /* The scale (bias) words of the super-steps in hand: load h serves super-steps
+         * [h * JPH, (h + 1) * JPH) and is split as the first of them begins, so that only one
+         * load's words are live at a time.  Word w of the chunk covers its groups 2w, 2w + 1. */
+        constexpr int JPH = CH / SB;
         SV rs_i, rb_i;
-        split_scale_bias(rsb[i], rs_i, rb_i);
+        auto sw_of = [&](const SV& a, int w) -> uint32_t {
+            if constexpr (CH > 1) return a[w & 3];
+            else return a;
+        };
+        auto split_for = [&](int j) {
+            if (j % JPH == 0) split_scale_bias(rsb[i][j / JPH], rs_i, rb_i);
+        };
         f32x4_t v;  // lanes 0-31: rows 0-7 (MT 1); all lanes: rows 4q..4q+3 (MT 2)
         if constexpr (MT == 1) {
             f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int j = 0; j < CH; ++j) {
                 const int css = cc * CH + j;  // super-step within the k-block
+                split_for(j);
                 uint32_t OW[C::NOW];
                 build_operand_words<BITS, GS>(rw[i][j], OW);
                 const uint32_t aoff = abase + (uint32_t)css * (C::CPS * 16);
@@ -1259,12 +1288,12 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
                     uint32_t sw, bw2, sel;
                     if constexpr (CH > 1) {
                         if constexpr (C::GPS == 4) {
-                            sw = (q >> 1) ? rs_i[2 * j + 1] : rs_i[2 * j];
-                            bw2 = (q >> 1) ? rb_i[2 * j + 1] : rb_i[2 * j];
+                            sw = (q >> 1) ? sw_of(rs_i, 2 * j + 1) : sw_of(rs_i, 2 * j);
+                            bw2 = (q >> 1) ? sw_of(rb_i, 2 * j + 1) : sw_of(rb_i, 2 * j);
                             sel = pp ? kSelHi : kSelLo;
                         } else {
-                            sw = rs_i[j];
-                            bw2 = rb_i[j];
+                            sw = sw_of(rs_i, j);
+                            bw2 = sw_of(rb_i, j);
                             sel = sel_half;
                         }
                     } else {
@@ -1297,6 +1326,7 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
 #pragma unroll
             for (int j = 0; j < CH; ++j) {
                 const int css = cc * CH + j;
+                split_for(j);
                 uint32_t OW[C::NOW];
                 build_operand_words_wide<BITS, GS>(rw[i][j], OW);
                 f32x4_t P[C::GPS];  // one partial per group of the super-step
@@ -1319,8 +1349,8 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
                 for (int gg = 0; gg < C::GPS; ++gg) {
                     const int gi = j * C::GPS + gg;  // group within the chunk
                     const uint32_t sel = (gi & 1) ? kSelHi : kSelLo;
-                    const float s = half_sel<F16>(rs_i[gi >> 1], sel);
-                    const float bb = half_sel<F16>(rb_i[gi >> 1], sel);
+                    const float s = half_sel<F16>(sw_of(rs_i, gi >> 1), sel);
+                    const float bb = half_sel<F16>(sw_of(rb_i, gi >> 1), sel);
                     const float bp = (kOff != 0.0f) ? __builtin_fmaf(-kOff, s, bb) : bb;
                     const f32x4_t X = *(const f32x4_t*)(lds + xo + gg * (XR * 4));
 #pragma unroll
@@ -1692,19 +1722,21 @@ extern "C" __global__ void __launch_bounds__(64) dfq_qmm_generic(QmmGenericParam
     }
 }
 
-/* The packed layout of a 4/8-bit weight with its scales and biases, for 8-group chunks:
- * unit (t, c) -- 16 rows of tile t, chunk c of K (8 groups) -- at (t * chunks + c) * ub
- * bytes, ub = cb + 512.  Its codes are cb / 1024 pieces of 1 KB: byte 16 * l of piece i holds
- * the 16 bytes lane l = 16 q + n loads for piece i from the MLX layout (row 16 t + n, bytes
- * 64 i + 16 q of the chunk's codes).  Then 512 bytes: for qq = 0 (scales) and 1 (biases) and
- * each row n, the 8 groups' 16 bytes at (16 qq + n) * 16.  Rows past N are zeros.  One thread
- * per 16-byte piece; a pure byte permutation of the MLX arrays. */
+/* The packed layout of a 4/8-bit weight with its scales and biases, for the c8 kernels'
+ * chunks of cg groups (8; 16 at 4-bit group 32), sb = cg / 8: unit (t, c) -- 16 rows of
+ * tile t, chunk c of K -- at (t * chunks + c) * ub bytes, ub = cb + 512 sb.  Its codes are
+ * cb / 1024 pieces of 1 KB: byte 16 * l of piece i holds the 16 bytes lane l = 16 q + n loads
+ * for piece i from the MLX layout (row 16 t + n, bytes 64 i + 16 q of the chunk's codes).
+ * Then 512 sb bytes: for qq = 0 (scales) and 1 (biases) and each row n, the chunk's groups
+ * (16 sb bytes) at (16 qq + n) * 16 sb.  Rows past N are zeros.  One thread per 16-byte
+ * piece; a pure byte permutation of the MLX arrays. */
 extern "C" __global__ void __launch_bounds__(256) dfq_pack_weights(
     const uint8_t* w, const uint8_t* scales, const uint8_t* biases, uint8_t* packed, int N,
     int K, int bits, int gs, uint64_t pieces) {
-    const uint32_t chunk_k = 8u * (uint32_t)gs;            // k of a chunk (8 groups)
+    const uint32_t sbu = (bits == 4 && gs == 32) ? 2u : 1u;  // 16-byte scale pieces a row
+    const uint32_t chunk_k = 8u * sbu * (uint32_t)gs;      // k of a chunk
     const uint32_t cb = 16u * chunk_k * (uint32_t)bits / 8u;  // code bytes of a unit
-    const uint32_t ppu = (cb + 512u) / 16u;                // 16-byte pieces of a unit
+    const uint32_t ppu = (cb + 512u * sbu) / 16u;          // 16-byte pieces of a unit
     const uint32_t chunks = (uint32_t)K / chunk_k;
     const size_t rb = (size_t)K * bits / 8;                // bytes per weight row
     const size_t sb = (size_t)(K / gs) * 2;                // bytes per scale row
@@ -1721,10 +1753,12 @@ extern "C" __global__ void __launch_bounds__(256) dfq_pack_weights(
                 v = *(const u32x4_t*)(w + row * rb + (size_t)c * chunk_k * bits / 8 +
                                       piece * 64u + q * 16u);
         } else {
-            const uint32_t k = r - cb / 16u, qq = k >> 4, n = k & 15u;
+            const uint32_t k = r - cb / 16u, qq = k / (16u * sbu), rem = k - qq * 16u * sbu;
+            const uint32_t n = rem / sbu, h = rem - n * sbu;
             const uint32_t row = t * 16u + n;
             if ((int)row < N)
-                v = *(const u32x4_t*)((qq ? biases : scales) + row * sb + (size_t)c * 16u);
+                v = *(const u32x4_t*)((qq ? biases : scales) + row * sb +
+                                      ((size_t)c * sbu + h) * 16u);
         }
         *(u32x4_t*)(packed + i * 16u) = v;
     }
@@ -2018,7 +2052,9 @@ constexpr int prefetch_depth() {
     }
 /* per format: one super-step or 8-group chunks at up to 8 rows; 8-group chunks at up to 16;
  * the greedy-accept forms (_am) of the 8-group-chunk kernels; and all of the 8-group-chunk
- * kernels again over the packed layout (_pk) */
+ * kernels again over the packed layout (_pk).  4-bit group 32 also has 16-group chunks at up
+ * to 8 rows (c16, in every form); at 16 rows they would need more than the 128 VGPRs a
+ * 14-wave workgroup allows (about 90 spilled), so 9..16 rows keep 8-group chunks. */
 #define DFQ_MT8_FORMAT(BITS, GS, F16, NAME)                                                    \
     DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c1, 1, mt8, 1, false, false, )                        \
     DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt8, 1, false, false, ) \
@@ -2034,6 +2070,14 @@ constexpr int prefetch_depth() {
     DFQ_MT8_KERNEL(BITS, GS, F16, NAME, c8, (8 / Cfg<BITS, GS>::GPS), mt16, 2, true, true,     \
                    _am_pk)
 
+#define DFQ_MT8_C16(F16, NAME)                                                                 \
+    DFQ_MT8_KERNEL(4, 32, F16, NAME, c16, 4, mt8, 1, false, false, )                          \
+    DFQ_MT8_KERNEL(4, 32, F16, NAME, c16, 4, mt8, 1, true, false, _am)                        \
+    DFQ_MT8_KERNEL(4, 32, F16, NAME, c16, 4, mt8, 1, false, true, _pk)                        \
+    DFQ_MT8_KERNEL(4, 32, F16, NAME, c16, 4, mt8, 1, true, true, _am_pk)
+
+DFQ_MT8_C16(false, bf16)
+DFQ_MT8_C16(true, f16)
 DFQ_MT8_FORMAT(4, 32, false, bf16)
 DFQ_MT8_FORMAT(4, 64, false, bf16)
 DFQ_MT8_FORMAT(4, 128, false, bf16)

@@ -90,6 +90,8 @@ struct dfq_ctx {
     hipFunction_t am[2][3][2][2] = {};   // greedy-accept forms, 8-group chunks [..][rows 8/16]
     hipFunction_t pk[2][3][2][2] = {};   // over the packed layout [bits][gs][dt][rows 8/16]
     hipFunction_t pk_am[2][3][2][2] = {};  // greedy-accept forms over the packed layout
+    /* 4-bit group 32, 16-group chunks at up to 8 rows [bf16/f16][plain, _am, _pk, _am_pk] */
+    hipFunction_t c16[2][4] = {};
     hipFunction_t pack = nullptr;        // MLX arrays -> the packed layout
     hipFunction_t reduce[2] = {};        // second pass of reduce splits [bf16/f16]
     hipFunction_t silu_mul[2] = {};      // SiLU-mul of a fused gate||up output [bf16/f16]
@@ -161,6 +163,13 @@ DeviceScope::~DeviceScope() {
     if (prev_ >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev_) (void)hipSetDevice(prev_);
 }
 
+/* Groups of a unit of the packed layout, and of the chunks the 1..8-row kernels prefer: 8
+ * (one 16-byte scale load per lane); 16 at 4-bit group 32, whose 8-group chunk holds only
+ * 2 KB of codes a unit and pays the per-unit costs twice as often as group 64.  Measured on
+ * MI355X, M = 8 (us, 16-group chunks against 8, same box): N = 17408, K = 5120 17.1 against
+ * 19.0; one row 16.3 against 18.0; N = 7168 11.9 against 12.9; N = 5120 10.6 against 10.9. */
+int chunk_groups(int bits, int gs) { return (bits == 4 && gs == 32) ? 16 : 8; }
+
 int kss_for(int bits, int gs) {
     const int kstep = 512 / bits;
     const int ns = bits == 4 ? (gs == 128 ? 2 : 1) : gs / 32;
@@ -205,11 +214,15 @@ static constexpr int kAlignedMaxTiles = 12;
 bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_max, Plan* pl) {
     const int kss = kss_for(bits, gs);
     if (M < 1 || M > 16 || N < 1 || K < kss || K % kss) return false;
-    /* A chunk of 8 groups lets each lane fetch its row's scales with one 16-byte load. */
+    /* A chunk of 8 groups lets each lane fetch its row's scales with one 16-byte load; up to
+     * 8 rows, 4-bit group 32 takes 16 groups (two loads) where K allows. */
     const int gps = kss / gs;
-    const int ch = (K % (kss * (8 / gps)) == 0) ? 8 / gps : 1;
-    /* 9..16 rows: two row tiles per weight tile, built for 8-group chunks only */
     const int mt = M > 8 ? 2 : 1;
+    const int cg = mt == 1 ? chunk_groups(bits, gs) : 8;
+    const int ch = (K % (kss * (cg / gps)) == 0)  ? cg / gps
+                   : (K % (kss * (8 / gps)) == 0) ? 8 / gps
+                                                  : 1;
+    /* 9..16 rows: two row tiles per weight tile, built for 8-group chunks only */
     if (mt == 2 && ch == 1) return false;
     const int kch = kss * ch;
     const int chunks = K / kch;
@@ -515,6 +528,17 @@ dfq_status dfq_init(int device, dfq_ctx** out) {
                         }
                     }
                 }
+    for (int d = 0; d < 2; ++d)
+        for (int f = 0; f < 4; ++f) {
+            static const char* kSfx[4] = {"", "_am", "_pk", "_am_pk"};
+            char name[64];
+            snprintf(name, sizeof name, "dfq_qmm_mt8_b4_g32_%s_c16%s", kDt[d], kSfx[f]);
+            if ((e = hipModuleGetFunction(&ctx->c16[d][f], ctx->module, name)) != hipSuccess) {
+                (void)hipModuleUnload(ctx->module);
+                delete ctx;
+                return hip_fail(e, name);
+            }
+        }
     if ((e = hipModuleGetFunction(&ctx->generic, ctx->module, "dfq_qmm_generic")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->reduce[0], ctx->module, "dfq_qmm_reduce_bf16")) != hipSuccess ||
         (e = hipModuleGetFunction(&ctx->reduce[1], ctx->module, "dfq_qmm_reduce_f16")) != hipSuccess ||
@@ -738,10 +762,10 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
     Plan pl;
     dfq_status s = get_plan(ctx, M, N, K, bits, gs, &pl, cache);
     if (s) return s;
-    if (packed && pl.ch == 1)
+    if (packed && (pl.ch == 1 || K % (chunk_groups(bits, gs) * gs)))
         return fail(DFQ_ERR_UNSUPPORTED,
-                    "the packed layout holds chunks of 8 groups: K=%d is not a multiple of %d", K,
-                    8 * gs);
+                    "the packed layout holds chunks of %d groups: K=%d is not a multiple of %d",
+                    chunk_groups(bits, gs), K, chunk_groups(bits, gs) * gs);
     if (acc && (pl.reduce || epi || pl.ch == 1))
         return fail(DFQ_ERR_STATE,
                     "greedy-accept mode needs 8-group chunks and a split without a second pass");
@@ -765,9 +789,11 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
     const int di = dt == DFQ_BF16 ? 0 : 1;
     void* args[] = {&p};
     const int ci = pl.ch > 1 ? 1 : 0;
-    hipFunction_t fn = packed ? (acc ? ctx->pk_am[bi][gi][di][pl.mt - 1]
-                                     : ctx->pk[bi][gi][di][pl.mt - 1])
-                       : acc           ? ctx->am[bi][gi][di][pl.mt - 1]
+    const bool c16 = pl.ch * (pl.kss / gs) == 16;  // 4-bit group 32, up to 8 rows
+    hipFunction_t fn = c16      ? ctx->c16[di][(acc ? 1 : 0) + (packed ? 2 : 0)]
+                       : packed ? (acc ? ctx->pk_am[bi][gi][di][pl.mt - 1]
+                                       : ctx->pk[bi][gi][di][pl.mt - 1])
+                       : acc        ? ctx->am[bi][gi][di][pl.mt - 1]
                        : pl.mt == 2 ? ctx->mt16[bi][gi][di]
                                     : ctx->mt8[bi][gi][di][ci];
     hipError_t e = hipModuleLaunchKernel(fn, (unsigned)(pl.nkb * pl.Gkb), 1, 1, kBlockThreads, 1,
@@ -841,12 +867,13 @@ dfq_status dfq_packed_bytes(int N, int K, int bits, int gs, size_t* bytes) {
     if (bits != 4 && bits != 8) return fail(DFQ_ERR_UNSUPPORTED, "bits must be 4 or 8");
     if (gs != 32 && gs != 64 && gs != 128)
         return fail(DFQ_ERR_UNSUPPORTED, "group size must be 32, 64 or 128");
-    if (K % (8 * gs))
+    const int cg = chunk_groups(bits, gs);
+    if (K % (cg * gs))
         return fail(DFQ_ERR_UNSUPPORTED,
-                    "the packed layout holds chunks of 8 groups: K=%d is not a multiple of %d", K,
-                    8 * gs);
-    const size_t unit = (size_t)16 * 8 * gs * bits / 8 + 512;
-    *bytes = (size_t)((N + 15) / 16) * (K / (8 * gs)) * unit;
+                    "the packed layout holds chunks of %d groups: K=%d is not a multiple of %d",
+                    cg, K, cg * gs);
+    const size_t unit = (size_t)16 * cg * gs * bits / 8 + 512 * (cg / 8);
+    *bytes = (size_t)((N + 15) / 16) * (K / (cg * gs)) * unit;
     return DFQ_OK;
 }
 
@@ -936,8 +963,8 @@ static dfq_status qmm_any(dfq_ctx* ctx, const void* x, const uint32_t* w, const 
                           (hipStream_t)stream, epi, cache, nullptr, packed);
     if (packed)
         return fail(DFQ_ERR_UNSUPPORTED,
-                    "the packed layout holds chunks of 8 groups: K=%d is not a multiple of %d", K,
-                    8 * gs);
+                    "the packed layout holds chunks of %d groups: K=%d is not a multiple of %d",
+                    chunk_groups(bits, gs), K, chunk_groups(bits, gs) * gs);
     /* 9..16 rows with one-super-step chunks: two passes of up to 8 rows over the weights. */
     const size_t ypitch = (size_t)(epi ? N / 2 : N) * esz;
     for (int m0 = 0; m0 < M; m0 += 8) {

@@ -19,11 +19,12 @@ pytestmark = pytest.mark.gpu
 
 
 def pack_reference(w_words, s_bits, b_bits, N, K, bits, gs):
-    """The packed layout on the CPU: unit (t, c) of 16 rows x 8 groups at (t*chunks + c) *
-    ub; piece i of its codes holds, at 16 * (16 q + n), bytes 64 i + 16 q of the chunk's codes
-    of row 16 t + n; then scales (qq = 0) and biases (qq = 1) of row n at (16 qq + n) * 16;
-    rows past N zero."""
-    ck = 8 * gs
+    """The packed layout on the CPU: unit (t, c) of 16 rows x cg groups (8; 16 at 4-bit group
+    32) at (t*chunks + c) * ub; piece i of its codes holds, at 16 * (16 q + n), bytes
+    64 i + 16 q of the chunk's codes of row 16 t + n; then scales (qq = 0) and biases (qq = 1)
+    of row n, 2 cg bytes, at (16 qq + n) * 2 cg; rows past N zero."""
+    cg = 16 if (bits, gs) == (4, 32) else 8
+    ck = cg * gs
     cb = 16 * ck * bits // 8
     chunks, T = K // ck, -(-N // 16)
     wb = np.zeros((T * 16, K * bits // 8), dtype=np.uint8)
@@ -32,20 +33,21 @@ def pack_reference(w_words, s_bits, b_bits, N, K, bits, gs):
     bb = np.zeros_like(sb)
     sb[:N] = np.ascontiguousarray(s_bits).view(np.uint8).reshape(N, -1)
     bb[:N] = np.ascontiguousarray(b_bits).view(np.uint8).reshape(N, -1)
-    out = np.zeros((T, chunks, cb + 512), dtype=np.uint8)
+    out = np.zeros((T, chunks, cb + 64 * cg), dtype=np.uint8)
     for t in range(T):
         rows = slice(16 * t, 16 * t + 16)
         for c in range(chunks):
             codes = wb[rows, c * cb // 16:(c + 1) * cb // 16]          # [16 n][cb/16]
             pieces = codes.reshape(16, cb // 1024, 4, 16)               # [n][i][q][16]
             out[t, c, :cb] = pieces.transpose(1, 2, 0, 3).reshape(-1)   # [i][q][n][16]
-            out[t, c, cb:cb + 256] = sb[rows, c * 16:(c + 1) * 16].reshape(-1)
-            out[t, c, cb + 256:] = bb[rows, c * 16:(c + 1) * 16].reshape(-1)
+            sbytes = 2 * cg                                             # a row's scales
+            out[t, c, cb:cb + 16 * sbytes] = sb[rows, c * sbytes:(c + 1) * sbytes].reshape(-1)
+            out[t, c, cb + 16 * sbytes:] = bb[rows, c * sbytes:(c + 1) * sbytes].reshape(-1)
     return out.reshape(-1)
 
 
 @pytest.mark.parametrize("N,K,bits,gs,dt", [(40, 512, 4, 64, BF16), (33, 1024, 8, 64, F16),
-                                            (16, 256, 4, 32, BF16), (50, 2048, 4, 128, F16),
+                                            (16, 512, 4, 32, BF16), (50, 2048, 4, 128, F16),
                                             (17, 1024, 8, 128, BF16), (100, 768, 8, 32, BF16)])
 def test_pack_matches_the_layout(ctx, N, K, bits, gs, dt):
     import torch
@@ -138,6 +140,9 @@ def test_packed_refuses_k_without_whole_chunks(ctx):
     assert ctx.lib.dfq_packed_bytes(64, 640, 4, 64, ctypes.byref(nb)) != 0 and nb.value == 0
     assert ctx.lib.dfq_packed_bytes(64, 1024, 4, 64, ctypes.byref(nb)) == 0
     assert nb.value == 4 * 2 * (4096 + 512)
+    assert ctx.lib.dfq_packed_bytes(64, 256, 4, 32, ctypes.byref(nb)) != 0   # 16 groups a chunk
+    assert ctx.lib.dfq_packed_bytes(64, 1024, 4, 32, ctypes.byref(nb)) == 0
+    assert nb.value == 4 * 2 * (4096 + 1024)
 
 
 # ---- the drop-in layer over the packed layout ------------------------------------------------
@@ -192,7 +197,8 @@ def test_checkpoint_loads_packed_and_matches_the_mlx_layout(ctx, tmp_path):
     plain = ck.load_model(ctx)
     packed = ck.load_model(ctx, packed=True)
     assert len(plain) == len(packed) == len(CK_LAYERS)
-    packs = {p for (p, N, K, bits, gs, lb, sdt) in CK_LAYERS if K % (8 * gs) == 0}
+    packs = {p for (p, N, K, bits, gs, lb, sdt) in CK_LAYERS
+             if K % ((16 if (bits, gs) == (4, 32) else 8) * gs) == 0}
     for (prefix, N, K, bits, gs, lb, sdt) in CK_LAYERS:
         leaf = packed.leaf(prefix)
         assert (leaf.packed is not None) == (prefix in packs), prefix

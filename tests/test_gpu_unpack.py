@@ -33,8 +33,14 @@ def kss(bits, gs):
     return (512 // bits) * ((2 if gs == 128 else 1) if bits == 4 else gs // 32)
 
 
-def chunk_k(bits, gs):
-    return 8 * gs  # 8 groups: the chunk of the c8 kernels
+def chunk_groups(bits, gs, M=8):
+    """Groups of the chunks the planner picks where K allows: 8; 16 for 4-bit group 32 at up
+    to 8 rows (the c16 kernels)."""
+    return 16 if (bits, gs) == (4, 32) and M <= 8 else 8
+
+
+def chunk_k(bits, gs, M=8):
+    return chunk_groups(bits, gs, M) * gs
 
 
 def run_one_hot(ctx, N, K, bits, gs, dt, M, positions, seed, expect_plan=None, packed=False):
@@ -78,20 +84,28 @@ def test_unpack_is_exact_up_to_8_rows(ctx, bits, gs, dt):
     """1..8 rows, 8-group chunks: every k of two chunks, ragged N (a partial last tile)."""
     K = 2 * chunk_k(bits, gs)
     run_one_hot(ctx, 40, K, bits, gs, dt, 8, range(K), seed=bits * 1000 + gs + dt,
-                expect_plan={"ch": 8 * gs // kss(bits, gs), "nkb": 1})
+                expect_plan={"ch": chunk_k(bits, gs) // kss(bits, gs), "nkb": 1})
 
 
 @pytest.mark.parametrize("bits,gs,dt", FORMATS)
 def test_unpack_is_exact_for_16_rows(ctx, bits, gs, dt):
     """9..16 rows in one launch (two row tiles per weight tile): every k of one chunk."""
-    K = chunk_k(bits, gs)
+    K = chunk_k(bits, gs, 16)
     run_one_hot(ctx, 48, K, bits, gs, dt, 16, range(K), seed=bits * 2000 + gs + dt,
-                expect_plan={"ch": 8 * gs // kss(bits, gs)})
+                expect_plan={"ch": chunk_k(bits, gs, 16) // kss(bits, gs)})
+
+
+@pytest.mark.parametrize("dt", [BF16, F16])
+def test_unpack_is_exact_with_8_group_chunks_at_4bit_group_32(ctx, dt):
+    """4-bit group 32 with K a multiple of 8 groups but not of 16 (K = 768): the 1..8-row
+    kernels take 8-group chunks there; every k."""
+    run_one_hot(ctx, 40, 768, 4, 32, dt, 8, range(768), seed=9100 + dt,
+                expect_plan={"ch": 2})
 
 
 @pytest.mark.parametrize("bits,gs,dt", FORMATS)
 def test_unpack_is_exact_with_one_super_step_chunks(ctx, bits, gs, dt):
-    """K not a multiple of 8 groups: one-super-step chunks (c1), every k."""
+    """K not a multiple of a chunk: one-super-step chunks (c1), every k."""
     K = 3 * kss(bits, gs)
     if K % chunk_k(bits, gs) == 0:
         K += kss(bits, gs)
@@ -158,6 +172,9 @@ def test_unpack_is_exact_over_the_packed_layout(ctx, bits, gs, dt, M):
     (4, 64, BF16, 8, 64, 8, {"nkb": 2, "reduce": 0, "nslot_kb": 1}),    # narrow
     (8, 64, F16, 12, 256, 10, {"nkb": 2, "aligned": 1, "reduce": 0}),   # aligned
     (4, 64, BF16, 8, 48, 64, {"reduce": 1}),                           # reduce
+    # 4-bit group 32 at 16 rows: 8-group chunks over 16-group packed units, six k-blocks,
+    # two of which start half way into a unit
+    (4, 32, F16, 16, 48, 34, {"reduce": 1, "nkb": 6, "ch": 2}),
 ])
 def test_unpack_is_exact_over_the_packed_layout_in_each_split(ctx, bits, gs, dt, M, N, chunks,
                                                               plan):

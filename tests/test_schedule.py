@@ -184,7 +184,7 @@ def _unpack_test_shapes():
     for bits in (4, 8):
         for gs in (32, 64, 128):
             kss = (512 // bits) * ((2 if gs == 128 else 1) if bits == 4 else gs // 32)
-            ck = 8 * gs
+            ck = (16 if (bits, gs) == (4, 32) else 8) * gs   # the c8 kernels' chunk
             k1 = 3 * kss + (kss if (3 * kss) % ck == 0 else 0)
             out += [(8, 40, 2 * ck, bits, gs), (16, 48, ck, bits, gs), (7, 24, k1, bits, gs)]
     out += [(M, 64, 64 * gs, bits, gs) for (bits, gs, M) in
