@@ -679,6 +679,10 @@ def main():
                     default=None,
                     help="only time this form of the 64-layer verify forward (for profiling) "
                          "and print its figures")
+    ap.add_argument("--shape", metavar="M,N,K,BITS,GS[,f16]", default=None,
+                    help="time only this call, rotated over enough weight sets to exceed the "
+                         "Infinity Cache and replayed like the headline, print its figures and "
+                         "exit (with --profile-timed, for a kernel trace of one shape)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run 20 plain device copies of this many MiB (the reference "
                          "point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -722,6 +726,30 @@ def main():
         print(json.dumps({"copy_bytes_per_launch": n, "launches": 20}), flush=True)
         return
     ctx = dflash_qmm.Context(0)
+    if args.shape:
+        parts = args.shape.split(",")
+        M, N, K, bits, gs = (int(v) for v in parts[:5])
+        f16 = len(parts) > 5 and parts[5] == "f16"
+        nsets = max(2, -(-400_000_000 // algorithmic_bytes(0, N, K, bits, gs)))
+        sets = make_sets(torch, nsets, N, K, bits, gs, dev, seed=3,
+                         dtype=torch.float16 if f16 else torch.bfloat16,
+                         scale_sd=0.02 if bits == 4 else 0.004)
+        wsb = ctx.workspace_bytes(M, N, K, bits, gs)
+        ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
+        stream = torch.cuda.Stream(device=dev)
+        d = stats(time_m(torch, ctx, stream, sets, M, args.steps, args.warmup, N, K, bits, gs,
+                         ws, ws.numel(), f16=f16))
+        nb = algorithmic_bytes(M, N, K, bits, gs)
+        print(json.dumps({"shape": {"M": M, "N": N, "K": K, "bits": bits, "group_size": gs,
+                                    "dtype": "f16" if f16 else "bf16"},
+                          "us_per_call": round(d["median"], 3), "p10": round(d["p10"], 3),
+                          "p90": round(d["p90"], 3), "replays": d["replays"],
+                          "bytes": nb, "gbs": round(nb / (d["median"] * 1e-6) / 1e9, 1),
+                          "frac": round(nb / (d["median"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                          "rotated_sets": nsets, **rotation(nsets, args.steps,
+                                                            set_bytes_of(sets))}), flush=True)
+        ctx.close()
+        return
     if args.c5_only:
         fused = args.c5_only.startswith("fused")
         form = {"separate": "per_layer", "fused": "per_layer", "fused_composed": "composed",

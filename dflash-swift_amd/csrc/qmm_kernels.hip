@@ -406,6 +406,31 @@ __device__ __forceinline__ u32x4_t nibble_permute(u32x4_t v) {
     return o;
 }
 
+#ifndef DFQ_XCD_ORDER
+#define DFQ_XCD_ORDER 1
+#endif
+/* The range a workgroup takes.  Workgroup b of a launch runs on XCD b % 8 (MI355X deals
+ * workgroups to its eight XCDs round-robin), and each XCD has its own L2.  Neighbouring ranges
+ * share a tile, and with it the cache lines of that tile's scales and biases (and, in the MLX
+ * layout, of its rows' codes at the chunk boundary); so XCD x takes one contiguous block of
+ * ranges -- blocks of G / 8, the first G % 8 XCDs one more -- and a line two neighbours share
+ * is fetched from HBM once, into one L2. */
+__device__ __forceinline__ int xcd_order(int b, int G) {
+    if (!DFQ_XCD_ORDER) return b;
+    const int per = G >> 3, rem = G & 7, x = b & 7;
+    return x * per + min(x, rem) + (b >> 3);
+}
+
+/* With p.xcd_pair (Gkb a multiple of 8): the i-th workgroup of XCD x takes range
+ * x * Gkb / 8 + i / nkb of k-block i % nkb, so that the nkb parts of a tile (the same range
+ * index in every k-block) run on one XCD. */
+__device__ __forceinline__ int launch_order(const QmmParams& p, int b, int G) {
+    if (!p.xcd_pair) return xcd_order(b, G);
+    const int x = b & 7, i = b >> 3;
+    const int kb = i % p.nkb;
+    return kb * p.Gkb + x * (p.Gkb >> 3) + i / p.nkb;
+}
+
 /* The split of the U units of a k-block over G workgroups: workgroup c owns
  * [c*base + min(c, rem), +base + (c < rem)), with base = U / G and rem = U % G computed on
  * the host. */
@@ -555,6 +580,12 @@ __device__ __forceinline__ void store_y(const QmmParams& p, int t, int lane, f32
     }
 }
 
+/* Scopes of the exchange atomics: device (agent) scope is coherent across the XCDs' L2s, so
+ * the atomics are performed past them, in memory; between workgroups on one XCD the L2 they
+ * share performs them (workgroup scope: not written through to memory). */
+constexpr int kDeviceScope = __HIP_MEMORY_SCOPE_AGENT;
+constexpr int kL2Scope = __HIP_MEMORY_SCOPE_WORKGROUP;
+
 /* Two fp32 values in one 64-bit exchange word, each as the bitwise complement of its bits, so
  * that a word is zero only when empty: both values would have to be 0xFFFFFFFF, a NaN
  * payload that bf16/fp16 arithmetic does not produce and that is mapped to another NaN. */
@@ -571,20 +602,21 @@ __device__ __forceinline__ float pair_value(uint64_t w, int e) {
 /* One two-party exchange of the plain path at the words sl[0..1] (two elements each), for
  * the words with go[h] set: the party that gets back a non-zero word adds the other's pair
  * into w, zeroes the word and keeps go[h]; the other clears go[h]. */
+template <int SCOPE>
 __device__ __forceinline__ void pair_exchange(uint64_t* sl, bool (&go)[2], f32x4_t& w) {
     uint64_t old[2] = {0, 0};
 #pragma unroll
     for (int h = 0; h < 2; ++h)
         if (go[h])
             old[h] = __hip_atomic_exchange(sl + h, pair_word(w[2 * h], w[2 * h + 1]),
-                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                           __ATOMIC_RELAXED, SCOPE);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         go[h] = old[h] != 0;
         if (!go[h]) continue;
         w[2 * h] += pair_value(old[h], 0);
         w[2 * h + 1] += pair_value(old[h], 1);
-        __hip_atomic_store(sl + h, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(sl + h, 0ull, __ATOMIC_RELAXED, SCOPE);
     }
 }
 
@@ -593,6 +625,7 @@ __device__ __forceinline__ void pair_exchange(uint64_t* sl, bool (&go)[2], f32x4
  * that has completed, g is exchanged, and the party that gets back a non-zero g word
  * finishes: the other's u is in its u word by then (deposited before the other's g), or came
  * back from our own u exchange (then our u sits in the word and is cleared). */
+template <int SCOPE>
 __device__ __forceinline__ void pair_exchange_gu(uint64_t* sg, uint64_t* su, bool (&go)[2],
                                                  f32x4_t& g, f32x4_t& u) {
     uint64_t ou[2] = {0, 0}, og[2] = {0, 0};
@@ -600,13 +633,13 @@ __device__ __forceinline__ void pair_exchange_gu(uint64_t* sg, uint64_t* su, boo
     for (int h = 0; h < 2; ++h)
         if (go[h])
             ou[h] = __hip_atomic_exchange(su + h, pair_word(u[2 * h], u[2 * h + 1]),
-                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                          __ATOMIC_RELAXED, SCOPE);
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
     for (int h = 0; h < 2; ++h)
         if (go[h])
             og[h] = __hip_atomic_exchange(sg + h, pair_word(g[2 * h], g[2 * h + 1]),
-                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                          __ATOMIC_RELAXED, SCOPE);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         go[h] = og[h] != 0;
@@ -614,16 +647,16 @@ __device__ __forceinline__ void pair_exchange_gu(uint64_t* sg, uint64_t* su, boo
         uint64_t upw;
         if (ou[h]) {
             upw = ou[h];
-            __hip_atomic_store(su + h, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(su + h, 0ull, __ATOMIC_RELAXED, SCOPE);
         } else {
-            upw = __hip_atomic_exchange(su + h, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            upw = __hip_atomic_exchange(su + h, 0ull, __ATOMIC_RELAXED, SCOPE);
         }
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             g[2 * h + e] += pair_value(og[h], e);
             u[2 * h + e] += pair_value(upw, e);
         }
-        __hip_atomic_store(sg + h, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(sg + h, 0ull, __ATOMIC_RELAXED, SCOPE);
     }
 }
 
@@ -668,6 +701,14 @@ __device__ __forceinline__ void publish(const QmmParams& p, const KBlock& kbk, i
     uint32_t* base = (uint32_t*)p.slots + (size_t)t * p.nkb * p.nslot_kb * p.mt * 128;
     uint64_t* s1 = (uint64_t*)base + (tile_off(lane) >> 1);
     uint64_t* s2 = s1 + 64 * p.mt;
+    /* exchanged through one XCD's L2 when both parts come from it: a paired launch, or a
+     * one-k-block split whose two owners (neighbouring ranges) lie in one XCD's block of
+     * ranges (xcd_order) */
+    bool l2 = p.xcd_pair != 0;
+    if (!l2 && p.xcd8 && p.nkb == 1 && DFQ_XCD_ORDER) {
+        const int r0 = tile_first_owner(kbk, t), per = p.Gkb >> 3, rem = p.Gkb & 7;
+        l2 = owner_wg(r0, per, rem) == owner_wg(r0 + 1, per, rem);
+    }
     bool go[2] = {true, true};
     if (p.epi) {
         /* lanes n < 8 hold g and take u from lane n + 8 (g words, then u words) */
@@ -676,8 +717,13 @@ __device__ __forceinline__ void publish(const QmmParams& p, const KBlock& kbk, i
         for (int r = 0; r < 4; ++r) u[r] = dpp_f32<0x128>(v[r]);
         if (!act || n >= 8) return;
         f32x4_t g = v;
-        if (!chain || kb < 2) pair_exchange_gu(s1, s1 + 32, go, g, u);
-        if (chain) pair_exchange_gu(s2, s2 + 32, go, g, u);
+        if (l2) {
+            if (!chain || kb < 2) pair_exchange_gu<kL2Scope>(s1, s1 + 32, go, g, u);
+            if (chain) pair_exchange_gu<kL2Scope>(s2, s2 + 32, go, g, u);
+        } else {
+            if (!chain || kb < 2) pair_exchange_gu<kDeviceScope>(s1, s1 + 32, go, g, u);
+            if (chain) pair_exchange_gu<kDeviceScope>(s2, s2 + 32, go, g, u);
+        }
         const int H = p.N / 2;
         float lbg = 0.0f, lbu = 0.0f;
         if (p.lbias) {
@@ -695,8 +741,13 @@ __device__ __forceinline__ void publish(const QmmParams& p, const KBlock& kbk, i
     }
     if (!act) return;
     f32x4_t w = v;
-    if (!chain || kb < 2) pair_exchange(s1, go, w);
-    if (chain) pair_exchange(s2, go, w);
+    if (l2) {
+        if (!chain || kb < 2) pair_exchange<kL2Scope>(s1, go, w);
+        if (chain) pair_exchange<kL2Scope>(s2, go, w);
+    } else {
+        if (!chain || kb < 2) pair_exchange<kDeviceScope>(s1, go, w);
+        if (chain) pair_exchange<kDeviceScope>(s2, go, w);
+    }
     const int col = t * 16 + n;
     float lb = 0.0f;
     if (p.lbias && col < p.N) lb = elem_to_f32<F16>(((const uint16_t*)p.lbias)[col]);
@@ -1775,7 +1826,7 @@ extern "C" __global__ void __launch_bounds__(256) dfq_fill_u32(uint32_t* ptr, ui
 /* The fast kernel's own read, with no compute: the units of a one-k-block 4-bit group-64
  * split -- the same ranges, and per unit the same loads: one 16-byte scale-or-bias load a
  * lane and four 16-byte weight loads of 16 rows x 64 bytes -- taken in order by 12 waves, one
- * unit in flight each, XORed into one word per wave (sink[12 * blockIdx.x + wave]).  It is
+ * unit in flight each, XORed into one word per wave (sink[12 * range + wave]).  It is
  * the weight stream the matmul would reach if its x staging, arithmetic and output cost
  * nothing: the bound its own access pattern sets.  A wave issues nothing past its last unit
  * (a re-read of it there would hold the wave, and the launch's end, for one more round
@@ -1787,7 +1838,8 @@ extern "C" __global__ void __launch_bounds__(768) dfq_read_units_b4_g64(QmmParam
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int q = lane >> 4, n = lane & 15;
     const KBlock kbk = kblock(p, 0);
-    const int a = range_start(kbk, blockIdx.x), b = range_start(kbk, blockIdx.x + 1);
+    const int wr = xcd_order((int)blockIdx.x, (int)gridDim.x);  // this workgroup's range
+    const int a = range_start(kbk, wr), b = range_start(kbk, wr + 1);
     const int SS = kbk.SS;
     const int RB = p.K / 2, GPR = p.K / 64;
     const uint8_t* wbytes = (const uint8_t*)p.w;
@@ -1817,7 +1869,7 @@ extern "C" __global__ void __launch_bounds__(768) dfq_read_units_b4_g64(QmmParam
         }
     }
     const uint32_t v = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
-    if (lane == 0) sink[blockIdx.x * 12 + wave] = v;
+    if (lane == 0) sink[wr * 12 + wave] = v;
 }
 
 /* The same read over a packed weight array: unit (t, c) is 4608 contiguous bytes at
@@ -1829,7 +1881,8 @@ extern "C" __global__ void __launch_bounds__(768) dfq_read_units_packed_b4_g64(Q
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int q = lane >> 4, n = lane & 15;
     const KBlock kbk = kblock(p, 0);
-    const int a = range_start(kbk, blockIdx.x), b = range_start(kbk, blockIdx.x + 1);
+    const int wr = xcd_order((int)blockIdx.x, (int)gridDim.x);  // this workgroup's range
+    const int a = range_start(kbk, wr), b = range_start(kbk, wr + 1);
     const uint8_t* pk = (const uint8_t*)p.w;
     u32x4_t acc = {0u, 0u, 0u, 0u};
     u32x4_t r[5];
@@ -1852,7 +1905,7 @@ extern "C" __global__ void __launch_bounds__(768) dfq_read_units_packed_b4_g64(Q
         }
     }
     const uint32_t v = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
-    if (lane == 0) sink[blockIdx.x * 12 + wave] = v;
+    if (lane == 0) sink[wr * 12 + wave] = v;
 }
 
 /* The read ceiling: a plain streaming read of `units` 4 KB blocks, the best single-launch
@@ -2048,7 +2101,8 @@ constexpr int prefetch_depth() {
 #define DFQ_MT8_KERNEL(BITS, GS, F16, NAME, CHN, CH, MTN, MT, AM, PK, SFX)                 \
     extern "C" __global__ void __launch_bounds__(kBlock)                                     \
         dfq_qmm_##MTN##_b##BITS##_g##GS##_##NAME##_##CHN##SFX(QmmParams p) {                  \
-        qmm_mt8<BITS, GS, F16, CH, prefetch_depth<BITS, GS, CH>(), MT, AM, PK>(p, blockIdx.x); \
+        qmm_mt8<BITS, GS, F16, CH, prefetch_depth<BITS, GS, CH>(), MT, AM, PK>(               \
+            p, launch_order(p, (int)blockIdx.x, (int)gridDim.x));                             \
     }
 /* per format: one super-step or 8-group chunks at up to 8 rows; 8-group chunks at up to 16;
  * the greedy-accept forms (_am) of the 8-group-chunk kernels; and all of the 8-group-chunk

@@ -78,6 +78,11 @@ typedef struct QmmParams {
                                workgroup; 0: the publisher waves write them as they finish */
     int32_t umax;           /* most units one workgroup holds                         */
     int32_t ring;           /* partial-tile slots in LDS (a ring over the take order) */
+    int32_t xcd8;           /* 1: the launch's workgroups are dealt to eight XCDs
+                               round-robin (workgroup b on XCD b % 8: the whole chip)  */
+    int32_t xcd_pair;       /* 1 (with xcd8): every shared tile has one part per k-block,
+                               from the same range index, and the launch places those
+                               workgroups on one XCD (whose L2 performs their exchange) */
     uint32_t w_bytes;       /* size of w in bytes (< 2^31)                            */
     uint32_t s_bytes;       /* size of scales (= size of biases) in bytes             */
     /* greedy-accept mode (am_keys != NULL; splits without a second pass only): every

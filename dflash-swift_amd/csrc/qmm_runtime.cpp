@@ -303,8 +303,12 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
         const int ss_max = (chunks + dd - 1) / dd;
         const int kr = ss_max * kch;
         if (!stage_fits(M, kr, gs)) return false;
-        const int64_t G = std::min<int64_t>(std::max<int64_t>(1, G0), T);
+        int64_t G = std::min<int64_t>(std::max<int64_t>(1, G0), T);
         const int64_t tmax = (T + G - 1) / G;
+        /* a multiple of 8 workgroups where that leaves the most tiles a workgroup takes as it
+         * is (three k-blocks: 85 -> 80 at N = 5120), so that the launch can place each tile's
+         * workgroups on one XCD */
+        if ((G & 7) && G > 8 && (T + (G & ~7) - 1) / (G & ~7) == tmax) G &= ~7;
         Plan p{};
         p.kss = kss;
         p.mt = mt;
@@ -707,6 +711,10 @@ dfq_status dfq_workspace_clear(dfq_ctx* ctx, void* ws, size_t bytes, void* strea
     return e == hipSuccess ? DFQ_OK : hip_fail(e, "launch dfq_fill_u32");
 }
 
+#ifndef DFQ_XCD_PAIR
+#define DFQ_XCD_PAIR 1
+#endif
+
 /* The kernel argument of one call of a plan (ws: the workspace, NULL when none is needed). */
 static QmmParams fill_params(const Plan& pl, const void* x, const uint32_t* w,
                              const void* scales, const void* biases, const void* lbias, void* y,
@@ -777,6 +785,16 @@ static dfq_status launch_mt8(dfq_ctx* ctx, const void* x, const uint32_t* w, con
     }
     QmmParams p = fill_params(pl, x, w, scales, biases, lbias, y, M, N, K, bits, gs, ws);
     p.epi = epi;
+    /* On the whole chip (256 CUs: eight XCDs, dealt workgroups round-robin) a tile whose two
+     * parts come from workgroups on one XCD is exchanged through that XCD's L2.  Splits whose
+     * tiles have one part per k-block at the same range index (aligned, or ranges of the same
+     * whole tiles in every k-block), with workgroup counts per k-block that the eight XCDs
+     * share evenly, place each tile's workgroups on one XCD. */
+    p.xcd8 = (DFQ_XCD_PAIR && ctx->num_cus == 256) ? 1 : 0;
+    p.xcd_pair = (p.xcd8 && pl.nkb > 1 && !pl.reduce && (pl.aligned || pl.T % pl.Gkb == 0) &&
+                  pl.Gkb % 8 == 0)
+                     ? 1
+                     : 0;
     if (acc) {
         p.am_keys = acc->keys;
         p.am_count = acc->count;
