@@ -584,6 +584,8 @@ __device__ __forceinline__ void store_y(const QmmParams& p, int t, int lane, f32
  * the atomics are performed past them, in memory; between workgroups on one XCD the L2 they
  * share performs them (workgroup scope: not written through to memory). */
 constexpr int kDeviceScope = __HIP_MEMORY_SCOPE_AGENT;
+/* Levels of the exchange tree of an aligned split: up to 8 k-blocks (the host plan's most) */
+constexpr int kTreeLevels = 3;
 constexpr int kL2Scope = __HIP_MEMORY_SCOPE_WORKGROUP;
 
 /* Two fp32 values in one 64-bit exchange word, each as the bitwise complement of its bits, so
@@ -671,12 +673,14 @@ __device__ __forceinline__ void pair_exchange_gu(uint64_t* sg, uint64_t* su, boo
  * one value halve the device-scope atomics and resets: the headline call measured 15.87 ->
  * 15.58 us, N = 1024 (every tile exchanged) 7.86 -> 7.64 us.
  *
- * Three contributors in an aligned split of three k-blocks (whole tiles per workgroup):
- * k-blocks 0 and 1 exchange at the tile's first word set, and whoever completes a word
- * carries the pair's sum into the second set, where k-block 2's part waits or arrives; the
- * second arrival there writes y.  The sum is (A + B) + C whatever the order of arrival, so
- * the result does not depend on timing.  This replaces the second pass of such splits: the
- * down projection (M=8, N=5120, K=17408) measured 18.3-18.5 -> 16.9-17.1 us.
+ * Three or more contributors in an aligned split (whole tiles per workgroup, one part per
+ * k-block): the parts meet over a binary tree of the k-blocks, one exchange per internal node
+ * (see publish), and the second arrival at the root writes y.  For three: k-blocks 0 and 1
+ * exchange at the tile's first word set, and whoever completes a word carries the pair's sum
+ * into the second set, where k-block 2's part waits or arrives; the sum is (A + B) + C
+ * whatever the order of arrival, so the result does not depend on timing.  This replaces the
+ * second pass of such splits: the down projection (M=8, N=5120, K=17408) measured
+ * 18.3-18.5 -> 16.9-17.1 us.
  *
  * Other tiles with more contributors belong to reduce splits, which store their parts with no
  * round trip and leave the sum to the second pass (a per-tile arrival counter here costs
@@ -694,13 +698,22 @@ __device__ __forceinline__ void publish(const QmmParams& p, const KBlock& kbk, i
     const int nwg = tile_owners(kbk, t);
     const uint32_t total = (uint32_t)(p.nkb * nwg);
     /* one part: stored by the caller; more than two outside an aligned split: reduce splits */
-    const bool chain = total == 3 && p.aligned;
+    const bool chain = total >= 3 && p.aligned;
     if (total != 2 && !chain) return;
     /* the tile's workspace area: nkb*nslot_kb slots of mt*128 floats.  A lane's pairs sit at
-     * two words of the first set (64*mt words); a chain's second exchange uses the second */
-    uint32_t* base = (uint32_t*)p.slots + (size_t)t * p.nkb * p.nslot_kb * p.mt * 128;
-    uint64_t* s1 = (uint64_t*)base + (tile_off(lane) >> 1);
-    uint64_t* s2 = s1 + 64 * p.mt;
+     * two words of each set of 64*mt words.  The parts of an aligned split (one per k-block)
+     * are summed over a binary tree of the k-blocks: at level L, node i adds the sums of its
+     * children 2i and 2i+1 (k-blocks [2i << (L-1), (2i+1) << (L-1)) and the next such run),
+     * exchanged at set r - 1, r = (2i+1) << (L-1) being the right child's first k-block (a
+     * node without a right child passes its sum up); whoever completes a node carries its
+     * sum up, and the second arrival at the root writes y.  The sum's order is fixed by the
+     * tree, whatever the order of arrival: (P0 + P1) + P2 for three k-blocks. */
+    /* the tile's words as a uniform base plus a 32-bit lane offset (a 64-bit per-lane pointer
+     * live across the exchanges costs registers the 16-row kernels do not have) */
+    uint64_t* const tb =
+        (uint64_t*)((uint32_t*)p.slots + (size_t)t * p.nkb * p.nslot_kb * p.mt * 128);
+    const uint32_t lw = (uint32_t)tile_off(lane) >> 1;
+    const int nparts = chain ? (int)total : 2, leaf = chain ? kb : 0;
     /* exchanged through one XCD's L2 when both parts come from it: a paired launch, or a
      * one-k-block split whose two owners (neighbouring ranges) lie in one XCD's block of
      * ranges (xcd_order) */
@@ -717,12 +730,13 @@ __device__ __forceinline__ void publish(const QmmParams& p, const KBlock& kbk, i
         for (int r = 0; r < 4; ++r) u[r] = dpp_f32<0x128>(v[r]);
         if (!act || n >= 8) return;
         f32x4_t g = v;
-        if (l2) {
-            if (!chain || kb < 2) pair_exchange_gu<kL2Scope>(s1, s1 + 32, go, g, u);
-            if (chain) pair_exchange_gu<kL2Scope>(s2, s2 + 32, go, g, u);
-        } else {
-            if (!chain || kb < 2) pair_exchange_gu<kDeviceScope>(s1, s1 + 32, go, g, u);
-            if (chain) pair_exchange_gu<kDeviceScope>(s2, s2 + 32, go, g, u);
+#pragma unroll
+        for (int L = 1; L <= kTreeLevels; ++L) {
+            const int r = ((leaf >> L) * 2 + 1) << (L - 1);
+            if (r >= nparts || !(go[0] || go[1])) continue;
+            uint64_t* sj = tb + (lw + (uint32_t)((r - 1) * 64 * p.mt));
+            if (l2) pair_exchange_gu<kL2Scope>(sj, sj + 32, go, g, u);
+            else pair_exchange_gu<kDeviceScope>(sj, sj + 32, go, g, u);
         }
         const int H = p.N / 2;
         float lbg = 0.0f, lbu = 0.0f;
@@ -741,12 +755,13 @@ __device__ __forceinline__ void publish(const QmmParams& p, const KBlock& kbk, i
     }
     if (!act) return;
     f32x4_t w = v;
-    if (l2) {
-        if (!chain || kb < 2) pair_exchange<kL2Scope>(s1, go, w);
-        if (chain) pair_exchange<kL2Scope>(s2, go, w);
-    } else {
-        if (!chain || kb < 2) pair_exchange<kDeviceScope>(s1, go, w);
-        if (chain) pair_exchange<kDeviceScope>(s2, go, w);
+#pragma unroll
+    for (int L = 1; L <= kTreeLevels; ++L) {
+        const int r = ((leaf >> L) * 2 + 1) << (L - 1);
+        if (r >= nparts || !(go[0] || go[1])) continue;
+        uint64_t* sj = tb + (lw + (uint32_t)((r - 1) * 64 * p.mt));
+        if (l2) pair_exchange<kL2Scope>(sj, go, w);
+        else pair_exchange<kDeviceScope>(sj, go, w);
     }
     const int col = t * 16 + n;
     float lb = 0.0f;

@@ -210,6 +210,15 @@ static constexpr int kBurstTiles = 8;
  * 29.6 against 28.8-29.3; N = 60000 (thirty) 42.5 against 38.9-39.3; N = 80000 (forty) 54.2
  * against 48.6-48.8. */
 static constexpr int kAlignedMaxTiles = 12;
+/* Most k-blocks of an aligned split: from four on, each tile's parts meet over a tree of
+ * exchanges (k-blocks - 1 of them, ceil(log2 k-blocks) deep), taken where the launch can place
+ * a tile's workgroups on one XCD so that the exchanges run in its L2 (the whole chip,
+ * workgroups per k-block a multiple of 8). */
+static constexpr int kAlignedMaxKBlocks = 8;
+static_assert(kAlignedMaxKBlocks <= 8, "the kernels' exchange tree has three levels");
+#ifndef DFQ_LONG_CHAIN
+#define DFQ_LONG_CHAIN 1
+#endif
 
 bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_max, Plan* pl) {
     const int kss = kss_for(bits, gs);
@@ -354,6 +363,27 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
             *pl = al;
             return true;
         }
+        /* From four k-blocks on, the first aligned split of d .. kAlignedMaxKBlocks k-blocks
+         * that fits and whose launch can place each tile's workgroups on one XCD (the parts
+         * then meet over a tree of exchanges in its L2): where it holds at most two tiles a
+         * workgroup, or where the second pass's split needs more workgroups than the chip has
+         * CUs (a second round of workgroups) and the aligned one deals every workgroup the
+         * same tiles.  Measured on MI355X (us, against the second pass's split, same box):
+         * N = 1024, K = 32768 at 8 rows (two tiles) 12.2 against 13.4; 16 rows at N = 5120,
+         * K = 17408 (eight k-blocks of ten tiles, against 6 x 47 workgroups) 25.1 against
+         * 30.0.  Taken elsewhere it lost: 12 rows at that shape (eight tiles, against
+         * 5 x 51 workgroups) 22.0 against 20.3, 8 rows at N = 5120, K = 32768 (eight tiles)
+         * 30.6 against 26.3; 9 rows gained 0.3 us. */
+        if (pl->reduce && d >= 4 && DFQ_LONG_CHAIN && num_cus == 256)
+            for (int dd = d; dd <= std::min(kAlignedMaxKBlocks, chunks); ++dd) {
+                if (!split_aligned(dd, num_cus / dd, &al) || al.Gkb % 8) continue;
+                const int64_t tpw = (T + al.Gkb - 1) / al.Gkb;  // most tiles a workgroup
+                if (tpw <= 2 ||
+                    ((int64_t)pl->nkb * pl->Gkb > num_cus && T % al.Gkb == 0)) {
+                    *pl = al;
+                    return true;
+                }
+            }
 
         /* Few tiles (a narrow N): one k-block over every CU spreads each tile over more than
          * two workgroups, which needs the second pass.  Two k-blocks of one tile per

@@ -137,6 +137,27 @@ THREE_BLOCK_CASES = [
 ]
 
 
+# Four to eight k-blocks of whole tiles, each tile's parts summed over a tree of exchanges in
+# one XCD's L2 (at most two tiles a workgroup, or where the second pass's split would need a
+# second round of workgroups): 9..16 rows at long K, a narrow N at very long K, 8-bit and
+# group 32.
+TREE_CASES = [
+    (16, 640, 17408, 4, 64, BF16),           # six k-blocks, one tile a workgroup
+    (16, 5120, 17408, 4, 64, F16),           # eight k-blocks, ten tiles in every workgroup
+    (9, 1000, 17408, 4, 64, BF16),           # four k-blocks
+    (8, 1024, 32768, 4, 64, BF16),           # six k-blocks at 8 rows
+    (12, 1280, 17408, 8, 128, BF16),
+    (16, 1024, 17408, 4, 32, F16),
+]
+
+
+@pytest.mark.parametrize("M,N,K,bits,gs,dt", TREE_CASES)
+def test_tree_of_exchanges_matches_oracle_and_repeats(ctx, oracle, M, N, K, bits, gs, dt):
+    p = ctx.plan(M, N, K, bits, gs)
+    assert 4 <= p["nkb"] <= 8, p
+    check_aligned(ctx, oracle, M, N, K, bits, gs, dt, p["nkb"])
+
+
 @pytest.mark.parametrize("M,N,K,bits,gs,dt", ALIGNED_CASES)
 def test_aligned_split_matches_oracle_and_repeats(ctx, oracle, M, N, K, bits, gs, dt):
     check_aligned(ctx, oracle, M, N, K, bits, gs, dt, 2)

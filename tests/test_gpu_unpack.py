@@ -187,3 +187,17 @@ def test_unpack_is_exact_over_the_packed_layout_in_each_split(ctx, bits, gs, dt,
         list(range((chunks - 1) * ck, chunks * ck))
     run_one_hot(ctx, N, K, bits, gs, dt, M, pos, seed=bits * 8000 + gs + dt, expect_plan=plan,
                 packed=True)
+
+
+@pytest.mark.parametrize("bits,gs,dt,M,N,K", [(4, 64, BF16, 16, 640, 17408),
+                                              (8, 64, F16, 16, 640, 17408),
+                                              (4, 64, BF16, 8, 1024, 32768)])
+def test_unpack_is_exact_in_a_tree_of_exchanges(ctx, bits, gs, dt, M, N, K):
+    """Six k-blocks of whole tiles, each tile's parts summed over a tree of exchanges: every k
+    of the first chunk of each k-block and of the last chunk."""
+    p = ctx.plan(M, N, K, bits, gs)
+    assert p["nkb"] == 6 and p["aligned"] == 1 and p["reduce"] == 0, p
+    ck = chunk_k(bits, gs, M)
+    starts = [kb * p["chunks"] // p["nkb"] for kb in range(p["nkb"])] + [p["chunks"] - 1]
+    pos = [c * ck + k for c in sorted(set(starts)) for k in range(ck)]
+    run_one_hot(ctx, N, K, bits, gs, dt, M, pos, seed=bits * 9000 + gs + dt + M)

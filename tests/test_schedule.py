@@ -12,6 +12,7 @@ replaying the workgroup's take order covers every interleaving of its waves.
 """
 import ctypes
 
+import numpy as np
 import pytest
 
 import dflash_qmm
@@ -92,11 +93,11 @@ def replay(p):
         for t in range(T):
             parts_of[t] = parts_of.get(t, 0) + tile_owners(p, kb, t)
     max_parts = max(parts_of.values())
-    # aligned splits (two or three k-blocks) finish every tile in the kernel, by the pair
-    # exchange or a chain of two of them; other splits with three or more parts take the
-    # second pass
+    # aligned splits (two to eight k-blocks, the kernels' exchange tree has three levels)
+    # finish every tile in the kernel, by the pair exchange or a tree of them; other splits
+    # with three or more parts take the second pass
     if p["aligned"]:
-        assert nkb in (2, 3) and max_parts == nkb and not p["reduce"], (max_parts, p)
+        assert 2 <= nkb <= 8 and max_parts == nkb and not p["reduce"], (max_parts, p)
     else:
         assert p["reduce"] == int(max_parts > 2), (max_parts, p["reduce"])
 
@@ -283,8 +284,25 @@ def test_narrow_n_splits_k_in_two_with_one_tile_per_workgroup():
     assert (p["nkb"], p["Gkb"], p["nslot_kb"], p["reduce"]) == (2, 64, 1, 0)
     # wide enough N keeps one k-block over every CU
     assert make_plan(8, 2048, 5120, 4, 64)["nkb"] == 1
-    # long K: a workgroup's share would be too long; the reduce split stays
-    assert make_plan(8, 1024, 32768, 4, 64)["reduce"] == 1
+    # long K: a workgroup's share of two k-blocks would be too long; six k-blocks of whole
+    # tiles (at most two a workgroup, 40 workgroups each) sum each tile over a tree of exchanges
+    p = make_plan(8, 1024, 32768, 4, 64)
+    assert (p["nkb"], p["Gkb"], p["aligned"], p["reduce"]) == (6, 40, 1, 0), p
+
+
+def test_tree_splits_only_where_they_measured_faster():
+    # 16 rows at N = 5120, K = 17408: the second pass's split would take 6 x 47 workgroups (a
+    # second round on 256 CUs); eight k-blocks of exactly ten tiles a workgroup instead
+    p = make_plan(16, 5120, 17408, 4, 64)
+    assert (p["nkb"], p["Gkb"], p["aligned"], p["reduce"]) == (8, 32, 1, 0), p
+    # 12 rows there (5 x 51 workgroups, one round) and eight tiles a workgroup at K = 32768:
+    # the second pass's split stays
+    assert make_plan(12, 5120, 17408, 4, 64)["reduce"] == 1
+    assert make_plan(8, 5120, 32768, 4, 64)["reduce"] == 1
+    # other CU counts (another partition of the chip) never take a tree of four or more
+    for cus in (32, 64, 128, 304):
+        p = make_plan(16, 5120, 17408, 4, 64, cus=cus)
+        assert not (p["aligned"] and p["nkb"] >= 4), (cus, p)
 
 
 def test_outputs_leave_at_the_end_where_workgroups_hold_many_tiles():
@@ -433,3 +451,63 @@ def test_stock_gemv_split_writes_every_row_once(shape):
                     c = min(lane + 64 * min(j, nsteps - 1), nchunk - 1)
                     assert 0 <= c < nchunk and (c * kpl) // 32 < K // 32
     assert sorted(written) == list(range(N))
+
+
+def _tree_sets(kb, nparts):
+    """The word sets part kb exchanges at, level by level, as the kernel's publish walks its
+    tree: at level L the node holding kb meets its sibling at set r - 1, r = the right
+    child's first k-block, when that child exists."""
+    out, L = [], 1
+    while (1 << (L - 1)) < nparts:
+        r = ((kb >> L) * 2 + 1) << (L - 1)
+        if r < nparts:
+            out.append(r)
+        L += 1
+    return out
+
+
+@pytest.mark.parametrize("nparts", range(2, 9))
+def test_exchange_tree_has_one_writer_and_a_fixed_order(nparts):
+    """Every arrival order of the parts at the tree's exchanges (first arrival deposits, the
+    second adds and carries on) ends with exactly one writer holding the same fp32 sum, the
+    tree's own order: (P0 + P1) + P2 for three parts."""
+    import random
+
+    def tree_sum(v, lo, hi):
+        if hi - lo == 1:
+            return np.float32(v[lo])
+        h = 1
+        while 2 * h < hi - lo:
+            h *= 2
+        return np.float32(tree_sum(v, lo, lo + h) + tree_sum(v, lo + h, hi))
+
+    sets_used = sorted({r for kb in range(nparts) for r in _tree_sets(kb, nparts)})
+    assert sets_used == list(range(1, nparts))          # nparts - 1 sets, all distinct
+    rng = random.Random(nparts)
+    for trial in range(200):
+        v = np.random.default_rng(trial).normal(size=nparts).astype(np.float32) * 1000
+        words, writers = {}, []
+
+        def party(kb):
+            w, go = np.float32(v[kb]), True
+            for r in _tree_sets(kb, nparts):
+                if not go:
+                    break
+                yield
+                old = words.get(r)
+                if old is None:
+                    words[r], go = w, False
+                else:
+                    w, words[r] = np.float32(w + old), None
+            if go:
+                writers.append(w)
+
+        live = {kb: party(kb) for kb in range(nparts)}
+        while live:
+            kb = rng.choice(sorted(live))
+            try:
+                next(live[kb])
+            except StopIteration:
+                del live[kb]
+        assert len(writers) == 1
+        assert writers[0] == tree_sum(v, 0, nparts)
