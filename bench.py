@@ -79,8 +79,8 @@ def stats(per_call):
 
 
 def replays_for(steps):
-    """Replays of a `steps`-call graph: at least 10, and at least 200 calls in all."""
-    return max(10, -(-200 // max(1, steps)))
+    """Replays of a graph (of at least MIN_CALLS_PER_GRAPH calls): 10."""
+    return 10
 
 
 def algorithmic_bytes(M, N=N_OUT, K=K_IN, bits=BITS, gs=GS):
@@ -117,13 +117,20 @@ def time_replays(torch, stream, graph, steps, reps):
     return [e0.elapsed_time(e1) * 1000.0 / steps for e0, e1 in events]
 
 
+# Fewest calls one timed graph holds.  Each replay's boundary (the graph launch) costs the
+# calls around it time that is not the kernel's: measured on MI355X with 24 calls a graph
+# against 200 (us per call, same box): the headline M=1 14.96 against 14.53, M=8 15.18-15.40
+# against 15.00-15.07, C1 7.03-7.14 against 6.84, C3 17.63 against 16.02-16.17.
+MIN_CALLS_PER_GRAPH = 200
+
+
 def rotation(nsets, steps, set_bytes):
     """The calls one graph captures over `nsets` rotated weight sets of `set_bytes` each: the
-    fewest whole cycles through every set that hold at least `steps` calls, so that every set
-    is used equally often and the bytes read between two uses of one set -- within a replay
-    and across the boundary into the next replay, which starts again at set 0 -- are always
-    (nsets - 1) * set_bytes."""
-    calls = -(-max(1, steps) // nsets) * nsets
+    fewest whole cycles through every set that hold at least max(steps, MIN_CALLS_PER_GRAPH)
+    calls, so that every set is used equally often and the bytes read between two uses of one
+    set -- within a replay and across the boundary into the next replay, which starts again at
+    set 0 -- are always (nsets - 1) * set_bytes."""
+    calls = -(-max(1, steps, MIN_CALLS_PER_GRAPH) // nsets) * nsets
     return {"calls_per_graph": calls, "sets_touched": nsets,
             "min_reuse_bytes": (nsets - 1) * set_bytes}
 
@@ -137,8 +144,8 @@ def time_m(torch, ctx, stream, sets, M, steps, warmup, N, K, bits, gs, ws, wsb, 
            x_sd=1.0, packed=None):
     """Per-call microseconds (one figure per replay) of graph-replayed calls at row count M
     (fp16 throughout with f16, else bf16): the graph holds rotation(...)["calls_per_graph"]
-    calls, at least `steps`, cycling through every weight set; replays_for(steps) replays,
-    each divided by the calls it holds.  With `packed` (the sets in the packed layout,
+    calls (at least `steps` and MIN_CALLS_PER_GRAPH), cycling through every weight set;
+    replays_for(steps) replays, each divided by the calls it holds.  With `packed` (the sets in the packed layout,
     Context.pack), the calls are dfq_qmm_packed over those instead."""
     import dflash_qmm
     dev = sets[0][0].device
@@ -303,12 +310,13 @@ def time_copy(torch, stream, nbytes, nsets, steps):
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
+        calls = max(steps, MIN_CALLS_PER_GRAPH)
         e0.record(stream)
-        for i in range(steps):
+        for i in range(calls):
             dst[i % nsets].copy_(src[(i + 1) % nsets])
         e1.record(stream)
         torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1000.0 / steps
+    return e0.elapsed_time(e1) * 1000.0 / calls
 
 
 # One verify-pass layer of the C5 chain (N, K): q, k, v, o, gate, up, down; then the lm_head.
@@ -782,7 +790,8 @@ def main():
         d = dist[m]
         print(f"[bench] M={m}: {d['median']:.2f} us/call (mean {d['mean']:.2f}, p10 "
               f"{d['p10']:.2f}, p90 "
-              f"{d['p90']:.2f}, {d['replays']} replays of {args.steps}), "
+              f"{d['p90']:.2f}, {d['replays']} replays of "
+              f"{rotation(args.sets, args.steps, 0)['calls_per_graph']}), "
               f"{algorithmic_bytes(m) / d['median'] / 1e3:.0f} GB/s", file=sys.stderr,
               flush=True)
     us = {m: dist[m]["median"] for m in ms}
@@ -807,6 +816,7 @@ def main():
             "M_sweep": ms,
             "rotated_weight_sets": args.sets,
             "replays_per_M": replays_for(args.steps),
+            "min_calls_per_graph": MIN_CALLS_PER_GRAPH,
             "rotation": rotation(args.sets, args.steps, set_bytes_of(sets)),
             "mall_bytes": MALL_BYTES,
         },
