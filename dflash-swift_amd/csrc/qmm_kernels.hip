@@ -93,7 +93,6 @@ constexpr int kBlock = kThreads + 64 * kPublishers;  // + the publisher waves
  * (eight units a workgroup: the four waves with none fetch an unused unit, now ahead of the
  * staging waves' weights) 7.35 against 7.05. */
 constexpr int kStageThreads = DFQ_STAGE_THREADS;
-constexpr int kMaxStageItems = DFQ_STAGE_ITEMS;  // 16-byte x chunks staged per thread
 static_assert(kStageThreads == 8 * 64, "x is staged by the first eight waves");
 static_assert(kThreads >= kStageThreads, "the staging waves are streaming waves");
 
@@ -1116,6 +1115,7 @@ __device__ __forceinline__ void qmm_mt8(const QmmParams& p, int wg) {
      * same value again); threads past row M stage nothing. */
     const int CPR = kr / 8;                  // 16-byte chunks per row of the k-block
     const int TPR = DFQ_STAGE_TPR(p.M, GS);  // wave-uniform
+    constexpr int kMaxStageItems = DFQ_STAGE_ITEMS(MT);  // 16-byte x chunks a thread at most
     const int NI = (CPR + TPR - 1) / TPR;    // items per staging thread (the host plan
                                              // keeps it within kMaxStageItems)
     const int sr = tid / TPR;

@@ -11,10 +11,14 @@
 /* x staging: 512 threads (8 waves) of a workgroup stage the M rows of its k-block's x.  Row r
  * goes to the DFQ_STAGE_TPR threads r*TPR .. r*TPR + TPR - 1 (a multiple of gs/8, so that a
  * group's gs/8 16-byte chunks sit in aligned neighbouring lanes), thread r*TPR + j taking
- * chunks j, j + TPR, j + 2 TPR, ... of the row; DFQ_STAGE_ITEMS chunks a thread at most. */
+ * chunks j, j + TPR, j + 2 TPR, ... of the row; DFQ_STAGE_ITEMS(mt) chunks a thread at most
+ * (mt = 2 for the 9..16-row kernels, whose one k-block of x at K = 5120 needs up to 16). */
 #define DFQ_STAGE_THREADS 512
 #define DFQ_STAGE_TPR(M, gs) (((DFQ_STAGE_THREADS / (M)) / ((gs) / 8)) * ((gs) / 8))
-#define DFQ_STAGE_ITEMS 12
+#ifndef DFQ_STAGE_ITEMS_16
+#define DFQ_STAGE_ITEMS_16 16
+#endif
+#define DFQ_STAGE_ITEMS(mt) ((mt) == 2 ? DFQ_STAGE_ITEMS_16 : 12)
 
 /* Work decomposition of the fast kernel (a "stream-K" split with a deterministic fix-up):
  *

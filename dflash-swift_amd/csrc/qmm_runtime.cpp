@@ -54,11 +54,27 @@ constexpr int kThreads = kWaves * 64;             // qmm_mt8 streaming threads
 #define DFQ_PUBLISHERS 2               // must match the kernels' build
 #endif
 constexpr int kBlockThreads = kThreads + 64 * DFQ_PUBLISHERS;  // + the publisher waves
-/* Whether the x of a k-block of kr elements at M rows fits the kernel's staging: each
- * staging thread holds at most DFQ_STAGE_ITEMS 16-byte chunks of its row. */
-static bool stage_fits(int M, int kr, int gs) {
+/* 16-byte x chunks a staging thread holds for a k-block of kr elements at M rows (0 when no
+ * thread layout exists); the kernels take up to DFQ_STAGE_ITEMS(mt). */
+static int stage_items(int M, int kr, int gs) {
     const int tpr = DFQ_STAGE_TPR(M, gs);
-    return tpr > 0 && (kr / 8 + tpr - 1) / tpr <= DFQ_STAGE_ITEMS;
+    return tpr > 0 ? (kr / 8 + tpr - 1) / tpr : 0;
+}
+/* Whether that x fits the staging of a split of nkb k-blocks.  Past DFQ_STAGE_ITEMS(1) items
+ * (the 9..16-row kernels only) the staging costs more than a second k-block saves unless the
+ * x is read for enough weights: such a split must be one k-block (up to 12 rows at
+ * K = 5120), and is kept only where each range holds at least three tiles' units and one
+ * round of workgroups covers the split (checked by the caller).  Measured on MI355X (us,
+ * one k-block against two): N = 17408, K = 5120 at 10 rows 16.2 against 18.4, 11 rows 16.6
+ * against 18.2, 12 rows 16.7 against 18.2; gate|up N = 34816 at 12 rows 27.9 against 31.7;
+ * N = 7168 at 12 rows (1.8 tiles a range) 12.2 against 11.45; 16 rows at N = 40000,
+ * K = 4096 (two rounds of workgroups) 31.1 against 28.6, N = 80000 (four) 58.6 against
+ * 49.0. */
+static bool stage_fits(int M, int kr, int gs, int nkb) {
+    const int items = stage_items(M, kr, gs);
+    if (items < 1) return false;
+    if (items <= DFQ_STAGE_ITEMS(1)) return true;
+    return M > 8 && nkb == 1 && items <= DFQ_STAGE_ITEMS(2);
 }
 
 struct PlanKey {
@@ -219,6 +235,16 @@ static_assert(kAlignedMaxKBlocks <= 8, "the kernels' exchange tree has three lev
 #ifndef DFQ_LONG_CHAIN
 #define DFQ_LONG_CHAIN 1
 #endif
+/* Smallest ring of partial slots a split shrinks to (beyond the units of one tile, which it
+ * must hold to stay free of deadlock) before it takes more workgroups than CUs.  The ring's
+ * size measured within noise down to this (N = 17408, K = 5120: 11 rows with 28 slots 16.7
+ * against 16.9 us with 43), while the LDS it frees lets more shapes take one k-block and one
+ * round of workgroups: 12 rows (14 slots) 16.7 against 18.2 us with two k-blocks, gate|up
+ * N = 34816 at 12 rows 27.9 against 31.7. */
+#ifndef DFQ_RING_SPARE
+#define DFQ_RING_SPARE 4
+#endif
+
 
 bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_max, Plan* pl) {
     const int kss = kss_for(bits, gs);
@@ -244,7 +270,7 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
     auto split = [&](int d, int64_t G0, Plan* out) -> bool {
         const int ss_max = (chunks + d - 1) / d, ss_min = chunks / d;
         const int kr = ss_max * kch;
-        if (!stage_fits(M, kr, gs)) return false;
+        if (!stage_fits(M, kr, gs, d)) return false;
         Plan p{};
         p.kss = kss;
         p.mt = mt;
@@ -261,26 +287,39 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
          * whole length when it is short, else enough for the units in flight plus a few
          * tiles waiting for their sum (at least the units one tile can have in a range, which
          * keeps the ring free of deadlock), plus a 4-byte generation per slot and a counter
-         * per tile.  More workgroups than one per CU shorten the ranges when even that would
-         * not fit. */
+         * per tile.  Where even the smallest ring does not fit beside x and the output blocks,
+         * whole rounds of workgroups (2, 3, ... per CU, one at a time) shorten the ranges: a
+         * partial last round leaves its few workgroups running alone for a whole range.
+         * Measured on MI355X at N = 151936, K = 5120 (us, against growing the workgroups an
+         * eighth at a time with the largest ring): 9 rows 91.8 against 125.6, 10 rows 92.9
+         * against 130.1, 12 rows 114.0 against 118.9, 16 rows 115.7 against 135.1. */
         const int64_t U = (int64_t)T * ss_max;
         int64_t G = std::min<int64_t>(std::max<int64_t>(1, G0), U);
         size_t need = 0;
-        for (;; G = std::min<int64_t>(U, G + std::max<int64_t>(1, G / 8))) {
+        for (int64_t rounds = 2;; G = std::min<int64_t>(U, std::max<int64_t>(1, G0) * rounds++)) {
             const int64_t umax = U / G + ((U % G) ? 1 : 0);
-            const int64_t ring = std::min<int64_t>(umax, 4 * ss_max + 24);
             const int64_t ntl_max = (umax + ss_min - 1) / ss_min + 1;  // tiles a range touches
-            p.umax = (int)umax;
-            p.ring = (int)ring;
-            p.gen_off = p.part_off + (int)ring * 512 * mt;
-            p.cnt_off = p.gen_off + (int)ring * 4;
-            /* then each touched tile's finished sum, and 16 per-row 64-bit keys */
-            p.tout_off = (int)(((size_t)p.cnt_off + (size_t)(ntl_max + 2) * 4 + 15) & ~(size_t)15);
-            p.key_off = p.tout_off + (int)ntl_max * 512 * mt;
-            need = (size_t)p.key_off + 16 * 8;
+            /* the largest ring from 4 tiles + 24 units down to one tile + DFQ_RING_SPARE units
+             * that fits: a smaller ring before more workgroups than CUs */
+            const int64_t ring_hi = std::min<int64_t>(umax, 4 * ss_max + 24);
+            const int64_t ring_lo = std::min<int64_t>(ring_hi, ss_max + DFQ_RING_SPARE);
+            for (int64_t ring = ring_hi; ring >= ring_lo; --ring) {
+                p.umax = (int)umax;
+                p.ring = (int)ring;
+                p.gen_off = p.part_off + (int)ring * 512 * mt;
+                p.cnt_off = p.gen_off + (int)ring * 4;
+                /* then each touched tile's finished sum, and 16 per-row 64-bit keys */
+                p.tout_off =
+                    (int)(((size_t)p.cnt_off + (size_t)(ntl_max + 2) * 4 + 15) & ~(size_t)15);
+                p.key_off = p.tout_off + (int)ntl_max * 512 * mt;
+                need = (size_t)p.key_off + 16 * 8;
+                if (need <= lds_max) break;
+            }
             if (need <= lds_max || G == U) break;
         }
         if (need > lds_max) return false;
+        if (stage_items(M, kr, gs) > DFQ_STAGE_ITEMS(1) && (p.umax < 3 * ss_max || G > G0))
+            return false;
         p.Gkb = (int)G;
         int nslot = 1;
         for (int ss : {ss_min, ss_max})
@@ -311,7 +350,7 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
         if (chunks < dd) return false;
         const int ss_max = (chunks + dd - 1) / dd;
         const int kr = ss_max * kch;
-        if (!stage_fits(M, kr, gs)) return false;
+        if (!stage_fits(M, kr, gs, dd)) return false;
         int64_t G = std::min<int64_t>(std::max<int64_t>(1, G0), T);
         const int64_t tmax = (T + G - 1) / G;
         /* a multiple of 8 workgroups where that leaves the most tiles a workgroup takes as it
@@ -367,19 +406,22 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
          * that fits and whose launch can place each tile's workgroups on one XCD (the parts
          * then meet over a tree of exchanges in its L2): where it holds at most two tiles a
          * workgroup, or where the second pass's split needs more workgroups than the chip has
-         * CUs (a second round of workgroups) and the aligned one deals every workgroup the
-         * same tiles.  Measured on MI355X (us, against the second pass's split, same box):
-         * N = 1024, K = 32768 at 8 rows (two tiles) 12.2 against 13.4; 16 rows at N = 5120,
-         * K = 17408 (eight k-blocks of ten tiles, against 6 x 47 workgroups) 25.1 against
-         * 30.0.  Taken elsewhere it lost: 12 rows at that shape (eight tiles, against
-         * 5 x 51 workgroups) 22.0 against 20.3, 8 rows at N = 5120, K = 32768 (eight tiles)
-         * 30.6 against 26.3; 9 rows gained 0.3 us. */
+         * CUs (whole rounds of workgroups) and the aligned one deals every workgroup the same
+         * tiles, at most kAlignedMaxTiles of them.  Measured on MI355X (us, against the
+         * second pass's split, same box): N = 1024, K = 32768 at 8 rows (two tiles) 12.2
+         * against 13.4; 16 rows at N = 5120, K = 17408 (eight k-blocks of ten tiles, against
+         * 6 x 47 workgroups with the largest ring) 25.1 against 30.0, but 25.0 against 20.0
+         * once the ring's shrinking fits that split in one round of 6 x 42.  Taken elsewhere
+         * it lost: 12 rows at that shape (eight tiles, against 5 x 51 workgroups) 22.0
+         * against 20.3, 8 rows at N = 5120, K = 32768 (eight tiles) 30.6 against 26.3; 9 rows
+         * gained 0.3 us; 56 tiles a workgroup (16 rows, N = 28672, K = 16384, 4-bit g128)
+         * 111.8 against 63.9, 68 tiles (11 rows, N = 34816) 134.1 against 76.5. */
         if (pl->reduce && d >= 4 && DFQ_LONG_CHAIN && num_cus == 256)
             for (int dd = d; dd <= std::min(kAlignedMaxKBlocks, chunks); ++dd) {
                 if (!split_aligned(dd, num_cus / dd, &al) || al.Gkb % 8) continue;
                 const int64_t tpw = (T + al.Gkb - 1) / al.Gkb;  // most tiles a workgroup
-                if (tpw <= 2 ||
-                    ((int64_t)pl->nkb * pl->Gkb > num_cus && T % al.Gkb == 0)) {
+                if (tpw <= 2 || ((int64_t)pl->nkb * pl->Gkb > num_cus && T % al.Gkb == 0 &&
+                                 tpw <= kAlignedMaxTiles)) {
                     *pl = al;
                     return true;
                 }

@@ -33,9 +33,11 @@ CASES = [
     # two k-blocks of stream-K ranges: parts to the workspace at the end, second pass
     (16, 40000, 4096, 4, 64, BF16, True, 1),
     (16, 40000, 4096, 8, 64, F16, False, 1),
-    (13, 40000, 4096, 4, 32, BF16, False, 1),   # group 32, one super-step per chunk half
-    (16, 40000, 4096, 4, 128, F16, True, 1),    # g128
+    (16, 40000, 4096, 4, 32, BF16, False, 1),   # group 32, one super-step per chunk half
     (12, 40000, 6144, 4, 64, BF16, False, 1),
+    # 9..16 rows whose x fits one k-block with a shrunk ring: no second pass
+    (13, 40000, 4096, 4, 32, BF16, False, 0),
+    (16, 40000, 4096, 4, 128, F16, True, 0),    # g128, a ring of ten slots
 ]
 
 

@@ -143,7 +143,7 @@ THREE_BLOCK_CASES = [
 # group 32.
 TREE_CASES = [
     (16, 640, 17408, 4, 64, BF16),           # six k-blocks, one tile a workgroup
-    (16, 5120, 17408, 4, 64, F16),           # eight k-blocks, ten tiles in every workgroup
+    (16, 1024, 24576, 4, 64, F16),           # eight k-blocks, two tiles a workgroup
     (9, 1000, 17408, 4, 64, BF16),           # four k-blocks
     (8, 1024, 32768, 4, 64, BF16),           # six k-blocks at 8 rows
     (12, 1280, 17408, 8, 128, BF16),
@@ -187,6 +187,53 @@ def check_aligned(ctx, oracle, M, N, K, bits, gs, dt, nkb):
         assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
 
 
+# 9..12 rows whose x fits one k-block (up to 16 staged items a thread, a ring shrunk to fit):
+# a stream-K split of one round with the pair exchange at range boundaries
+ONE_K_BLOCK_CASES = [
+    (10, 17408, 5120, 4, 64, BF16),
+    (11, 34816, 5120, 4, 64, F16),           # burst: tiles written at the end
+    (12, 17408, 5120, 8, 64, BF16),
+    (9, 20000, 5120, 4, 64, F16),
+]
+
+# splits that take whole rounds of workgroups (2, 3, ... per CU)
+ROUND_CASES = [
+    (4, 11008, 11008, 4, 64, BF16),          # one-super-step chunks, two rounds
+    (1, 2000, 32768, 4, 64, F16),            # two rounds, the second pass
+]
+
+
+def check_repeat(ctx, oracle, M, N, K, bits, gs, dt, what):
+    import torch
+    c = make_case(M, N, K, bits=bits, gs=gs, xdt=dt, seed=13 * M + N + K + bits + gs,
+                  lbias=(N % 2 == 0))
+    announce(f"{what} M={M} N={N} K={K} bits={bits} gs={gs} dt={dt}")
+    x, w, s, b, lb = upload(c)
+    y = ctx.qmm(x, w, s, b, c.bits, c.gs, lbias=lb)
+    torch.cuda.synchronize()
+    rel, ok = tolerance_check(download(y), oracle.qmm_f64(c))
+    assert rel <= TOL and ok, f"max rel err {rel:.3e}"
+    for _ in range(2):
+        y2 = ctx.qmm(x, w, s, b, c.bits, c.gs, lbias=lb)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
+
+
+@pytest.mark.parametrize("M,N,K,bits,gs,dt", ONE_K_BLOCK_CASES)
+def test_one_k_block_at_nine_to_twelve_rows(ctx, oracle, M, N, K, bits, gs, dt):
+    p = ctx.plan(M, N, K, bits, gs)
+    assert p["nkb"] == 1 and p["Gkb"] <= ctx.num_cus and p["reduce"] == 0, p
+    check_repeat(ctx, oracle, M, N, K, bits, gs, dt, "one k-block")
+
+
+@pytest.mark.parametrize("M,N,K,bits,gs,dt", ROUND_CASES)
+def test_whole_rounds_of_workgroups(ctx, oracle, M, N, K, bits, gs, dt):
+    p = ctx.plan(M, N, K, bits, gs)
+    g0 = ctx.num_cus // p["nkb"]
+    assert p["Gkb"] > g0 and p["Gkb"] % g0 == 0, p
+    check_repeat(ctx, oracle, M, N, K, bits, gs, dt, "rounds")
+
+
 @pytest.mark.parametrize("M,N,K,bits,gs,dt", SIXTEEN_ROW_CASES)
 def test_sixteen_row_shapes_match_oracle(ctx, oracle, M, N, K, bits, gs, dt):
     c = make_case(M, N, K, bits=bits, gs=gs, xdt=dt, seed=M * 1000 + N + K + bits + gs,
@@ -206,7 +253,9 @@ def test_sixteen_row_shapes_match_oracle(ctx, oracle, M, N, K, bits, gs, dt):
     ("c3_down_k17408_n5120", 8),
     ("c4_qkv_8bit_g64", 8), ("c4_o_8bit_g64", 8),
     ("c4_qkv_4bit_g32", 8), ("c4_o_4bit_g32", 8),
-    ("c2_gateup_k5120_n17408", 9), ("c2_gateup_k5120_n17408", 12),
+    ("c2_gateup_k5120_n17408", 9), ("c2_gateup_k5120_n17408", 10),
+    ("c2_gateup_k5120_n17408", 11), ("c2_gateup_k5120_n17408", 12),
+    ("c3_down_k17408_n5120", 12),
     ("c2_gateup_k5120_n17408", 16), ("c3_down_k17408_n5120", 16),
     ("c4_qkv_8bit_g64", 16), ("c4_o_4bit_g32", 16),
 ])

@@ -232,6 +232,35 @@ def test_the_aligned_split_stops_at_twelve_tiles_per_workgroup():
         assert p["aligned"] == 0 and p["reduce"] == 1 and p["nkb"] == 2, (shape, p)
 
 
+def test_up_to_twelve_rows_take_one_k_block_where_it_pays():
+    """9..12 rows at K = 5120 stage one k-block of x (up to 16 items a staging thread) with a
+    ring shrunk to fit, where each range holds at least three tiles and one round of
+    workgroups covers the split; elsewhere two k-blocks stay."""
+    for M in (9, 10, 11, 12):
+        for N in (17408, 34816):
+            p = make_plan(M, N, 5120, 4, 64)
+            assert (p["nkb"], p["Gkb"], p["reduce"]) == (1, 256, 0), (M, N, p)
+            assert p["ring"] >= p["SS"] and p["lds_bytes"] <= 163840, (M, N, p)
+    for shape in [(12, 7168, 5120, 4, 64),     # under two tiles a range
+                  (16, 40000, 4096, 4, 64),    # would need two rounds of workgroups
+                  (13, 17408, 5120, 4, 64)]:   # over 16 items a staging thread
+        assert make_plan(*shape)["nkb"] == 2, shape
+
+
+def test_more_workgroups_than_cus_come_in_whole_rounds():
+    """A split that does not fit one workgroup per CU takes 2, 3, ... times as many, so that
+    no round of workgroups runs with a few of them alone."""
+    for shape in [(9, 151936, 5120, 4, 64), (16, 151936, 5120, 4, 64),
+                  (16, 151936, 5120, 4, 128), (10, 151936, 5120, 4, 128)]:
+        p = make_plan(*shape)
+        g0 = 256 // p["nkb"]
+        assert p["Gkb"] % g0 == 0, (shape, p)
+    for cus in (80, 304):
+        p = make_plan(16, 151936, 5120, 4, 64, cus=cus)
+        assert p["Gkb"] % (cus // p["nkb"]) == 0, (cus, p)
+        replay(p)
+
+
 @pytest.mark.parametrize("shape", SHAPES + EXTRA_SHAPES)
 def test_split_covers_every_unit_once(shape):
     p = make_plan(*shape)
@@ -248,9 +277,11 @@ def test_split_for_other_cu_counts(cus):
 def test_planner_respects_lds_and_staging_limits():
     for (M, N, K, bits, gs) in [(8, 5120, 17408, 4, 64), (1, 5120, 17408, 4, 64),
                                 (8, 64, 65536, 4, 128), (16, 5120, 17408, 4, 64),
-                                (16, 17408, 5120, 8, 32)]:
+                                (16, 17408, 5120, 8, 32), (12, 17408, 5120, 4, 64),
+                                (10, 151936, 5120, 4, 64)]:
         p = make_plan(M, N, K, bits, gs)
-        assert M * p["kr"] // 8 <= 8 * 12 * 64          # x items a workgroup stages
+        items = 16 if (M > 8 and p["nkb"] == 1) else 12  # x items a staging thread holds
+        assert M * p["kr"] // 8 <= 8 * items * 64
         assert p["lds_bytes"] <= 163840
         assert p["SS"] == -(-p["chunks"] // p["nkb"]) and p["kr"] * p["chunks"] == K * p["SS"]
 
@@ -291,10 +322,14 @@ def test_narrow_n_splits_k_in_two_with_one_tile_per_workgroup():
 
 
 def test_tree_splits_only_where_they_measured_faster():
-    # 16 rows at N = 5120, K = 17408: the second pass's split would take 6 x 47 workgroups (a
-    # second round on 256 CUs); eight k-blocks of exactly ten tiles a workgroup instead
+    # 16 rows at N = 5120, K = 17408: with its ring shrunk the second pass's split fits one
+    # round of 6 x 42 workgroups, which measured faster than eight k-blocks of ten tiles
     p = make_plan(16, 5120, 17408, 4, 64)
-    assert (p["nkb"], p["Gkb"], p["aligned"], p["reduce"]) == (8, 32, 1, 0), p
+    assert (p["nkb"], p["Gkb"], p["aligned"], p["reduce"]) == (6, 42, 0, 1), p
+    # many tiles a workgroup (56 and 68 here) keep the second pass's split
+    for shape in [(16, 28672, 16384, 4, 128), (11, 34816, 16384, 4, 128)]:
+        p = make_plan(*shape)
+        assert p["reduce"] == 1 and p["aligned"] == 0, (shape, p)
     # 12 rows there (5 x 51 workgroups, one round) and eight tiles a workgroup at K = 32768:
     # the second pass's split stays
     assert make_plan(12, 5120, 17408, 4, 64)["reduce"] == 1
