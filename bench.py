@@ -687,6 +687,8 @@ def main():
                     default=None,
                     help="only time this form of the 64-layer verify forward (for profiling) "
                          "and print its figures")
+    ap.add_argument("--c5-m", type=int, default=8,
+                    help="rows of the verify forward that --c5-only times (1..16)")
     ap.add_argument("--shape", metavar="M,N,K,BITS,GS[,f16]", default=None,
                     help="time only this call, rotated over enough weight sets to exceed the "
                          "Infinity Cache and replayed like the headline, print its figures and "
@@ -766,7 +768,7 @@ def main():
         W = c5_weights(torch, dev, fused)
         if args.c5_only.endswith("_packed"):
             W = pack_c5(ctx, W)
-        r = chain_c5(torch, ctx, dev, W, form=form)
+        r = chain_c5(torch, ctx, dev, W, M=args.c5_m, form=form)
         print(json.dumps({"c5_" + args.c5_only: r}), flush=True)
         ctx.close()
         return

@@ -622,42 +622,28 @@ __device__ __forceinline__ void pair_exchange(uint64_t* sl, bool (&go)[2], f32x4
 }
 
 /* The same for the gate|up epilogue, which needs g and u of one element summed by the same
- * party: each pair of elements has a g word sg[h] and a u word su[h].  u goes in first; once
- * that has completed, g is exchanged, and the party that gets back a non-zero g word
- * finishes: the other's u is in its u word by then (deposited before the other's g), or came
- * back from our own u exchange (then our u sits in the word and is cleared). */
+ * party: an element's g and u share one 64-bit word (their complements, as in pair_word), so
+ * a single exchange per element carries both in one round trip, and the party that gets back
+ * a non-zero word adds the other's g and u and finishes that element.  Element r of the
+ * lane's four uses word r of sg[0..1], su[0..1].  The two-round form (the u words exchanged
+ * first, then the g words) cost two device round trips per tile: 16 rows at N = 34816,
+ * K = 5120 (every tile exchanged) measured 40.2 us against 31.8 for the plain matmul. */
 template <int SCOPE>
-__device__ __forceinline__ void pair_exchange_gu(uint64_t* sg, uint64_t* su, bool (&go)[2],
+__device__ __forceinline__ void pair_exchange_gu(uint64_t* sg, uint64_t* su, bool (&go)[4],
                                                  f32x4_t& g, f32x4_t& u) {
-    uint64_t ou[2] = {0, 0}, og[2] = {0, 0};
+    uint64_t o[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-        if (go[h])
-            ou[h] = __hip_atomic_exchange(su + h, pair_word(u[2 * h], u[2 * h + 1]),
-                                          __ATOMIC_RELAXED, SCOPE);
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    for (int r = 0; r < 4; ++r)
+        if (go[r])
+            o[r] = __hip_atomic_exchange(r < 2 ? sg + r : su + (r - 2), pair_word(g[r], u[r]),
+                                         __ATOMIC_RELAXED, SCOPE);
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-        if (go[h])
-            og[h] = __hip_atomic_exchange(sg + h, pair_word(g[2 * h], g[2 * h + 1]),
-                                          __ATOMIC_RELAXED, SCOPE);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        go[h] = og[h] != 0;
-        if (!go[h]) continue;
-        uint64_t upw;
-        if (ou[h]) {
-            upw = ou[h];
-            __hip_atomic_store(su + h, 0ull, __ATOMIC_RELAXED, SCOPE);
-        } else {
-            upw = __hip_atomic_exchange(su + h, 0ull, __ATOMIC_RELAXED, SCOPE);
-        }
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            g[2 * h + e] += pair_value(og[h], e);
-            u[2 * h + e] += pair_value(upw, e);
-        }
-        __hip_atomic_store(sg + h, 0ull, __ATOMIC_RELAXED, SCOPE);
+    for (int r = 0; r < 4; ++r) {
+        go[r] = o[r] != 0;
+        if (!go[r]) continue;
+        g[r] += pair_value(o[r], 0);
+        u[r] += pair_value(o[r], 1);
+        __hip_atomic_store(r < 2 ? sg + r : su + (r - 2), 0ull, __ATOMIC_RELAXED, SCOPE);
     }
 }
 
@@ -723,19 +709,20 @@ __device__ __forceinline__ void publish(const QmmParams& p, const KBlock& kbk, i
     }
     bool go[2] = {true, true};
     if (p.epi) {
-        /* lanes n < 8 hold g and take u from lane n + 8 (g words, then u words) */
+        /* lanes n < 8 hold g and take u from lane n + 8 (one (g, u) word per element) */
         f32x4_t u;
 #pragma unroll
         for (int r = 0; r < 4; ++r) u[r] = dpp_f32<0x128>(v[r]);
         if (!act || n >= 8) return;
         f32x4_t g = v;
+        bool ge[4] = {true, true, true, true};
 #pragma unroll
         for (int L = 1; L <= kTreeLevels; ++L) {
             const int r = ((leaf >> L) * 2 + 1) << (L - 1);
-            if (r >= nparts || !(go[0] || go[1])) continue;
+            if (r >= nparts || !(ge[0] || ge[1] || ge[2] || ge[3])) continue;
             uint64_t* sj = tb + (lw + (uint32_t)((r - 1) * 64 * p.mt));
-            if (l2) pair_exchange_gu<kL2Scope>(sj, sj + 32, go, g, u);
-            else pair_exchange_gu<kDeviceScope>(sj, sj + 32, go, g, u);
+            if (l2) pair_exchange_gu<kL2Scope>(sj, sj + 32, ge, g, u);
+            else pair_exchange_gu<kDeviceScope>(sj, sj + 32, ge, g, u);
         }
         const int H = p.N / 2;
         float lbg = 0.0f, lbu = 0.0f;
@@ -746,7 +733,7 @@ __device__ __forceinline__ void publish(const QmmParams& p, const KBlock& kbk, i
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int m = 4 * q + r;
-            if (go[r >> 1] && m < p.M)
+            if (ge[r] && m < p.M)
                 put16((uint16_t*)p.y + (size_t)m * H + t * 8 + n,
                       silu_mul_round<F16>(g[r] + lbg, u[r] + lbu));
         }

@@ -31,6 +31,8 @@ CASES = [
     (8, 2560, 17408, 4, 64, BF16, True),    # three k-blocks of whole tiles: chained exchange
     (7, 512, 16384, 8, 64, F16, False),     # the same, one tile per workgroup
     (16, 1504, 7680, 4, 64, BF16, True),    # the same with two row tiles
+    (16, 17408, 5120, 4, 64, BF16, False),  # two k-blocks: every tile's (g, u) words exchanged
+    (16, 512, 24576, 4, 64, F16, True),     # eight k-blocks: a tree of (g, u) exchanges
 ]
 
 
