@@ -621,29 +621,46 @@ __device__ __forceinline__ void pair_exchange(uint64_t* sl, bool (&go)[2], f32x4
     }
 }
 
-/* The same for the gate|up epilogue, which needs g and u of one element summed by the same
- * party: an element's g and u share one 64-bit word (their complements, as in pair_word), so
- * a single exchange per element carries both in one round trip, and the party that gets back
- * a non-zero word adds the other's g and u and finishes that element.  Element r of the
- * lane's four uses word r of sg[0..1], su[0..1].  The two-round form (the u words exchanged
- * first, then the g words) cost two device round trips per tile: 16 rows at N = 34816,
- * K = 5120 (every tile exchanged) measured 40.2 us against 31.8 for the plain matmul. */
+/* The gate|up epilogue of the 1..8-row kernels, which needs g and u of one element summed by
+ * the same party, on the lanes that hold g (with u taken from the partner lane): each pair of
+ * elements has a g word sg[h] and a u word su[h].  u goes in first; once that has completed,
+ * g is exchanged, and the party that gets back a non-zero g word finishes: the other's u is
+ * in its u word by then (deposited before the other's g), or came back from our own u
+ * exchange (then our u sits in the word and is cleared).  The 16-row form (publish) measured
+ * 0.3 us slower here (24.6 against 24.3 us at 8 rows, 2 x 17408 x 5120, where only the tiles
+ * cut by a range are exchanged). */
 template <int SCOPE>
-__device__ __forceinline__ void pair_exchange_gu(uint64_t* sg, uint64_t* su, bool (&go)[4],
+__device__ __forceinline__ void pair_exchange_gu(uint64_t* sg, uint64_t* su, bool (&go)[2],
                                                  f32x4_t& g, f32x4_t& u) {
-    uint64_t o[4] = {0, 0, 0, 0};
+    uint64_t ou[2] = {0, 0}, og[2] = {0, 0};
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-        if (go[r])
-            o[r] = __hip_atomic_exchange(r < 2 ? sg + r : su + (r - 2), pair_word(g[r], u[r]),
-                                         __ATOMIC_RELAXED, SCOPE);
+    for (int h = 0; h < 2; ++h)
+        if (go[h])
+            ou[h] = __hip_atomic_exchange(su + h, pair_word(u[2 * h], u[2 * h + 1]),
+                                          __ATOMIC_RELAXED, SCOPE);
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        go[r] = o[r] != 0;
-        if (!go[r]) continue;
-        g[r] += pair_value(o[r], 0);
-        u[r] += pair_value(o[r], 1);
-        __hip_atomic_store(r < 2 ? sg + r : su + (r - 2), 0ull, __ATOMIC_RELAXED, SCOPE);
+    for (int h = 0; h < 2; ++h)
+        if (go[h])
+            og[h] = __hip_atomic_exchange(sg + h, pair_word(g[2 * h], g[2 * h + 1]),
+                                          __ATOMIC_RELAXED, SCOPE);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        go[h] = og[h] != 0;
+        if (!go[h]) continue;
+        uint64_t upw;
+        if (ou[h]) {
+            upw = ou[h];
+            __hip_atomic_store(su + h, 0ull, __ATOMIC_RELAXED, SCOPE);
+        } else {
+            upw = __hip_atomic_exchange(su + h, 0ull, __ATOMIC_RELAXED, SCOPE);
+        }
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            g[2 * h + e] += pair_value(og[h], e);
+            u[2 * h + e] += pair_value(upw, e);
+        }
+        __hip_atomic_store(sg + h, 0ull, __ATOMIC_RELAXED, SCOPE);
     }
 }
 
@@ -675,7 +692,7 @@ __device__ __forceinline__ void pair_exchange_gu(uint64_t* sg, uint64_t* su, boo
  * The workspace is zero again when the kernel ends.  Workgroups on different XCDs exchange
  * these partials: every access to a slot is an agent-scope atomic (coherent across the
  * XCDs' L2s without a whole-cache write-back or invalidate). */
-template <bool F16, bool AM>
+template <bool F16, int MT, bool AM>
 __device__ __forceinline__ void publish(const QmmParams& p, const KBlock& kbk, int t, int kb,
                                         int lane, f32x4_t v, uint64_t (&best)[4]) {
     const int q = lane >> 4, n = lane & 15;
@@ -708,21 +725,20 @@ __device__ __forceinline__ void publish(const QmmParams& p, const KBlock& kbk, i
         l2 = owner_wg(r0, per, rem) == owner_wg(r0 + 1, per, rem);
     }
     bool go[2] = {true, true};
-    if (p.epi) {
-        /* lanes n < 8 hold g and take u from lane n + 8 (one (g, u) word per element) */
+    if (MT == 1 && p.epi) {
+        /* lanes n < 8 hold g and take u from lane n + 8 (g words, then u words) */
         f32x4_t u;
 #pragma unroll
         for (int r = 0; r < 4; ++r) u[r] = dpp_f32<0x128>(v[r]);
         if (!act || n >= 8) return;
         f32x4_t g = v;
-        bool ge[4] = {true, true, true, true};
 #pragma unroll
         for (int L = 1; L <= kTreeLevels; ++L) {
             const int r = ((leaf >> L) * 2 + 1) << (L - 1);
-            if (r >= nparts || !(ge[0] || ge[1] || ge[2] || ge[3])) continue;
+            if (r >= nparts || !(go[0] || go[1])) continue;
             uint64_t* sj = tb + (lw + (uint32_t)((r - 1) * 64 * p.mt));
-            if (l2) pair_exchange_gu<kL2Scope>(sj, sj + 32, ge, g, u);
-            else pair_exchange_gu<kDeviceScope>(sj, sj + 32, ge, g, u);
+            if (l2) pair_exchange_gu<kL2Scope>(sj, sj + 32, go, g, u);
+            else pair_exchange_gu<kDeviceScope>(sj, sj + 32, go, g, u);
         }
         const int H = p.N / 2;
         float lbg = 0.0f, lbu = 0.0f;
@@ -733,9 +749,49 @@ __device__ __forceinline__ void publish(const QmmParams& p, const KBlock& kbk, i
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int m = 4 * q + r;
-            if (ge[r] && m < p.M)
+            if (go[r >> 1] && m < p.M)
                 put16((uint16_t*)p.y + (size_t)m * H + t * 8 + n,
                       silu_mul_round<F16>(g[r] + lbg, u[r] + lbu));
+        }
+        return;
+    }
+    if (p.epi) {
+        /* 9..16 rows.  Lane n < 8 of a 16-lane row holds g of column n for its four rows,
+         * lane n + 8 the u of that column.  Each takes its partner's four values (row_ror:8), and each pair
+         * of lanes splits the rows: the g lane carries rows 0 and 1 of the four, the u lane
+         * rows 2 and 3, each element as one (g, u) word of the plain exchange.  Every lane
+         * of the tile then exchanges two words in one round trip, and the party that
+         * completes an element has its g and u together.  With the u words exchanged first
+         * and then the g words on half the lanes (two round trips), 16 rows at
+         * 2 x 17408 x 5120 (every tile exchanged) measured 40.0 us; with one (g, u) word per
+         * element on half the lanes, 35.4 us; this form 32.8 us. */
+        f32x4_t o;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = dpp_f32<0x128>(v[r]);
+        if (!act) return;
+        const bool gl = n < 8;
+        const int e0 = gl ? 0 : 2;  // the first of this lane's two rows (of four)
+        f32x4_t w = gl ? f32x4_t{v[0], o[0], v[1], o[1]} : f32x4_t{o[2], v[2], o[3], v[3]};
+#pragma unroll
+        for (int L = 1; L <= kTreeLevels; ++L) {
+            const int r = ((leaf >> L) * 2 + 1) << (L - 1);
+            if (r >= nparts || !(go[0] || go[1])) continue;
+            uint64_t* sj = tb + (lw + (uint32_t)((r - 1) * 64 * p.mt));
+            if (l2) pair_exchange<kL2Scope>(sj, go, w);
+            else pair_exchange<kDeviceScope>(sj, go, w);
+        }
+        const int H = p.N / 2, j = n & 7;
+        float lbg = 0.0f, lbu = 0.0f;
+        if (p.lbias) {
+            lbg = elem_to_f32<F16>(((const uint16_t*)p.lbias)[t * 16 + j]);
+            lbu = elem_to_f32<F16>(((const uint16_t*)p.lbias)[t * 16 + 8 + j]);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int m = 4 * q + e0 + h;
+            if (go[h] && m < p.M)
+                put16((uint16_t*)p.y + (size_t)m * H + t * 8 + j,
+                      silu_mul_round<F16>(w[2 * h] + lbg, w[2 * h + 1] + lbu));
         }
         return;
     }
@@ -878,7 +934,7 @@ __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
                     else if (lane < 32 * MT)  /* summed by the second pass: no round trip here */
                         put_tile4(tile_slot(p, t, kb, cl - tile_first_owner(kbk, t), lane), v);
                 } else {
-                    publish<F16, AM>(p, kbk, t, kb, lane, v, best);
+                    publish<F16, MT, AM>(p, kbk, t, kb, lane, v, best);
                 }
                 if (lane == 0) tcnt[tlb] = kTileOut;
                 ++found;
