@@ -2032,7 +2032,7 @@ extern "C" __global__ void __launch_bounds__(256) dfq_silu_mul_f16(const uint16_
  * skipped.  The last block to arrive (counter) turns the keys into tokens, finds the leading
  * run of tokens[i] == proposals[i] (i < M-1), writes both, and re-arms keys and counter.
  *
- * A thread issues both of its 16-byte loads before using either (rows 16-byte aligned: V a
+ * A thread issues all of its 16-byte loads before using any (rows 16-byte aligned: V a
  * multiple of 8); other rows take 2-byte loads, four in flight.  Keys are only touched by
  * agent-scope atomics, so a block's max is visible to the last block once it has completed
  * (vmcnt) before the block's relaxed counter increment: no cache write-back or invalidate. */
@@ -2049,14 +2049,15 @@ __device__ __forceinline__ void argmax_accept(const uint16_t* logits, int M, int
     const uint16_t* lr = logits + (size_t)row * V;
     uint64_t best = 0;
     if ((V & 7) == 0 && ((uintptr_t)logits & 15) == 0) {
-        u32x4_t v[2];
+        constexpr int UN = C / 2048;  // 16-byte loads a thread, all in flight before any use
+        u32x4_t v[UN];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < UN; ++u) {
             const int i = lo + (u * 256 + tid) * 8;
             if (i < hi) v[u] = *(const u32x4_t*)(lr + i);
         }
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < UN; ++u) {
             const int i = lo + (u * 256 + tid) * 8;
             if (i >= hi) continue;
 #pragma unroll

@@ -129,7 +129,13 @@ typedef struct QmvParams {
     int32_t lds_out_off;    /* byte offset of the workgroup's outputs [M][rows_max] fp32 */
 } QmvParams;
 
-/* Logits per block of dfq_argmax_accept: 256 threads x two 16-byte loads of 8 logits. */
-#define DFQ_ACCEPT_CHUNK 4096
+/* Logits per block of dfq_argmax_accept: 256 threads x DFQ_ACCEPT_CHUNK / 2048 16-byte loads
+ * of 8 logits (a multiple of 2048).  Fewer, longer blocks mean fewer arrivals on the one
+ * device-wide counter; measured on MI355X over [M, 151936] bf16 logits (us, M = 8 / 12 / 16):
+ * 4096 logits a block 8.8 / 11.9 / 13.4, 8192 6.6 / 8.4 / 9.3, 16384 7.0 / 8.0 / 8.6.  The
+ * standalone accept serves the LM heads of 10..16 rows (below that it is fused). */
+#ifndef DFQ_ACCEPT_CHUNK
+#define DFQ_ACCEPT_CHUNK 16384
+#endif
 
 #endif
