@@ -634,25 +634,31 @@ def c5_trace_summary(path, layers=64):
                              r["Kernel_Name"]))
     rows.sort()
     ends = [i for i, r in enumerate(rows) if r[2].endswith("_am") or "argmax_accept" in r[2]]
-    fwds = []
+    fwds, tail = [], 0
     for i0, i1 in zip(ends, ends[1:]):
         seg = rows[i0 + 1:i1 + 1]
-        if len(seg) < layers + 1 or (len(seg) - 1) % layers:
-            continue
-        fwds.append(seg)
+        # the LM head's dispatches: the fused head, or the head, its second pass and the
+        # accept (splits with a second pass)
+        for tl in (1, 2, 3):
+            if len(seg) >= layers + tl and (len(seg) - tl) % layers == 0:
+                fwds.append(seg)
+                tail = tl
+                break
     if not fwds:
         return {"forwards": 0}
-    per = (len(fwds[0]) - 1) // layers
+    fwds = [seg for seg in fwds if len(seg) == len(fwds[0])]
+    per = (len(fwds[0]) - tail) // layers
     ops = []
-    for j in range(per + 1):
+    for j in range(per + tail):
         dur, gap = [], []
         for seg in fwds:
-            idx = [j + per * li for li in range(layers)] if j < per else [len(seg) - 1]
+            idx = ([j + per * li for li in range(layers)] if j < per
+                   else [len(seg) - tail + (j - per)])
             for i in idx:
                 dur.append(seg[i][1] - seg[i][0])
                 if i:
                     gap.append(seg[i][0] - seg[i - 1][1])
-        name = fwds[0][j][2] if j < per else fwds[0][-1][2]
+        name = fwds[0][j][2] if j < per else fwds[0][len(fwds[0]) - tail + (j - per)][2]
         ops.append({"kernel": name, "mean_us": round(sum(dur) / len(dur) / 1e3, 2),
                     "gap_before_us": round(sum(gap) / max(1, len(gap)) / 1e3, 2)})
     spans = [(seg[-1][1] - seg[0][0]) / 1e3 for seg in fwds]
