@@ -673,7 +673,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--sets", type=int, default=8, help="rotated weight sets")
-    ap.add_argument("--ms", default="1,2,3,4,5,6,8,16")
+    ap.add_argument("--ms", default="1,2,3,4,5,6,8,12,16")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-chain", action="store_true",
