@@ -74,6 +74,7 @@ CASES = [  # (M, N, K, bits, gs, dtype, linear bias)
     (8, 5120, 17408, 4, 64, BF16, True),    # three k-blocks of whole tiles
     (8, 1024, 5120, 4, 64, BF16, False),    # narrow: two k-blocks, one tile each
     (12, 40000, 4096, 4, 64, F16, False),   # 12 rows, pair exchange
+    (12, 17408, 5120, 4, 64, BF16, True),   # 12 rows in one k-block: 16 x items a thread
     (8, 1024, 32768, 4, 64, BF16, True),    # the reduce split's second pass
     (8, 7168, 5120, 8, 64, BF16, False),
     (5, 5120, 5120, 4, 32, BF16, True),
