@@ -26,15 +26,19 @@ def noalloc(ctx, c, x, w, s, b, lb, y, stream=None):
 
 
 # decreasing in size (M, N, K, bits, gs, dtype, linear bias, split the planner must give):
+#   12 rows of the headline shape: one k-block with 16 staged x items a thread;
 #   the headline shape: one k-block, the pair exchange of tiles shared by two workgroups;
 #   a 16-row reduce split: parts in workspace slots, summed and re-zeroed by the second pass;
+#   a one-row split over two whole rounds of workgroups;
 #   the down projection: three k-blocks of whole tiles, a chain of two pair exchanges;
 #   16 rows of 8-bit: two k-blocks, each tile in one workgroup of each, paired;
 #   a narrow N at six rows: two k-blocks of one tile per workgroup;
 #   a tiny shape that needs no workspace
 CASES = [
+    (12, 17408, 5120, 4, 64, BF16, False, dict(nkb=1, Gkb=256, reduce=0)),
     (8, 17408, 5120, 4, 64, BF16, False, dict(nkb=1, reduce=0)),
     (16, 40000, 4096, 4, 64, BF16, False, dict(reduce=1)),
+    (4, 11008, 11008, 4, 64, F16, True, dict(nkb=1, Gkb=512, reduce=0)),
     (8, 5120, 17408, 4, 64, BF16, True, dict(nkb=3, aligned=1, reduce=0)),
     (16, 4096, 5120, 8, 64, F16, False, dict(nkb=2, reduce=0, nslot_kb=1)),
     (6, 1024, 5120, 4, 128, BF16, True, dict(nkb=2, reduce=0)),
