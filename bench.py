@@ -31,7 +31,7 @@ Method:
 --profile-timed dispatches the matmul only as graph replays (one warm-up replay, then the
 timed ones), so that `rocprofv3 --kernel-trace --stats` averages the calls the figures time.
 
-Prints ONE JSON line.  --gpus > 1 is refused: this build measures one GPU.
+Prints ONE JSON line.  --gpus > 1 is refused: the benchmark measures one GPU.
 """
 import argparse
 import json
@@ -299,7 +299,7 @@ def time_copy(torch, stream, nbytes, nsets, steps):
     """A plain device copy moving `nbytes` per launch (nbytes/2 read, nbytes/2 written),
     rotated over buffers larger than the Infinity Cache and timed back to back like the
     matmul: the launch-for-launch bandwidth a memory-bound kernel of this size reaches on
-    the box.  Microseconds per copy."""
+    this GPU.  Microseconds per copy."""
     dev = torch.device("cuda:0")
     half = nbytes // 2
     src = [torch.ones(half, dtype=torch.uint8, device=dev) for _ in range(nsets)]

@@ -2,8 +2,8 @@
  * qmm_oracle.c -- CPU restatement of DFlashKit's small-M affine-quantised matmul.
  *
  * TEST INFRASTRUCTURE ONLY.  Nothing in the product path may link, load or call
- * this file: it is the checker that tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py compare the HIP kernels against.
+ * this file: it is the reference result that tests/, __graft_entry__.smoke() and
+ * the cpu_baseline leg of bench.py compare the HIP kernels against.
  *
  * What it restates (paths relative to the reference repository root):
  *

@@ -1,7 +1,8 @@
 """CPU oracle for the small-M affine-quantised matmul (TEST INFRASTRUCTURE ONLY).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py``
-may import this module, and only as the checker: nothing in the product path calls it.
+may import this module, and only to compare the HIP kernels against: nothing in the
+product path calls it.
 
 It holds two independent restatements of the same arithmetic -- numpy code here and the
 C code in ``qmm_oracle.c`` (loaded through ctypes) -- so that each pins the other, plus the
