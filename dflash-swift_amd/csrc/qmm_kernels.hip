@@ -75,14 +75,19 @@ constexpr uint32_t kTileDone = 0x80000000u;  // tile counter value once its unit
 constexpr uint32_t kTileOut = 0x80000001u;   // ... and once its publisher wave wrote it
 constexpr int kThreads = kWaves * 64;        // streaming threads
 #ifndef DFQ_PUBLISHERS
-/* publisher waves per workgroup; the host is built with the same value.  A second one takes
- * half the tiles, so that two tiles' fix-ups (device-scope round trips) overlap: measured on
- * MI355X, M = 8, K = 5120: N = 17408 16.6 -> 15.7 us, N = 5120 10.6 -> 9.6 us; more than two
- * gained nothing further. */
-#define DFQ_PUBLISHERS 2
+/* publisher waves per workgroup (one per SIMD); the host is built with the same value.  They
+ * take the workgroup's tiles round-robin, so that several tiles' fix-ups (round trips through
+ * the L2) overlap.  Measured on MI355X, M = 8, K = 5120: N = 17408 16.6 -> 15.7 us and
+ * N = 5120 10.6 -> 9.6 us from one publisher to two.  From two to four, 8 rows stay within
+ * 0.15 us at every shape, but 13..16 rows over two k-blocks, where every tile is exchanged,
+ * gain (us, 4-bit g64, K = 5120): 16 rows N = 17408 18.16 -> 16.72, 13 rows 18.05 -> 16.59,
+ * N = 34816 31.97 -> 27.82 (g128 33.49 -> 29.01), the gate|up epilogue 32.70 -> 28.34, the LM
+ * head 115.4 -> 114.9; the 16-row verify forward 4,918 -> 4,613 us (8 rows 3,949 -> 3,953). */
+#define DFQ_PUBLISHERS 4
 #endif
 constexpr int kPublishers = DFQ_PUBLISHERS;
 constexpr int kBlock = kThreads + 64 * kPublishers;  // + the publisher waves
+static_assert(kBlock <= 1024, "a workgroup holds at most 1024 threads");
 /* x is staged by the first 8 waves only (two per SIMD).  A workgroup's waves start over
  * about 1 us, and staging is VALU-bound: spread over all 12 streaming waves, the last waves
  * to start finish it last and hold up the staging barrier.  With the late waves free of it
@@ -911,15 +916,6 @@ __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
                          (!p.burst || exchange_tile(p, ta + tile_of(rk), a, b, SS));
         remaining += __builtin_popcountll(__builtin_amdgcn_ballot_w64(own));
     }
-    /* A workgroup of 9..16 rows that exchanges at least 8 tiles with the other k-block (no
-     * second pass) has its publishers on the critical path: while one works on ready tiles,
-     * it takes issue priority over the streaming waves of its SIMD (the SIMD otherwise
-     * favours the older waves, and the publishers are the workgroup's last).  Measured on
-     * MI355X, 4-bit at K = 5120, 16 rows (us, against no raise): N = 34816 31.0 against 32.0,
-     * g128 31.6 against 33.8, the gate|up epilogue 31.5 against 32.9, N = 17408 18.2 against
-     * 18.3, 13 rows 18.0 against 18.2; the 16-row verify forward 4,856 against 4,921 us.
-     * Raised for every split, it cost 0.2-0.3 us at 8 rows with K = 17408 and on 4-bit g32. */
-    const bool raise = MT == 2 && p.nkb > 1 && !p.reduce && ntl >= 8;
     while (remaining > 0) {
         int found = 0;
         for (int base = 0; base < nrank; base += 64) {
@@ -929,7 +925,6 @@ __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
                 ready = __hip_atomic_load(tcnt + tile_of(rk), __ATOMIC_ACQUIRE,
                                           __HIP_MEMORY_SCOPE_WORKGROUP) == kTileDone;
             uint64_t m = __builtin_amdgcn_ballot_w64(ready);
-            if (raise && m) __builtin_amdgcn_s_setprio(2);
             while (m) {
                 const int bit = __builtin_ctzll(m);
                 m &= m - 1;
@@ -951,7 +946,6 @@ __device__ void publisher_wave(const QmmParams& p, int kb, int cl, int a, int b,
             }
         }
         remaining -= found;
-        if (raise) __builtin_amdgcn_s_setprio(0);
         if (!found) __builtin_amdgcn_s_sleep(1);
     }
     if constexpr (AM) {

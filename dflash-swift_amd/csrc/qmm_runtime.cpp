@@ -51,7 +51,7 @@ thread_local std::string g_last_error;
 constexpr int kWaves = DFQ_WAVES;
 constexpr int kThreads = kWaves * 64;             // qmm_mt8 streaming threads
 #ifndef DFQ_PUBLISHERS
-#define DFQ_PUBLISHERS 2               // must match the kernels' build
+#define DFQ_PUBLISHERS 4               // must match the kernels' build
 #endif
 constexpr int kBlockThreads = kThreads + 64 * DFQ_PUBLISHERS;  // + the publisher waves
 /* 16-byte x chunks a staging thread holds for a k-block of kr elements at M rows (0 when no
