@@ -65,11 +65,14 @@ static int stage_items(int M, int kr, int gs) {
  * x is read for enough weights: such a split must be one k-block (up to 12 rows at
  * K = 5120), and is kept only where each range holds at least three tiles' units and one
  * round of workgroups covers the split (checked by the caller).  Measured on MI355X (us,
- * one k-block against two): N = 17408, K = 5120 at 10 rows 16.2 against 18.4, 11 rows 16.6
- * against 18.2, 12 rows 16.7 against 18.2; gate|up N = 34816 at 12 rows 27.9 against 31.7;
- * N = 7168 at 12 rows (1.8 tiles a range) 12.2 against 11.45; 16 rows at N = 40000,
- * K = 4096 (two rounds of workgroups) 31.1 against 28.6, N = 80000 (four) 58.6 against
- * 49.0. */
+ * one k-block against two) with two publisher waves: N = 17408, K = 5120 at 10 rows 16.2
+ * against 18.4, 11 rows 16.6 against 18.2, 12 rows 16.7 against 18.2; gate|up N = 34816 at
+ * 12 rows 27.9 against 31.7; N = 7168 at 12 rows (1.8 tiles a range) 12.2 against 11.45;
+ * 16 rows at N = 40000, K = 4096 (two rounds of workgroups) 31.1 against 28.6, N = 80000
+ * (four) 58.6 against 49.0.  With four, two k-blocks cost less but still more: N = 17408 at
+ * 9 rows 16.0 against 17.0, 10 rows 16.5 against 17.1, 12 rows 16.8 against 17.2 (8-bit
+ * 23.5 against 25.2, g128 at 9 rows 14.9 against 17.0); N = 34816 at 9 rows 25.5 against
+ * 28.2, at 12 rows 28.1 against 27.9. */
 static bool stage_fits(int M, int kr, int gs, int nkb) {
     const int items = stage_items(M, kr, gs);
     if (items < 1) return false;
