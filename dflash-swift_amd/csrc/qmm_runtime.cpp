@@ -229,6 +229,9 @@ static constexpr int kBurstTiles = 8;
  * 29.6 against 28.8-29.3; N = 60000 (thirty) 42.5 against 38.9-39.3; N = 80000 (forty) 54.2
  * against 48.6-48.8. */
 static constexpr int kAlignedMaxTiles = 12;
+/* Most tiles a workgroup of an aligned split of four or more k-blocks (the tree of exchanges)
+ * holds at 9..16 rows, where the second pass's split fits one round of workgroups. */
+static constexpr int kAlignedRowsMaxTiles = 8;
 /* Most k-blocks of an aligned split: from four on, each tile's parts meet over a tree of
  * exchanges (k-blocks - 1 of them, ceil(log2 k-blocks) deep), taken where the launch can place
  * a tile's workgroups on one XCD so that the exchanges run in its L2 (the whole chip,
@@ -418,13 +421,23 @@ bool make_plan(int M, int N, int K, int bits, int gs, int num_cus, size_t lds_ma
          * it lost: 12 rows at that shape (eight tiles, against 5 x 51 workgroups) 22.0
          * against 20.3, 8 rows at N = 5120, K = 32768 (eight tiles) 30.6 against 26.3; 9 rows
          * gained 0.3 us; 56 tiles a workgroup (16 rows, N = 28672, K = 16384, 4-bit g128)
-         * 111.8 against 63.9, 68 tiles (11 rows, N = 34816) 134.1 against 76.5. */
+         * 111.8 against 63.9, 68 tiles (11 rows, N = 34816) 134.1 against 76.5.
+         * With four publisher waves, 9..16 rows also take it where it needs no more k-blocks
+         * than the second pass's split and a workgroup holds at most 8 tiles (us, same
+         * comparison, 4-bit g64): N = 5120, K = 17408 at 9 rows 16.86 against 18.15, 10 rows
+         * 16.94 against 18.29, 12 rows 18.60 against 19.30, 13 rows 18.33 against 19.83, 15
+         * rows 18.57 against 20.17; N = 4096, K = 16384 at 16 rows 16.32 against 18.24;
+         * N = 7168, K = 14336 at 10 rows 18.39 against 19.80; g128 at 11 rows 17.37 against
+         * 18.72; 8-bit at 12 rows 25.37 against 25.37.  With more k-blocks than the second
+         * pass's split it lost: 16 rows at N = 5120 (eight k-blocks of ten tiles against six)
+         * 20.76 against 20.52, 4-bit g32 at 10 rows (six against four) 22.05 against 21.31. */
         if (pl->reduce && d >= 4 && DFQ_LONG_CHAIN && num_cus == 256)
             for (int dd = d; dd <= std::min(kAlignedMaxKBlocks, chunks); ++dd) {
                 if (!split_aligned(dd, num_cus / dd, &al) || al.Gkb % 8) continue;
                 const int64_t tpw = (T + al.Gkb - 1) / al.Gkb;  // most tiles a workgroup
-                if (tpw <= 2 || ((int64_t)pl->nkb * pl->Gkb > num_cus && T % al.Gkb == 0 &&
-                                 tpw <= kAlignedMaxTiles)) {
+                if (tpw <= 2 || (mt == 2 && dd == d && tpw <= kAlignedRowsMaxTiles) ||
+                    ((int64_t)pl->nkb * pl->Gkb > num_cus && T % al.Gkb == 0 &&
+                     tpw <= kAlignedMaxTiles)) {
                     *pl = al;
                     return true;
                 }

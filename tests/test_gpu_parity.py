@@ -158,6 +158,24 @@ def test_tree_of_exchanges_matches_oracle_and_repeats(ctx, oracle, M, N, K, bits
     check_aligned(ctx, oracle, M, N, K, bits, gs, dt, p["nkb"])
 
 
+# 9..16 rows at long K whose second pass's split fits one round: the tree of as many k-blocks,
+# up to 8 tiles a workgroup
+ROWS_TREE_CASES = [
+    (9, 5120, 17408, 4, 64, BF16),           # four k-blocks, five tiles a workgroup
+    (13, 5120, 17408, 4, 64, F16),           # six k-blocks, eight tiles
+    (16, 4096, 16384, 4, 64, BF16),          # six k-blocks
+    (11, 5120, 17408, 4, 128, BF16),
+    (12, 5120, 17408, 8, 64, F16),           # five k-blocks, 8-bit
+]
+
+
+@pytest.mark.parametrize("M,N,K,bits,gs,dt", ROWS_TREE_CASES)
+def test_tree_at_nine_to_sixteen_rows(ctx, oracle, M, N, K, bits, gs, dt):
+    p = ctx.plan(M, N, K, bits, gs)
+    assert 4 <= p["nkb"] <= 8 and -(-((N + 15) // 16) // p["Gkb"]) <= 8, p
+    check_aligned(ctx, oracle, M, N, K, bits, gs, dt, p["nkb"])
+
+
 @pytest.mark.parametrize("M,N,K,bits,gs,dt", ALIGNED_CASES)
 def test_aligned_split_matches_oracle_and_repeats(ctx, oracle, M, N, K, bits, gs, dt):
     check_aligned(ctx, oracle, M, N, K, bits, gs, dt, 2)

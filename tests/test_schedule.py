@@ -330,9 +330,15 @@ def test_tree_splits_only_where_they_measured_faster():
     for shape in [(16, 28672, 16384, 4, 128), (11, 34816, 16384, 4, 128)]:
         p = make_plan(*shape)
         assert p["reduce"] == 1 and p["aligned"] == 0, (shape, p)
-    # 12 rows there (5 x 51 workgroups, one round) and eight tiles a workgroup at K = 32768:
-    # the second pass's split stays
-    assert make_plan(12, 5120, 17408, 4, 64)["reduce"] == 1
+    # 9..15 rows there: the tree of as many k-blocks as the second pass's split, at most 8
+    # tiles a workgroup (12 rows: five k-blocks of 48 workgroups, seven tiles each)
+    for m, nkb in [(9, 4), (10, 4), (12, 5), (13, 6), (15, 6)]:
+        p = make_plan(m, 5120, 17408, 4, 64)
+        assert (p["nkb"], p["aligned"], p["reduce"]) == (nkb, 1, 0), (m, p)
+        assert -(-320 // p["Gkb"]) <= 8 and p["Gkb"] % 8 == 0, (m, p)
+    # ... but not where the tree needs more k-blocks than the second pass's split (4-bit g32
+    # at 10 rows: six against four), nor at 8 rows (eight tiles a workgroup at K = 32768)
+    assert make_plan(10, 5120, 17408, 4, 32)["reduce"] == 1
     assert make_plan(8, 5120, 32768, 4, 64)["reduce"] == 1
     # other CU counts (another partition of the chip) never take a tree of four or more
     for cus in (32, 64, 128, 304):
