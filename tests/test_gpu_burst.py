@@ -30,11 +30,12 @@ CASES = [
     (5, 40000, 1024, 8, 64, F16, True, 0),      # 8-bit, two chunks per tile
     (8, 36000, 1024, 4, 32, BF16, False, 0),    # group 32
     (3, 40000, 2048, 8, 128, BF16, True, 0),    # 8-bit g128
-    # two k-blocks of stream-K ranges: parts to the workspace at the end, second pass
-    (16, 40000, 4096, 4, 64, BF16, True, 1),
-    (16, 40000, 4096, 8, 64, F16, False, 1),
-    (16, 40000, 4096, 4, 32, BF16, False, 1),   # group 32, one super-step per chunk half
-    (12, 40000, 6144, 4, 64, BF16, False, 1),
+    # two k-blocks of stream-K ranges (over 24 tiles a workgroup): parts to the workspace at
+    # the end, second pass
+    (16, 60000, 4096, 4, 64, BF16, True, 1),
+    (16, 60000, 4096, 8, 64, F16, False, 1),
+    (16, 52000, 4096, 4, 32, BF16, False, 1),   # group 32, one super-step per chunk half
+    (12, 60000, 6144, 4, 64, BF16, False, 1),
     # 9..16 rows whose x fits one k-block with a shrunk ring: no second pass
     (13, 40000, 4096, 4, 32, BF16, False, 0),
     (16, 40000, 4096, 4, 128, F16, True, 0),    # g128, a ring of ten slots
@@ -66,7 +67,7 @@ def deinterleave(torch, y, H):
 
 @pytest.mark.parametrize("M,H,K,dt,lb", [(8, 16384, 512, BF16, True), (16, 16384, 512, F16, False),
                                          (1, 20000, 512, BF16, False),
-                                         (16, 20000, 4096, BF16, True)])  # reduce split
+                                         (16, 30000, 4096, BF16, True)])  # reduce split
 def test_burst_gate_up_epilogue(ctx, oracle, M, H, K, dt, lb):
     import torch
     assert ctx.plan(M, 2 * H, K, 4, 64)["burst"] == 1

@@ -85,6 +85,10 @@ ALIGNED_CASES = [
     (16, 4000, 5120, 8, 32, BF16),
     (16, 2000, 4096, 4, 64, BF16),
     (16, 40, 5120, 4, 64, F16),
+    # twenty tiles a workgroup (two k-blocks at 9..16 rows take up to 24)
+    (16, 40000, 4096, 4, 64, BF16),
+    (16, 40000, 4096, 4, 32, F16),
+    (12, 40000, 6144, 8, 64, BF16),
 ]
 
 

@@ -222,12 +222,17 @@ def test_aligned_shapes_take_the_aligned_split(shape):
 
 def test_the_aligned_split_stops_at_twelve_tiles_per_workgroup():
     """Up to twelve tiles per workgroup the aligned split measured faster than the second
-    pass (the 16-row headline shape has nine); from twenty on, slower.  A split whose
+    pass (the 16-row headline shape has nine), and at 9..16 rows over two k-blocks up to
+    twenty-four (twenty at N = 40000); from thirty on, the second pass.  A split whose
     output blocks would not fit in LDS keeps the second pass too."""
     p = make_plan(16, 17408, 5120, 4, 64)
     assert p["aligned"] == 1 and p["reduce"] == 0 and p["nkb"] == 2, p
     assert -(-p["T"] // p["Gkb"]) == 9, p
-    for shape in [(16, 40000, 4096, 4, 64), (16, 151936, 5120, 4, 64)]:
+    for shape in [(16, 40000, 4096, 4, 64), (16, 40000, 4096, 4, 32), (16, 40000, 4096, 8, 64)]:
+        p = make_plan(*shape)
+        assert p["aligned"] == 1 and p["reduce"] == 0 and p["nkb"] == 2, (shape, p)
+        assert -(-p["T"] // p["Gkb"]) == 20, (shape, p)
+    for shape in [(16, 60000, 4096, 4, 64), (13, 80000, 4096, 4, 32), (16, 151936, 5120, 4, 64)]:
         p = make_plan(*shape)
         assert p["aligned"] == 0 and p["reduce"] == 1 and p["nkb"] == 2, (shape, p)
 
@@ -357,7 +362,7 @@ def test_outputs_leave_at_the_end_where_workgroups_hold_many_tiles():
     p = make_plan(8, 5120, 17408, 4, 64)
     assert p["aligned"] == 1 and p["burst"] == 0
     # reduce splits holding many tiles per workgroup leave their parts at the end too
-    for shape in [(16, 40000, 4096, 4, 64), (12, 40000, 6144, 4, 64), (16, 151936, 5120, 4, 64)]:
+    for shape in [(16, 60000, 4096, 4, 64), (12, 60000, 6144, 4, 64), (16, 151936, 5120, 4, 64)]:
         p = make_plan(*shape)
         assert p["reduce"] == 1 and p["burst"] == 1, shape
     # aligned and narrow splits pair every tile: nothing left for the end

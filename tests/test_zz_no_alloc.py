@@ -37,7 +37,7 @@ def noalloc(ctx, c, x, w, s, b, lb, y, stream=None):
 CASES = [
     (12, 17408, 5120, 4, 64, BF16, False, dict(nkb=1, Gkb=256, reduce=0)),
     (8, 17408, 5120, 4, 64, BF16, False, dict(nkb=1, reduce=0)),
-    (16, 40000, 4096, 4, 64, BF16, False, dict(reduce=1)),
+    (16, 60000, 4096, 4, 64, BF16, False, dict(reduce=1)),
     (4, 11008, 11008, 4, 64, F16, True, dict(nkb=1, Gkb=512, reduce=0)),
     (8, 5120, 17408, 4, 64, BF16, True, dict(nkb=3, aligned=1, reduce=0)),
     (16, 4096, 5120, 8, 64, F16, False, dict(nkb=2, reduce=0, nslot_kb=1)),
