@@ -229,14 +229,15 @@ static constexpr int kBurstTiles = 8;
  * 29.6 against 28.8-29.3; N = 60000 (thirty) 42.5 against 38.9-39.3; N = 80000 (forty) 54.2
  * against 48.6-48.8. */
 static constexpr int kAlignedMaxTiles = 12;
-/* ... two k-blocks at 9..16 rows, with four publisher waves: measured on MI355X at K = 4096,
- * 16 rows (us, aligned against the second pass; 4-bit g64 unless stated): N = 40000 (twenty
- * tiles a workgroup) 26.05 against 28.13, 4-bit g32 30.71 against 32.52, 8-bit 39.72
- * against 39.75; N = 60000 (thirty) 37.51 against 38.88 but 4-bit g128 38.29 against 37.49;
- * 13 rows, N = 80000 (forty), 4-bit g32: 56.45 against 55.77. */
+/* Most tiles a workgroup of a two-k-block aligned split holds at 9..16 rows, where four
+ * publisher waves share the exchanges.  Measured on MI355X at K = 4096, 16 rows (us, aligned
+ * against the second pass; 4-bit g64 unless stated): N = 40000 (twenty tiles a workgroup)
+ * 26.05 against 28.13, 4-bit g32 30.71 against 32.52, 8-bit 39.72 against 39.75; N = 60000
+ * (thirty) 37.51 against 38.88 but 4-bit g128 38.29 against 37.49; 13 rows, N = 80000
+ * (forty), 4-bit g32: 56.45 against 55.77. */
 static constexpr int kAligned16MaxTiles = 24;
 /* Most tiles a workgroup of an aligned split of four or more k-blocks (the tree of exchanges)
- * holds at 9..16 rows, where the second pass's split fits one round of workgroups. */
+ * holds at 9..16 rows where the tree needs no more k-blocks than the second pass's split. */
 static constexpr int kAlignedRowsMaxTiles = 8;
 /* Most k-blocks of an aligned split: from four on, each tile's parts meet over a tree of
  * exchanges (k-blocks - 1 of them, ceil(log2 k-blocks) deep), taken where the launch can place
