@@ -22,15 +22,16 @@ def kss(bits, gs):
     return (512 // bits) * ((2 if gs == 128 else 1) if bits == 4 else gs // 32)
 
 
-def sweep_cases(n, seed, nk_min, nk_max, n_max, k_max):
+def sweep_cases(n, seed, nk_min, nk_max, n_max, k_max, m_min=1, k_min=1, whole_chunks=False):
     rng = np.random.default_rng(seed)
     cases = []
     while len(cases) < n:
         bits = int(rng.choice([4, 8]))
         gs = int(rng.choice([32, 64, 128]))
-        M = int(rng.integers(1, 17))
-        step = kss(bits, gs)
-        K = step * int(rng.integers(1, max(2, k_max // step)))
+        M = int(rng.integers(m_min, 17))
+        # whole_chunks: K a multiple of 8 groups, which 9..16 rows take in one launch
+        step = 8 * gs if whole_chunks else kss(bits, gs)
+        K = step * int(rng.integers(max(1, -(-k_min // step)), max(2, k_max // step)))
         N = int(rng.integers(1, n_max))
         if not nk_min <= N * K <= nk_max:
             continue
@@ -40,10 +41,13 @@ def sweep_cases(n, seed, nk_min, nk_max, n_max, k_max):
     return cases
 
 
-# 100 small shapes, and 20 of 12..48 M weights (long K and wide N: several k-blocks, the tree
-# of exchanges, the second pass, one k-block at 9..12 rows)
+# 100 small shapes, 20 of 12..48 M weights (long K and wide N: several k-blocks, the tree
+# of exchanges, the second pass, one k-block at 9..12 rows), and 20 at 9..16 rows with
+# K >= 12288 (two k-blocks of up to 24 whole tiles, trees of four to eight k-blocks)
 CASES = (sweep_cases(100, 20261202, 1, 12_000_000, 6000, 12288)
-         + sweep_cases(20, 1202, 12_000_001, 48_000_000, 40000, 32768))
+         + sweep_cases(20, 1202, 12_000_001, 48_000_000, 40000, 32768)
+         + sweep_cases(20, 31202, 24_000_000, 160_000_000, 16000, 32768, m_min=9, k_min=12288,
+                       whole_chunks=True))
 
 
 @pytest.mark.parametrize("M,N,K,bits,gs,dt,lb", CASES)
